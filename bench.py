@@ -1,0 +1,314 @@
+"""Benchmark of the MI355X hybrid-layer hot path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+
+A step is one forward of the hybrid Mamba layer (BitLinear
+in_proj 1024 -> 4096, causal conv 4 + SiLU, selective scan d_inner 2048 x
+d_state 16 over 32 ragged sequences, gate, BitLinear out_proj 2048 -> 1024;
+bf16 activations, fp32 scan state) over one packed batch already resident in
+HBM.  `value` is tokens/s of the whole layer.  Per-kernel times come from
+stream events recorded between the layer's launches on the launch stream;
+the roofline object is for the kernel with the largest share.  The extra
+figures are the other two parts of the metric: the prefill ternary GEMM
+(config 3) in int8 TOPS and the HBM-bound kernels (decode GEMV over 128
+rotated weight sets, the decode step over 8 rotated state buffers) in GB/s.
+The CPU baseline is the oracle's restatement of the reference CPU path on a
+bounded sample of the same workload, timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _bf16(torch, a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).to(dev)
+
+
+def _f32(torch, a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+class StageTimer:
+    """Records a stream event after each kernel; per-stage durations per step."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.events = []
+
+    def start(self):
+        ev = self.torch.cuda.Event(enable_timing=True)
+        ev.record()
+        self.events.append(("start", ev))
+
+    def __call__(self, name):
+        ev = self.torch.cuda.Event(enable_timing=True)
+        ev.record()
+        self.events.append((name, ev))
+
+    def totals_ms(self):
+        out = {}
+        for (_, a), (name, b) in zip(self.events[:-1], self.events[1:]):
+            if name == "start":
+                continue
+            out[name] = out.get(name, 0.0) + a.elapsed_time(b)
+        return out
+
+
+def bench_layer(torch, dev, steps, warmup):
+    from reimagined_amd import workloads
+    from reimagined_amd.layers import HybridMambaLayer
+
+    params, inp = workloads.config4()
+    T = int(inp["cu_seqlens"][-1])
+    layer = HybridMambaLayer(params, dev, rms_input=True)
+    x = _bf16(torch, inp["x"], dev)
+    dt = _bf16(torch, inp["dt"], dev)
+    B = _bf16(torch, inp["B"], dev)
+    C = _bf16(torch, inp["C"], dev)
+    cu = _f32(torch, inp["cu_seqlens"], dev)
+    fin = torch.empty((cu.numel() - 1, layer.d_inner, layer.d_state), dtype=torch.float32,
+                      device=dev)
+    for _ in range(warmup):
+        layer.forward(x, dt, B, C, cu, final_state=fin)
+    torch.cuda.synchronize()
+    _log(f"layer warm: T={T}")
+    # wall-clock timed region: K steps, no per-kernel events
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        layer.forward(x, dt, B, C, cu, final_state=fin)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    # per-kernel breakdown: the same K steps with an event after every launch
+    timer = StageTimer(torch)
+    for _ in range(steps):
+        timer.start()
+        layer.forward(x, dt, B, C, cu, final_state=fin, marker=timer)
+    torch.cuda.synchronize()
+    stages = {k: v / steps for k, v in timer.totals_ms().items()}
+    return T, wall, stages, params, inp
+
+
+def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=32):
+    """Algorithmic work of each layer kernel per launch (bytes or int8 ops)."""
+    work = {
+        "in_proj_gemm": ("mfma", 2.0 * T * (2 * d_inner) * d_model),
+        "out_proj_gemm": ("mfma", 2.0 * T * d_model * d_inner),
+        # bf16 x, dt, z in + y out per (token, channel); B, C per token; fp32 final state
+        "scan": ("hbm", T * d_inner * 2 * 4 + T * d_state * 2 * 2 + num_seqs * d_inner * d_state * 4
+                 + d_inner * d_state * 4 + d_inner * 4),
+        # bf16 x in (strided) + bf16 out per (token, channel)
+        "conv": ("hbm", T * d_inner * 2 * 2),
+        "in_proj_quant": ("hbm", T * d_model * (2 + 2 + 1) + T * 8),
+        "out_proj_quant": ("hbm", T * d_inner * (2 + 2 + 1) + T * 8),
+    }
+    name = max((k for k in stages if k in work), key=lambda k: stages[k])
+    bound, amount = work[name]
+    sec = stages[name] / 1e3
+    if bound == "mfma":
+        achieved = amount / sec / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None,
+                "kernel": name, "note": "int8 ops (TOPS) against the dense int8 MFMA peak"}
+    else:
+        achieved = amount / sec / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": name}
+    return roof, work
+
+
+def bench_prefill_gemm(torch, dev, reps=20):
+    from reimagined_amd import ops, workloads
+    M, K, N = 4096, 2048, 8192
+    c3 = workloads.config3(M=M, K=K, N=N)
+    packed, ws = ops.pack_ternary(c3["w"])
+    pk = torch.from_numpy(packed.view(np.int32)).to(dev)
+    x = _f32(torch, c3["x"], dev)
+    q, s = ops.quantize_activations_bitnet(x, 8)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    from reimagined_amd._lib import call
+    from reimagined_amd.ops import _p, _stream
+
+    def run():
+        call("nsosx_ternary_gemm_path", _p(q), _p(s), _p(pk), ws, M, K, N, None, None, _p(y), 1,
+             None, 1, _stream())
+    for _ in range(3):
+        run()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    tops = 2.0 * M * N * K / (ms / 1e3) / 1e12
+    return {"shape": [M, K, N], "ms": round(ms, 4), "tops": round(tops, 1),
+            "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+
+
+def bench_decode_gemv(torch, dev, m=1, sets=128, reps=5):
+    """Grouped GEMV over `sets` distinct copies of the config-3 weight shape (> MALL)."""
+    from reimagined_amd import ops
+    K, N = 2048, 8192
+    rng = np.random.default_rng(31)
+    words = N * K // 16
+    # distinct random packed sets generated on the device; a reserved code 3 (both bits
+    # set) is turned into code 1 so every word is a valid ternary pattern
+    packed = torch.randint(-2**31, 2**31 - 1, (sets, words), dtype=torch.int32, device=dev)
+    both = packed & (packed >> 1) & 0x55555555
+    packed = (packed ^ (both << 1)).contiguous()
+    views = ops.LinearViewArray([(packed[i], 1.0, K, N, None, None) for i in range(sets)], dev)
+    q = torch.from_numpy(rng.integers(-127, 128, size=(sets, m, K)).astype(np.int8)).to(dev)
+    s = torch.full((sets, m), 0.01, dtype=torch.float32, device=dev)
+    y = torch.empty((sets, m, N), dtype=torch.bfloat16, device=dev)
+    from reimagined_amd._lib import call
+    from reimagined_amd.ops import _p, _stream
+
+    def run():
+        call("nsosx_grouped_gemv", views.ptr, sets, _p(q), m * K, _p(s), m, m, _p(y), m * N, 1,
+             _stream())
+    run()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    bytes_ = sets * (N * K / 4 + m * K + m * N * 2)
+    gbs = bytes_ / (ms / 1e3) / 1e9
+    return {"m": m, "weight_sets": sets, "bytes_per_launch": int(bytes_), "ms": round(ms, 4),
+            "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def bench_decode_step(torch, dev, reps=8):
+    from reimagined_amd import ops, workloads
+    _, dec = workloads.config5(rows=16, experts=2, d_model=64, d_ff=64)
+    R, Dm, N = dec["state"].shape
+    x, dt, z = (_bf16(torch, dec[k], dev) for k in ("x", "dt", "z"))
+    B, C = _bf16(torch, dec["B"], dev), _bf16(torch, dec["C"], dev)
+    a_log, Dk = _f32(torch, dec["a_log"], dev), _f32(torch, dec["D"], dev)
+    states = [_f32(torch, dec["state"], dev) for _ in range(8)]
+    for st in states:
+        ops.selective_scan_step(x, dt, a_log, B, C, Dk, z, st, Dm, 1, N, 1)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(reps * len(states)):
+        ops.selective_scan_step(x, dt, a_log, B, C, Dk, z, states[i % len(states)], Dm, 1, N, 1)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / (reps * len(states))
+    bytes_ = R * Dm * N * 4 * 2 + R * Dm * 2 * 4 + R * N * 2 * 2
+    gbs = bytes_ / (ms / 1e3) / 1e9
+    return {"rows": R, "ms": round(ms, 4), "gbs": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def cpu_baseline(params, inp, seq_tokens=1024):
+    """The oracle's C4 layer on one sequence of `seq_tokens` tokens (fp32 on bf16 inputs)."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import oracle as orc
+    import torch
+    r = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).float().numpy()
+    T = seq_tokens
+    x = r(inp["x"][:T])
+    dt = r(inp["dt"][:T])
+    B, C = r(inp["B"][:T]), r(inp["C"][:T])
+    cu = np.array([0, T], np.int32)
+    pin, wsi, _ = orc.pack_weights(params["w_in"])
+    pout, wso, _ = orc.pack_weights(params["w_out"])
+    di = params["w_out"].shape[1]
+    n = params["a_log"].shape[1]
+    t0 = time.perf_counter()
+    xz = orc.bitlinear_forward(x, pin, wsi, 2 * di, rms_input=True)
+    xc = orc.conv1d_causal(np.ascontiguousarray(xz[:, :di]), params["conv_w"], cu,
+                           bias=params["conv_b"], silu_act=True)
+    ys, _ = orc.selective_scan(xc, dt, params["a_log"], B, C, params["d_skip"],
+                               np.ascontiguousarray(xz[:, di:]), cu, di, 1, n, 1)
+    orc.bitlinear_forward(ys, pout, wso, params["w_out"].shape[0], rms_input=True)
+    sec = time.perf_counter() - t0
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(T / sec, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"one sequence of {T} tokens through the config-4 layer (in_proj, conv, "
+                      f"scan, out_proj) in {sec:.2f} s; int8 GEMM and scan single-threaded as "
+                      f"in the reference, row quantization/RMSNorm OpenMP"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the hot path's kernels run on one MI355X; "
+              "multi-GPU sharding is a design note only", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    import reimagined_amd
+    reimagined_amd.lib()
+    _log("library loaded")
+    T, wall, stages, params, inp = bench_layer(torch, dev, args.steps, args.warmup)
+    ms_step = wall / args.steps * 1e3
+    roof, _ = layer_roofline(T, stages)
+    _log(f"layer: {ms_step:.3f} ms/step, stages {stages}")
+    extra = {}
+    if not args.no_extra:
+        extra["prefill_gemm_c3"] = bench_prefill_gemm(torch, dev)
+        _log(f"prefill gemm {extra['prefill_gemm_c3']}")
+        extra["decode_gemv_c3_m1"] = bench_decode_gemv(torch, dev, m=1)
+        _log(f"decode gemv {extra['decode_gemv_c3_m1']}")
+        extra["decode_step_c5"] = bench_decode_step(torch, dev)
+        _log(f"decode step {extra['decode_step_c5']}")
+        sc = stages.get("scan")
+        if sc:
+            _, work = layer_roofline(T, {"scan": sc})
+            gbs = work["scan"][1] / (sc / 1e3) / 1e9
+            extra["scan_c4"] = {"ms": round(sc, 4), "gbs": round(gbs, 1),
+                                "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    cpu = None if args.no_cpu else cpu_baseline(params, inp)
+    if cpu:
+        _log(f"cpu baseline {cpu}")
+    line = {
+        "metric": "hybrid-layer tokens/s; ternary GEMM int8 TOPS; scan HBM GB/s vs peak",
+        "value": round(T * args.steps / wall, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 GEMM (int32 acc) + fp32 scan, bf16 I/O",
+        "data": "synthetic (seeded; ternary weights uniform {-1,0,+1}, random-init)",
+        "config": {"workload": "config 4: hybrid Mamba layer d_model 1024, d_inner 2048, "
+                               "d_state 16, conv 4, 32 ragged sequences U[64,2048]",
+                   "tokens": T, "num_seqs": 32, "rms_peri": True},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "stages_ms": {k: round(v, 4) for k, v in stages.items()},
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

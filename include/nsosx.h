@@ -1,0 +1,232 @@
+/*
+ * nsosx.h -- C ABI of the MI355X (gfx950) hybrid-layer hot path.
+ *
+ * Plain pointers and sizes, no torch or C++ types.  Every device pointer is a
+ * HIP device address; `stream` is a hipStream_t passed as void* (NULL = the
+ * null stream).  Every call enqueues work on `stream` and returns without
+ * synchronising; buffers are owned by the caller and must stay alive until
+ * the enqueued work has finished.  Every entry point returns an nsosx_status;
+ * on any status other than NSOSX_OK nothing was enqueued and no output was
+ * touched.
+ *
+ * Citations are into OXN/nsos/ of vitorGgC569/reimagined and name the
+ * reference interface each entry point replaces.
+ *
+ * Data formats shared with the reference:
+ *   packed ternary weights  uint32 words, 16 codes per word, code j of a word
+ *                           at bits 2j; -1 -> 0, 0 -> 1, +1 -> 2; flat over
+ *                           the row-major [N, K] matrix; K % 16 == 0 so rows
+ *                           are word-aligned.  Code 3 is reserved and decodes
+ *                           to 0 (src/bitnet_adapter.cpp:31,570-606).
+ *   activation codes        int8 [M, K] row-major, |code| <= 127.
+ *   act_scale               float [M], (max|x| + 1e-8f) / q_max.
+ */
+#ifndef NSOSX_H
+#define NSOSX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum nsosx_status {
+    NSOSX_OK = 0,
+    NSOSX_ERR_INVALID = 1,   /* bad shape, null pointer or argument range */
+    NSOSX_ERR_OVERFLOW = 2,  /* size product exceeds what the kernels index */
+    NSOSX_ERR_RESERVED = 3,  /* packed weights hold the reserved code 3 */
+    NSOSX_ERR_LAUNCH = 4,    /* the HIP runtime refused a launch or copy */
+} nsosx_status;
+
+typedef enum nsosx_dtype {
+    NSOSX_F32 = 0,
+    NSOSX_BF16 = 1,
+} nsosx_dtype;
+
+/* Last error text of the calling thread (never NULL). */
+const char* nsosx_last_error(void);
+/* Library version string. */
+const char* nsosx_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Host-side weight preparation (CPU, no device work).
+ * ------------------------------------------------------------------------- */
+
+/* BitLinear::pack_weights + quantize_weights (src/bitlinear.cpp:152-193,
+ * 1359-1379): weight_scale = float(sum|w| / n in double) + 1e-8f; code = +1
+ * if w/(weight_scale+1e-8f) > 0.5, -1 if < -0.5, else 0; packed as above.
+ * w: float [N, K] host; packed: uint32 [N*K/16] host. */
+int nsosx_pack_ternary(const float* w, int N, int K, uint32_t* packed, float* weight_scale);
+
+/* BitNetAdapter::unpack_weights_microsoft_style_to_i8
+ * (src/bitnet_adapter.cpp:590-606): codes int8 [n] host. */
+int nsosx_unpack_ternary(const uint32_t* packed, int64_t n, int8_t* codes);
+
+/* Import check of BitLinear::import_packed_state (src/bitlinear.cpp:876-885),
+ * on the device: *first_bad (device int64) receives the index of the first
+ * reserved code, or -1.  Pre-upload weights go through this once. */
+int nsosx_find_reserved_code(const uint32_t* packed, int64_t n_codes, int64_t* first_bad,
+                             void* stream);
+
+/* ---------------------------------------------------------------------------
+ * BitLinear activations and ternary GEMM.
+ * ------------------------------------------------------------------------- */
+
+/* BitLinear::quantize_activations_bitnet on an AVX2 host
+ * (src/bitlinear.cpp:240-291, src/bitlinear_quantize_avx2.cpp:65-103) plus the
+ * GEMM's int8 clamp (src/bitnet_adapter_avx2.cpp:95-126); optionally preceded
+ * by the RMS_PERI input norm (src/bitlinear.cpp:460-466 -> Tensor::rmsnorm,
+ * src/tensor.cpp:3455-3492, eps 1e-6).  Replaces
+ * launch_quantize_activations_bitnet_kernel (include/cuda/kernels.cuh).
+ *   x: [M, K] f32 or bf16 (x_dtype), q: int8 [M, K], act_scale: f32 [M].
+ *   bits in [2, 8]; rms_input 0/1.
+ *   rms_workspace: f32 [M] device scratch, required when rms_input != 0. */
+int nsosx_quantize_act_i8(const void* x, int x_dtype, int M, int K, int bits, int rms_input,
+                          int8_t* q, float* act_scale, float* rms_workspace, void* stream);
+
+/* Integer core + dequantizing epilogue of BitNetAdapter::gemm_158bit_i8
+ * (src/bitnet_adapter.cpp:520-568, src/bitnet_adapter_avx2.cpp:52-158):
+ *   acc[m,n] = sum_k q[m,k] * w[n,k]                       (exact int32)
+ *   y[m,n]   = float(acc) * (act_scale[m] * weight_scale)
+ *              then * magnitude[n] and + bias[n] (one fma when both are given)
+ * Replaces launch_bitnet_gemm / launch_bitnet_gemv_scaled /
+ * launch_bitnet_apply_act_scales_kernel (include/cuda/kernels.cuh:106-110).
+ * M <= 8 runs the packed-weight streaming GEMV, larger M the int8 MFMA GEMM.
+ *   y: [M, N] f32 or bf16 (y_dtype), may be NULL when acc_out is given.
+ *   acc_out: int32 [M, N] or NULL (exposes the accumulators).
+ *   magnitude, bias: f32 [N] or NULL. */
+int nsosx_ternary_gemm(const int8_t* q, const float* act_scale, const uint32_t* packed,
+                       float weight_scale, int M, int K, int N, const float* magnitude,
+                       const float* bias, void* y, int y_dtype, int32_t* acc_out, void* stream);
+
+/* Same contract, forcing one kernel: path 0 = streaming GEMV (M <= 8),
+ * path 1 = MFMA GEMM (any M).  For tests and measurement. */
+int nsosx_ternary_gemm_path(const int8_t* q, const float* act_scale, const uint32_t* packed,
+                            float weight_scale, int M, int K, int N, const float* magnitude,
+                            const float* bias, void* y, int y_dtype, int32_t* acc_out,
+                            int path, void* stream);
+
+/* bitnet_gemm_158bit_gpu (include/bitnet_gpu_dispatch.h:46-51,
+ * src/bitnet_gpu_dispatch.cpp:65-174): quantize x then ternary GEMM.
+ * q_workspace: int8 [M, K]; scale_workspace: f32 [M];
+ * rms_workspace: f32 [M] (only with rms_input). */
+int nsosx_bitlinear_forward(const void* x, int x_dtype, const uint32_t* packed,
+                            float weight_scale, int M, int K, int N, int precision_bits,
+                            int rms_input, const float* magnitude, const float* bias, void* y,
+                            int y_dtype, int8_t* q_workspace, float* scale_workspace,
+                            float* rms_workspace, void* stream);
+
+/* One borrowed descriptor per weight set, the C shape of nsos::GpuLinearView
+ * (include/gpu_linear_view.h:8-26) restricted to the packed path. */
+typedef struct nsosx_linear_view {
+    const uint32_t* packed;   /* device, [outputs * inputs / 16] */
+    const float* magnitude;   /* device [outputs] or NULL */
+    const float* bias;        /* device [outputs] or NULL */
+    int inputs;
+    int outputs;
+    float weight_scale;
+} nsosx_linear_view;
+
+/* Grouped decode GEMV: `groups` independent ternary GEMVs in one launch, the
+ * role of launch_grouped_decode_projections (include/cuda/kernels.cuh:27-29).
+ * Group g multiplies q + g*q_stride (int8 [M, inputs]) with views[g] and
+ * writes y + g*y_stride elements ([M, outputs], y_dtype).  All views share
+ * `inputs`; M <= 8.  views: host array, copied into the launch arguments
+ * through `views_dev` (device array of `groups` descriptors the caller
+ * uploaded with nsosx_upload_views or its own copy). */
+int nsosx_grouped_gemv(const nsosx_linear_view* views_dev, int groups, const int8_t* q,
+                       int64_t q_stride, const float* act_scale, int64_t scale_stride, int M,
+                       void* y, int64_t y_stride, int y_dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Mamba selective scan.
+ * ------------------------------------------------------------------------- */
+
+/* Depthwise causal convolution restarted at every cu_seqlens boundary, plus
+ * bias and SiLU (src/mamba2.cpp:1056-1076, 2437-2446):
+ *   out[t,c] = silu(bias[c] + sum_{j<W} w[c,j] * in[t-(W-1)+j, c])
+ * in: [T, channels] with row stride in_stride elements (in_dtype);
+ * out: [T, channels] contiguous (out_dtype).  w: f32 [channels, W]. */
+int nsosx_conv1d_causal(const void* in, int in_dtype, int64_t in_stride, const float* weight,
+                        const float* bias, const int32_t* cu_seqlens, int num_seqs,
+                        int total_tokens, int channels, int width, int apply_silu, void* out,
+                        int out_dtype, void* stream);
+
+/* Packed ragged selective-scan forward: the faithful recurrence of
+ * src/mamba2.cpp:2602-2675 (GPU twin src/cuda/mamba_kernels.cu:1690-1754)
+ * with the decay of mamba_decay_terms (src/mamba2.cpp:443-473), generalised
+ * to A_log per (head, state) when a_per_state != 0 (Mamba-1 A[D, N]).
+ * For each sequence s (tokens cu_seqlens[s] .. cu_seqlens[s+1]-1), head h,
+ * channel c = h*P + p, state n, group g = h*G/H:
+ *   delta = softplus(dt[t,h]);  decay = exp(-delta * exp(A_log[h(,n)]))
+ *   state = decay * state + (delta * B[t,g,n]) * x[t,c]
+ *   y[t,c] = D[h] * x[t,c] + sum_n state * C[t,g,n]
+ *   y[t,c] *= silu(z[t,c])                              (when z != NULL)
+ * Layouts (row-major, act_dtype for x, dt, B, C, z, y; f32 for the rest):
+ *   x, z, y [T, H*P] with row strides x_stride, z_stride (y contiguous);
+ *   dt [T, H]; B, C [T, G*N]; A_log [H] or [H, N]; D [H];
+ *   initial_state, final_state f32 [num_seqs, H*P, N] or NULL.
+ * N <= 64. */
+int nsosx_selective_scan_fwd(const void* x, int64_t x_stride, const void* dt, const float* A_log,
+                             int a_per_state, const void* B, const void* C, const float* D,
+                             const void* z, int64_t z_stride, const int32_t* cu_seqlens,
+                             int num_seqs, int total_tokens, int H, int P, int N, int G,
+                             int act_dtype, const float* initial_state, float* final_state,
+                             void* y, void* stream);
+
+/* Decode step over `rows` independent sequences, one token each, state
+ * updated in place (src/mamba2.cpp:4038-4125; GPU twin
+ * launch_mamba2_faithful_step, src/cuda/mamba_kernels.cu:3332-3419).
+ * x, z, y [rows, H*P]; dt [rows, H]; B, C [rows, G*N] (act_dtype);
+ * state f32 [rows, H*P, N]. */
+int nsosx_selective_scan_step(const void* x, const void* dt, const float* A_log, int a_per_state,
+                              const void* B, const void* C, const float* D, const void* z,
+                              int rows, int H, int P, int N, int G, int act_dtype, float* state,
+                              void* y, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Top-k MoE routing.
+ * ------------------------------------------------------------------------- */
+
+/* MoERouter::forward from logits (src/jamba.cpp:8140-8319): softmax
+ * (src/tensor.cpp:3428-3450), top-k by (probability desc, index asc),
+ * renormalised by 1/max(sum, 1e-9f); then the expert-major, rows-ascending
+ * dispatch of JambaBlock::forward_moe (src/jamba.cpp:3882-3894).
+ *   logits f32 [rows, E]; weights f32 [rows, E] (masked, renormalised);
+ *   selected int32 [rows, k] (rank order); counts int32 [E];
+ *   offsets int32 [E+1] (exclusive scan); perm int32 [rows*k] (slot -> row);
+ *   slot_of int32 [rows, k]: slot of the row's r-th selected expert, ordered
+ *   by ascending expert id (the combine order).
+ *   workspace: int32, nsosx_moe_route_workspace(rows, E) elements.
+ * E <= 64, k <= E. */
+int64_t nsosx_moe_route_workspace(int rows, int experts);
+int nsosx_moe_route(const float* logits, int rows, int experts, int k, float* weights,
+                    int32_t* selected, int32_t* counts, int32_t* offsets, int32_t* perm,
+                    int32_t* slot_of, int32_t* workspace, void* stream);
+
+/* Grouped ternary GEMM over expert segments: for each expert e the rows
+ * perm[offsets[e] .. offsets[e+1]) of q (int8 [rows_in, K], gathered through
+ * perm when gather != 0, else read as the slot-ordered q itself) multiply
+ * views[e]; the result goes to slot order y [slots, N] with the view's
+ * epilogue and then, when squared_relu != 0, max(v,0)^2 (Tensor::squared_relu,
+ * src/tensor.cpp:3209-3226).  act_scale is indexed like q.
+ * offsets is a device array; max_rows_per_expert bounds the launch grid. */
+int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, int experts,
+                               const int32_t* offsets, const int32_t* perm, int gather,
+                               const int8_t* q, const float* act_scale, int K, int N,
+                               int max_rows_per_expert, int squared_relu, void* y, int y_dtype,
+                               void* stream);
+
+/* Weighted combine in ascending expert order (src/jamba.cpp:3947-3969):
+ * out[r] = sum over the row's selected experts, lowest id first, of
+ * expert_out[slot] * weights[r, e], starting from 0.
+ * expert_out [slots, dim] (in_dtype), out [rows, dim] (out_dtype). */
+int nsosx_moe_combine(const void* expert_out, int in_dtype, const int32_t* slot_of,
+                      const int32_t* selected, const float* weights, int rows, int experts, int k,
+                      int dim, void* out, int out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSOSX_H */

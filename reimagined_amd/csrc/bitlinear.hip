@@ -1,0 +1,803 @@
+// BitLinear hot path on gfx950: activation quantization, the packed-weight
+// streaming GEMV (decode) and the int8-MFMA GEMM (prefill, grouped experts).
+//
+// Reference semantics (OXN/nsos/ of vitorGgC569/reimagined):
+//   quantization  src/bitlinear.cpp:240-291, src/bitlinear_quantize_avx2.cpp:65-103
+//   RMS_PERI norm src/bitlinear.cpp:460-466, src/tensor.cpp:3455-3492
+//   GEMM + affine src/bitnet_adapter_avx2.cpp:52-158
+//   packed format src/bitnet_adapter.cpp:570-606
+#include "common.hpp"
+
+#include <algorithm>
+#include <cmath>
+
+namespace nsosx {
+
+// ===========================================================================
+// RMS_PERI: inv[r] = 1 / sqrt(sum_sq / K + eps) with the float sum taken in
+// index order (rounded square, then add) as the reference's sequential loop
+// does; a remainder of K % 4 elements is accumulated with fma, which is how
+// that loop is compiled.  Lane r of a wave owns row r of a 64-row block; the
+// block is staged through LDS 64 columns at a time so the global loads stay
+// coalesced while each lane walks its own row in order.
+// ===========================================================================
+template <int DT>
+__global__ __launch_bounds__(64) void rms_inv_kernel(const void* __restrict__ x, int M, int K,
+                                                     float eps, float* __restrict__ inv) {
+    __shared__ float tile[64][65];
+    const int lane = threadIdx.x;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int row = static_cast<int>(row0) + lane;
+    const int body = K & ~3;
+    float sum = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += 64) {
+        const int kc = min(64, K - k0);
+        for (int r = 0; r < 64; ++r) {
+            float v = 0.0f;
+            if (row0 + r < M && lane < kc) v = load_act<DT>(x, (row0 + r) * K + k0 + lane);
+            tile[r][lane] = v;
+        }
+        __syncthreads();
+        for (int j = 0; j < kc; ++j) {
+            const float v = tile[lane][j];
+            if (k0 + j < body) {
+                sum = __fadd_rn(sum, __fmul_rn(v, v));
+            } else {
+                sum = __fmaf_rn(v, v, sum);
+            }
+        }
+        __syncthreads();
+    }
+    if (row < M) {
+        const float mean = __fdiv_rn(sum, static_cast<float>(K > 1 ? K : 1));
+        inv[row] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    }
+}
+
+// ===========================================================================
+// Per-row absmax quantization, one wave per row.
+//   m = max|x|; s = q_max / (m + 1e-8f); act_scale = (m + 1e-8f) / q_max;
+//   code = round(x * s), ties to even for the first K & ~7 elements (the
+//   AVX2 body) and half away from zero for the K % 8 tail (std::round);
+//   int8 = clamp(code, -127, 127).
+// VEC: K % 8 == 0, every row 16-byte aligned -> 8 elements per lane-load,
+// the row kept in registers between the two passes when K <= 4096.
+// ===========================================================================
+template <int DT>
+__device__ __forceinline__ void load8(const void* x, int64_t off, float v[8]) {
+    if constexpr (DT == NSOSX_F32) {
+        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + off);
+        const float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const uint4 a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + off);
+        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t pack4_i8(float a, float b, float c, float d) {
+    const uint32_t ia = static_cast<uint32_t>(static_cast<int>(a)) & 0xffu;
+    const uint32_t ib = static_cast<uint32_t>(static_cast<int>(b)) & 0xffu;
+    const uint32_t ic = static_cast<uint32_t>(static_cast<int>(c)) & 0xffu;
+    const uint32_t id = static_cast<uint32_t>(static_cast<int>(d)) & 0xffu;
+    return ia | (ib << 8) | (ic << 16) | (id << 24);
+}
+
+__device__ __forceinline__ float clamp127(float c) { return fminf(fmaxf(c, -127.0f), 127.0f); }
+
+template <int DT, bool RMS>
+__global__ __launch_bounds__(256) void quantize_rows_vec_kernel(
+    const void* __restrict__ x, int M, int K, float q_max, const float* __restrict__ rms_inv,
+    int8_t* __restrict__ q, float* __restrict__ act_scale) {
+    constexpr int kMaxChunks = 8;  // 8 chunks x 8 elements x 64 lanes = 4096 (K <= 4096)
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int64_t base = static_cast<int64_t>(row) * K;
+    const float inv = RMS ? rms_inv[row] : 1.0f;
+    float v[kMaxChunks][8];
+    float m = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+        const int e0 = (c * kWave + lane) * 8;
+        if (e0 < K) {
+            load8<DT>(x, base + e0, v[c]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[c][j] = 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (RMS) v[c][j] = __fmul_rn(v[c][j], inv);
+            m = fmaxf(m, fabsf(v[c][j]));
+        }
+    }
+    m = wave_max(m);
+    const float denom = __fadd_rn(m, 1e-8f);
+    const float s = __fdiv_rn(q_max, denom);
+    if (lane == 0) act_scale[row] = __fdiv_rn(denom, q_max);
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+        const int e0 = (c * kWave + lane) * 8;
+        if (e0 < K) {
+            float code[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) code[j] = clamp127(rintf(__fmul_rn(v[c][j], s)));
+            uint2 out;
+            out.x = pack4_i8(code[0], code[1], code[2], code[3]);
+            out.y = pack4_i8(code[4], code[5], code[6], code[7]);
+            *reinterpret_cast<uint2*>(q + base + e0) = out;
+        }
+    }
+}
+
+// Any K: element-wise loads, the ties-to-even body / half-away tail split.
+template <int DT, bool RMS>
+__global__ __launch_bounds__(256) void quantize_rows_generic_kernel(
+    const void* __restrict__ x, int M, int K, float q_max, const float* __restrict__ rms_inv,
+    int8_t* __restrict__ q, float* __restrict__ act_scale) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const int64_t base = static_cast<int64_t>(row) * K;
+    const float inv = RMS ? rms_inv[row] : 1.0f;
+    float m = 0.0f;
+    for (int j = lane; j < K; j += kWave) {
+        float t = load_act<DT>(x, base + j);
+        if (RMS) t = __fmul_rn(t, inv);
+        m = fmaxf(m, fabsf(t));
+    }
+    m = wave_max(m);
+    const float denom = __fadd_rn(m, 1e-8f);
+    const float s = __fdiv_rn(q_max, denom);
+    if (lane == 0) act_scale[row] = __fdiv_rn(denom, q_max);
+    const int body = K & ~7;
+    for (int j = lane; j < K; j += kWave) {
+        float t = load_act<DT>(x, base + j);
+        if (RMS) t = __fmul_rn(t, inv);
+        const float val = __fmul_rn(t, s);
+        const float code = j < body ? rintf(val) : roundf(val);
+        q[base + j] = static_cast<int8_t>(static_cast<int>(clamp127(code)));
+    }
+}
+
+static float q_max_for_bits(int bits) {
+    if (bits <= 2) return 1.0f;
+    return static_cast<float>((1 << (bits - 1)) - 1);
+}
+
+template <int DT>
+static int launch_quantize(const void* x, int M, int K, int bits, int rms_input, int8_t* q,
+                           float* act_scale, float* rms_ws, hipStream_t st) {
+    const float qm = q_max_for_bits(bits);
+    if (rms_input) {
+        hipLaunchKernelGGL(rms_inv_kernel<DT>, dim3((M + 63) / 64), dim3(64), 0, st, x, M, K,
+                           1e-6f, rms_ws);
+    }
+    const int elem = DT == NSOSX_F32 ? 4 : 2;
+    const bool vec = (K % 8 == 0) && K <= 4096 && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(q) % 8 == 0) && ((int64_t)K * elem) % 16 == 0;
+    const dim3 grid((M + 3) / 4), block(256);
+    if (vec) {
+        if (rms_input)
+            hipLaunchKernelGGL((quantize_rows_vec_kernel<DT, true>), grid, block, 0, st, x, M, K,
+                               qm, rms_ws, q, act_scale);
+        else
+            hipLaunchKernelGGL((quantize_rows_vec_kernel<DT, false>), grid, block, 0, st, x, M, K,
+                               qm, rms_ws, q, act_scale);
+    } else {
+        if (rms_input)
+            hipLaunchKernelGGL((quantize_rows_generic_kernel<DT, true>), grid, block, 0, st, x, M,
+                               K, qm, rms_ws, q, act_scale);
+        else
+            hipLaunchKernelGGL((quantize_rows_generic_kernel<DT, false>), grid, block, 0, st, x, M,
+                               K, qm, rms_ws, q, act_scale);
+    }
+    return check_launch("quantize_act");
+}
+
+// ===========================================================================
+// Streaming GEMV (M <= 8).  A row of W is K/16 words; a lane takes a chunk
+// of 4 words (64 weights, one 16-byte load) and LPR lanes share a row, LPR
+// the smallest power of two >= K/64 (capped at 64), so one wave-load covers
+// 64/LPR rows.  The lane's activation chunk is byte-transposed into the
+// unpack order once and reused for every row the wave visits; partial sums
+// meet in a butterfly over the row's lanes.
+// ===========================================================================
+struct GemvProblem {
+    const uint32_t* packed;
+    const float* mag;
+    const float* bias;
+    float ws;
+    int N;
+    int K;
+};
+
+// Exact int32 accumulators of the streaming GEMV for K > 4096 rows are summed
+// over chunk rounds before the epilogue: this variant keeps the accumulators
+// of one row step across all rounds (rows outer, chunks inner).
+template <int MT, int YDT, bool ACC_OUT>
+__device__ __forceinline__ void gemv_body_long(const GemvProblem& pb,
+                                               const int8_t* __restrict__ q,
+                                               const float* __restrict__ act_scale, int M,
+                                               void* y, int32_t* acc_out, int wave_id,
+                                               int num_waves) {
+    const int lane = threadIdx.x & 63;
+    const int W16 = pb.K >> 4;
+    const int cpr = (W16 + 3) >> 2;
+    int lpr = 1;
+    while (lpr < cpr && lpr < 64) lpr <<= 1;
+    const int rpw = 64 / lpr;
+    const int lr = lane & (lpr - 1);
+    const int sub = lane / lpr;
+    const bool aligned16 = (W16 & 3) == 0;
+    const int nsteps = (pb.N + rpw - 1) / rpw;
+    const bool single_round = cpr <= lpr;
+
+    // X fragments of the first (often only) chunk round stay in registers
+    uint32_t xa[MT][4][4];
+    {
+        const int c = lr;
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                uint32_t d[4] = {0u, 0u, 0u, 0u};
+                const int k = c * 64 + g * 16;
+                if (c < cpr && mi < M && k < pb.K) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(q + (int64_t)mi * pb.K + k);
+                    d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+                }
+                transpose16(d, xa[mi][g]);
+            }
+    }
+
+    for (int step = wave_id; step < nsteps; step += num_waves) {
+        const int n = step * rpw + sub;
+        int acc[MT];
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi) acc[mi] = 0;
+        for (int c = lr; c < cpr; c += lpr) {
+            uint32_t w[4] = {0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u};
+            if (n < pb.N) {
+                const uint32_t* src = pb.packed + (int64_t)n * W16 + c * 4;
+                if (aligned16 && c * 4 + 3 < W16) {
+                    const uint4 v = load_stream16(src);
+                    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (c * 4 + i < W16) w[i] = src[i];
+                }
+            }
+            uint32_t xr[MT][4][4];
+            if (single_round || c == lr) {
+#pragma unroll
+                for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+#pragma unroll
+                        for (int s = 0; s < 4; ++s) xr[mi][g][s] = xa[mi][g][s];
+            } else {
+#pragma unroll
+                for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        uint32_t d[4] = {0u, 0u, 0u, 0u};
+                        const int k = c * 64 + g * 16;
+                        if (mi < M && k < pb.K) {
+                            const uint4 v =
+                                *reinterpret_cast<const uint4*>(q + (int64_t)mi * pb.K + k);
+                            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+                        }
+                        transpose16(d, xr[mi][g]);
+                    }
+            }
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                uint32_t wv[4];
+                unpack_word(w[g], wv);
+#pragma unroll
+                for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) acc[mi] = sdot4(wv[s], xr[mi][g][s], acc[mi]);
+            }
+        }
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi)
+            for (int o = lpr >> 1; o > 0; o >>= 1) acc[mi] += __shfl_xor(acc[mi], o, kWave);
+        if (lr == 0 && n < pb.N) {
+#pragma unroll
+            for (int mi = 0; mi < MT; ++mi) {
+                if (mi < M) {
+                    if (ACC_OUT) acc_out[(int64_t)mi * pb.N + n] = acc[mi];
+                    if (y) {
+                        const float comb = __fmul_rn(act_scale[mi], pb.ws);
+                        store_act<YDT>(y, (int64_t)mi * pb.N + n,
+                                       dequant(acc[mi], comb, pb.mag, pb.bias, n));
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int MT, int YDT, bool ACC_OUT>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvProblem pb, const int8_t* __restrict__ q,
+                                                   const float* __restrict__ act_scale, int M,
+                                                   void* y, int32_t* acc_out) {
+    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int num_waves = gridDim.x * 4;
+    gemv_body_long<MT, YDT, ACC_OUT>(pb, q, act_scale, M, y, acc_out, wave_id, num_waves);
+}
+
+template <int MT, int YDT>
+__global__ __launch_bounds__(256) void grouped_gemv_kernel(const nsosx_linear_view* views,
+                                                           const int8_t* __restrict__ q,
+                                                           int64_t q_stride,
+                                                           const float* __restrict__ act_scale,
+                                                           int64_t scale_stride, int M, void* y,
+                                                           int64_t y_stride) {
+    const int g = blockIdx.y;
+    const nsosx_linear_view v = views[g];
+    GemvProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
+    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int num_waves = gridDim.x * 4;
+    char* yb = static_cast<char*>(y) + g * y_stride * (YDT == NSOSX_F32 ? 4 : 2);
+    gemv_body_long<MT, YDT, false>(pb, q + g * q_stride, act_scale + g * scale_stride, M, yb,
+                                   nullptr, wave_id, num_waves);
+}
+
+static int gemv_grid(int N, int K) {
+    const int W16 = K / 16;
+    const int cpr = (W16 + 3) / 4;
+    int lpr = 1;
+    while (lpr < cpr && lpr < 64) lpr <<= 1;
+    const int rpw = 64 / lpr;
+    const int nsteps = (N + rpw - 1) / rpw;
+    // one wave step per wave, up to 8 resident waves per CU on 256 CUs
+    int waves = std::min(nsteps, 256 * 8);
+    return std::max(1, (waves + 3) / 4);
+}
+
+template <int YDT>
+static void launch_gemv_t(const GemvProblem& pb, const int8_t* q, const float* as, int M,
+                          void* y, int32_t* acc, hipStream_t st) {
+    const dim3 grid(gemv_grid(pb.N, pb.K)), block(256);
+#define NSOSX_GEMV(MT)                                                                       \
+    if (acc)                                                                                 \
+        hipLaunchKernelGGL((gemv_kernel<MT, YDT, true>), grid, block, 0, st, pb, q, as, M, y, \
+                           acc);                                                             \
+    else                                                                                     \
+        hipLaunchKernelGGL((gemv_kernel<MT, YDT, false>), grid, block, 0, st, pb, q, as, M, y, \
+                           acc);
+    if (M == 1) { NSOSX_GEMV(1) }
+    else if (M == 2) { NSOSX_GEMV(2) }
+    else if (M <= 4) { NSOSX_GEMV(4) }
+    else { NSOSX_GEMV(8) }
+#undef NSOSX_GEMV
+}
+
+// ===========================================================================
+// int8 MFMA GEMM.  The packed weight rows are the MFMA's A operand (rows i =
+// output columns n) and the activation rows its B operand (columns j = tokens
+// m), so each lane's four accumulators are four consecutive n of one token.
+// Block tile 256 (n) x 128 (m) x 64 (k), 4 waves in 2x2, each wave 128 x 64
+// = 8 x 4 tiles of v_mfma_i32_16x16x64_i8.  Weights stay 2-bit in LDS (4 KB
+// per k step) and are expanded to int8 in registers right before the MFMA;
+// activation rows are byte-transposed into the same k order on their way to
+// LDS (row stride 80 bytes: conflict-free 16-byte reads).  Two LDS stages,
+// the next k step's global loads in flight during the current MFMAs.
+// GATHER: token rows come through perm[] (MoE slots -> token rows); the m
+// range of each expert is its segment [offsets[e], offsets[e+1]).
+// ===========================================================================
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int kBN = 256, kBM = 128, kBK = 64;
+constexpr int kXStride = 80;  // bytes per activation row in LDS
+
+struct GemmProblem {
+    const uint32_t* packed;
+    const float* mag;
+    const float* bias;
+    float ws;
+    int N;
+    int K;
+};
+
+template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU>
+__device__ __forceinline__ void gemm_tile(const GemmProblem& pb, const int8_t* __restrict__ q,
+                                          const float* __restrict__ act_scale,
+                                          const int32_t* __restrict__ perm, int seg_begin,
+                                          int seg_rows, int n0, int m0, void* y,
+                                          int32_t* acc_out, char* smem) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave & 1, wm = wave >> 1;
+    const int W16 = pb.K >> 4;
+    const int KT = (pb.K + kBK - 1) / kBK;
+    const bool waligned = (W16 & 3) == 0;
+
+    uint32_t* wlds[2] = {reinterpret_cast<uint32_t*>(smem),
+                         reinterpret_cast<uint32_t*>(smem + kBN * 16)};
+    char* xlds[2] = {smem + 2 * kBN * 16, smem + 2 * kBN * 16 + kBM * kXStride};
+
+    // global -> register staging: one weight row chunk and two activation chunks per thread
+    const int wrow = n0 + tid;
+    const uint32_t* wsrc = pb.packed + (int64_t)wrow * W16;
+    int xrow_src[2];
+    bool xrow_ok[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int ml = (tid >> 2) + 64 * i;
+        const int m = m0 + ml;
+        xrow_ok[i] = m < seg_rows;
+        int src = seg_begin + m;
+        if (GATHER && xrow_ok[i]) src = perm[src];
+        xrow_src[i] = src;
+    }
+    const int xchunk = tid & 3;
+
+    uint32_t wreg[4];
+    uint32_t xreg[2][4];
+    auto load_global = [&](int kt) {
+        const int w0 = kt * (kBK / 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wreg[i] = 0x55555555u;
+        if (wrow < pb.N) {
+            if (waligned && w0 + 3 < W16) {
+                const uint4 v = *reinterpret_cast<const uint4*>(wsrc + w0);
+                wreg[0] = v.x; wreg[1] = v.y; wreg[2] = v.z; wreg[3] = v.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (w0 + i < W16) wreg[i] = wsrc[w0 + i];
+            }
+        }
+        const int k = kt * kBK + xchunk * 16;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            uint32_t d[4] = {0u, 0u, 0u, 0u};
+            if (xrow_ok[i] && k < pb.K) {
+                const uint4 v =
+                    *reinterpret_cast<const uint4*>(q + (int64_t)xrow_src[i] * pb.K + k);
+                d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+            }
+            transpose16(d, xreg[i]);
+        }
+    };
+    auto store_lds = [&](int buf) {
+        *reinterpret_cast<uint4*>(wlds[buf] + tid * 4) =
+            make_uint4(wreg[0], wreg[1], wreg[2], wreg[3]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int ml = (tid >> 2) + 64 * i;
+            *reinterpret_cast<uint4*>(xlds[buf] + ml * kXStride + xchunk * 16) =
+                make_uint4(xreg[i][0], xreg[i][1], xreg[i][2], xreg[i][3]);
+        }
+    };
+
+    v4i acc[8][4];
+#pragma unroll
+    for (int a = 0; a < 8; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+
+    load_global(0);
+    store_lds(0);
+    __syncthreads();
+
+    const int g = lane >> 4;     // k group of 16
+    const int li = lane & 15;    // row / column within a 16 x 16 tile
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < KT) load_global(kt + 1);
+        v4i bx[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const int ml = wm * 64 + mb * 16 + li;
+            const uint4 v = *reinterpret_cast<const uint4*>(xlds[cur] + ml * kXStride + g * 16);
+            bx[mb] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        }
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+            const int nl = wn * 128 + nb * 16 + li;
+            const uint32_t p = wlds[cur][nl * 4 + g];
+            uint32_t wv[4];
+            unpack_word(p, wv);
+            const v4i aw = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+                acc[nb][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aw, bx[mb], acc[nb][mb], 0, 0, 0);
+        }
+        if (kt + 1 < KT) store_lds(cur ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds n = n_base + 4*g + r for token m = m_base + li
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+        const int ml = m0 + wm * 64 + mb * 16 + li;
+        if (ml >= seg_rows) continue;
+        const int64_t orow = (int64_t)(seg_begin + ml);
+        const int arow = GATHER ? perm[seg_begin + ml] : (int)orow;
+        const float comb = __fmul_rn(act_scale[arow], pb.ws);
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb) {
+            const int nbase = n0 + wn * 128 + nb * 16 + 4 * g;
+            const v4i a = acc[nb][mb];
+            const int av[4] = {a.x, a.y, a.z, a.w};
+            if (ACC_OUT) {
+                if (nbase + 3 < pb.N && (pb.N & 3) == 0) {
+                    *reinterpret_cast<int4*>(acc_out + orow * pb.N + nbase) =
+                        make_int4(av[0], av[1], av[2], av[3]);
+                } else {
+                    for (int r = 0; r < 4; ++r)
+                        if (nbase + r < pb.N) acc_out[orow * pb.N + nbase + r] = av[r];
+                }
+            }
+            if (y) {
+                float o[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int n = min(nbase + r, pb.N - 1);
+                    float v = dequant(av[r], comb, pb.mag, pb.bias, n);
+                    if (SQRELU) {
+                        v = v > 0.0f ? v : 0.0f;
+                        v = __fmul_rn(v, v);
+                    }
+                    o[r] = v;
+                }
+                if (nbase + 3 < pb.N && (pb.N & 3) == 0) {
+                    if constexpr (YDT == NSOSX_F32) {
+                        *reinterpret_cast<float4*>(static_cast<float*>(y) + orow * pb.N + nbase) =
+                            make_float4(o[0], o[1], o[2], o[3]);
+                    } else {
+                        const uint32_t lo = f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
+                        const uint32_t hi = f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
+                        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + orow * pb.N + nbase) =
+                            make_uint2(lo, hi);
+                    }
+                } else {
+                    for (int r = 0; r < 4; ++r)
+                        if (nbase + r < pb.N) store_act<YDT>(y, orow * pb.N + nbase + r, o[r]);
+                }
+            }
+        }
+    }
+}
+
+constexpr int kGemmSmem = 2 * kBN * 16 + 2 * kBM * kXStride;
+
+template <int YDT, bool ACC_OUT>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmProblem pb, const int8_t* __restrict__ q,
+                                                   const float* __restrict__ act_scale, int M,
+                                                   void* y, int32_t* acc_out) {
+    __shared__ __align__(16) char smem[kGemmSmem];
+    const int n0 = blockIdx.x * kBN;
+    const int m0 = blockIdx.y * kBM;
+    gemm_tile<YDT, ACC_OUT, false, false>(pb, q, act_scale, nullptr, 0, M, n0, m0, y, acc_out,
+                                          smem);
+}
+
+template <int YDT, bool GATHER, bool SQRELU>
+__global__ __launch_bounds__(256) void grouped_gemm_kernel(const nsosx_linear_view* views,
+                                                           const int32_t* __restrict__ offsets,
+                                                           const int32_t* __restrict__ perm,
+                                                           const int8_t* __restrict__ q,
+                                                           const float* __restrict__ act_scale,
+                                                           void* y) {
+    __shared__ __align__(16) char smem[kGemmSmem];
+    const int e = blockIdx.z;
+    const int seg_begin = offsets[e];
+    const int seg_rows = offsets[e + 1] - seg_begin;
+    const int m0 = blockIdx.y * kBM;
+    if (m0 >= seg_rows) return;
+    const nsosx_linear_view v = views[e];
+    const int n0 = blockIdx.x * kBN;
+    if (n0 >= v.outputs) return;
+    GemmProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
+    gemm_tile<YDT, false, GATHER, SQRELU>(pb, q, act_scale, perm, seg_begin, seg_rows, n0, m0, y,
+                                          nullptr, smem);
+}
+
+template <int YDT>
+static void launch_gemm_t(const GemmProblem& pb, const int8_t* q, const float* as, int M,
+                          void* y, int32_t* acc, hipStream_t st) {
+    const dim3 grid((pb.N + kBN - 1) / kBN, (M + kBM - 1) / kBM), block(256);
+    if (acc)
+        hipLaunchKernelGGL((gemm_kernel<YDT, true>), grid, block, 0, st, pb, q, as, M, y, acc);
+    else
+        hipLaunchKernelGGL((gemm_kernel<YDT, false>), grid, block, 0, st, pb, q, as, M, y, acc);
+}
+
+// ===========================================================================
+// Reserved-code scan (import check).
+// ===========================================================================
+__global__ void find_reserved_kernel(const uint32_t* __restrict__ packed, int64_t n_codes,
+                                     unsigned long long* __restrict__ first_bad) {
+    const int64_t words = (n_codes + 15) / 16;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < words;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const uint32_t p = packed[i];
+        // a code is 3 when both of its bits are set
+        uint32_t both = p & (p >> 1) & 0x55555555u;
+        const int64_t valid = n_codes - i * 16;
+        if (valid < 16) both &= (1u << (2 * valid)) - 1u;
+        if (both) {
+            const int j = __builtin_ctz(both) >> 1;
+            atomicMin(first_bad, static_cast<unsigned long long>(i * 16 + j));
+        }
+    }
+}
+
+__global__ void finish_reserved_kernel(unsigned long long* v) {
+    if (*v == ~0ull) *reinterpret_cast<long long*>(v) = -1;
+}
+
+__global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v) { *p = v; }
+
+}  // namespace nsosx
+
+using namespace nsosx;
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" int nsosx_quantize_act_i8(const void* x, int x_dtype, int M, int K, int bits,
+                                     int rms_input, int8_t* q, float* act_scale,
+                                     float* rms_workspace, void* stream) {
+    if (!x || !q || !act_scale) return fail(NSOSX_ERR_INVALID, "quantize_act: null pointer");
+    if (M <= 0 || K <= 0) return fail(NSOSX_ERR_INVALID, "quantize_act: M and K must be > 0");
+    if (bits < 2 || bits > 8) return fail(NSOSX_ERR_INVALID, "quantize_act: bits must be in [2, 8]");
+    if (!valid_dtype(x_dtype)) return fail(NSOSX_ERR_INVALID, "quantize_act: bad dtype");
+    if (rms_input && !rms_workspace)
+        return fail(NSOSX_ERR_INVALID, "quantize_act: rms_input needs rms_workspace");
+    if ((int64_t)M * K > ((int64_t)1 << 40))
+        return fail(NSOSX_ERR_OVERFLOW, "quantize_act: M*K too large");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (x_dtype == NSOSX_F32)
+        return launch_quantize<NSOSX_F32>(x, M, K, bits, rms_input, q, act_scale, rms_workspace, st);
+    return launch_quantize<NSOSX_BF16>(x, M, K, bits, rms_input, q, act_scale, rms_workspace, st);
+}
+
+static int check_gemm_args(const int8_t* q, const float* as, const uint32_t* packed, float ws,
+                           int M, int K, int N, const void* y, int y_dtype, const int32_t* acc) {
+    if (!q || !as || !packed) return fail(NSOSX_ERR_INVALID, "ternary_gemm: null pointer");
+    if (!y && !acc) return fail(NSOSX_ERR_INVALID, "ternary_gemm: no output");
+    if (M <= 0 || K <= 0 || N <= 0) return fail(NSOSX_ERR_INVALID, "ternary_gemm: empty shape");
+    if (K % 16 != 0) return fail(NSOSX_ERR_INVALID, "ternary_gemm: K must be a multiple of 16");
+    if (!(ws > 0.0f) || !std::isfinite(ws))
+        return fail(NSOSX_ERR_INVALID, "ternary_gemm: weight_scale must be finite and > 0");
+    if (!valid_dtype(y_dtype)) return fail(NSOSX_ERR_INVALID, "ternary_gemm: bad dtype");
+    if (K > 2147483647 / 254)  // |acc| <= 127 * K must fit int32 (bitnet_gpu_dispatch.cpp:97-101)
+        return fail(NSOSX_ERR_OVERFLOW, "ternary_gemm: K too large for int32 accumulation");
+    if ((int64_t)M * N > ((int64_t)1 << 40) || (int64_t)M * K > ((int64_t)1 << 40))
+        return fail(NSOSX_ERR_OVERFLOW, "ternary_gemm: size too large");
+    if (reinterpret_cast<uintptr_t>(q) % 16 || reinterpret_cast<uintptr_t>(packed) % 16)
+        return fail(NSOSX_ERR_INVALID, "ternary_gemm: q and packed must be 16-byte aligned");
+    return NSOSX_OK;
+}
+
+extern "C" int nsosx_ternary_gemm_path(const int8_t* q, const float* act_scale,
+                                       const uint32_t* packed, float weight_scale, int M, int K,
+                                       int N, const float* magnitude, const float* bias, void* y,
+                                       int y_dtype, int32_t* acc_out, int path, void* stream) {
+    int rc = check_gemm_args(q, act_scale, packed, weight_scale, M, K, N, y, y_dtype, acc_out);
+    if (rc) return rc;
+    if (path == 0 && M > 8) return fail(NSOSX_ERR_INVALID, "ternary_gemm: GEMV path needs M <= 8");
+    if (path != 0 && path != 1) return fail(NSOSX_ERR_INVALID, "ternary_gemm: bad path");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (path == 0) {
+        GemvProblem pb{packed, magnitude, bias, weight_scale, N, K};
+        if (y_dtype == NSOSX_F32) launch_gemv_t<NSOSX_F32>(pb, q, act_scale, M, y, acc_out, st);
+        else launch_gemv_t<NSOSX_BF16>(pb, q, act_scale, M, y, acc_out, st);
+    } else {
+        GemmProblem pb{packed, magnitude, bias, weight_scale, N, K};
+        if (y_dtype == NSOSX_F32) launch_gemm_t<NSOSX_F32>(pb, q, act_scale, M, y, acc_out, st);
+        else launch_gemm_t<NSOSX_BF16>(pb, q, act_scale, M, y, acc_out, st);
+    }
+    return check_launch("ternary_gemm");
+}
+
+extern "C" int nsosx_ternary_gemm(const int8_t* q, const float* act_scale, const uint32_t* packed,
+                                  float weight_scale, int M, int K, int N, const float* magnitude,
+                                  const float* bias, void* y, int y_dtype, int32_t* acc_out,
+                                  void* stream) {
+    return nsosx_ternary_gemm_path(q, act_scale, packed, weight_scale, M, K, N, magnitude, bias, y,
+                                   y_dtype, acc_out, M <= 8 ? 0 : 1, stream);
+}
+
+extern "C" int nsosx_bitlinear_forward(const void* x, int x_dtype, const uint32_t* packed,
+                                       float weight_scale, int M, int K, int N,
+                                       int precision_bits, int rms_input, const float* magnitude,
+                                       const float* bias, void* y, int y_dtype,
+                                       int8_t* q_workspace, float* scale_workspace,
+                                       float* rms_workspace, void* stream) {
+    if (!y) return fail(NSOSX_ERR_INVALID, "bitlinear_forward: null output");
+    int rc = check_gemm_args(q_workspace, scale_workspace, packed, weight_scale, M, K, N, y,
+                             y_dtype, nullptr);
+    if (rc) return rc;
+    rc = nsosx_quantize_act_i8(x, x_dtype, M, K, precision_bits, rms_input, q_workspace,
+                               scale_workspace, rms_workspace, stream);
+    if (rc) return rc;
+    return nsosx_ternary_gemm(q_workspace, scale_workspace, packed, weight_scale, M, K, N,
+                              magnitude, bias, y, y_dtype, nullptr, stream);
+}
+
+extern "C" int nsosx_grouped_gemv(const nsosx_linear_view* views_dev, int groups, const int8_t* q,
+                                  int64_t q_stride, const float* act_scale, int64_t scale_stride,
+                                  int M, void* y, int64_t y_stride, int y_dtype, void* stream) {
+    if (!views_dev || !q || !act_scale || !y) return fail(NSOSX_ERR_INVALID, "grouped_gemv: null");
+    if (groups <= 0 || groups > 65535 || M <= 0 || M > 8)
+        return fail(NSOSX_ERR_INVALID, "grouped_gemv: groups in [1, 65535], M in [1, 8]");
+    if (!valid_dtype(y_dtype)) return fail(NSOSX_ERR_INVALID, "grouped_gemv: bad dtype");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // the grid is sized from the first view's shape read back by the caller's contract:
+    // all views share `inputs`; outputs may differ and each wave strides its own rows
+    const dim3 grid(256 * 2, groups), block(256);
+#define NSOSX_GG(MT)                                                                          \
+    if (y_dtype == NSOSX_F32)                                                                 \
+        hipLaunchKernelGGL((grouped_gemv_kernel<MT, NSOSX_F32>), grid, block, 0, st, views_dev, \
+                           q, q_stride, act_scale, scale_stride, M, y, y_stride);            \
+    else                                                                                      \
+        hipLaunchKernelGGL((grouped_gemv_kernel<MT, NSOSX_BF16>), grid, block, 0, st,        \
+                           views_dev, q, q_stride, act_scale, scale_stride, M, y, y_stride);
+    if (M == 1) { NSOSX_GG(1) }
+    else if (M == 2) { NSOSX_GG(2) }
+    else if (M <= 4) { NSOSX_GG(4) }
+    else { NSOSX_GG(8) }
+#undef NSOSX_GG
+    return check_launch("grouped_gemv");
+}
+
+extern "C" int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, int experts,
+                                          const int32_t* offsets, const int32_t* perm, int gather,
+                                          const int8_t* q, const float* act_scale, int K, int N,
+                                          int max_rows_per_expert, int squared_relu, void* y,
+                                          int y_dtype, void* stream) {
+    if (!views_dev || !offsets || !q || !act_scale || !y || (gather && !perm))
+        return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm: null pointer");
+    if (experts <= 0 || experts > 65535 || K <= 0 || K % 16 || N <= 0 || max_rows_per_expert < 0)
+        return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm: bad shape");
+    if (!valid_dtype(y_dtype)) return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm: bad dtype");
+    if (max_rows_per_expert == 0) return NSOSX_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid((N + kBN - 1) / kBN, (max_rows_per_expert + kBM - 1) / kBM, experts);
+    const dim3 block(256);
+#define NSOSX_GGEMM(YDT, G, S)                                                                 \
+    hipLaunchKernelGGL((grouped_gemm_kernel<YDT, G, S>), grid, block, 0, st, views_dev, offsets, \
+                       perm, q, act_scale, y);
+    if (y_dtype == NSOSX_F32) {
+        if (gather) { if (squared_relu) { NSOSX_GGEMM(NSOSX_F32, true, true) } else { NSOSX_GGEMM(NSOSX_F32, true, false) } }
+        else { if (squared_relu) { NSOSX_GGEMM(NSOSX_F32, false, true) } else { NSOSX_GGEMM(NSOSX_F32, false, false) } }
+    } else {
+        if (gather) { if (squared_relu) { NSOSX_GGEMM(NSOSX_BF16, true, true) } else { NSOSX_GGEMM(NSOSX_BF16, true, false) } }
+        else { if (squared_relu) { NSOSX_GGEMM(NSOSX_BF16, false, true) } else { NSOSX_GGEMM(NSOSX_BF16, false, false) } }
+    }
+#undef NSOSX_GGEMM
+    return check_launch("grouped_ternary_gemm");
+}
+
+extern "C" int nsosx_find_reserved_code(const uint32_t* packed, int64_t n_codes, int64_t* first_bad,
+                                        void* stream) {
+    if (!packed || !first_bad || n_codes < 0)
+        return fail(NSOSX_ERR_INVALID, "find_reserved_code: bad argument");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    unsigned long long* fb = reinterpret_cast<unsigned long long*>(first_bad);
+    hipLaunchKernelGGL(fill_u64_kernel, dim3(1), dim3(1), 0, st, fb, ~0ull);
+    const int64_t words = (n_codes + 15) / 16;
+    if (words > 0) {
+        const int blocks = (int)std::min<int64_t>((words + 255) / 256, 4096);
+        hipLaunchKernelGGL(find_reserved_kernel, dim3(blocks), dim3(256), 0, st, packed, n_codes, fb);
+    }
+    hipLaunchKernelGGL(finish_reserved_kernel, dim3(1), dim3(1), 0, st, fb);
+    return check_launch("find_reserved_code");
+}

@@ -1,0 +1,134 @@
+// Shared device/host helpers of the nsosx HIP library (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/nsosx.h"
+
+namespace nsosx {
+
+constexpr int kWave = 64;
+
+// ---- error reporting -------------------------------------------------------
+
+void set_error(const std::string& msg);
+
+inline int fail(int status, const std::string& msg) {
+    set_error(msg);
+    return status;
+}
+
+inline int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return fail(NSOSX_ERR_LAUNCH, std::string(what) + ": " + hipGetErrorString(e));
+    }
+    return NSOSX_OK;
+}
+
+inline bool valid_dtype(int d) { return d == NSOSX_F32 || d == NSOSX_BF16; }
+
+// ---- bf16 <-> f32 -----------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return static_cast<uint16_t>(u >> 16);
+}
+
+template <int DT>
+__device__ __forceinline__ float load_act(const void* p, int64_t i) {
+    if constexpr (DT == NSOSX_F32) {
+        return static_cast<const float*>(p)[i];
+    } else {
+        return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
+    if constexpr (DT == NSOSX_F32) {
+        static_cast<float*>(p)[i] = v;
+    } else {
+        static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+    }
+}
+
+// ---- wave reductions (wave64) ---------------------------------------------
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// ---- ternary unpack ----------------------------------------------------------
+//
+// One packed word holds 16 codes, code j at bits 2j.  unpack_word() returns
+// four dwords of int8 values; dword s, byte b holds the value of code 4b+s
+// (an order in which every step is a shift, a mask and a byte permute).
+// The byte permute looks the 2-bit code up in the table {-1, 0, +1, 0}
+// (code 3 is reserved and decodes to 0, as on the reference CPU path).
+constexpr uint32_t kTernaryLut = 0x000100FFu;  // bytes: 0xFF, 0x00, 0x01, 0x00
+
+__device__ __forceinline__ void unpack_word(uint32_t p, uint32_t out[4]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const uint32_t t = (p >> (2 * s)) & 0x03030303u;
+        out[s] = __builtin_amdgcn_perm(0u, kTernaryLut, t);
+    }
+}
+
+// 4x4 byte transpose of 16 activation bytes in natural order (dword d, byte c
+// = element 4d+c) into the order unpack_word() produces (dword s, byte b =
+// element 4b+s).
+__device__ __forceinline__ void transpose16(const uint32_t d[4], uint32_t e[4]) {
+    const uint32_t t0 = __builtin_amdgcn_perm(d[1], d[0], 0x05010400u);
+    const uint32_t t1 = __builtin_amdgcn_perm(d[1], d[0], 0x07030602u);
+    const uint32_t t2 = __builtin_amdgcn_perm(d[3], d[2], 0x05010400u);
+    const uint32_t t3 = __builtin_amdgcn_perm(d[3], d[2], 0x07030602u);
+    e[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+    e[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+    e[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+    e[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load that is not expected to be reused (weights of a GEMV).
+__device__ __forceinline__ uint4 load_stream16(const uint32_t* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+// ---- dequantizing epilogue (bitnet_adapter_avx2.cpp:93,150-156) ----------
+__device__ __forceinline__ float dequant(int acc, float combined, const float* mag,
+                                         const float* bias, int n) {
+    float v = __fmul_rn(static_cast<float>(acc), combined);
+    if (mag && bias) return __fmaf_rn(v, mag[n], bias[n]);
+    if (mag) return __fmul_rn(v, mag[n]);
+    if (bias) return __fadd_rn(v, bias[n]);
+    return v;
+}
+
+}  // namespace nsosx

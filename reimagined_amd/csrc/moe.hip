@@ -1,0 +1,232 @@
+// Top-k MoE routing on gfx950: softmax + top-k + renormalisation per row,
+// then the deterministic expert-major, rows-ascending token permutation
+// (counts -> exclusive scan -> stable ranks) with no host round trip, and
+// the weighted combine in ascending expert order.
+//
+// Reference semantics (OXN/nsos/ of vitorGgC569/reimagined):
+//   softmax           Tensor::softmax, src/tensor.cpp:3428-3450
+//   top-k + renorm    MoERouter::forward CPU path, src/jamba.cpp:8268-8297
+//   permutation       JambaBlock::forward_moe, src/jamba.cpp:3882-3894
+//   combine           src/jamba.cpp:3947-3969
+#include "common.hpp"
+
+namespace nsosx {
+
+constexpr int kMaxExperts = 64;
+constexpr int kRouteBlock = 256;  // rows per dispatch block
+
+// One thread per row.  The softmax keeps the reference's order of
+// operations: running max, exp(x - max), an in-order float sum, one
+// multiply by 1/max(sum, 1e-8f).  Top-k is a selection under the strict
+// order (value desc, index asc); renormalisation sums the selected values in
+// rank order and multiplies by 1/max(sum, 1e-9f).
+__global__ __launch_bounds__(256) void route_rows_kernel(const float* __restrict__ logits, int rows,
+                                                         int E, int k, float* __restrict__ weights,
+                                                         int32_t* __restrict__ selected) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const float* src = logits + (int64_t)r * E;
+    float p[kMaxExperts];
+    float mx = src[0];
+    for (int j = 1; j < E; ++j) mx = src[j] > mx ? src[j] : mx;
+    float sum = 0.0f;
+    for (int j = 0; j < E; ++j) {
+        p[j] = expf(src[j] - mx);
+        sum = sum + p[j];
+    }
+    const float inv = 1.0f / (sum > 1e-8f ? sum : 1e-8f);
+    for (int j = 0; j < E; ++j) p[j] = p[j] * inv;
+    uint64_t taken = 0;
+    int sel[kMaxExperts];
+    float ssum = 0.0f;
+    for (int i = 0; i < k; ++i) {
+        int best = -1;
+        for (int j = 0; j < E; ++j) {
+            if ((taken >> j) & 1ull) continue;
+            if (best < 0 || p[j] > p[best]) best = j;  // ties keep the lower index
+        }
+        taken |= 1ull << best;
+        sel[i] = best;
+        ssum = ssum + p[best];
+    }
+    const float inv2 = 1.0f / (ssum > 1e-9f ? ssum : 1e-9f);
+    float* w = weights + (int64_t)r * E;
+    for (int j = 0; j < E; ++j) w[j] = ((taken >> j) & 1ull) ? p[j] * inv2 : 0.0f;
+    for (int i = 0; i < k; ++i) selected[(int64_t)r * k + i] = sel[i];
+}
+
+// Per dispatch block of 256 rows: how many of its rows selected each expert.
+__global__ __launch_bounds__(256) void route_count_kernel(const int32_t* __restrict__ selected,
+                                                          int rows, int E, int k,
+                                                          int32_t* __restrict__ block_counts) {
+    __shared__ int32_t cnt[kMaxExperts];
+    const int tid = threadIdx.x;
+    if (tid < E) cnt[tid] = 0;
+    __syncthreads();
+    const int r = blockIdx.x * kRouteBlock + tid;
+    if (r < rows)
+        for (int i = 0; i < k; ++i) atomicAdd(&cnt[selected[(int64_t)r * k + i]], 1);
+    __syncthreads();
+    if (tid < E) block_counts[(int64_t)blockIdx.x * E + tid] = cnt[tid];
+}
+
+// Single workgroup: counts[e], offsets = exclusive scan over experts, and the
+// exclusive scan over blocks of each expert's per-block counts (in place).
+__global__ __launch_bounds__(64) void route_scan_kernel(int32_t* __restrict__ block_counts,
+                                                        int nblocks, int E,
+                                                        int32_t* __restrict__ counts,
+                                                        int32_t* __restrict__ offsets) {
+    __shared__ int32_t tot[kMaxExperts];
+    const int e = threadIdx.x;
+    if (e < E) {
+        int run = 0;
+        for (int b = 0; b < nblocks; ++b) {
+            const int v = block_counts[(int64_t)b * E + e];
+            block_counts[(int64_t)b * E + e] = run;
+            run += v;
+        }
+        tot[e] = run;
+        counts[e] = run;
+    }
+    __syncthreads();
+    if (e == 0) {
+        int run = 0;
+        for (int j = 0; j < E; ++j) {
+            offsets[j] = run;
+            run += tot[j];
+        }
+        offsets[E] = run;
+    }
+}
+
+// Stable ranks: within a block, rows are ranked per expert in ascending row
+// order with wave ballots and a prefix over the block's four waves.
+__global__ __launch_bounds__(256) void route_assign_kernel(const int32_t* __restrict__ selected,
+                                                           int rows, int E, int k,
+                                                           const int32_t* __restrict__ block_base,
+                                                           const int32_t* __restrict__ offsets,
+                                                           int32_t* __restrict__ perm,
+                                                           int32_t* __restrict__ slot_of) {
+    __shared__ int32_t wave_cnt[4][kMaxExperts];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int r = blockIdx.x * kRouteBlock + tid;
+    const bool valid = r < rows;
+    int mine[kMaxExperts > 8 ? 8 : kMaxExperts];  // k <= 8 handled here
+    const int kk = k < 8 ? k : 8;
+    for (int i = 0; i < kk; ++i) mine[i] = valid ? selected[(int64_t)r * k + i] : -1;
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int e = 0; e < E; ++e) {
+        bool has = false;
+        for (int i = 0; i < kk; ++i) has |= mine[i] == e;
+        const uint64_t bal = __ballot(has);
+        if (lane == 0) wave_cnt[wave][e] = __popcll(bal);
+    }
+    __syncthreads();
+    for (int e = 0; e < E; ++e) {
+        bool has = false;
+        int which = -1;
+        for (int i = 0; i < kk; ++i)
+            if (mine[i] == e) { has = true; which = i; }
+        const uint64_t bal = __ballot(has);
+        if (has) {
+            int before = 0;
+            for (int w = 0; w < wave; ++w) before += wave_cnt[w][e];
+            const int rank = before + __popcll(bal & lt);
+            const int slot = offsets[e] + block_base[(int64_t)blockIdx.x * E + e] + rank;
+            perm[slot] = r;
+            slot_of[(int64_t)r * k + which] = slot;
+        }
+    }
+}
+
+// out[r, d] = sum over the row's experts in ascending id order of
+// expert_out[slot, d] * w[r, e], starting from 0.
+template <int IDT, int ODT>
+__global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ expert_out,
+                                                      const int32_t* __restrict__ slot_of,
+                                                      const int32_t* __restrict__ selected,
+                                                      const float* __restrict__ weights, int rows,
+                                                      int E, int k, int dim,
+                                                      void* __restrict__ out) {
+    const int r = blockIdx.y;
+    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows || d >= dim) return;
+    int es[8], ss[8];
+    const int kk = k < 8 ? k : 8;
+    for (int i = 0; i < kk; ++i) {
+        es[i] = selected[(int64_t)r * k + i];
+        ss[i] = slot_of[(int64_t)r * k + i];
+    }
+    // insertion sort by expert id (k is tiny)
+    for (int i = 1; i < kk; ++i) {
+        const int e = es[i], s = ss[i];
+        int j = i - 1;
+        while (j >= 0 && es[j] > e) { es[j + 1] = es[j]; ss[j + 1] = ss[j]; --j; }
+        es[j + 1] = e;
+        ss[j + 1] = s;
+    }
+    float acc = 0.0f;
+    for (int i = 0; i < kk; ++i) {
+        const float v = load_act<IDT>(expert_out, (int64_t)ss[i] * dim + d);
+        acc = acc + __fmul_rn(v, weights[(int64_t)r * E + es[i]]);
+    }
+    store_act<ODT>(out, (int64_t)r * dim + d, acc);
+}
+
+}  // namespace nsosx
+
+using namespace nsosx;
+
+extern "C" int64_t nsosx_moe_route_workspace(int rows, int experts) {
+    if (rows <= 0 || experts <= 0) return 0;
+    const int64_t nblocks = (rows + kRouteBlock - 1) / kRouteBlock;
+    return nblocks * experts;
+}
+
+extern "C" int nsosx_moe_route(const float* logits, int rows, int experts, int k, float* weights,
+                               int32_t* selected, int32_t* counts, int32_t* offsets, int32_t* perm,
+                               int32_t* slot_of, int32_t* workspace, void* stream) {
+    if (!logits || !weights || !selected || !counts || !offsets || !perm || !slot_of || !workspace)
+        return fail(NSOSX_ERR_INVALID, "moe_route: null pointer");
+    if (rows <= 0 || experts <= 0 || experts > kMaxExperts || k <= 0 || k > experts || k > 8)
+        return fail(NSOSX_ERR_INVALID, "moe_route: need rows > 0, 0 < k <= min(E, 8), E <= 64");
+    if ((int64_t)rows * k > 2147483647LL) return fail(NSOSX_ERR_OVERFLOW, "moe_route: rows*k too large");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int nblocks = (rows + kRouteBlock - 1) / kRouteBlock;
+    hipLaunchKernelGGL(route_rows_kernel, dim3((rows + 255) / 256), dim3(256), 0, st, logits, rows,
+                       experts, k, weights, selected);
+    hipLaunchKernelGGL(route_count_kernel, dim3(nblocks), dim3(kRouteBlock), 0, st, selected, rows,
+                       experts, k, workspace);
+    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(64), 0, st, workspace, nblocks, experts,
+                       counts, offsets);
+    hipLaunchKernelGGL(route_assign_kernel, dim3(nblocks), dim3(kRouteBlock), 0, st, selected, rows,
+                       experts, k, workspace, offsets, perm, slot_of);
+    return check_launch("moe_route");
+}
+
+extern "C" int nsosx_moe_combine(const void* expert_out, int in_dtype, const int32_t* slot_of,
+                                 const int32_t* selected, const float* weights, int rows,
+                                 int experts, int k, int dim, void* out, int out_dtype,
+                                 void* stream) {
+    if (!expert_out || !slot_of || !selected || !weights || !out)
+        return fail(NSOSX_ERR_INVALID, "moe_combine: null pointer");
+    if (rows <= 0 || rows > 65535 * 256 || experts <= 0 || experts > kMaxExperts || k <= 0 ||
+        k > 8 || k > experts || dim <= 0)
+        return fail(NSOSX_ERR_INVALID, "moe_combine: bad shape");
+    if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype))
+        return fail(NSOSX_ERR_INVALID, "moe_combine: bad dtype");
+    if (rows > 65535) return fail(NSOSX_ERR_INVALID, "moe_combine: rows must be <= 65535");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid((dim + 255) / 256, rows), block(256);
+#define NSOSX_COMB(I, O)                                                                        \
+    hipLaunchKernelGGL((combine_kernel<I, O>), grid, block, 0, st, expert_out, slot_of, selected, \
+                       weights, rows, experts, k, dim, out);
+    if (in_dtype == NSOSX_F32) {
+        if (out_dtype == NSOSX_F32) { NSOSX_COMB(NSOSX_F32, NSOSX_F32) } else { NSOSX_COMB(NSOSX_F32, NSOSX_BF16) }
+    } else {
+        if (out_dtype == NSOSX_F32) { NSOSX_COMB(NSOSX_BF16, NSOSX_F32) } else { NSOSX_COMB(NSOSX_BF16, NSOSX_BF16) }
+    }
+#undef NSOSX_COMB
+    return check_launch("moe_combine");
+}

@@ -1,0 +1,437 @@
+// Mamba selective scan on gfx950: packed ragged prefill (cu_seqlens), the
+// decode step, and the depthwise causal convolution that feeds them.
+//
+// Reference semantics (OXN/nsos/ of vitorGgC569/reimagined):
+//   decay terms    src/mamba2.cpp:443-473 (softplus src/mamba2.cpp:718-726)
+//   recurrence     src/mamba2.cpp:2602-2675 (faithful CPU scan)
+//   decode step    src/mamba2.cpp:4038-4125
+//   causal conv    src/mamba2.cpp:1056-1076, bias + SiLU 2437-2446
+//   gate           Tensor::silu_gate, src/tensor.cpp:3323-3343 (silu 3261-3282)
+//
+// decay = exp(-exp(log(delta) + A_log)) of the reference is evaluated as
+// exp2(delta * A2) with A2 = -exp(A_log) * log2(e) formed once per (channel,
+// state) in double and rounded to float; v_exp_f32 then costs one
+// transcendental per (token, channel, state).
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace nsosx {
+
+__device__ __forceinline__ float softplus_ref(float v) {
+    if (v > 20.0f) return v;
+    if (v < -20.0f) return expf(v);
+    return log1pf(expf(v));
+}
+
+__device__ __forceinline__ float silu_ref(float v) {
+    const float sig = v >= 0.0f ? 1.0f / (1.0f + expf(-v)) : expf(v) / (1.0f + expf(v));
+    return v * sig;
+}
+
+__device__ __forceinline__ float a2_from_log(float a_log) {
+    return static_cast<float>(-exp(static_cast<double>(a_log)) * 1.4426950408889634);
+}
+
+__device__ __forceinline__ float dpp_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float dpp_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
+}
+
+// ===========================================================================
+// Prefill scan.  A workgroup owns 64 channels of one sequence and walks its
+// tokens in order; lane l of the workgroup is channel c0 + l/4 and state
+// quad q = l%4, holding states n = q*SPL .. q*SPL+SPL-1 in registers.  Token
+// chunks of TC rows are staged in LDS with the per-(token, channel) terms
+// already formed (delta = softplus(dt), delta*x, x, silu(z)) and B/C of the
+// chunk.  After every 4 tokens the four lanes of a channel exchange partial
+// readouts with two DPP steps (a 4x4 transpose-reduce), so each lane
+// finishes one token's sum; y goes back through LDS for coalesced stores.
+// Requires channels-per-group (H*P/G) to be a multiple of 64 so a workgroup
+// sees one B/C group.
+// ===========================================================================
+constexpr int kScanTC = 32;       // tokens per LDS chunk
+constexpr int kScanCh = 64;       // channels per workgroup
+
+template <int ADT, int SPL, bool GATE>
+__global__ __launch_bounds__(256) void scan_fwd_kernel(
+    const void* __restrict__ x, int64_t x_stride, const void* __restrict__ dt,
+    const float* __restrict__ a_log, int a_per_state, const void* __restrict__ Bm,
+    const void* __restrict__ Cm, const float* __restrict__ Dskip, const void* __restrict__ z,
+    int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int H, int P, int N, int G,
+    const float* __restrict__ init_state, float* __restrict__ final_state, void* __restrict__ y) {
+    constexpr int NPAD = 4 * SPL;
+    __shared__ float s_delta[kScanTC][kScanCh];
+    __shared__ float s_dx[kScanTC][kScanCh];
+    __shared__ float s_x[kScanTC][kScanCh];
+    __shared__ float s_gz[kScanTC][kScanCh];
+    __shared__ __align__(16) float s_B[kScanTC][NPAD];
+    __shared__ __align__(16) float s_C[kScanTC][NPAD];
+    __shared__ float s_y[kScanTC][kScanCh + 1];
+
+    const int tid = threadIdx.x;
+    const int D = H * P;
+    const int GN = G * N;
+    const int c0 = blockIdx.x * kScanCh;
+    const int seq = blockIdx.y;
+    const int t0 = cu_seqlens[seq];
+    const int t1 = cu_seqlens[seq + 1];
+    const int cl = tid >> 2;          // channel within the block
+    const int q = tid & 3;            // state quad
+    const int c = c0 + cl;
+    const int h = c / P;
+    const int grp = (h * G) / H;
+    const float dsk = Dskip[h];
+
+    float a2[SPL], st[SPL];
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) {
+        const int n = q * SPL + i;
+        const bool ok = n < N;
+        const float al = a_per_state ? a_log[(int64_t)h * N + min(n, N - 1)] : a_log[h];
+        a2[i] = ok ? a2_from_log(al) : 0.0f;
+        st[i] = (ok && init_state) ? init_state[((int64_t)seq * D + c) * N + n] : 0.0f;
+    }
+
+    for (int tb = t0; tb < t1; tb += kScanTC) {
+        const int tc = min(kScanTC, t1 - tb);
+        // ---- stage the chunk -------------------------------------------------
+        for (int e = tid; e < kScanTC * kScanCh; e += 256) {
+            const int r = e / kScanCh, cc = e % kScanCh;
+            float dl = 0.0f, xv = 0.0f, gz = 1.0f;
+            if (r < tc) {
+                const int64_t t = tb + r;
+                const int ch = c0 + cc;
+                xv = load_act<ADT>(x, t * x_stride + ch);
+                dl = softplus_ref(load_act<ADT>(dt, t * H + ch / P));
+                if (GATE) gz = silu_ref(load_act<ADT>(z, t * z_stride + ch));
+            }
+            s_delta[r][cc] = dl;
+            s_dx[r][cc] = dl * xv;
+            s_x[r][cc] = xv;
+            s_gz[r][cc] = gz;
+        }
+        for (int e = tid; e < kScanTC * NPAD; e += 256) {
+            const int r = e / NPAD, n = e % NPAD;
+            float bv = 0.0f, cv = 0.0f;
+            if (r < tc && n < N) {
+                const int64_t off = (int64_t)(tb + r) * GN + grp * N + n;
+                bv = load_act<ADT>(Bm, off);
+                cv = load_act<ADT>(Cm, off);
+            }
+            s_B[r][n] = bv;
+            s_C[r][n] = cv;
+        }
+        __syncthreads();
+        // ---- recurrence, four tokens per transpose-reduce ---------------------
+        for (int r0 = 0; r0 < tc; r0 += 4) {
+            float part[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int r = r0 + u;  // rows past tc hold delta = 0, B = C = 0: state unchanged
+                const float dl = s_delta[r][cl];
+                const float dx = s_dx[r][cl];
+                float p = 0.0f;
+#pragma unroll
+                for (int i = 0; i < SPL; ++i) {
+                    const int n = q * SPL + i;
+                    const float a = __builtin_amdgcn_exp2f(dl * a2[i]);
+                    st[i] = __fmaf_rn(a, st[i], dx * s_B[r][n]);
+                    p = __fmaf_rn(st[i], s_C[r][n], p);
+                }
+                part[u] = p;
+            }
+            // lanes q: after xor-2 exchange keep tokens {0,1} (q<2) or {2,3};
+            // after xor-1 exchange keep one token: lane q owns token kq.
+            const bool hi2 = (q & 2) != 0;
+            const float s0 = hi2 ? part[0] : part[2];
+            const float s1 = hi2 ? part[1] : part[3];
+            const float k0 = hi2 ? part[2] : part[0];
+            const float k1 = hi2 ? part[3] : part[1];
+            const float m0 = k0 + dpp_xor2(s0);
+            const float m1 = k1 + dpp_xor2(s1);
+            const bool hi1 = (q & 1) != 0;
+            const float send = hi1 ? m0 : m1;
+            const float keep = hi1 ? m1 : m0;
+            const float tot = keep + dpp_xor1(send);
+            const int kq = (hi2 ? 2 : 0) + (hi1 ? 1 : 0);
+            const int r = r0 + kq;
+            if (r < tc) {
+                const float out = __fmaf_rn(dsk, s_x[r][cl], tot);
+                s_y[r][cl] = GATE ? out * s_gz[r][cl] : out;
+            }
+        }
+        __syncthreads();
+        // ---- coalesced store of y ---------------------------------------------
+        for (int e = tid; e < tc * kScanCh; e += 256) {
+            const int r = e / kScanCh, cc = e % kScanCh;
+            store_act<ADT>(y, (int64_t)(tb + r) * D + c0 + cc, s_y[r][cc]);
+        }
+        __syncthreads();
+    }
+    if (final_state) {
+#pragma unroll
+        for (int i = 0; i < SPL; ++i) {
+            const int n = q * SPL + i;
+            if (n < N) final_state[((int64_t)seq * D + c) * N + n] = st[i];
+        }
+    }
+}
+
+// Any shape: one lane per (sequence, channel), states in a loop, in the
+// reference's own order of operations.
+template <int ADT>
+__global__ __launch_bounds__(64) void scan_fwd_generic_kernel(
+    const void* __restrict__ x, int64_t x_stride, const void* __restrict__ dt,
+    const float* __restrict__ a_log, int a_per_state, const void* __restrict__ Bm,
+    const void* __restrict__ Cm, const float* __restrict__ Dskip, const void* __restrict__ z,
+    int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int num_seqs, int H, int P, int N,
+    int G, const float* __restrict__ init_state, float* __restrict__ final_state,
+    void* __restrict__ y) {
+    const int D = H * P;
+    const int GN = G * N;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)num_seqs * D) return;
+    const int seq = static_cast<int>(idx / D);
+    const int c = static_cast<int>(idx % D);
+    const int h = c / P;
+    const int grp = (h * G) / H;
+    float st[64];
+    for (int n = 0; n < N; ++n) st[n] = init_state ? init_state[((int64_t)seq * D + c) * N + n] : 0.0f;
+    for (int t = cu_seqlens[seq]; t < cu_seqlens[seq + 1]; ++t) {
+        const float xv = load_act<ADT>(x, (int64_t)t * x_stride + c);
+        const float dl = softplus_ref(load_act<ADT>(dt, (int64_t)t * H + h));
+        float out = Dskip[h] * xv;
+        for (int n = 0; n < N; ++n) {
+            const float al = a_per_state ? a_log[(int64_t)h * N + n] : a_log[h];
+            const float a = __builtin_amdgcn_exp2f(dl * a2_from_log(al));
+            const int64_t off = (int64_t)t * GN + grp * N + n;
+            st[n] = __fmaf_rn(a, st[n], (dl * load_act<ADT>(Bm, off)) * xv);
+            out = __fmaf_rn(st[n], load_act<ADT>(Cm, off), out);
+        }
+        if (z) out = out * silu_ref(load_act<ADT>(z, (int64_t)t * z_stride + c));
+        store_act<ADT>(y, (int64_t)t * D + c, out);
+    }
+    if (final_state)
+        for (int n = 0; n < N; ++n) final_state[((int64_t)seq * D + c) * N + n] = st[n];
+}
+
+// ===========================================================================
+// Decode step: one token per row against its own state [D, N], in place.
+// Lane = (row, channel, state quad); each lane streams its SPL states with
+// one 16-byte load and store per 4 states; the four lanes of a channel meet
+// with two DPP reductions.
+// ===========================================================================
+template <int ADT, int SPL, bool GATE>
+__global__ __launch_bounds__(256) void scan_step_kernel(
+    const void* __restrict__ x, const void* __restrict__ dt, const float* __restrict__ a_log,
+    int a_per_state, const void* __restrict__ Bm, const void* __restrict__ Cm,
+    const float* __restrict__ Dskip, const void* __restrict__ z, int rows, int H, int P, int N,
+    int G, float* __restrict__ state, void* __restrict__ y) {
+    const int D = H * P;
+    const int GN = G * N;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t lanes = (int64_t)rows * D * 4;
+    if (gid >= lanes) return;  // rows * D * 4 is a multiple of 4: whole quads exit together
+    const int q = static_cast<int>(gid & 3);
+    const int64_t rc = gid >> 2;
+    const int r = static_cast<int>(rc / D);
+    const int c = static_cast<int>(rc % D);
+    const int h = c / P;
+    const int grp = (h * G) / H;
+    const float xv = load_act<ADT>(x, (int64_t)r * D + c);
+    const float dl = softplus_ref(load_act<ADT>(dt, (int64_t)r * H + h));
+    const float dx = dl * xv;
+    float* sp = state + rc * N + q * SPL;
+    float p = 0.0f;
+    if (SPL == 4 && N == 16) {
+        float4 s4 = *reinterpret_cast<const float4*>(sp);
+        float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int n = q * 4 + i;
+            const float al = a_per_state ? a_log[(int64_t)h * N + n] : a_log[h];
+            const float a = __builtin_amdgcn_exp2f(dl * a2_from_log(al));
+            const int64_t off = (int64_t)r * GN + grp * N + n;
+            sv[i] = __fmaf_rn(a, sv[i], dx * load_act<ADT>(Bm, off));
+            p = __fmaf_rn(sv[i], load_act<ADT>(Cm, off), p);
+        }
+        *reinterpret_cast<float4*>(sp) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < SPL; ++i) {
+            const int n = q * SPL + i;
+            if (n < N) {
+                const float al = a_per_state ? a_log[(int64_t)h * N + n] : a_log[h];
+                const float a = __builtin_amdgcn_exp2f(dl * a2_from_log(al));
+                const int64_t off = (int64_t)r * GN + grp * N + n;
+                const float sv = __fmaf_rn(a, sp[i], dx * load_act<ADT>(Bm, off));
+                sp[i] = sv;
+                p = __fmaf_rn(sv, load_act<ADT>(Cm, off), p);
+            }
+        }
+    }
+    p += dpp_xor2(p);
+    p += dpp_xor1(p);
+    if (q == 0) {
+        float out = __fmaf_rn(Dskip[h], xv, p);
+        if (GATE) out = out * silu_ref(load_act<ADT>(z, (int64_t)r * D + c));
+        store_act<ADT>(y, (int64_t)r * D + c, out);
+    }
+}
+
+// ===========================================================================
+// Depthwise causal convolution + bias + SiLU, restarted per sequence.
+// Thread = (token, channel); the sequence start comes from a binary search
+// of cu_seqlens.
+// ===========================================================================
+template <int IDT, int ODT>
+__global__ __launch_bounds__(256) void conv1d_kernel(const void* __restrict__ in, int64_t in_stride,
+                                                     const float* __restrict__ w,
+                                                     const float* __restrict__ bias,
+                                                     const int32_t* __restrict__ cu_seqlens,
+                                                     int num_seqs, int T, int C, int W, int silu,
+                                                     void* __restrict__ out) {
+    const int c = blockIdx.y * blockDim.x + threadIdx.x;
+    const int t = blockIdx.x;
+    if (c >= C || t >= T) return;
+    int lo = 0, hi = num_seqs;  // find s with cu[s] <= t < cu[s+1]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (cu_seqlens[mid] <= t) lo = mid; else hi = mid;
+    }
+    const int ts = cu_seqlens[lo];
+    float acc = 0.0f;
+    for (int j = 0; j < W; ++j) {
+        const int src = t - (W - 1) + j;
+        if (src < ts) continue;
+        acc = __fmaf_rn(w[(int64_t)c * W + j], load_act<IDT>(in, (int64_t)src * in_stride + c), acc);
+    }
+    if (bias) acc = acc + bias[c];
+    if (silu) acc = silu_ref(acc);
+    store_act<ODT>(out, (int64_t)t * C + c, acc);
+}
+
+}  // namespace nsosx
+
+using namespace nsosx;
+
+extern "C" int nsosx_selective_scan_fwd(const void* x, int64_t x_stride, const void* dt,
+                                        const float* A_log, int a_per_state, const void* B,
+                                        const void* C, const float* D, const void* z,
+                                        int64_t z_stride, const int32_t* cu_seqlens, int num_seqs,
+                                        int total_tokens, int H, int P, int N, int G,
+                                        int act_dtype, const float* initial_state,
+                                        float* final_state, void* y, void* stream) {
+    if (!x || !dt || !A_log || !B || !C || !D || !cu_seqlens || !y)
+        return fail(NSOSX_ERR_INVALID, "selective_scan_fwd: null pointer");
+    if (num_seqs <= 0 || num_seqs > 65535 || total_tokens < 0 || H <= 0 || P <= 0 || N <= 0 ||
+        N > 64 || G <= 0 || H % G != 0)
+        return fail(NSOSX_ERR_INVALID, "selective_scan_fwd: bad shape (N <= 64, H % G == 0)");
+    if (!valid_dtype(act_dtype)) return fail(NSOSX_ERR_INVALID, "selective_scan_fwd: bad dtype");
+    const int Dm = H * P;
+    if (x_stride < Dm || (z && z_stride < Dm))
+        return fail(NSOSX_ERR_INVALID, "selective_scan_fwd: row stride smaller than H*P");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int per_group = Dm / G;
+    const bool fast = (per_group % kScanCh == 0) && N <= 64;
+    if (fast) {
+        const dim3 grid(Dm / kScanCh, num_seqs), block(256);
+        const int spl = N <= 4 ? 1 : N <= 8 ? 2 : N <= 16 ? 4 : N <= 32 ? 8 : 16;
+#define NSOSX_SCAN(ADT, SPL, GATE)                                                              \
+    hipLaunchKernelGGL((scan_fwd_kernel<ADT, SPL, GATE>), grid, block, 0, st, x, x_stride, dt,   \
+                       A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens, H, P, N, G,        \
+                       initial_state, final_state, y);
+#define NSOSX_SCAN_G(ADT, SPL) \
+    if (z) { NSOSX_SCAN(ADT, SPL, true) } else { NSOSX_SCAN(ADT, SPL, false) }
+#define NSOSX_SCAN_S(ADT)                          \
+    switch (spl) {                                 \
+        case 1: NSOSX_SCAN_G(ADT, 1) break;        \
+        case 2: NSOSX_SCAN_G(ADT, 2) break;        \
+        case 4: NSOSX_SCAN_G(ADT, 4) break;        \
+        case 8: NSOSX_SCAN_G(ADT, 8) break;        \
+        default: NSOSX_SCAN_G(ADT, 16) break;      \
+    }
+        if (act_dtype == NSOSX_F32) { NSOSX_SCAN_S(NSOSX_F32) } else { NSOSX_SCAN_S(NSOSX_BF16) }
+#undef NSOSX_SCAN_S
+#undef NSOSX_SCAN_G
+#undef NSOSX_SCAN
+    } else {
+        const int64_t lanes = (int64_t)num_seqs * Dm;
+        const dim3 grid((unsigned)((lanes + 63) / 64)), block(64);
+        if (act_dtype == NSOSX_F32)
+            hipLaunchKernelGGL(scan_fwd_generic_kernel<NSOSX_F32>, grid, block, 0, st, x, x_stride,
+                               dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens, num_seqs,
+                               H, P, N, G, initial_state, final_state, y);
+        else
+            hipLaunchKernelGGL(scan_fwd_generic_kernel<NSOSX_BF16>, grid, block, 0, st, x,
+                               x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens,
+                               num_seqs, H, P, N, G, initial_state, final_state, y);
+    }
+    return check_launch("selective_scan_fwd");
+}
+
+extern "C" int nsosx_selective_scan_step(const void* x, const void* dt, const float* A_log,
+                                         int a_per_state, const void* B, const void* C,
+                                         const float* D, const void* z, int rows, int H, int P,
+                                         int N, int G, int act_dtype, float* state, void* y,
+                                         void* stream) {
+    if (!x || !dt || !A_log || !B || !C || !D || !state || !y)
+        return fail(NSOSX_ERR_INVALID, "selective_scan_step: null pointer");
+    if (rows <= 0 || H <= 0 || P <= 0 || N <= 0 || N > 64 || G <= 0 || H % G != 0)
+        return fail(NSOSX_ERR_INVALID, "selective_scan_step: bad shape");
+    if (!valid_dtype(act_dtype)) return fail(NSOSX_ERR_INVALID, "selective_scan_step: bad dtype");
+    if (reinterpret_cast<uintptr_t>(state) % 16)
+        return fail(NSOSX_ERR_INVALID, "selective_scan_step: state must be 16-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int64_t lanes = (int64_t)rows * H * P * 4;
+    const dim3 grid((unsigned)((lanes + 255) / 256)), block(256);
+    const int spl = N <= 4 ? 1 : N <= 8 ? 2 : N <= 16 ? 4 : N <= 32 ? 8 : 16;
+#define NSOSX_STEP(ADT, SPL, GATE)                                                              \
+    hipLaunchKernelGGL((scan_step_kernel<ADT, SPL, GATE>), grid, block, 0, st, x, dt, A_log,     \
+                       a_per_state, B, C, D, z, rows, H, P, N, G, state, y);
+#define NSOSX_STEP_G(ADT, SPL) \
+    if (z) { NSOSX_STEP(ADT, SPL, true) } else { NSOSX_STEP(ADT, SPL, false) }
+#define NSOSX_STEP_S(ADT)                          \
+    switch (spl) {                                 \
+        case 1: NSOSX_STEP_G(ADT, 1) break;        \
+        case 2: NSOSX_STEP_G(ADT, 2) break;        \
+        case 4: NSOSX_STEP_G(ADT, 4) break;        \
+        case 8: NSOSX_STEP_G(ADT, 8) break;        \
+        default: NSOSX_STEP_G(ADT, 16) break;      \
+    }
+    if (act_dtype == NSOSX_F32) { NSOSX_STEP_S(NSOSX_F32) } else { NSOSX_STEP_S(NSOSX_BF16) }
+#undef NSOSX_STEP_S
+#undef NSOSX_STEP_G
+#undef NSOSX_STEP
+    return check_launch("selective_scan_step");
+}
+
+extern "C" int nsosx_conv1d_causal(const void* in, int in_dtype, int64_t in_stride,
+                                   const float* weight, const float* bias,
+                                   const int32_t* cu_seqlens, int num_seqs, int total_tokens,
+                                   int channels, int width, int apply_silu, void* out,
+                                   int out_dtype, void* stream) {
+    if (!in || !weight || !cu_seqlens || !out)
+        return fail(NSOSX_ERR_INVALID, "conv1d_causal: null pointer");
+    if (num_seqs <= 0 || total_tokens < 0 || channels <= 0 || channels > 65535 * 256 ||
+        width <= 0 || width > 64 || in_stride < channels)
+        return fail(NSOSX_ERR_INVALID, "conv1d_causal: bad shape");
+    if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype))
+        return fail(NSOSX_ERR_INVALID, "conv1d_causal: bad dtype");
+    if (total_tokens == 0) return NSOSX_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid(total_tokens, (channels + 255) / 256), block(256);
+#define NSOSX_CONV(I, O)                                                                        \
+    hipLaunchKernelGGL((conv1d_kernel<I, O>), grid, block, 0, st, in, in_stride, weight, bias,    \
+                       cu_seqlens, num_seqs, total_tokens, channels, width, apply_silu, out);
+    if (in_dtype == NSOSX_F32) {
+        if (out_dtype == NSOSX_F32) { NSOSX_CONV(NSOSX_F32, NSOSX_F32) } else { NSOSX_CONV(NSOSX_F32, NSOSX_BF16) }
+    } else {
+        if (out_dtype == NSOSX_F32) { NSOSX_CONV(NSOSX_BF16, NSOSX_F32) } else { NSOSX_CONV(NSOSX_BF16, NSOSX_BF16) }
+    }
+#undef NSOSX_CONV
+    return check_launch("conv1d_causal");
+}

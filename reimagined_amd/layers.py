@@ -1,0 +1,225 @@
+"""Layer-level compositions over the nsosx operators.
+
+  BitLinear          packed-path BitLinear::forward (src/bitlinear.cpp:439-741)
+  HybridMambaLayer   BitLinear in_proj -> causal conv + SiLU -> selective scan
+                     gated by SiLU(z) -> BitLinear out_proj over a packed
+                     ragged batch (the Mamba layer of JambaBlock::forward,
+                     src/jamba.cpp:3158-3375, with Mamba-1 A[D, N])
+  MoEFFN             MoERouter::forward from logits + JambaBlock::forward_moe
+                     (src/jamba.cpp:3692-3973, 8140-8319): device routing,
+                     grouped ternary GEMMs, squared ReLU, weighted combine
+
+Workspaces are allocated once per shape and reused, so a forward enqueues
+kernels only.  Citations are into OXN/nsos/ of vitorGgC569/reimagined.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import ops
+from ._lib import call
+from .ops import _DT, _p, _stream
+
+
+class BitLinear:
+    """Packed-path BitLinear: 2-bit ternary weights + per-tensor scale on the device.
+
+    rms_input: the RMS_PERI input norm (eps 1e-6) the reference applies by default.
+    """
+
+    def __init__(self, w_float: np.ndarray, device="cuda", bits: int = 8, rms_input: bool = True,
+                 magnitude=None, bias=None):
+        w_float = np.ascontiguousarray(w_float, dtype=np.float32)
+        self.out_features, self.in_features = w_float.shape
+        packed, ws = ops.pack_ternary(w_float)
+        self.packed = torch.from_numpy(packed.view(np.int32)).to(device)
+        self.weight_scale = ws
+        self.bits = bits
+        self.rms_input = rms_input
+        self.magnitude = None if magnitude is None else torch.as_tensor(
+            magnitude, dtype=torch.float32).to(device)
+        self.bias = None if bias is None else torch.as_tensor(bias, dtype=torch.float32).to(device)
+        self._ws = {}
+
+    @classmethod
+    def from_packed(cls, packed_u32: np.ndarray, weight_scale: float, out_features: int,
+                    in_features: int, device="cuda", **kw):
+        """import_packed_state (src/bitlinear.cpp:834-1036): rejects the reserved code 3."""
+        self = cls.__new__(cls)
+        self.out_features, self.in_features = out_features, in_features
+        if in_features % 16 or packed_u32.size != out_features * in_features // 16:
+            raise ValueError("packed weights do not match [out, in] with in % 16 == 0")
+        self.packed = torch.from_numpy(np.ascontiguousarray(packed_u32).view(np.int32)).to(device)
+        bad = ops.find_reserved_code(self.packed, out_features * in_features)
+        if bad >= 0:
+            raise ValueError(f"packed weights hold the reserved code 3 at index {bad}")
+        self.weight_scale = float(weight_scale)
+        self.bits = kw.get("bits", 8)
+        self.rms_input = kw.get("rms_input", True)
+        self.magnitude = kw.get("magnitude")
+        self.bias = kw.get("bias")
+        self._ws = {}
+        return self
+
+    def workspace(self, m: int, device):
+        ws = self._ws.get(m)
+        if ws is None:
+            ws = (torch.empty((m, self.in_features), dtype=torch.int8, device=device),
+                  torch.empty(m, dtype=torch.float32, device=device),
+                  torch.empty(m, dtype=torch.float32, device=device))
+            self._ws[m] = ws
+        return ws
+
+    def forward_into(self, x: torch.Tensor, y: torch.Tensor, marker=None) -> torch.Tensor:
+        """Quantize (with RMS_PERI when set) then the ternary GEMM/GEMV into y.
+
+        marker(name) is called after each kernel (e.g. to record a stream event).
+        """
+        m = x.shape[0]
+        qw, sw, rw = self.workspace(m, x.device)
+        st = _stream()
+        call("nsosx_quantize_act_i8", _p(x), ops._dt(x), m, self.in_features, self.bits,
+             int(self.rms_input), _p(qw), _p(sw), _p(rw), st)
+        if marker:
+            marker("quant")
+        call("nsosx_ternary_gemm", _p(qw), _p(sw), _p(self.packed), self.weight_scale, m,
+             self.in_features, self.out_features, _p(self.magnitude), _p(self.bias), _p(y),
+             _DT[y.dtype], None, st)
+        if marker:
+            marker("gemm")
+        return y
+
+    def forward(self, x: torch.Tensor, out_dtype=None) -> torch.Tensor:
+        y = torch.empty((x.shape[0], self.out_features), dtype=out_dtype or x.dtype,
+                        device=x.device)
+        return self.forward_into(x, y)
+
+    def view_entry(self):
+        return (self.packed, self.weight_scale, self.in_features, self.out_features,
+                self.magnitude, self.bias)
+
+
+class HybridMambaLayer:
+    """d_model -> in_proj [x | z] -> conv4 + SiLU -> scan -> gate -> out_proj."""
+
+    def __init__(self, params: dict, device="cuda", rms_input: bool = True):
+        self.d_model = params["w_in"].shape[1]
+        self.d_inner = params["w_out"].shape[1]
+        self.d_state = params["a_log"].shape[1]
+        self.in_proj = BitLinear(params["w_in"], device, rms_input=rms_input)
+        self.out_proj = BitLinear(params["w_out"], device, rms_input=rms_input)
+        f32 = dict(dtype=torch.float32, device=device)
+        self.conv_w = torch.as_tensor(params["conv_w"], **f32)
+        self.conv_b = torch.as_tensor(params["conv_b"], **f32)
+        self.a_log = torch.as_tensor(params["a_log"], **f32)
+        self.d_skip = torch.as_tensor(params["d_skip"], **f32)
+        self._buf = {}
+
+    def _buffers(self, t: int, device, dtype):
+        b = self._buf.get(t)
+        if b is None:
+            b = {
+                "xz": torch.empty((t, 2 * self.d_inner), dtype=dtype, device=device),
+                "xc": torch.empty((t, self.d_inner), dtype=dtype, device=device),
+                "ys": torch.empty((t, self.d_inner), dtype=dtype, device=device),
+                "out": torch.empty((t, self.d_model), dtype=dtype, device=device),
+            }
+            self._buf[t] = b
+        return b
+
+    def forward(self, x, dt, B, C, cu_seqlens, final_state=None, marker=None):
+        """x [T, d_model]; dt [T, d_inner]; B, C [T, d_state]; cu_seqlens int32 [S+1].
+
+        marker(name), when given, is called after each kernel of the layer.
+        """
+        t = x.shape[0]
+        s = cu_seqlens.numel() - 1
+        b = self._buffers(t, x.device, x.dtype)
+        di, n = self.d_inner, self.d_state
+        mk = (lambda pre: (lambda name: marker(f"{pre}_{name}"))) if marker else (lambda pre: None)
+        self.in_proj.forward_into(x, b["xz"], mk("in_proj"))
+        xin = b["xz"][:, :di]
+        z = b["xz"][:, di:]
+        call("nsosx_conv1d_causal", _p(xin), ops._dt(xin), xin.stride(0), _p(self.conv_w),
+             _p(self.conv_b), _p(cu_seqlens), s, t, di, self.conv_w.shape[1], 1, _p(b["xc"]),
+             ops._dt(b["xc"]), _stream())
+        if marker:
+            marker("conv")
+        call("nsosx_selective_scan_fwd", _p(b["xc"]), di, _p(dt), _p(self.a_log), 1, _p(B), _p(C),
+             _p(self.d_skip), _p(z), z.stride(0), _p(cu_seqlens), s, t, di, 1, n, 1,
+             ops._dt(x), None, _p(final_state), _p(b["ys"]), _stream())
+        if marker:
+            marker("scan")
+        self.out_proj.forward_into(b["ys"], b["out"], mk("out_proj"))
+        return b["out"]
+
+
+class MoEFFN:
+    """BASELINE config 5 MoE: top-k routing, expert gate_up -> squared ReLU -> down, combine."""
+
+    def __init__(self, w_up: list, w_down: list, device="cuda", k: int = 2,
+                 rms_input: bool = True, hidden_dtype=torch.float32):
+        self.experts = len(w_up)
+        self.k = k
+        self.up = [BitLinear(w, device, rms_input=rms_input) for w in w_up]
+        self.down = [BitLinear(w, device, rms_input=rms_input) for w in w_down]
+        self.d_model = self.up[0].in_features
+        self.d_ff = self.up[0].out_features
+        self.rms_input = rms_input
+        self.hidden_dtype = hidden_dtype
+        self.up_views = ops.LinearViewArray([e.view_entry() for e in self.up], device)
+        self.down_views = ops.LinearViewArray([e.view_entry() for e in self.down], device)
+        self._buf = {}
+
+    def _buffers(self, rows: int, device):
+        b = self._buf.get(rows)
+        if b is None:
+            slots = rows * self.k
+            i32 = dict(dtype=torch.int32, device=device)
+            b = {
+                "weights": torch.empty((rows, self.experts), dtype=torch.float32, device=device),
+                "selected": torch.empty((rows, self.k), **i32),
+                "counts": torch.empty(self.experts, **i32),
+                "offsets": torch.empty(self.experts + 1, **i32),
+                "perm": torch.empty(slots, **i32),
+                "slot_of": torch.empty((rows, self.k), **i32),
+                "route_ws": torch.empty(max(1, int(ops.lib().nsosx_moe_route_workspace(
+                    rows, self.experts))), **i32),
+                "q1": torch.empty((rows, self.d_model), dtype=torch.int8, device=device),
+                "s1": torch.empty(rows, dtype=torch.float32, device=device),
+                "r1": torch.empty(rows, dtype=torch.float32, device=device),
+                "h": torch.empty((slots, self.d_ff), dtype=self.hidden_dtype, device=device),
+                "q2": torch.empty((slots, self.d_ff), dtype=torch.int8, device=device),
+                "s2": torch.empty(slots, dtype=torch.float32, device=device),
+                "r2": torch.empty(slots, dtype=torch.float32, device=device),
+                "o": torch.empty((slots, self.d_model), dtype=torch.float32, device=device),
+            }
+            self._buf[rows] = b
+        return b
+
+    def forward(self, x: torch.Tensor, logits: torch.Tensor, out_dtype=None) -> dict:
+        rows = x.shape[0]
+        b = self._buffers(rows, x.device)
+        e, k = self.experts, self.k
+        st = _stream()
+        call("nsosx_moe_route", _p(logits), rows, e, k, _p(b["weights"]), _p(b["selected"]),
+             _p(b["counts"]), _p(b["offsets"]), _p(b["perm"]), _p(b["slot_of"]),
+             _p(b["route_ws"]), st)
+        call("nsosx_quantize_act_i8", _p(x), ops._dt(x), rows, self.d_model, 8,
+             int(self.rms_input), _p(b["q1"]), _p(b["s1"]), _p(b["r1"]), st)
+        call("nsosx_grouped_ternary_gemm", self.up_views.ptr, e, _p(b["offsets"]), _p(b["perm"]),
+             1, _p(b["q1"]), _p(b["s1"]), self.d_model, self.d_ff, rows, 1, _p(b["h"]),
+             _DT[self.hidden_dtype], st)
+        slots = rows * k
+        call("nsosx_quantize_act_i8", _p(b["h"]), _DT[self.hidden_dtype], slots, self.d_ff, 8,
+             int(self.rms_input), _p(b["q2"]), _p(b["s2"]), _p(b["r2"]), st)
+        call("nsosx_grouped_ternary_gemm", self.down_views.ptr, e, _p(b["offsets"]), None, 0,
+             _p(b["q2"]), _p(b["s2"]), self.d_ff, self.d_model, rows, 0, _p(b["o"]),
+             _DT[torch.float32], st)
+        out = torch.empty((rows, self.d_model), dtype=out_dtype or x.dtype, device=x.device)
+        call("nsosx_moe_combine", _p(b["o"]), _DT[torch.float32], _p(b["slot_of"]),
+             _p(b["selected"]), _p(b["weights"]), rows, e, k, self.d_model, _p(out),
+             _DT[out.dtype], st)
+        return {"out": out, **{n: b[n] for n in ("weights", "selected", "counts", "offsets",
+                                                 "perm", "slot_of", "h", "o")}}

@@ -1,0 +1,267 @@
+"""Host-side operators over the nsosx C ABI (torch supplies device memory and streams).
+
+Each function mirrors the reference operator it replaces (OXN/nsos/ of
+vitorGgC569/reimagined): argument meaning, shapes and error behaviour
+(ValueError for rejected shapes, as the reference's std::invalid_argument).
+All work is enqueued on torch's current stream without synchronising.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from ._lib import call, lib
+
+F32, BF16 = 0, 1
+_DT = {torch.float32: F32, torch.bfloat16: BF16}
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}: float32 or bfloat16") from None
+
+
+def _p(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dev(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+# ---- weights -------------------------------------------------------------------
+
+def pack_ternary(w) -> tuple[np.ndarray, float]:
+    """BitLinear::pack_weights (src/bitlinear.cpp:152-193) on the host.
+
+    w: float [N, K] (numpy or CPU tensor).  Returns (packed uint32 [N*K/16], weight_scale).
+    """
+    w = np.ascontiguousarray(w.numpy() if isinstance(w, torch.Tensor) else w, dtype=np.float32)
+    if w.ndim != 2:
+        raise ValueError("pack_ternary expects a 2-D [N, K] matrix")
+    n, k = w.shape
+    packed = np.zeros(n * k // 16 if k % 16 == 0 else 0, np.uint32)
+    ws = ctypes.c_float()
+    call("nsosx_pack_ternary", w.ctypes.data_as(ctypes.c_void_p), n, k,
+         packed.ctypes.data_as(ctypes.c_void_p), ctypes.byref(ws))
+    return packed, float(ws.value)
+
+
+def unpack_ternary(packed, n: int) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.uint32)
+    out = np.empty(n, np.int8)
+    call("nsosx_unpack_ternary", packed.ctypes.data_as(ctypes.c_void_p), n,
+         out.ctypes.data_as(ctypes.c_void_p))
+    return out
+
+
+def find_reserved_code(packed: torch.Tensor, n_codes: int) -> int:
+    """Device import check (src/bitlinear.cpp:876-885): index of the first code 3, or -1."""
+    _dev(packed, "packed")
+    out = torch.empty(1, dtype=torch.int64, device=packed.device)
+    call("nsosx_find_reserved_code", _p(packed), n_codes, _p(out), _stream())
+    return int(out.item())
+
+
+# ---- BitLinear ------------------------------------------------------------------
+
+def quantize_activations_bitnet(x: torch.Tensor, bits: int = 8, rms_input: bool = False):
+    """quantize_activations_bitnet (+ RMS_PERI) -> (q int8 [M,K], act_scale f32 [M])."""
+    _dev(x, "x")
+    m, k = x.shape
+    q = torch.empty((m, k), dtype=torch.int8, device=x.device)
+    s = torch.empty(m, dtype=torch.float32, device=x.device)
+    ws = torch.empty(m, dtype=torch.float32, device=x.device) if rms_input else None
+    call("nsosx_quantize_act_i8", _p(x), _dt(x), m, k, bits, int(rms_input), _p(q), _p(s), _p(ws),
+         _stream())
+    return q, s
+
+
+def ternary_gemm(q: torch.Tensor, act_scale: torch.Tensor, packed: torch.Tensor, ws: float,
+                 n_out: int, magnitude=None, bias=None, out_dtype=torch.float32,
+                 want_acc: bool = False, path: int | None = None, want_y: bool = True):
+    """gemm_158bit_i8 integer core + affine (src/bitnet_adapter_avx2.cpp:52-158).
+
+    Returns y [M, N] (or (y, acc int32 [M, N]) with want_acc).
+    """
+    for t, nm in ((q, "q"), (act_scale, "act_scale"), (packed, "packed")):
+        _dev(t, nm)
+    m, k = q.shape
+    y = torch.empty((m, n_out), dtype=out_dtype, device=q.device) if want_y else None
+    acc = torch.empty((m, n_out), dtype=torch.int32, device=q.device) if want_acc else None
+    ydt = _DT[out_dtype]
+    if path is None:
+        call("nsosx_ternary_gemm", _p(q), _p(act_scale), _p(packed), ws, m, k, n_out,
+             _p(magnitude), _p(bias), _p(y), ydt, _p(acc), _stream())
+    else:
+        call("nsosx_ternary_gemm_path", _p(q), _p(act_scale), _p(packed), ws, m, k, n_out,
+             _p(magnitude), _p(bias), _p(y), ydt, _p(acc), path, _stream())
+    if want_acc:
+        return y, acc
+    return y
+
+
+def bitnet_gemm_158bit_gpu(x: torch.Tensor, packed: torch.Tensor, weight_scale: float, M: int,
+                           K: int, N: int, precision_bits: int = 8, magnitude=None, bias=None,
+                           rms_input: bool = False, out_dtype=torch.float32) -> torch.Tensor:
+    """bitnet_gemm_158bit_gpu (include/bitnet_gpu_dispatch.h:46-51): quantize + ternary GEMM."""
+    _dev(x, "x")
+    _dev(packed, "packed")
+    if x.numel() != M * K:
+        raise ValueError("bitnet_gemm_158bit_gpu: x does not hold M*K elements")
+    qw = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    sw = torch.empty(M, dtype=torch.float32, device=x.device)
+    rw = torch.empty(M, dtype=torch.float32, device=x.device) if rms_input else None
+    y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    call("nsosx_bitlinear_forward", _p(x), _dt(x), _p(packed), weight_scale, M, K, N,
+         precision_bits, int(rms_input), _p(magnitude), _p(bias), _p(y), _DT[out_dtype], _p(qw),
+         _p(sw), _p(rw), _stream())
+    return y
+
+
+class LinearViewArray:
+    """Device array of nsosx_linear_view descriptors (GpuLinearView's C shape).
+
+    Borrows the tensors it points at; keeps Python references so they outlive it.
+    """
+
+    class _View(ctypes.Structure):
+        _fields_ = [("packed", ctypes.c_void_p), ("magnitude", ctypes.c_void_p),
+                    ("bias", ctypes.c_void_p), ("inputs", ctypes.c_int),
+                    ("outputs", ctypes.c_int), ("weight_scale", ctypes.c_float)]
+
+    def __init__(self, entries, device):
+        self._keep = []
+        arr = (self._View * len(entries))()
+        for i, (packed, ws, inputs, outputs, mag, bias) in enumerate(entries):
+            self._keep += [packed, mag, bias]
+            arr[i].packed = packed.data_ptr()
+            arr[i].magnitude = None if mag is None else mag.data_ptr()
+            arr[i].bias = None if bias is None else bias.data_ptr()
+            arr[i].inputs = inputs
+            arr[i].outputs = outputs
+            arr[i].weight_scale = ws
+        raw = bytes(arr)
+        host = torch.frombuffer(bytearray(raw), dtype=torch.uint8)
+        self.tensor = host.to(device)
+        self.count = len(entries)
+
+    @property
+    def ptr(self):
+        return ctypes.c_void_p(self.tensor.data_ptr())
+
+
+def grouped_gemv(views: LinearViewArray, q: torch.Tensor, act_scale: torch.Tensor, n_out: int,
+                 out_dtype=torch.bfloat16) -> torch.Tensor:
+    """Grouped decode projections (include/cuda/kernels.cuh:27-29).
+
+    q: int8 [G, M, K]; act_scale [G, M]; returns y [G, M, n_out].
+    """
+    g, m, k = q.shape
+    y = torch.empty((g, m, n_out), dtype=out_dtype, device=q.device)
+    call("nsosx_grouped_gemv", views.ptr, g, _p(q), m * k, _p(act_scale), m, m, _p(y), m * n_out,
+         _DT[out_dtype], _stream())
+    return y
+
+
+# ---- Mamba ----------------------------------------------------------------------
+
+def conv1d_causal(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tensor, bias=None,
+                  silu: bool = True, out_dtype=None) -> torch.Tensor:
+    """Depthwise causal conv + bias + SiLU per sequence (src/mamba2.cpp:1056-1076, 2437-2446).
+
+    x may be a column slice of a wider row-major tensor (unit stride in the last dim).
+    """
+    if x.stride(1) != 1:
+        raise ValueError("conv1d_causal: x must have unit stride in the channel dim")
+    t, c = x.shape
+    out_dtype = out_dtype or x.dtype
+    out = torch.empty((t, c), dtype=out_dtype, device=x.device)
+    call("nsosx_conv1d_causal", _p(x), _dt(x), x.stride(0), _p(weight), _p(bias), _p(cu_seqlens),
+         cu_seqlens.numel() - 1, t, c, weight.shape[1], int(silu), _p(out), _DT[out_dtype],
+         _stream())
+    return out
+
+
+def selective_scan_fwd(x, dt, a_log, B, C, D, z, cu_seqlens, H, P, N, G, initial_state=None,
+                       want_final: bool = True):
+    """Packed ragged faithful scan (src/mamba2.cpp:2602-2675) -> (y [T, H*P], final [S, H*P, N])."""
+    t = x.shape[0]
+    s = cu_seqlens.numel() - 1
+    if x.stride(1) != 1 or (z is not None and z.stride(1) != 1):
+        raise ValueError("selective_scan_fwd: x and z need unit stride in the channel dim")
+    a_per_state = int(a_log.numel() == H * N and N > 1)
+    y = torch.empty((t, H * P), dtype=x.dtype, device=x.device)
+    fin = torch.empty((s, H * P, N), dtype=torch.float32, device=x.device) if want_final else None
+    call("nsosx_selective_scan_fwd", _p(x), x.stride(0), _p(dt), _p(a_log), a_per_state, _p(B),
+         _p(C), _p(D), _p(z), 0 if z is None else z.stride(0), _p(cu_seqlens), s, t, H, P, N, G,
+         _dt(x), _p(initial_state), _p(fin), _p(y), _stream())
+    return y, fin
+
+
+def selective_scan_step(x, dt, a_log, B, C, D, z, state, H, P, N, G):
+    """Decode step in place on `state` [R, H*P, N] (src/mamba2.cpp:4038-4125) -> y [R, H*P]."""
+    r = x.shape[0]
+    a_per_state = int(a_log.numel() == H * N and N > 1)
+    y = torch.empty_like(x)
+    call("nsosx_selective_scan_step", _p(x), _p(dt), _p(a_log), a_per_state, _p(B), _p(C), _p(D),
+         _p(z), r, H, P, N, G, _dt(x), _p(state), _p(y), _stream())
+    return y
+
+
+# ---- MoE ------------------------------------------------------------------------
+
+def moe_route(logits: torch.Tensor, k: int = 2) -> dict:
+    """MoERouter::forward from logits + forward_moe's ordered dispatch, on the device."""
+    _dev(logits, "logits")
+    rows, e = logits.shape
+    dev = logits.device
+    out = {
+        "weights": torch.empty((rows, e), dtype=torch.float32, device=dev),
+        "selected": torch.empty((rows, k), dtype=torch.int32, device=dev),
+        "counts": torch.empty(e, dtype=torch.int32, device=dev),
+        "offsets": torch.empty(e + 1, dtype=torch.int32, device=dev),
+        "perm": torch.empty(rows * k, dtype=torch.int32, device=dev),
+        "slot_of": torch.empty((rows, k), dtype=torch.int32, device=dev),
+    }
+    ws = torch.empty(max(1, int(lib().nsosx_moe_route_workspace(rows, e))), dtype=torch.int32,
+                     device=dev)
+    call("nsosx_moe_route", _p(logits), rows, e, k, _p(out["weights"]), _p(out["selected"]),
+         _p(out["counts"]), _p(out["offsets"]), _p(out["perm"]), _p(out["slot_of"]), _p(ws),
+         _stream())
+    return out
+
+
+def grouped_ternary_gemm(views: LinearViewArray, offsets, perm, q, act_scale, n_out: int,
+                         max_rows_per_expert: int, squared_relu: bool = False,
+                         gather: bool = True, out_dtype=torch.float32) -> torch.Tensor:
+    """Per-expert ternary GEMMs over slot segments -> y [slots, n_out] in slot order."""
+    slots = int(perm.numel()) if gather else q.shape[0]
+    k = q.shape[1]
+    y = torch.empty((slots, n_out), dtype=out_dtype, device=q.device)
+    call("nsosx_grouped_ternary_gemm", views.ptr, views.count, _p(offsets), _p(perm), int(gather),
+         _p(q), _p(act_scale), k, n_out, max_rows_per_expert, int(squared_relu), _p(y),
+         _DT[out_dtype], _stream())
+    return y
+
+
+def moe_combine(expert_out, slot_of, selected, weights, out_dtype=torch.float32) -> torch.Tensor:
+    rows, e = weights.shape
+    k = selected.shape[1]
+    dim = expert_out.shape[1]
+    out = torch.empty((rows, dim), dtype=out_dtype, device=expert_out.device)
+    call("nsosx_moe_combine", _p(expert_out), _dt(expert_out), _p(slot_of), _p(selected),
+         _p(weights), rows, e, k, dim, _p(out), _DT[out_dtype], _stream())
+    return out

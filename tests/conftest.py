@@ -16,3 +16,13 @@ def pytest_configure(config):
 def orc():
     from oracle import oracle
     return oracle
+
+
+@pytest.fixture(scope="session")
+def dev():
+    """The GPU under test; a GPU test without one fails rather than skips."""
+    import torch
+    assert torch.cuda.is_available(), "gpu-marked test needs a GPU"
+    import reimagined_amd
+    reimagined_amd.lib()
+    return torch.device("cuda:0")

@@ -1,0 +1,178 @@
+"""BitLinear on the GPU against the CPU oracle: activation codes, int32
+accumulators and fp32 outputs bit-exact; bf16 outputs equal to the oracle's
+fp32 value rounded to bf16.  Covers the reference's golden quantizer vectors,
+ragged and tail shapes, the decode GEMV for M = 1..8 and the MFMA GEMM."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from reimagined_amd import ops
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quant_ref.npz")
+
+
+def _bf16_round(a: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def _weights(rng, n, k):
+    return rng.standard_normal((n, k)).astype(np.float32)
+
+
+def test_quantize_matches_reference_golden(dev, orc):
+    g = np.load(GOLDEN, allow_pickle=False)
+    names = sorted({k.split("__")[0] for k in g.files if not k.startswith("rowsum")})
+    for name in names:
+        x = g[f"{name}__x"]
+        xt = torch.from_numpy(x).to(dev)
+        for bits in (2, 4, 8):
+            q, s = ops.quantize_activations_bitnet(xt, bits)
+            want = np.clip(g[f"{name}__b{bits}__codes"], -127, 127).astype(np.int8)
+            np.testing.assert_array_equal(q.cpu().numpy(), want, err_msg=f"{name} b{bits}")
+            np.testing.assert_array_equal(s.cpu().numpy(), g[f"{name}__b{bits}__scales"])
+
+
+@pytest.mark.parametrize("m,k", [(1, 16), (5, 1003), (33, 768), (7, 4096), (3, 8200), (64, 2048)])
+@pytest.mark.parametrize("rms", [False, True])
+def test_quantize_random_f32(dev, orc, m, k, rms):
+    rng = np.random.default_rng(m * 1000 + k)
+    x = (rng.standard_normal((m, k)) * rng.uniform(0.1, 30)).astype(np.float32)
+    q, s = ops.quantize_activations_bitnet(torch.from_numpy(x).to(dev), 8, rms_input=rms)
+    src = orc.rmsnorm(x, 1e-6) if rms else x
+    wq, ws = orc.quantize_act(src, 8)
+    np.testing.assert_array_equal(q.cpu().numpy(), wq)
+    np.testing.assert_array_equal(s.cpu().numpy(), ws)
+
+
+@pytest.mark.parametrize("rms", [False, True])
+def test_quantize_bf16_input(dev, orc, rms):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((37, 1024)).astype(np.float32)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    q, s = ops.quantize_activations_bitnet(xb.to(dev), 8, rms_input=rms)
+    xf = xb.float().numpy()
+    wq, ws = orc.quantize_act(orc.rmsnorm(xf, 1e-6) if rms else xf, 8)
+    np.testing.assert_array_equal(q.cpu().numpy(), wq)
+    np.testing.assert_array_equal(s.cpu().numpy(), ws)
+
+
+def _gemm_case(dev, orc, m, n, k, path, mag=False, bias=False, seed=0):
+    rng = np.random.default_rng(seed + m * 7 + n * 13 + k)
+    w = _weights(rng, n, k)
+    packed, ws, codes = orc.pack_weights(w)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    q, s = orc.quantize_act(x, 8)
+    mg = rng.uniform(0.5, 1.5, n).astype(np.float32) if mag else None
+    bs = rng.standard_normal(n).astype(np.float32) if bias else None
+    acc_want = orc.gemm_i8(q, codes)
+    y_want = orc.dequant(acc_want, s, ws, mg, bs)
+    t = lambda a: None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    pk = torch.from_numpy(packed.view(np.int32)).to(dev)
+    y, acc = ops.ternary_gemm(t(q), t(s), pk, ws, n, t(mg), t(bs), torch.float32, want_acc=True,
+                              path=path)
+    np.testing.assert_array_equal(acc.cpu().numpy(), acc_want)
+    np.testing.assert_array_equal(y.cpu().numpy(), y_want)
+    yb = ops.ternary_gemm(t(q), t(s), pk, ws, n, t(mg), t(bs), torch.bfloat16, path=path)
+    np.testing.assert_array_equal(yb.float().cpu().numpy(), _bf16_round(y_want))
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("n,k", [(768, 768), (130, 2048), (64, 48), (33, 4096), (40, 8192)])
+def test_gemv_bit_exact(dev, orc, m, n, k):
+    _gemm_case(dev, orc, m, n, k, path=0, mag=(m % 2 == 0), bias=(m % 3 == 0))
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 768, 768), (1, 64, 64), (129, 257, 1040), (300, 520, 2048),
+                                   (256, 512, 48), (77, 1024, 4096)])
+def test_mfma_gemm_bit_exact(dev, orc, m, n, k):
+    _gemm_case(dev, orc, m, n, k, path=1, mag=True, bias=(n % 2 == 0))
+
+
+def test_gemm_dispatch_and_extremes(dev, orc):
+    # |acc| = 127 * K at the extremes: int32 accumulation must not saturate or wrap
+    k, n = 4096, 64
+    q = np.full((9, k), 127, np.int8)
+    q[1::2] = -127
+    codes = np.ones((n, k), np.int8)
+    codes[1::2] = -1
+    packed = orc.pack_codes(codes).view(np.uint32)
+    s = np.ones(9, np.float32)
+    for path in (0, 1):
+        m = 8 if path == 0 else 9
+        y, acc = ops.ternary_gemm(torch.from_numpy(q[:m]).to(dev), torch.from_numpy(s[:m]).to(dev),
+                                  torch.from_numpy(packed.view(np.int32)).to(dev), 1.0, n,
+                                  want_acc=True, path=path)
+        np.testing.assert_array_equal(acc.cpu().numpy(), orc.gemm_i8(q[:m], codes))
+
+
+def test_reserved_code_is_zero_and_detected(dev, orc):
+    rng = np.random.default_rng(5)
+    n, k = 32, 64
+    codes = rng.integers(-1, 2, size=(n, k)).astype(np.int8)
+    packed = orc.pack_codes(codes).view(np.uint32).copy()
+    packed[7] |= 0x3 << 10  # element 7*16 + 5 becomes code 3
+    pk = torch.from_numpy(packed.view(np.int32)).to(dev)
+    assert ops.find_reserved_code(pk, n * k) == 7 * 16 + 5
+    codes_ref = orc.unpack_codes(packed, n * k).reshape(n, k)
+    q = rng.integers(-127, 128, size=(4, k)).astype(np.int8)
+    s = np.ones(4, np.float32)
+    _, acc = ops.ternary_gemm(torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev), pk, 1.0,
+                              n, want_acc=True, path=0)
+    np.testing.assert_array_equal(acc.cpu().numpy(), orc.gemm_i8(q, codes_ref))
+    clean = torch.from_numpy(orc.pack_codes(codes).view(np.int32)).to(dev)
+    assert ops.find_reserved_code(clean, n * k) == -1
+
+
+@pytest.mark.parametrize("m", [1, 16, 200])
+@pytest.mark.parametrize("rms", [False, True])
+def test_bitlinear_forward_end_to_end(dev, orc, m, rms):
+    rng = np.random.default_rng(m)
+    n, k = 768, 768
+    w = _weights(rng, n, k)
+    packed, ws, _ = orc.pack_weights(w)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    mg = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    bs = rng.standard_normal(n).astype(np.float32)
+    want = orc.bitlinear_forward(x, packed, ws, n, bits=8, rms_input=rms, magnitude=mg, bias=bs)
+    y = ops.bitnet_gemm_158bit_gpu(torch.from_numpy(x).to(dev),
+                                   torch.from_numpy(packed.view(np.int32)).to(dev), ws, m, k, n, 8,
+                                   torch.from_numpy(mg).to(dev), torch.from_numpy(bs).to(dev),
+                                   rms_input=rms)
+    np.testing.assert_array_equal(y.cpu().numpy(), want)
+
+
+def test_grouped_gemv_matches_per_group(dev, orc):
+    rng = np.random.default_rng(9)
+    groups, m, k, n = 5, 3, 1024, 256
+    entries, wants, qs, ss = [], [], [], []
+    for g in range(groups):
+        w = _weights(rng, n, k)
+        packed, ws, codes = orc.pack_weights(w)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        q, s = orc.quantize_act(x, 8)
+        bias = rng.standard_normal(n).astype(np.float32) if g % 2 else None
+        wants.append(orc.dequant(orc.gemm_i8(q, codes), s, ws, None, bias))
+        entries.append((torch.from_numpy(packed.view(np.int32)).to(dev), ws, k, n, None,
+                        None if bias is None else torch.from_numpy(bias).to(dev)))
+        qs.append(q)
+        ss.append(s)
+    views = ops.LinearViewArray(entries, dev)
+    y = ops.grouped_gemv(views, torch.from_numpy(np.stack(qs)).to(dev),
+                         torch.from_numpy(np.stack(ss)).to(dev), n, out_dtype=torch.float32)
+    np.testing.assert_array_equal(y.cpu().numpy(), np.stack(wants))
+
+
+def test_rejects_bad_arguments(dev):
+    q = torch.zeros((2, 24), dtype=torch.int8, device=dev)
+    s = torch.ones(2, device=dev)
+    pk = torch.zeros(6, dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):
+        ops.ternary_gemm(q, s, pk, 1.0, 4)  # K % 16 != 0
+    q = torch.zeros((2, 32), dtype=torch.int8, device=dev)
+    with pytest.raises(ValueError):
+        ops.ternary_gemm(q, s, pk, 0.0, 4)  # weight_scale must be > 0
+    with pytest.raises(ValueError):
+        ops.ternary_gemm(q, s, pk, 1.0, 4, path=0, want_y=False)  # no output

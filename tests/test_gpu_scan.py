@@ -1,0 +1,146 @@
+"""Selective scan, decode step and causal conv on the GPU against the CPU oracle.
+
+Tolerance (fp32 I/O): |gpu - oracle| <= 1e-5 + 1e-4 * |oracle| elementwise, the
+north-star bound; the oracle forms decay in double, the GPU as exp2 of a float
+product, and the readout sums states in a different order.  bf16 I/O: the
+oracle runs in fp32 on the same bf16-rounded inputs; outputs within 2e-2
+relative of the output scale (atol 2e-2 * max|oracle| / 64 plus rtol 2e-2)."""
+import numpy as np
+import pytest
+import torch
+
+from reimagined_amd import ops
+
+pytestmark = pytest.mark.gpu
+RTOL, ATOL = 1e-4, 1e-5
+
+
+def _inputs(rng, T, H, P, N, G, per_state=True):
+    D = H * P
+    return dict(
+        x=rng.standard_normal((T, D)).astype(np.float32),
+        dt=rng.normal(-2.0, 0.5, (T, H)).astype(np.float32),
+        a_log=rng.standard_normal((H, N) if per_state else (H,)).astype(np.float32),
+        B=(rng.standard_normal((T, G * N)) * 0.25).astype(np.float32),
+        C=(rng.standard_normal((T, G * N)) * 0.25).astype(np.float32),
+        D=rng.standard_normal(H).astype(np.float32),
+        z=rng.standard_normal((T, D)).astype(np.float32),
+    )
+
+
+def _t(dev, a, dtype=torch.float32):
+    return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(dtype).to(dev)
+
+
+def _cu(lengths):
+    return np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
+
+
+def _run(dev, orc, inp, cu, H, P, N, G, gate=True, init=None, dtype=torch.float32):
+    args = [_t(dev, inp[k], dtype) for k in ("x", "dt")]
+    y, fin = ops.selective_scan_fwd(
+        args[0], args[1], _t(dev, inp["a_log"]), _t(dev, inp["B"], dtype), _t(dev, inp["C"], dtype),
+        _t(dev, inp["D"]), _t(dev, inp["z"], dtype) if gate else None, _t(dev, cu), H, P, N, G,
+        initial_state=_t(dev, init))
+    return y.float().cpu().numpy(), fin.cpu().numpy()
+
+
+@pytest.mark.parametrize("H,P,N,G,per_state,lengths", [
+    (768, 1, 16, 1, True, [512]),                 # BASELINE config 2 shape
+    (128, 1, 16, 1, True, [5, 64, 1, 33, 100]),   # ragged, lengths not multiples of 4
+    (2, 64, 16, 1, False, [40, 7]),               # reference faithful: per-head A, P = 64
+    (64, 1, 8, 1, True, [17]),                    # N = 8
+    (4, 32, 16, 2, False, [9, 30]),               # G = 2, one group per workgroup
+    (6, 1, 5, 1, True, [11, 3]),                  # D = 6, N = 5 -> generic kernel
+    (6, 2, 4, 3, False, [8, 2, 5]),               # 4 channels per group -> generic kernel
+])
+def test_scan_matches_oracle(dev, orc, H, P, N, G, per_state, lengths):
+    rng = np.random.default_rng(H * 31 + N)
+    cu = _cu(lengths)
+    inp = _inputs(rng, int(cu[-1]), H, P, N, G, per_state)
+    y, fin = _run(dev, orc, inp, cu, H, P, N, G)
+    wy, wfin = orc.selective_scan(inp["x"], inp["dt"], inp["a_log"], inp["B"], inp["C"], inp["D"],
+                                  inp["z"], cu, H, P, N, G)
+    np.testing.assert_allclose(y, wy, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(fin, wfin, rtol=RTOL, atol=ATOL)
+
+
+def test_scan_initial_state_and_no_gate(dev, orc):
+    rng = np.random.default_rng(4)
+    H, P, N, G = 128, 1, 16, 1
+    cu = _cu([20, 45, 3])
+    inp = _inputs(rng, int(cu[-1]), H, P, N, G)
+    init = rng.normal(0, 0.1, (3, H * P, N)).astype(np.float32)
+    y, fin = _run(dev, orc, inp, cu, H, P, N, G, gate=False, init=init)
+    wy, wfin = orc.selective_scan(inp["x"], inp["dt"], inp["a_log"], inp["B"], inp["C"], inp["D"],
+                                  None, cu, H, P, N, G, initial_state=init, gate_silu=False)
+    np.testing.assert_allclose(y, wy, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(fin, wfin, rtol=RTOL, atol=ATOL)
+
+
+def test_scan_ragged_equals_per_sequence(dev, orc):
+    """A packed batch gives each sequence exactly what it gets alone (no leakage)."""
+    rng = np.random.default_rng(8)
+    H, P, N, G = 64, 1, 16, 1
+    lengths = [13, 1, 70]
+    cu = _cu(lengths)
+    inp = _inputs(rng, int(cu[-1]), H, P, N, G)
+    y, fin = _run(dev, orc, inp, cu, H, P, N, G)
+    for s, (a, b) in enumerate(zip(cu[:-1], cu[1:])):
+        part = {k: (v[a:b] if v.ndim == 2 and v.shape[0] == cu[-1] else v) for k, v in inp.items()}
+        ys, fs = _run(dev, orc, part, _cu([b - a]), H, P, N, G)
+        np.testing.assert_array_equal(ys, y[a:b])
+        np.testing.assert_array_equal(fs[0], fin[s])
+
+
+def test_scan_bf16_io(dev, orc):
+    rng = np.random.default_rng(12)
+    H, P, N, G = 256, 1, 16, 1
+    cu = _cu([100, 37, 256])
+    inp = _inputs(rng, int(cu[-1]), H, P, N, G)
+    rb = {k: (torch.from_numpy(v).to(torch.bfloat16).float().numpy() if k in
+              ("x", "dt", "B", "C", "z") else v) for k, v in inp.items()}
+    y, fin = _run(dev, orc, inp, cu, H, P, N, G, dtype=torch.bfloat16)
+    wy, wfin = orc.selective_scan(rb["x"], rb["dt"], rb["a_log"], rb["B"], rb["C"], rb["D"],
+                                  rb["z"], cu, H, P, N, G)
+    scale = np.abs(wy).max()
+    np.testing.assert_allclose(y, wy, rtol=2e-2, atol=2e-2 * scale / 64)
+    np.testing.assert_allclose(fin, wfin, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("H,P,N,G,per_state", [(256, 1, 16, 1, True), (4, 64, 16, 1, False),
+                                               (8, 3, 5, 2, True)])
+def test_step_matches_oracle_and_prefill(dev, orc, H, P, N, G, per_state):
+    rng = np.random.default_rng(21 + N)
+    R = 33
+    inp = _inputs(rng, R, H, P, N, G, per_state)
+    st0 = rng.normal(0, 0.1, (R, H * P, N)).astype(np.float32)
+    state = _t(dev, st0)
+    y = ops.selective_scan_step(_t(dev, inp["x"]), _t(dev, inp["dt"]), _t(dev, inp["a_log"]),
+                                _t(dev, inp["B"]), _t(dev, inp["C"]), _t(dev, inp["D"]),
+                                _t(dev, inp["z"]), state, H, P, N, G)
+    wy, wst = orc.scan_step(inp["x"], inp["dt"], inp["a_log"], inp["B"], inp["C"], inp["D"],
+                            inp["z"], st0, H, P, N, G)
+    np.testing.assert_allclose(y.cpu().numpy(), wy, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(state.cpu().numpy(), wst, rtol=RTOL, atol=ATOL)
+    # step == one-token prefill from the same state (src/mamba2.cpp:2814-2818 relies on it)
+    yp, fp = _run(dev, orc, inp, _cu([1] * R), H, P, N, G, init=st0)
+    np.testing.assert_allclose(y.cpu().numpy(), yp, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(state.cpu().numpy(), fp, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_conv1d_matches_oracle(dev, orc, dtype):
+    rng = np.random.default_rng(2)
+    C, W = 96, 4
+    cu = _cu([1, 2, 3, 10, 40])
+    T = int(cu[-1])
+    wide = rng.standard_normal((T, 2 * C)).astype(np.float32)  # x is the first half of each row
+    w = rng.standard_normal((C, W)).astype(np.float32) * 0.5
+    b = rng.standard_normal(C).astype(np.float32)
+    wt = _t(dev, wide, dtype)
+    out = ops.conv1d_causal(wt[:, :C], _t(dev, w), _t(dev, cu), _t(dev, b), silu=True,
+                            out_dtype=torch.float32)
+    x = wt[:, :C].float().cpu().numpy()
+    want = orc.conv1d_causal(np.ascontiguousarray(x), w, cu, bias=b, silu_act=True)
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=RTOL, atol=ATOL)
