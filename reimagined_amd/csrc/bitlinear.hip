@@ -50,7 +50,9 @@ __global__ __launch_bounds__(64) void rms_inv_kernel(const void* __restrict__ x,
     }
     if (row < M) {
         const float mean = __fdiv_rn(sum, static_cast<float>(K > 1 ? K : 1));
-        inv[row] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+        // sqrtf is IEEE-rounded under -fhip-fp32-correctly-rounded-divide-sqrt;
+        // __fsqrt_rn is not (it maps to the native approximation)
+        inv[row] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
     }
 }
 

@@ -60,8 +60,9 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
     const void* __restrict__ x, int64_t x_stride, const void* __restrict__ dt,
     const float* __restrict__ a_log, int a_per_state, const void* __restrict__ Bm,
     const void* __restrict__ Cm, const float* __restrict__ Dskip, const void* __restrict__ z,
-    int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int H, int P, int N, int G,
-    const float* __restrict__ init_state, float* __restrict__ final_state, void* __restrict__ y) {
+    int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int total_tokens, int H, int P,
+    int N, int G, const float* __restrict__ init_state, float* __restrict__ final_state,
+    void* __restrict__ y) {
     constexpr int NPAD = 4 * SPL;
     __shared__ float s_delta[kScanTC][kScanCh];
     __shared__ float s_dx[kScanTC][kScanCh];
@@ -76,8 +77,9 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
     const int GN = G * N;
     const int c0 = blockIdx.x * kScanCh;
     const int seq = blockIdx.y;
-    const int t0 = cu_seqlens[seq];
-    const int t1 = cu_seqlens[seq + 1];
+    // a malformed cu_seqlens can only shorten a sequence, never address past T
+    const int t0 = min(max(cu_seqlens[seq], 0), total_tokens);
+    const int t1 = min(max(cu_seqlens[seq + 1], t0), total_tokens);
     const int cl = tid >> 2;          // channel within the block
     const int q = tid & 3;            // state quad
     const int c = c0 + cl;
@@ -187,9 +189,9 @@ __global__ __launch_bounds__(64) void scan_fwd_generic_kernel(
     const void* __restrict__ x, int64_t x_stride, const void* __restrict__ dt,
     const float* __restrict__ a_log, int a_per_state, const void* __restrict__ Bm,
     const void* __restrict__ Cm, const float* __restrict__ Dskip, const void* __restrict__ z,
-    int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int num_seqs, int H, int P, int N,
-    int G, const float* __restrict__ init_state, float* __restrict__ final_state,
-    void* __restrict__ y) {
+    int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int num_seqs, int total_tokens,
+    int H, int P, int N, int G, const float* __restrict__ init_state,
+    float* __restrict__ final_state, void* __restrict__ y) {
     const int D = H * P;
     const int GN = G * N;
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -200,7 +202,9 @@ __global__ __launch_bounds__(64) void scan_fwd_generic_kernel(
     const int grp = (h * G) / H;
     float st[64];
     for (int n = 0; n < N; ++n) st[n] = init_state ? init_state[((int64_t)seq * D + c) * N + n] : 0.0f;
-    for (int t = cu_seqlens[seq]; t < cu_seqlens[seq + 1]; ++t) {
+    const int t0 = min(max(cu_seqlens[seq], 0), total_tokens);
+    const int t1 = min(max(cu_seqlens[seq + 1], t0), total_tokens);
+    for (int t = t0; t < t1; ++t) {
         const float xv = load_act<ADT>(x, (int64_t)t * x_stride + c);
         const float dl = softplus_ref(load_act<ADT>(dt, (int64_t)t * H + h));
         float out = Dskip[h] * xv;
@@ -302,7 +306,7 @@ __global__ __launch_bounds__(256) void conv1d_kernel(const void* __restrict__ in
         const int mid = (lo + hi) >> 1;
         if (cu_seqlens[mid] <= t) lo = mid; else hi = mid;
     }
-    const int ts = cu_seqlens[lo];
+    const int ts = min(max(cu_seqlens[lo], 0), t);  // never reads before token 0
     float acc = 0.0f;
     for (int j = 0; j < W; ++j) {
         const int src = t - (W - 1) + j;
@@ -342,8 +346,8 @@ extern "C" int nsosx_selective_scan_fwd(const void* x, int64_t x_stride, const v
         const int spl = N <= 4 ? 1 : N <= 8 ? 2 : N <= 16 ? 4 : N <= 32 ? 8 : 16;
 #define NSOSX_SCAN(ADT, SPL, GATE)                                                              \
     hipLaunchKernelGGL((scan_fwd_kernel<ADT, SPL, GATE>), grid, block, 0, st, x, x_stride, dt,   \
-                       A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens, H, P, N, G,        \
-                       initial_state, final_state, y);
+                       A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens, total_tokens, H,   \
+                       P, N, G, initial_state, final_state, y);
 #define NSOSX_SCAN_G(ADT, SPL) \
     if (z) { NSOSX_SCAN(ADT, SPL, true) } else { NSOSX_SCAN(ADT, SPL, false) }
 #define NSOSX_SCAN_S(ADT)                          \
@@ -364,11 +368,11 @@ extern "C" int nsosx_selective_scan_fwd(const void* x, int64_t x_stride, const v
         if (act_dtype == NSOSX_F32)
             hipLaunchKernelGGL(scan_fwd_generic_kernel<NSOSX_F32>, grid, block, 0, st, x, x_stride,
                                dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens, num_seqs,
-                               H, P, N, G, initial_state, final_state, y);
+                               total_tokens, H, P, N, G, initial_state, final_state, y);
         else
             hipLaunchKernelGGL(scan_fwd_generic_kernel<NSOSX_BF16>, grid, block, 0, st, x,
                                x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens,
-                               num_seqs, H, P, N, G, initial_state, final_state, y);
+                               num_seqs, total_tokens, H, P, N, G, initial_state, final_state, y);
     }
     return check_launch("selective_scan_fwd");
 }

@@ -33,12 +33,18 @@ def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
-def _dev(t: torch.Tensor, name: str) -> torch.Tensor:
+def _dev(t: torch.Tensor, name: str, dtype=None) -> torch.Tensor:
     if not t.is_cuda:
         raise ValueError(f"{name} must be a device tensor")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
     return t
+
+
+def _opt(t, name: str, dtype=torch.float32):
+    return None if t is None else _dev(t, name, dtype)
 
 
 # ---- weights -------------------------------------------------------------------
@@ -96,8 +102,13 @@ def ternary_gemm(q: torch.Tensor, act_scale: torch.Tensor, packed: torch.Tensor,
 
     Returns y [M, N] (or (y, acc int32 [M, N]) with want_acc).
     """
-    for t, nm in ((q, "q"), (act_scale, "act_scale"), (packed, "packed")):
-        _dev(t, nm)
+    _dev(q, "q", torch.int8)
+    _dev(act_scale, "act_scale", torch.float32)
+    _dev(packed, "packed")
+    if packed.dtype not in (torch.int32, torch.uint32):
+        raise ValueError("packed must hold 32-bit words")
+    _opt(magnitude, "magnitude")
+    _opt(bias, "bias")
     m, k = q.shape
     y = torch.empty((m, n_out), dtype=out_dtype, device=q.device) if want_y else None
     acc = torch.empty((m, n_out), dtype=torch.int32, device=q.device) if want_acc else None
@@ -186,6 +197,9 @@ def conv1d_causal(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tenso
     """
     if x.stride(1) != 1:
         raise ValueError("conv1d_causal: x must have unit stride in the channel dim")
+    _dev(weight, "weight", torch.float32)
+    _dev(cu_seqlens, "cu_seqlens", torch.int32)
+    _opt(bias, "bias")
     t, c = x.shape
     out_dtype = out_dtype or x.dtype
     out = torch.empty((t, c), dtype=out_dtype, device=x.device)
@@ -202,6 +216,14 @@ def selective_scan_fwd(x, dt, a_log, B, C, D, z, cu_seqlens, H, P, N, G, initial
     s = cu_seqlens.numel() - 1
     if x.stride(1) != 1 or (z is not None and z.stride(1) != 1):
         raise ValueError("selective_scan_fwd: x and z need unit stride in the channel dim")
+    for name, v in (("dt", dt), ("B", B), ("C", C)):
+        _dev(v, name, x.dtype)
+    if z is not None and z.dtype != x.dtype:
+        raise ValueError("selective_scan_fwd: z must have x's dtype")
+    _dev(a_log, "a_log", torch.float32)
+    _dev(D, "D", torch.float32)
+    _dev(cu_seqlens, "cu_seqlens", torch.int32)
+    _opt(initial_state, "initial_state")
     a_per_state = int(a_log.numel() == H * N and N > 1)
     y = torch.empty((t, H * P), dtype=x.dtype, device=x.device)
     fin = torch.empty((s, H * P, N), dtype=torch.float32, device=x.device) if want_final else None
@@ -214,6 +236,11 @@ def selective_scan_fwd(x, dt, a_log, B, C, D, z, cu_seqlens, H, P, N, G, initial
 def selective_scan_step(x, dt, a_log, B, C, D, z, state, H, P, N, G):
     """Decode step in place on `state` [R, H*P, N] (src/mamba2.cpp:4038-4125) -> y [R, H*P]."""
     r = x.shape[0]
+    for name, v in (("x", x), ("dt", dt), ("B", B), ("C", C)):
+        _dev(v, name, x.dtype)
+    _dev(a_log, "a_log", torch.float32)
+    _dev(D, "D", torch.float32)
+    _dev(state, "state", torch.float32)
     a_per_state = int(a_log.numel() == H * N and N > 1)
     y = torch.empty_like(x)
     call("nsosx_selective_scan_step", _p(x), _p(dt), _p(a_log), a_per_state, _p(B), _p(C), _p(D),
@@ -225,7 +252,7 @@ def selective_scan_step(x, dt, a_log, B, C, D, z, state, H, P, N, G):
 
 def moe_route(logits: torch.Tensor, k: int = 2) -> dict:
     """MoERouter::forward from logits + forward_moe's ordered dispatch, on the device."""
-    _dev(logits, "logits")
+    _dev(logits, "logits", torch.float32)
     rows, e = logits.shape
     dev = logits.device
     out = {
@@ -248,6 +275,11 @@ def grouped_ternary_gemm(views: LinearViewArray, offsets, perm, q, act_scale, n_
                          max_rows_per_expert: int, squared_relu: bool = False,
                          gather: bool = True, out_dtype=torch.float32) -> torch.Tensor:
     """Per-expert ternary GEMMs over slot segments -> y [slots, n_out] in slot order."""
+    _dev(offsets, "offsets", torch.int32)
+    if gather:
+        _dev(perm, "perm", torch.int32)
+    _dev(q, "q", torch.int8)
+    _dev(act_scale, "act_scale", torch.float32)
     slots = int(perm.numel()) if gather else q.shape[0]
     k = q.shape[1]
     y = torch.empty((slots, n_out), dtype=out_dtype, device=q.device)
@@ -258,6 +290,9 @@ def grouped_ternary_gemm(views: LinearViewArray, offsets, perm, q, act_scale, n_
 
 
 def moe_combine(expert_out, slot_of, selected, weights, out_dtype=torch.float32) -> torch.Tensor:
+    _dev(slot_of, "slot_of", torch.int32)
+    _dev(selected, "selected", torch.int32)
+    _dev(weights, "weights", torch.float32)
     rows, e = weights.shape
     k = selected.shape[1]
     dim = expert_out.shape[1]

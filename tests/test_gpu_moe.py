@@ -86,5 +86,8 @@ def test_moe_ffn_matches_oracle(dev, orc, hidden_dtype):
     np.testing.assert_array_equal(out["o"].cpu().numpy(), o_want)
     want = orc.moe_combine(o_want, perm, offsets, out["weights"].cpu().numpy())
     np.testing.assert_array_equal(out["out"].cpu().numpy(), want)
+    # against the oracle's own routing weights: fp32 tolerance scaled to the output
+    # (two products summed can cancel, so a per-element relative bound is not meaningful)
     want_w = orc.moe_combine(o_want, perm, offsets, w)
-    np.testing.assert_allclose(out["out"].cpu().numpy(), want_w, rtol=1e-5, atol=1e-6)
+    got = out["out"].cpu().numpy()
+    np.testing.assert_allclose(got, want_w, rtol=1e-4, atol=1e-5 * np.abs(want_w).max())

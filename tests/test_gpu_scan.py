@@ -29,7 +29,13 @@ def _inputs(rng, T, H, P, N, G, per_state=True):
 
 
 def _t(dev, a, dtype=torch.float32):
-    return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(dtype).to(dev)
+    """Device copy; floating arrays are cast to `dtype`, integer arrays keep their type."""
+    if a is None:
+        return None
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if t.is_floating_point():
+        t = t.to(dtype)
+    return t.to(dev)
 
 
 def _cu(lengths):
@@ -38,9 +44,11 @@ def _cu(lengths):
 
 def _run(dev, orc, inp, cu, H, P, N, G, gate=True, init=None, dtype=torch.float32):
     args = [_t(dev, inp[k], dtype) for k in ("x", "dt")]
+    cu_t = _t(dev, cu)
+    assert cu_t.dtype == torch.int32
     y, fin = ops.selective_scan_fwd(
         args[0], args[1], _t(dev, inp["a_log"]), _t(dev, inp["B"], dtype), _t(dev, inp["C"], dtype),
-        _t(dev, inp["D"]), _t(dev, inp["z"], dtype) if gate else None, _t(dev, cu), H, P, N, G,
+        _t(dev, inp["D"]), _t(dev, inp["z"], dtype) if gate else None, cu_t, H, P, N, G,
         initial_state=_t(dev, init))
     return y.float().cpu().numpy(), fin.cpu().numpy()
 
@@ -144,3 +152,12 @@ def test_conv1d_matches_oracle(dev, orc, dtype):
     x = wt[:, :C].float().cpu().numpy()
     want = orc.conv1d_causal(np.ascontiguousarray(x), w, cu, bias=b, silu_act=True)
     np.testing.assert_allclose(out.cpu().numpy(), want, rtol=RTOL, atol=ATOL)
+
+
+def test_scan_rejects_float_cu_seqlens(dev):
+    x = torch.zeros((4, 64), device=dev)
+    with pytest.raises(ValueError):
+        ops.selective_scan_fwd(x, torch.zeros((4, 64), device=dev), torch.zeros((64, 16), device=dev),
+                               torch.zeros((4, 16), device=dev), torch.zeros((4, 16), device=dev),
+                               torch.zeros(64, device=dev), None,
+                               torch.tensor([0.0, 4.0], device=dev), 64, 1, 16, 1)
