@@ -110,7 +110,8 @@ def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=3
         "scan": ("hbm", T * d_inner * 2 * 4 + T * d_state * 2 * 2 + num_seqs * d_inner * d_state * 4
                  + d_inner * d_state * 4 + d_inner * 4),
         # bf16 x in (strided) + bf16 out per (token, channel)
-        "conv": ("hbm", T * d_inner * 2 * 2),
+        "conv_scan": ("hbm", T * d_inner * 2 * 4 + T * d_state * 2 * 2 + num_seqs * d_inner * d_state * 4
+                      + d_inner * d_state * 4 + d_inner * 4 * 6),
         "in_proj_quant": ("hbm", T * d_model * (2 + 2 + 1) + T * 8),
         "out_proj_quant": ("hbm", T * d_inner * (2 + 2 + 1) + T * 8),
     }
@@ -277,10 +278,10 @@ def main():
         _log(f"decode gemv {extra['decode_gemv_c3_m1']}")
         extra["decode_step_c5"] = bench_decode_step(torch, dev)
         _log(f"decode step {extra['decode_step_c5']}")
-        sc = stages.get("scan")
+        sc = stages.get("conv_scan")
         if sc:
-            _, work = layer_roofline(T, {"scan": sc})
-            gbs = work["scan"][1] / (sc / 1e3) / 1e9
+            _, work = layer_roofline(T, {"conv_scan": sc})
+            gbs = work["conv_scan"][1] / (sc / 1e3) / 1e9
             extra["scan_c4"] = {"ms": round(sc, 4), "gbs": round(gbs, 1),
                                 "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
     cpu = None if args.no_cpu else cpu_baseline(params, inp)

@@ -130,10 +130,9 @@ typedef struct nsosx_linear_view {
 /* Grouped decode GEMV: `groups` independent ternary GEMVs in one launch, the
  * role of launch_grouped_decode_projections (include/cuda/kernels.cuh:27-29).
  * Group g multiplies q + g*q_stride (int8 [M, inputs]) with views[g] and
- * writes y + g*y_stride elements ([M, outputs], y_dtype).  All views share
- * `inputs`; M <= 8.  views: host array, copied into the launch arguments
- * through `views_dev` (device array of `groups` descriptors the caller
- * uploaded with nsosx_upload_views or its own copy). */
+ * writes y + g*y_stride elements ([M, outputs], y_dtype); act_scale + g *
+ * scale_stride holds the group's M scales.  M <= 8.  views_dev: device array
+ * of `groups` descriptors (the caller uploads it once and reuses it). */
 int nsosx_grouped_gemv(const nsosx_linear_view* views_dev, int groups, const int8_t* q,
                        int64_t q_stride, const float* act_scale, int64_t scale_stride, int M,
                        void* y, int64_t y_stride, int y_dtype, void* stream);
@@ -174,6 +173,20 @@ int nsosx_selective_scan_fwd(const void* x, int64_t x_stride, const void* dt, co
                              int act_dtype, const float* initial_state, float* final_state,
                              void* y, void* stream);
 
+/* The scan with the depthwise causal convolution + bias + SiLU of the
+ * Mamba block fused into its input staging (src/mamba2.cpp:1056-1076,
+ * 2437-2446 feeding 2602-2675): x_raw is the convolution's input (row stride
+ * x_stride), conv_w f32 [H*P, conv_width] (conv_width <= 8), conv_b f32
+ * [H*P] or NULL; the convolution restarts at every sequence start.  The D
+ * skip uses the convolved x.  Other arguments as nsosx_selective_scan_fwd;
+ * channels per group must be a multiple of 64. */
+int nsosx_conv_scan_fwd(const void* x_raw, int64_t x_stride, const float* conv_w,
+                        const float* conv_b, int conv_width, const void* dt, const float* A_log,
+                        int a_per_state, const void* B, const void* C, const float* D,
+                        const void* z, int64_t z_stride, const int32_t* cu_seqlens, int num_seqs,
+                        int total_tokens, int H, int P, int N, int G, int act_dtype,
+                        const float* initial_state, float* final_state, void* y, void* stream);
+
 /* Decode step over `rows` independent sequences, one token each, state
  * updated in place (src/mamba2.cpp:4038-4125; GPU twin
  * launch_mamba2_faithful_step, src/cuda/mamba_kernels.cu:3332-3419).
@@ -195,8 +208,8 @@ int nsosx_selective_scan_step(const void* x, const void* dt, const float* A_log,
  *   logits f32 [rows, E]; weights f32 [rows, E] (masked, renormalised);
  *   selected int32 [rows, k] (rank order); counts int32 [E];
  *   offsets int32 [E+1] (exclusive scan); perm int32 [rows*k] (slot -> row);
- *   slot_of int32 [rows, k]: slot of the row's r-th selected expert, ordered
- *   by ascending expert id (the combine order).
+ *   slot_of int32 [rows, k]: slot_of[r, i] is the slot of selected[r, i]
+ *   (rank order), so perm[slot_of[r, i]] == r.
  *   workspace: int32, nsosx_moe_route_workspace(rows, E) elements.
  * E <= 64, k <= E. */
 int64_t nsosx_moe_route_workspace(int rows, int experts);

@@ -35,6 +35,8 @@ SIGNATURES = {
                                  _vp]),
     "nsosx_selective_scan_fwd": (_i, [_vp, _i64, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i64, _vp,
                                       _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp]),
+    "nsosx_conv_scan_fwd": (_i, [_vp, _i64, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i64,
+                                 _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "nsosx_selective_scan_step": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                                        _i, _i, _vp, _vp, _vp]),
     "nsosx_moe_route_workspace": (_i64, [_i, _i]),

@@ -17,43 +17,59 @@ namespace nsosx {
 // RMS_PERI: inv[r] = 1 / sqrt(sum_sq / K + eps) with the float sum taken in
 // index order (rounded square, then add) as the reference's sequential loop
 // does; a remainder of K % 4 elements is accumulated with fma, which is how
-// that loop is compiled.  Lane r of a wave owns row r of a 64-row block; the
-// block is staged through LDS 64 columns at a time so the global loads stay
-// coalesced while each lane walks its own row in order.
+// that loop is compiled.  The sum is a chain of K dependent adds, so the
+// parallelism is across rows: lane = row, each lane streaming its own row
+// with 16-byte loads (eight bf16 or four f32 values per load, four loads in
+// flight).
 // ===========================================================================
 template <int DT>
+__device__ __forceinline__ void load16_f32(const char* p, float v[DT == NSOSX_F32 ? 4 : 8]) {
+    const uint4 a = *reinterpret_cast<const uint4*>(p);
+    if constexpr (DT == NSOSX_F32) {
+        v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+        v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+    } else {
+        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[2 * i] = __uint_as_float(w[i] << 16);
+            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+}
+
+template <int DT, bool VEC>
 __global__ __launch_bounds__(64) void rms_inv_kernel(const void* __restrict__ x, int M, int K,
                                                      float eps, float* __restrict__ inv) {
-    __shared__ float tile[64][65];
-    const int lane = threadIdx.x;
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * 64;
-    const int row = static_cast<int>(row0) + lane;
+    const int row = blockIdx.x * 64 + threadIdx.x;
+    if (row >= M) return;
+    constexpr int ES = DT == NSOSX_F32 ? 4 : 2;
+    constexpr int PER = 16 / ES;  // elements per 16-byte load
+    const char* base = static_cast<const char*>(x) + (int64_t)row * K * ES;
     const int body = K & ~3;
     float sum = 0.0f;
-    for (int k0 = 0; k0 < K; k0 += 64) {
-        const int kc = min(64, K - k0);
-        for (int r = 0; r < 64; ++r) {
-            float v = 0.0f;
-            if (row0 + r < M && lane < kc) v = load_act<DT>(x, (row0 + r) * K + k0 + lane);
-            tile[r][lane] = v;
+    int k = 0;
+    if (VEC) {
+        constexpr int U = 4;  // loads in flight
+        for (; k + U * PER <= body; k += U * PER) {
+            float v[U][PER];
+#pragma unroll
+            for (int u = 0; u < U; ++u) load16_f32<DT>(base + (int64_t)(k + u * PER) * ES, v[u]);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int j = 0; j < PER; ++j) sum = __fadd_rn(sum, __fmul_rn(v[u][j], v[u][j]));
         }
-        __syncthreads();
-        for (int j = 0; j < kc; ++j) {
-            const float v = tile[lane][j];
-            if (k0 + j < body) {
-                sum = __fadd_rn(sum, __fmul_rn(v, v));
-            } else {
-                sum = __fmaf_rn(v, v, sum);
-            }
-        }
-        __syncthreads();
     }
-    if (row < M) {
-        const float mean = __fdiv_rn(sum, static_cast<float>(K > 1 ? K : 1));
-        // sqrtf is IEEE-rounded under -fhip-fp32-correctly-rounded-divide-sqrt;
-        // __fsqrt_rn is not (it maps to the native approximation)
-        inv[row] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
+    for (; k < K; ++k) {
+        const float v = load_act<DT>(x, (int64_t)row * K + k);
+        if (k < body) sum = __fadd_rn(sum, __fmul_rn(v, v));
+        else sum = __fmaf_rn(v, v, sum);
     }
+    const float mean = __fdiv_rn(sum, static_cast<float>(K > 1 ? K : 1));
+    // sqrtf is IEEE-rounded under -fhip-fp32-correctly-rounded-divide-sqrt;
+    // __fsqrt_rn is not (it maps to the native approximation)
+    inv[row] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
 }
 
 // ===========================================================================
@@ -178,11 +194,16 @@ template <int DT>
 static int launch_quantize(const void* x, int M, int K, int bits, int rms_input, int8_t* q,
                            float* act_scale, float* rms_ws, hipStream_t st) {
     const float qm = q_max_for_bits(bits);
-    if (rms_input) {
-        hipLaunchKernelGGL(rms_inv_kernel<DT>, dim3((M + 63) / 64), dim3(64), 0, st, x, M, K,
-                           1e-6f, rms_ws);
-    }
     const int elem = DT == NSOSX_F32 ? 4 : 2;
+    if (rms_input) {
+        const bool rvec = ((int64_t)K * elem) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+        if (rvec)
+            hipLaunchKernelGGL((rms_inv_kernel<DT, true>), dim3((M + 63) / 64), dim3(64), 0, st, x,
+                               M, K, 1e-6f, rms_ws);
+        else
+            hipLaunchKernelGGL((rms_inv_kernel<DT, false>), dim3((M + 63) / 64), dim3(64), 0, st,
+                               x, M, K, 1e-6f, rms_ws);
+    }
     const bool vec = (K % 8 == 0) && K <= 4096 && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                      (reinterpret_cast<uintptr_t>(q) % 8 == 0) && ((int64_t)K * elem) % 16 == 0;
     const dim3 grid((M + 3) / 4), block(256);

@@ -40,52 +40,112 @@ __device__ __forceinline__ float dpp_xor2(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
 }
 
+// Native-instruction forms of softplus and SiLU for the per-(token, channel)
+// terms (v_exp_f32 / v_log_f32 / v_rcp_f32, each about 1 ulp): log1p(e) is
+// taken as log(u) * e / (u - 1) with u = 1 + e, which cancels the rounding of
+// u (Kahan), so the relative error stays at a few ulp for all dt_raw.
+__device__ __forceinline__ float exp_native(float v) {
+    return __builtin_amdgcn_exp2f(v * 1.4426950408889634f);
+}
+
+__device__ __forceinline__ float softplus_fast(float v) {
+    if (v > 20.0f) return v;
+    if (v < -20.0f) return expf(v);
+    const float e = exp_native(v);
+    const float u = 1.0f + e;
+    if (u == 1.0f) return e;
+    return __builtin_amdgcn_logf(u) * 0.6931471805599453f * (e * __builtin_amdgcn_rcpf(u - 1.0f));
+}
+
+__device__ __forceinline__ float silu_fast(float v) {
+    return v * __builtin_amdgcn_rcpf(1.0f + exp_native(-v));
+}
+
 // ===========================================================================
 // Prefill scan.  A workgroup owns 64 channels of one sequence and walks its
 // tokens in order; lane l of the workgroup is channel c0 + l/4 and state
-// quad q = l%4, holding states n = q*SPL .. q*SPL+SPL-1 in registers.  Token
-// chunks of TC rows are staged in LDS with the per-(token, channel) terms
-// already formed (delta = softplus(dt), delta*x, x, silu(z)) and B/C of the
-// chunk.  After every 4 tokens the four lanes of a channel exchange partial
-// readouts with two DPP steps (a 4x4 transpose-reduce), so each lane
-// finishes one token's sum; y goes back through LDS for coalesced stores.
+// quad q = l%4, holding states n = q*SPL .. q*SPL+SPL-1 in registers.
+// Token chunks of TC rows are staged in LDS with the per-(token, channel)
+// terms already formed: delta = softplus(dt) and delta*x interleaved (one
+// 8-byte read per token), x itself, and B/C of the chunk.  With CONV the
+// staged x is the depthwise causal convolution + bias + SiLU of the raw
+// input, restarted at the sequence start (each staging thread slides a
+// W-tap window down 8 rows of one channel).  After every 4 tokens the four
+// lanes of a channel exchange partial readouts with two DPP steps (a 4x4
+// transpose-reduce), so each lane finishes one token's sum; the D skip and
+// the SiLU(z) gate are applied in the coalesced store pass.
 // Requires channels-per-group (H*P/G) to be a multiple of 64 so a workgroup
 // sees one B/C group.
 // ===========================================================================
 constexpr int kScanTC = 32;       // tokens per LDS chunk
 constexpr int kScanCh = 64;       // channels per workgroup
+constexpr int kMaxConvW = 8;
+constexpr int kOrderMax = 1024;   // sequences ordered longest-first up to this count
 
-template <int ADT, int SPL, bool GATE>
+// Workgroup y-index -> sequence, longest sequence first (ties by index), so
+// the longest recurrences start first and short ones fill in behind them.
+__device__ __forceinline__ int scan_pick_sequence(const int32_t* cu, int num_seqs, int T,
+                                                  int32_t* s_order) {
+    if (num_seqs > kOrderMax) return blockIdx.y;
+    for (int i = threadIdx.x; i < num_seqs; i += blockDim.x) {
+        const int a = min(max(cu[i], 0), T);
+        const int li = min(max(cu[i + 1], a), T) - a;
+        int rank = 0;
+        for (int k = 0; k < num_seqs; ++k) {
+            const int b = min(max(cu[k], 0), T);
+            const int lk = min(max(cu[k + 1], b), T) - b;
+            rank += (lk > li) || (lk == li && k < i);
+        }
+        s_order[rank] = i;
+    }
+    __syncthreads();
+    return s_order[blockIdx.y];
+}
+
+template <int ADT, int SPL, bool GATE, bool CONV>
 __global__ __launch_bounds__(256) void scan_fwd_kernel(
     const void* __restrict__ x, int64_t x_stride, const void* __restrict__ dt,
     const float* __restrict__ a_log, int a_per_state, const void* __restrict__ Bm,
     const void* __restrict__ Cm, const float* __restrict__ Dskip, const void* __restrict__ z,
-    int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int total_tokens, int H, int P,
-    int N, int G, const float* __restrict__ init_state, float* __restrict__ final_state,
+    int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int num_seqs, int total_tokens,
+    int H, int P, int N, int G, const float* __restrict__ conv_w, const float* __restrict__ conv_b,
+    int W, const float* __restrict__ init_state, float* __restrict__ final_state,
     void* __restrict__ y) {
     constexpr int NPAD = 4 * SPL;
-    __shared__ float s_delta[kScanTC][kScanCh];
-    __shared__ float s_dx[kScanTC][kScanCh];
+    constexpr int NRAW = CONV ? 8 + kMaxConvW - 1 : 8;
+    constexpr int BCPT = (kScanTC * NPAD + 255) / 256;  // B/C elements per thread per chunk
+    __shared__ float2 s_dd[kScanTC][kScanCh];
     __shared__ float s_x[kScanTC][kScanCh];
-    __shared__ float s_gz[kScanTC][kScanCh];
-    __shared__ __align__(16) float s_B[kScanTC][NPAD];
-    __shared__ __align__(16) float s_C[kScanTC][NPAD];
+    __shared__ __align__(16) float s_bc[kScanTC][2 * NPAD];
     __shared__ float s_y[kScanTC][kScanCh + 1];
+    __shared__ int32_t s_order[kOrderMax];
 
     const int tid = threadIdx.x;
     const int D = H * P;
     const int GN = G * N;
     const int c0 = blockIdx.x * kScanCh;
-    const int seq = blockIdx.y;
+    const int seq = scan_pick_sequence(cu_seqlens, num_seqs, total_tokens, s_order);
     // a malformed cu_seqlens can only shorten a sequence, never address past T
     const int t0 = min(max(cu_seqlens[seq], 0), total_tokens);
     const int t1 = min(max(cu_seqlens[seq + 1], t0), total_tokens);
-    const int cl = tid >> 2;          // channel within the block
-    const int q = tid & 3;            // state quad
+    const int cl = tid >> 2;          // recurrence: channel within the block
+    const int q = tid & 3;            // recurrence: state quad
     const int c = c0 + cl;
     const int h = c / P;
     const int grp = (h * G) / H;
-    const float dsk = Dskip[h];
+    // staging / store role: channel sc, rows 8*rg .. 8*rg+7 of the chunk
+    const int sc = tid & 63;
+    const int rg = tid >> 6;
+    const int sch = c0 + sc;
+    const int sh = sch / P;
+    const float sdsk = Dskip[sh];
+
+    float cw[kMaxConvW], cb = 0.0f;
+    if (CONV) {
+#pragma unroll
+        for (int j = 0; j < kMaxConvW; ++j) cw[j] = j < W ? conv_w[(int64_t)sch * W + j] : 0.0f;
+        if (conv_b) cb = conv_b[sch];
+    }
 
     float a2[SPL], st[SPL];
 #pragma unroll
@@ -97,51 +157,92 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
         st[i] = (ok && init_state) ? init_state[((int64_t)seq * D + c) * N + n] : 0.0f;
     }
 
-    for (int tb = t0; tb < t1; tb += kScanTC) {
-        const int tc = min(kScanTC, t1 - tb);
-        // ---- stage the chunk -------------------------------------------------
-        for (int e = tid; e < kScanTC * kScanCh; e += 256) {
-            const int r = e / kScanCh, cc = e % kScanCh;
-            float dl = 0.0f, xv = 0.0f, gz = 1.0f;
-            if (r < tc) {
-                const int64_t t = tb + r;
-                const int ch = c0 + cc;
-                xv = load_act<ADT>(x, t * x_stride + ch);
-                dl = softplus_ref(load_act<ADT>(dt, t * H + ch / P));
-                if (GATE) gz = silu_ref(load_act<ADT>(z, t * z_stride + ch));
-            }
-            s_delta[r][cc] = dl;
-            s_dx[r][cc] = dl * xv;
-            s_x[r][cc] = xv;
-            s_gz[r][cc] = gz;
+    // next chunk's global inputs, loaded one chunk ahead of their use
+    float raw[NRAW], dtv[8], zv[8], bcv[2][BCPT];
+    auto prefetch = [&](int tb) {
+        const int tcn = min(kScanTC, t1 - tb);
+        const int rbase = 8 * rg;
+#pragma unroll
+        for (int j = 0; j < NRAW; ++j) {
+            const int tr = tb + rbase + j - (CONV ? W - 1 : 0);
+            const bool ok = (!CONV || j < 8 + W - 1) && tr >= t0 && tr < tb + tcn;
+            raw[j] = ok ? load_act<ADT>(x, (int64_t)tr * x_stride + sch) : 0.0f;
         }
-        for (int e = tid; e < kScanTC * NPAD; e += 256) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = rbase + i;
+            const int64_t t = tb + r;
+            dtv[i] = r < tcn ? load_act<ADT>(dt, t * H + sh) : 0.0f;
+            zv[i] = (GATE && r < tcn) ? load_act<ADT>(z, t * z_stride + sch) : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < BCPT; ++k) {
+            const int e = tid + 256 * k;
             const int r = e / NPAD, n = e % NPAD;
             float bv = 0.0f, cv = 0.0f;
-            if (r < tc && n < N) {
+            if (e < kScanTC * NPAD && r < tcn && n < N) {
                 const int64_t off = (int64_t)(tb + r) * GN + grp * N + n;
                 bv = load_act<ADT>(Bm, off);
                 cv = load_act<ADT>(Cm, off);
             }
-            s_B[r][n] = bv;
-            s_C[r][n] = cv;
+            bcv[0][k] = bv;
+            bcv[1][k] = cv;
+        }
+    };
+
+    if (t0 < t1) prefetch(t0);
+    for (int tb = t0; tb < t1; tb += kScanTC) {
+        const int tc = min(kScanTC, t1 - tb);
+        // ---- stage the chunk from the prefetched registers ---------------------
+        float zcur[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 8 * rg + i;
+            float xv;
+            if (CONV) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < kMaxConvW; ++j)
+                    if (j < W) acc = __fmaf_rn(cw[j], raw[i + j], acc);
+                xv = r < tc ? silu_fast(acc + cb) : 0.0f;
+            } else {
+                xv = raw[i];
+            }
+            const float dl = r < tc ? softplus_fast(dtv[i]) : 0.0f;
+            s_dd[r][sc] = make_float2(dl, dl * xv);
+            s_x[r][sc] = xv;
+            zcur[i] = zv[i];
+        }
+#pragma unroll
+        for (int k = 0; k < BCPT; ++k) {
+            const int e = tid + 256 * k;
+            if (e < kScanTC * NPAD) {
+                const int r = e / NPAD, n = e % NPAD;
+                s_bc[r][n] = bcv[0][k];
+                s_bc[r][NPAD + n] = bcv[1][k];
+            }
         }
         __syncthreads();
+        if (tb + kScanTC < t1) prefetch(tb + kScanTC);
         // ---- recurrence, four tokens per transpose-reduce ---------------------
         for (int r0 = 0; r0 < tc; r0 += 4) {
             float part[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int r = r0 + u;  // rows past tc hold delta = 0, B = C = 0: state unchanged
-                const float dl = s_delta[r][cl];
-                const float dx = s_dx[r][cl];
+                const float2 dd = s_dd[r][cl];
+                float bq[SPL], cq[SPL];
+#pragma unroll
+                for (int i = 0; i < SPL; ++i) {
+                    bq[i] = s_bc[r][q * SPL + i];
+                    cq[i] = s_bc[r][NPAD + q * SPL + i];
+                }
                 float p = 0.0f;
 #pragma unroll
                 for (int i = 0; i < SPL; ++i) {
-                    const int n = q * SPL + i;
-                    const float a = __builtin_amdgcn_exp2f(dl * a2[i]);
-                    st[i] = __fmaf_rn(a, st[i], dx * s_B[r][n]);
-                    p = __fmaf_rn(st[i], s_C[r][n], p);
+                    const float a = __builtin_amdgcn_exp2f(dd.x * a2[i]);
+                    st[i] = __fmaf_rn(a, st[i], dd.y * bq[i]);
+                    p = __fmaf_rn(st[i], cq[i], p);
                 }
                 part[u] = p;
             }
@@ -159,17 +260,19 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
             const float keep = hi1 ? m1 : m0;
             const float tot = keep + dpp_xor1(send);
             const int kq = (hi2 ? 2 : 0) + (hi1 ? 1 : 0);
-            const int r = r0 + kq;
-            if (r < tc) {
-                const float out = __fmaf_rn(dsk, s_x[r][cl], tot);
-                s_y[r][cl] = GATE ? out * s_gz[r][cl] : out;
-            }
+            s_y[r0 + kq][cl] = tot;
         }
         __syncthreads();
-        // ---- coalesced store of y ---------------------------------------------
-        for (int e = tid; e < tc * kScanCh; e += 256) {
-            const int r = e / kScanCh, cc = e % kScanCh;
-            store_act<ADT>(y, (int64_t)(tb + r) * D + c0 + cc, s_y[r][cc]);
+        // ---- D skip, gate, coalesced store of y ---------------------------------
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 8 * rg + i;
+            if (r < tc) {
+                const int64_t t = tb + r;
+                float out = __fmaf_rn(sdsk, s_x[r][sc], s_y[r][sc]);
+                if (GATE) out = out * silu_fast(zcur[i]);
+                store_act<ADT>(y, t * D + sch, out);
+            }
         }
         __syncthreads();
     }
@@ -322,13 +425,13 @@ __global__ __launch_bounds__(256) void conv1d_kernel(const void* __restrict__ in
 
 using namespace nsosx;
 
-extern "C" int nsosx_selective_scan_fwd(const void* x, int64_t x_stride, const void* dt,
-                                        const float* A_log, int a_per_state, const void* B,
-                                        const void* C, const float* D, const void* z,
-                                        int64_t z_stride, const int32_t* cu_seqlens, int num_seqs,
-                                        int total_tokens, int H, int P, int N, int G,
-                                        int act_dtype, const float* initial_state,
-                                        float* final_state, void* y, void* stream) {
+static int scan_fwd_launch(const void* x, int64_t x_stride, const void* dt, const float* A_log,
+                           int a_per_state, const void* B, const void* C, const float* D,
+                           const void* z, int64_t z_stride, const int32_t* cu_seqlens,
+                           int num_seqs, int total_tokens, int H, int P, int N, int G,
+                           int act_dtype, const float* conv_w, const float* conv_b, int conv_width,
+                           const float* initial_state, float* final_state, void* y,
+                           void* stream) {
     if (!x || !dt || !A_log || !B || !C || !D || !cu_seqlens || !y)
         return fail(NSOSX_ERR_INVALID, "selective_scan_fwd: null pointer");
     if (num_seqs <= 0 || num_seqs > 65535 || total_tokens < 0 || H <= 0 || P <= 0 || N <= 0 ||
@@ -338,18 +441,25 @@ extern "C" int nsosx_selective_scan_fwd(const void* x, int64_t x_stride, const v
     const int Dm = H * P;
     if (x_stride < Dm || (z && z_stride < Dm))
         return fail(NSOSX_ERR_INVALID, "selective_scan_fwd: row stride smaller than H*P");
-    hipStream_t st = static_cast<hipStream_t>(stream);
     const int per_group = Dm / G;
-    const bool fast = (per_group % kScanCh == 0) && N <= 64;
-    if (fast) {
+    const bool conv = conv_w != nullptr;
+    if (conv && (conv_width <= 0 || conv_width > kMaxConvW))
+        return fail(NSOSX_ERR_INVALID, "conv_scan_fwd: conv width must be in [1, 8]");
+    if (conv && per_group % kScanCh != 0)
+        return fail(NSOSX_ERR_INVALID, "conv_scan_fwd: channels per group must be a multiple of 64");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (per_group % kScanCh == 0) {
         const dim3 grid(Dm / kScanCh, num_seqs), block(256);
         const int spl = N <= 4 ? 1 : N <= 8 ? 2 : N <= 16 ? 4 : N <= 32 ? 8 : 16;
-#define NSOSX_SCAN(ADT, SPL, GATE)                                                              \
-    hipLaunchKernelGGL((scan_fwd_kernel<ADT, SPL, GATE>), grid, block, 0, st, x, x_stride, dt,   \
-                       A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens, total_tokens, H,   \
-                       P, N, G, initial_state, final_state, y);
+#define NSOSX_SCAN(ADT, SPL, GATE, CONV)                                                        \
+    hipLaunchKernelGGL((scan_fwd_kernel<ADT, SPL, GATE, CONV>), grid, block, 0, st, x, x_stride, \
+                       dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens, num_seqs,      \
+                       total_tokens, H, P, N, G, conv_w, conv_b, conv_width, initial_state,     \
+                       final_state, y);
+#define NSOSX_SCAN_C(ADT, SPL, GATE) \
+    if (conv) { NSOSX_SCAN(ADT, SPL, GATE, true) } else { NSOSX_SCAN(ADT, SPL, GATE, false) }
 #define NSOSX_SCAN_G(ADT, SPL) \
-    if (z) { NSOSX_SCAN(ADT, SPL, true) } else { NSOSX_SCAN(ADT, SPL, false) }
+    if (z) { NSOSX_SCAN_C(ADT, SPL, true) } else { NSOSX_SCAN_C(ADT, SPL, false) }
 #define NSOSX_SCAN_S(ADT)                          \
     switch (spl) {                                 \
         case 1: NSOSX_SCAN_G(ADT, 1) break;        \
@@ -361,6 +471,7 @@ extern "C" int nsosx_selective_scan_fwd(const void* x, int64_t x_stride, const v
         if (act_dtype == NSOSX_F32) { NSOSX_SCAN_S(NSOSX_F32) } else { NSOSX_SCAN_S(NSOSX_BF16) }
 #undef NSOSX_SCAN_S
 #undef NSOSX_SCAN_G
+#undef NSOSX_SCAN_C
 #undef NSOSX_SCAN
     } else {
         const int64_t lanes = (int64_t)num_seqs * Dm;
@@ -375,6 +486,32 @@ extern "C" int nsosx_selective_scan_fwd(const void* x, int64_t x_stride, const v
                                num_seqs, total_tokens, H, P, N, G, initial_state, final_state, y);
     }
     return check_launch("selective_scan_fwd");
+}
+
+extern "C" int nsosx_selective_scan_fwd(const void* x, int64_t x_stride, const void* dt,
+                                        const float* A_log, int a_per_state, const void* B,
+                                        const void* C, const float* D, const void* z,
+                                        int64_t z_stride, const int32_t* cu_seqlens, int num_seqs,
+                                        int total_tokens, int H, int P, int N, int G,
+                                        int act_dtype, const float* initial_state,
+                                        float* final_state, void* y, void* stream) {
+    return scan_fwd_launch(x, x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens,
+                           num_seqs, total_tokens, H, P, N, G, act_dtype, nullptr, nullptr, 0,
+                           initial_state, final_state, y, stream);
+}
+
+extern "C" int nsosx_conv_scan_fwd(const void* x_raw, int64_t x_stride, const float* conv_w,
+                                   const float* conv_b, int conv_width, const void* dt,
+                                   const float* A_log, int a_per_state, const void* B,
+                                   const void* C, const float* D, const void* z, int64_t z_stride,
+                                   const int32_t* cu_seqlens, int num_seqs, int total_tokens,
+                                   int H, int P, int N, int G, int act_dtype,
+                                   const float* initial_state, float* final_state, void* y,
+                                   void* stream) {
+    if (!conv_w) return fail(NSOSX_ERR_INVALID, "conv_scan_fwd: null conv weight");
+    return scan_fwd_launch(x_raw, x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride,
+                           cu_seqlens, num_seqs, total_tokens, H, P, N, G, act_dtype, conv_w,
+                           conv_b, conv_width, initial_state, final_state, y, stream);
 }
 
 extern "C" int nsosx_selective_scan_step(const void* x, const void* dt, const float* A_log,

@@ -121,7 +121,6 @@ class HybridMambaLayer:
         if b is None:
             b = {
                 "xz": torch.empty((t, 2 * self.d_inner), dtype=dtype, device=device),
-                "xc": torch.empty((t, self.d_inner), dtype=dtype, device=device),
                 "ys": torch.empty((t, self.d_inner), dtype=dtype, device=device),
                 "out": torch.empty((t, self.d_model), dtype=dtype, device=device),
             }
@@ -141,16 +140,13 @@ class HybridMambaLayer:
         self.in_proj.forward_into(x, b["xz"], mk("in_proj"))
         xin = b["xz"][:, :di]
         z = b["xz"][:, di:]
-        call("nsosx_conv1d_causal", _p(xin), ops._dt(xin), xin.stride(0), _p(self.conv_w),
-             _p(self.conv_b), _p(cu_seqlens), s, t, di, self.conv_w.shape[1], 1, _p(b["xc"]),
-             ops._dt(b["xc"]), _stream())
+        # causal conv + bias + SiLU fused into the scan's input staging
+        call("nsosx_conv_scan_fwd", _p(xin), xin.stride(0), _p(self.conv_w), _p(self.conv_b),
+             self.conv_w.shape[1], _p(dt), _p(self.a_log), 1, _p(B), _p(C), _p(self.d_skip), _p(z),
+             z.stride(0), _p(cu_seqlens), s, t, di, 1, n, 1, ops._dt(x), None, _p(final_state),
+             _p(b["ys"]), _stream())
         if marker:
-            marker("conv")
-        call("nsosx_selective_scan_fwd", _p(b["xc"]), di, _p(dt), _p(self.a_log), 1, _p(B), _p(C),
-             _p(self.d_skip), _p(z), z.stride(0), _p(cu_seqlens), s, t, di, 1, n, 1,
-             ops._dt(x), None, _p(final_state), _p(b["ys"]), _stream())
-        if marker:
-            marker("scan")
+            marker("conv_scan")
         self.out_proj.forward_into(b["ys"], b["out"], mk("out_proj"))
         return b["out"]
 

@@ -233,6 +233,32 @@ def selective_scan_fwd(x, dt, a_log, B, C, D, z, cu_seqlens, H, P, N, G, initial
     return y, fin
 
 
+def conv_scan_fwd(x_raw, conv_w, conv_b, dt, a_log, B, C, D, z, cu_seqlens, H, P, N, G,
+                  initial_state=None, want_final: bool = True):
+    """Causal conv + bias + SiLU fused into the scan's staging -> (y, final state)."""
+    t = x_raw.shape[0]
+    s = cu_seqlens.numel() - 1
+    if x_raw.stride(1) != 1 or (z is not None and z.stride(1) != 1):
+        raise ValueError("conv_scan_fwd: x and z need unit stride in the channel dim")
+    for name, v in (("dt", dt), ("B", B), ("C", C)):
+        _dev(v, name, x_raw.dtype)
+    _dev(conv_w, "conv_w", torch.float32)
+    _opt(conv_b, "conv_b")
+    _dev(a_log, "a_log", torch.float32)
+    _dev(D, "D", torch.float32)
+    _dev(cu_seqlens, "cu_seqlens", torch.int32)
+    _opt(initial_state, "initial_state")
+    a_per_state = int(a_log.numel() == H * N and N > 1)
+    y = torch.empty((t, H * P), dtype=x_raw.dtype, device=x_raw.device)
+    fin = (torch.empty((s, H * P, N), dtype=torch.float32, device=x_raw.device)
+           if want_final else None)
+    call("nsosx_conv_scan_fwd", _p(x_raw), x_raw.stride(0), _p(conv_w), _p(conv_b),
+         conv_w.shape[1], _p(dt), _p(a_log), a_per_state, _p(B), _p(C), _p(D), _p(z),
+         0 if z is None else z.stride(0), _p(cu_seqlens), s, t, H, P, N, G, _dt(x_raw),
+         _p(initial_state), _p(fin), _p(y), _stream())
+    return y, fin
+
+
 def selective_scan_step(x, dt, a_log, B, C, D, z, state, H, P, N, G):
     """Decode step in place on `state` [R, H*P, N] (src/mamba2.cpp:4038-4125) -> y [R, H*P]."""
     r = x.shape[0]

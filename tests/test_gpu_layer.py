@@ -1,0 +1,58 @@
+"""The composed layers on the GPU against the oracle's composition.
+
+Hybrid Mamba layer (config 4 structure at reduced width): in_proj output is
+bit-exact (the bf16 rounding of the oracle's fp32 value), out_proj is
+bit-exact given the GPU's scan output, and the layer output is within the
+north-star bf16 bound (2e-2 relative to the output scale) of the all-oracle
+pipeline run in fp32 on the same bf16-rounded inputs."""
+import numpy as np
+import pytest
+import torch
+
+from reimagined_amd import workloads
+from reimagined_amd.layers import HybridMambaLayer
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16)
+
+
+def test_hybrid_layer_matches_oracle(dev, orc):
+    params, inp = workloads.config4(seed=11, num_seqs=5, d_model=256, lo=3, hi=150)
+    T = int(inp["cu_seqlens"][-1])
+    di = params["w_out"].shape[1]
+    n = params["a_log"].shape[1]
+    layer = HybridMambaLayer(params, dev, rms_input=True)
+    xb, dtb, Bb, Cb = (_bf(inp[k]) for k in ("x", "dt", "B", "C"))
+    cu = torch.from_numpy(inp["cu_seqlens"]).to(dev)
+    fin = torch.empty((cu.numel() - 1, di, n), dtype=torch.float32, device=dev)
+    out = layer.forward(xb.to(dev), dtb.to(dev), Bb.to(dev), Cb.to(dev), cu, final_state=fin)
+    buf = layer._buf[T]
+    xz_gpu = buf["xz"].float().cpu().numpy()
+    ys_gpu = buf["ys"].float().cpu().numpy()
+    # in_proj: bit-exact up to the bf16 store
+    pin, wsi, _ = orc.pack_weights(params["w_in"])
+    xz = orc.bitlinear_forward(xb.float().numpy(), pin, wsi, 2 * di, rms_input=True)
+    np.testing.assert_array_equal(xz_gpu, _bf(xz).float().numpy())
+    # conv + scan on the GPU's in_proj output
+    c = inp["cu_seqlens"]
+    xc = orc.conv1d_causal(np.ascontiguousarray(xz_gpu[:, :di]), params["conv_w"], c,
+                           bias=params["conv_b"], silu_act=True)
+    ys, wfin = orc.selective_scan(xc, dtb.float().numpy(), params["a_log"], Bb.float().numpy(),
+                                  Cb.float().numpy(), params["d_skip"],
+                                  np.ascontiguousarray(xz_gpu[:, di:]), c, di, 1, n, 1)
+    scale = np.abs(ys).max()
+    np.testing.assert_allclose(ys_gpu, ys, rtol=2e-2, atol=2e-2 * scale / 64)
+    np.testing.assert_allclose(fin.cpu().numpy(), wfin, rtol=1e-4, atol=1e-5)
+    # out_proj: bit-exact on the GPU's scan output
+    pout, wso, _ = orc.pack_weights(params["w_out"])
+    y = orc.bitlinear_forward(ys_gpu, pout, wso, params["w_out"].shape[0], rms_input=True)
+    np.testing.assert_array_equal(out.float().cpu().numpy(), _bf(y).float().numpy())
+    # whole layer against the all-oracle pipeline, rounding to bf16 where the layer's
+    # activations are bf16 tensors (in_proj output, scan output)
+    ys_b = _bf(ys).float().numpy()
+    y_ref = orc.bitlinear_forward(ys_b, pout, wso, params["w_out"].shape[0], rms_input=True)
+    s2 = np.abs(y_ref).max()
+    np.testing.assert_allclose(out.float().cpu().numpy(), y_ref, rtol=2e-2, atol=2e-2 * s2 / 16)

@@ -161,3 +161,37 @@ def test_scan_rejects_float_cu_seqlens(dev):
                                torch.zeros((4, 16), device=dev), torch.zeros((4, 16), device=dev),
                                torch.zeros(64, device=dev), None,
                                torch.tensor([0.0, 4.0], device=dev), 64, 1, 16, 1)
+
+
+@pytest.mark.parametrize("dtype,lengths", [(torch.float32, [5, 64, 1, 33]),
+                                           (torch.bfloat16, [200, 3, 77])])
+def test_conv_scan_fused_matches_oracle(dev, orc, dtype, lengths):
+    """conv + bias + SiLU fused into the scan == oracle conv, then oracle scan."""
+    rng = np.random.default_rng(len(lengths))
+    H, P, N, G, W = 128, 1, 16, 1, 4
+    cu = _cu(lengths)
+    T = int(cu[-1])
+    inp = _inputs(rng, T, H, P, N, G)
+    wide = rng.standard_normal((T, 2 * H)).astype(np.float32)  # raw x = left half of each row
+    w = (rng.standard_normal((H, W)) * 0.5).astype(np.float32)
+    b = (rng.standard_normal(H) * 0.1).astype(np.float32)
+    wt = _t(dev, wide, dtype)
+    zt = _t(dev, inp["z"], dtype)
+    y, fin = ops.conv_scan_fwd(wt[:, :H], _t(dev, w), _t(dev, b), _t(dev, inp["dt"], dtype),
+                               _t(dev, inp["a_log"]), _t(dev, inp["B"], dtype),
+                               _t(dev, inp["C"], dtype), _t(dev, inp["D"]), zt, _t(dev, cu),
+                               H, P, N, G)
+    rd = lambda a: torch.from_numpy(a).to(dtype).float().numpy()
+    xr = np.ascontiguousarray(wt[:, :H].float().cpu().numpy())
+    xc = orc.conv1d_causal(xr, w, cu, bias=b, silu_act=True)
+    if dtype == torch.float32:
+        wy, wfin = orc.selective_scan(xc, inp["dt"], inp["a_log"], inp["B"], inp["C"], inp["D"],
+                                      inp["z"], cu, H, P, N, G)
+        np.testing.assert_allclose(y.cpu().numpy(), wy, rtol=RTOL, atol=ATOL)
+        np.testing.assert_allclose(fin.cpu().numpy(), wfin, rtol=RTOL, atol=ATOL)
+    else:
+        wy, wfin = orc.selective_scan(xc, rd(inp["dt"]), inp["a_log"], rd(inp["B"]), rd(inp["C"]),
+                                      inp["D"], rd(inp["z"]), cu, H, P, N, G)
+        scale = np.abs(wy).max()
+        np.testing.assert_allclose(y.float().cpu().numpy(), wy, rtol=2e-2, atol=2e-2 * scale / 64)
+        np.testing.assert_allclose(fin.cpu().numpy(), wfin, rtol=1e-4, atol=1e-5)
