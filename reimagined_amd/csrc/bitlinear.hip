@@ -599,6 +599,240 @@ __device__ __forceinline__ void gemm_tile(const GemmProblem& pb, const int8_t* _
 
 constexpr int kGemmSmem = 2 * kBN * 16 + 2 * kBM * kXStride;
 
+// ===========================================================================
+// Large-tile int8 MFMA GEMM (M > 128).  Block tile 256 (n) x 256 (m), eight
+// waves in 4 (n) x 2 (m), each wave 64 x 128 = 4 x 8 tiles of
+// v_mfma_i32_16x16x64_i8 (128 accumulators per lane), two waves per SIMD.
+// A stage covers 128 of K (two MFMA k steps, 64 MFMAs per wave) and the two
+// LDS stages alternate, so the next stage's global loads are in flight
+// across a full stage of MFMAs.  Weights stay 2-bit in LDS (32 bytes per row
+// per stage; the two 16-byte halves of a row swap places for odd groups of
+// 8 rows so the lanes of a fragment read hit distinct banks) and are
+// expanded in registers; activation rows are byte-transposed into the
+// unpack order on their way to LDS (row stride 144 bytes: conflict-free
+// 16-byte fragment reads).
+// ===========================================================================
+constexpr int kBN2 = 256, kBM2 = 256, kBK2 = 128;
+constexpr int kXS2 = 144;
+constexpr int kW2Bytes = kBN2 * 32;
+constexpr int kX2Bytes = kBM2 * kXS2;
+constexpr int kGemm2Smem = 2 * (kW2Bytes + kX2Bytes);
+constexpr int kGemm2Threads = 512;
+
+template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU>
+__device__ __forceinline__ void gemm2_tile(const GemmProblem& pb, const int8_t* __restrict__ q,
+                                           const float* __restrict__ act_scale,
+                                           const int32_t* __restrict__ perm, int seg_begin,
+                                           int seg_rows, int n0, int m0, void* y,
+                                           int32_t* acc_out, char* smem) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave & 3, wm = wave >> 2;
+    const int W16 = pb.K >> 4;
+    const int KT = (pb.K + kBK2 - 1) / kBK2;
+    const bool waligned = (W16 & 3) == 0;
+
+    // global -> register staging: one 16-byte half of a weight row, four 16-byte
+    // activation chunks
+    const int wrow_l = tid >> 1, whalf = tid & 1;
+    const int wrow = n0 + wrow_l;
+    const uint32_t* wsrc = pb.packed + (int64_t)wrow * W16 + whalf * 4;
+    const int xchunk = tid & 7;
+    int xsrc[4];
+    bool xok[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + (tid >> 3) + 64 * i;
+        xok[i] = m < seg_rows;
+        int src = seg_begin + m;
+        if (GATHER && xok[i]) src = perm[src];
+        xsrc[i] = src;
+    }
+    uint4 wreg;
+    uint4 xraw[4];
+    auto load_global = [&](int kt) {
+        const int w0 = kt * (kBK2 / 16) + whalf * 4;
+        wreg = make_uint4(0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u);
+        if (wrow < pb.N) {
+            const uint32_t* src = wsrc + kt * (kBK2 / 16);
+            if (waligned && w0 + 3 < W16) {
+                wreg = *reinterpret_cast<const uint4*>(src);
+            } else {
+                if (w0 + 0 < W16) wreg.x = src[0];
+                if (w0 + 1 < W16) wreg.y = src[1];
+                if (w0 + 2 < W16) wreg.z = src[2];
+                if (w0 + 3 < W16) wreg.w = src[3];
+            }
+        }
+        const int k = kt * kBK2 + xchunk * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xraw[i] = make_uint4(0u, 0u, 0u, 0u);
+            if (xok[i] && k < pb.K)
+                xraw[i] = *reinterpret_cast<const uint4*>(q + (int64_t)xsrc[i] * pb.K + k);
+        }
+    };
+    auto store_lds = [&](int buf) {
+        char* wl = smem + buf * (kW2Bytes + kX2Bytes);
+        char* xl = wl + kW2Bytes;
+        const int pos = whalf ^ ((wrow_l >> 3) & 1);
+        *reinterpret_cast<uint4*>(wl + wrow_l * 32 + pos * 16) = wreg;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t d[4] = {xraw[i].x, xraw[i].y, xraw[i].z, xraw[i].w};
+            uint32_t e[4];
+            transpose16(d, e);
+            const int ml = (tid >> 3) + 64 * i;
+            *reinterpret_cast<uint4*>(xl + ml * kXS2 + xchunk * 16) = make_uint4(e[0], e[1], e[2], e[3]);
+        }
+    };
+
+    v4i acc[4][8];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+
+    load_global(0);
+    store_lds(0);
+    __syncthreads();
+
+    const int g = lane >> 4;
+    const int li = lane & 15;
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < KT) load_global(kt + 1);
+        const uint32_t* wl = reinterpret_cast<const uint32_t*>(smem + cur * (kW2Bytes + kX2Bytes));
+        const char* xl = smem + cur * (kW2Bytes + kX2Bytes) + kW2Bytes;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            v4i bx[8];
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb) {
+                const int ml = wm * 128 + mb * 16 + li;
+                const uint4 v = *reinterpret_cast<const uint4*>(xl + ml * kXS2 + ks * 64 + g * 16);
+                bx[mb] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            }
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) {
+                const int nl = wn * 64 + nb * 16 + li;
+                const int w = (ks * 4 + g) ^ (((nl >> 3) & 1) << 2);
+                const uint32_t p = wl[nl * 8 + w];
+                uint32_t wv[4];
+                unpack_word(p, wv);
+                const v4i aw = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+#pragma unroll
+                for (int mb = 0; mb < 8; ++mb)
+                    acc[nb][mb] =
+                        __builtin_amdgcn_mfma_i32_16x16x64_i8(aw, bx[mb], acc[nb][mb], 0, 0, 0);
+            }
+        }
+        if (kt + 1 < KT) store_lds(cur ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds n = n_base + 4*g + r for token m = m_base + li
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+        const int ml = m0 + wm * 128 + mb * 16 + li;
+        if (ml >= seg_rows) continue;
+        const int64_t orow = (int64_t)(seg_begin + ml);
+        const int arow = GATHER ? perm[seg_begin + ml] : (int)orow;
+        const float comb = __fmul_rn(act_scale[arow], pb.ws);
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+            const int nbase = n0 + wn * 64 + nb * 16 + 4 * g;
+            const v4i a = acc[nb][mb];
+            const int av[4] = {a.x, a.y, a.z, a.w};
+            const bool full = nbase + 3 < pb.N && (pb.N & 3) == 0;
+            if (ACC_OUT) {
+                if (full) {
+                    *reinterpret_cast<int4*>(acc_out + orow * pb.N + nbase) =
+                        make_int4(av[0], av[1], av[2], av[3]);
+                } else {
+                    for (int r = 0; r < 4; ++r)
+                        if (nbase + r < pb.N) acc_out[orow * pb.N + nbase + r] = av[r];
+                }
+            }
+            if (y) {
+                float o[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int n = min(nbase + r, pb.N - 1);
+                    float v = dequant(av[r], comb, pb.mag, pb.bias, n);
+                    if (SQRELU) {
+                        v = v > 0.0f ? v : 0.0f;
+                        v = __fmul_rn(v, v);
+                    }
+                    o[r] = v;
+                }
+                if (full) {
+                    if constexpr (YDT == NSOSX_F32) {
+                        *reinterpret_cast<float4*>(static_cast<float*>(y) + orow * pb.N + nbase) =
+                            make_float4(o[0], o[1], o[2], o[3]);
+                    } else {
+                        const uint32_t lo = f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
+                        const uint32_t hi = f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
+                        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + orow * pb.N + nbase) =
+                            make_uint2(lo, hi);
+                    }
+                } else {
+                    for (int r = 0; r < 4; ++r)
+                        if (nbase + r < pb.N) store_act<YDT>(y, orow * pb.N + nbase + r, o[r]);
+                }
+            }
+        }
+    }
+}
+
+// Linear workgroup id -> (n tile, m tile).  Consecutive ids go round-robin to
+// the 8 XCDs; this map hands each XCD a contiguous run of tiles, n fastest,
+// so the workgroups of one XCD share activation rows in their own L2.
+__device__ __forceinline__ void xcd_tile(int L, int ntn, int ntm, int& nt, int& mt) {
+    const int total = ntn * ntm;
+    const int per = total / 8;
+    int t = L;
+    if (L < per * 8) t = (L % 8) * per + L / 8;
+    nt = t % ntn;
+    mt = t / ntn;
+}
+
+template <int YDT, bool ACC_OUT>
+__global__ __launch_bounds__(kGemm2Threads) void gemm2_kernel(GemmProblem pb, const int8_t* __restrict__ q,
+                                                    const float* __restrict__ act_scale, int M,
+                                                    void* y, int32_t* acc_out) {
+    extern __shared__ __align__(16) char smem2[];
+    const int ntn = (pb.N + kBN2 - 1) / kBN2;
+    const int ntm = (M + kBM2 - 1) / kBM2;
+    int nt, mt;
+    xcd_tile(blockIdx.x, ntn, ntm, nt, mt);
+    gemm2_tile<YDT, ACC_OUT, false, false>(pb, q, act_scale, nullptr, 0, M, nt * kBN2, mt * kBM2,
+                                           y, acc_out, smem2);
+}
+
+template <int YDT, bool GATHER, bool SQRELU>
+__global__ __launch_bounds__(kGemm2Threads) void grouped_gemm2_kernel(const nsosx_linear_view* views,
+                                                            const int32_t* __restrict__ offsets,
+                                                            const int32_t* __restrict__ perm,
+                                                            const int8_t* __restrict__ q,
+                                                            const float* __restrict__ act_scale,
+                                                            void* y) {
+    extern __shared__ __align__(16) char smem2[];
+    const int e = blockIdx.z;
+    const int seg_begin = offsets[e];
+    const int seg_rows = offsets[e + 1] - seg_begin;
+    const int m0 = blockIdx.y * kBM2;
+    if (m0 >= seg_rows) return;
+    const nsosx_linear_view v = views[e];
+    const int n0 = blockIdx.x * kBN2;
+    if (n0 >= v.outputs) return;
+    GemmProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
+    gemm2_tile<YDT, false, GATHER, SQRELU>(pb, q, act_scale, perm, seg_begin, seg_rows, n0, m0, y,
+                                           nullptr, smem2);
+}
+
+
 template <int YDT, bool ACC_OUT>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmProblem pb, const int8_t* __restrict__ q,
                                                    const float* __restrict__ act_scale, int M,
@@ -634,6 +868,16 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(const nsosx_linear_vi
 template <int YDT>
 static void launch_gemm_t(const GemmProblem& pb, const int8_t* q, const float* as, int M,
                           void* y, int32_t* acc, hipStream_t st) {
+    if (M > kBM) {
+        const int tiles = ((pb.N + kBN2 - 1) / kBN2) * ((M + kBM2 - 1) / kBM2);
+        if (acc)
+            hipLaunchKernelGGL((gemm2_kernel<YDT, true>), dim3(tiles), dim3(kGemm2Threads), kGemm2Smem, st,
+                               pb, q, as, M, y, acc);
+        else
+            hipLaunchKernelGGL((gemm2_kernel<YDT, false>), dim3(tiles), dim3(kGemm2Threads), kGemm2Smem, st,
+                               pb, q, as, M, y, acc);
+        return;
+    }
     const dim3 grid((pb.N + kBN - 1) / kBN, (M + kBM - 1) / kBM), block(256);
     if (acc)
         hipLaunchKernelGGL((gemm_kernel<YDT, true>), grid, block, 0, st, pb, q, as, M, y, acc);
@@ -793,11 +1037,11 @@ extern "C" int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, in
     if (!valid_dtype(y_dtype)) return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm: bad dtype");
     if (max_rows_per_expert == 0) return NSOSX_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const dim3 grid((N + kBN - 1) / kBN, (max_rows_per_expert + kBM - 1) / kBM, experts);
-    const dim3 block(256);
-#define NSOSX_GGEMM(YDT, G, S)                                                                 \
-    hipLaunchKernelGGL((grouped_gemm_kernel<YDT, G, S>), grid, block, 0, st, views_dev, offsets, \
-                       perm, q, act_scale, y);
+    const dim3 grid((N + kBN2 - 1) / kBN2, (max_rows_per_expert + kBM2 - 1) / kBM2, experts);
+    const dim3 block(kGemm2Threads);
+#define NSOSX_GGEMM(YDT, G, S)                                                                  \
+    hipLaunchKernelGGL((grouped_gemm2_kernel<YDT, G, S>), grid, block, kGemm2Smem, st, views_dev, \
+                       offsets, perm, q, act_scale, y);
     if (y_dtype == NSOSX_F32) {
         if (gather) { if (squared_relu) { NSOSX_GGEMM(NSOSX_F32, true, true) } else { NSOSX_GGEMM(NSOSX_F32, true, false) } }
         else { if (squared_relu) { NSOSX_GGEMM(NSOSX_F32, false, true) } else { NSOSX_GGEMM(NSOSX_F32, false, false) } }
