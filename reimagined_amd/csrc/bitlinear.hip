@@ -562,6 +562,7 @@ __device__ __forceinline__ void gemm_tile(const GemmProblem& pb, const int8_t* _
                     *reinterpret_cast<int4*>(acc_out + orow * pb.N + nbase) =
                         make_int4(av[0], av[1], av[2], av[3]);
                 } else {
+#pragma unroll
                     for (int r = 0; r < 4; ++r)
                         if (nbase + r < pb.N) acc_out[orow * pb.N + nbase + r] = av[r];
                 }
@@ -589,6 +590,7 @@ __device__ __forceinline__ void gemm_tile(const GemmProblem& pb, const int8_t* _
                             make_uint2(lo, hi);
                     }
                 } else {
+#pragma unroll
                     for (int r = 0; r < 4; ++r)
                         if (nbase + r < pb.N) store_act<YDT>(y, orow * pb.N + nbase + r, o[r]);
                 }
@@ -601,17 +603,23 @@ constexpr int kGemmSmem = 2 * kBN * 16 + 2 * kBM * kXStride;
 
 // ===========================================================================
 // Large-tile int8 MFMA GEMM (M > 128).  Block tile 256 (n) x 256 (m), eight
-// waves in 4 (n) x 2 (m), each wave 64 x 128 = 4 x 8 tiles of
-// v_mfma_i32_16x16x64_i8 (128 accumulators per lane), two waves per SIMD.
-// A stage covers 128 of K (two MFMA k steps, 64 MFMAs per wave) and the two
-// LDS stages alternate, so the next stage's global loads are in flight
-// across a full stage of MFMAs.  Weights stay 2-bit in LDS (32 bytes per row
-// per stage; the two 16-byte halves of a row swap places for odd groups of
-// 8 rows so the lanes of a fragment read hit distinct banks) and are
-// expanded in registers; activation rows are byte-transposed into the
-// unpack order on their way to LDS (row stride 144 bytes: conflict-free
-// 16-byte fragment reads).
+// waves in 4 (n) x 2 (m), each wave 64 n x 128 m = 2 x 4 tiles of
+// v_mfma_i32_32x32x32_i8 (128 accumulators per lane, 8 independent chains:
+// the 32x32 shape keeps the matrix pipe full where 16x16x64 with as many
+// chains does not).  A stage covers 128 of K (four MFMA k steps, 32 MFMAs
+// per wave); two LDS stages alternate, the next stage's global loads in
+// flight across the current one's MFMAs.  Weights stay 2-bit in LDS (32
+// bytes per row per stage) and are expanded in registers right before the
+// MFMAs; the 8-byte pairs of a row are XOR-swizzled by (row / 8) % 4 so the
+// 64 lanes of a fragment read hit 64 distinct banks.  Activation rows are
+// byte-transposed into the unpack order on their way to LDS (row stride 144
+// bytes: conflict-free 16-byte fragment reads).
+// MFMA 32x32x32 lane layout: A row i = lane % 32 and B column j = lane % 32
+// with k group lane / 32 (16 consecutive k each); accumulator r of a lane is
+// C[i = 8 (r / 4) + 4 (lane / 32) + r % 4][j = lane % 32].
 // ===========================================================================
+typedef int v16i __attribute__((ext_vector_type(16)));
+
 constexpr int kBN2 = 256, kBM2 = 256, kBK2 = 128;
 constexpr int kXS2 = 144;
 constexpr int kW2Bytes = kBN2 * 32;
@@ -633,7 +641,7 @@ __device__ __forceinline__ void gemm2_tile(const GemmProblem& pb, const int8_t* 
     const int KT = (pb.K + kBK2 - 1) / kBK2;
     const bool waligned = (W16 & 3) == 0;
 
-    // global -> register staging: one 16-byte half of a weight row, four 16-byte
+    // global -> register staging: half of a weight row's 32 bytes, four 16-byte
     // activation chunks
     const int wrow_l = tid >> 1, whalf = tid & 1;
     const int wrow = n0 + wrow_l;
@@ -676,8 +684,11 @@ __device__ __forceinline__ void gemm2_tile(const GemmProblem& pb, const int8_t* 
     auto store_lds = [&](int buf) {
         char* wl = smem + buf * (kW2Bytes + kX2Bytes);
         char* xl = wl + kW2Bytes;
-        const int pos = whalf ^ ((wrow_l >> 3) & 1);
-        *reinterpret_cast<uint4*>(wl + wrow_l * 32 + pos * 16) = wreg;
+        // pairs 2h, 2h+1 of the row go to pair slots (2h)^f, (2h+1)^f
+        const int f = (wrow_l >> 3) & 3;
+        uint4 v = wreg;
+        if (f & 1) v = make_uint4(v.z, v.w, v.x, v.y);
+        *reinterpret_cast<uint4*>(wl + wrow_l * 32 + ((whalf ^ (f >> 1)) * 16)) = v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t d[4] = {xraw[i].x, xraw[i].y, xraw[i].z, xraw[i].w};
@@ -688,98 +699,314 @@ __device__ __forceinline__ void gemm2_tile(const GemmProblem& pb, const int8_t* 
         }
     };
 
-    v4i acc[4][8];
+    v16i acc[2][4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int b = 0; b < 8; ++b) acc[a][b] = v4i{0, 0, 0, 0};
+        for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
 
     load_global(0);
     store_lds(0);
     __syncthreads();
 
-    const int g = lane >> 4;
-    const int li = lane & 15;
+    const int g = lane >> 5;     // k group of 16
+    const int li = lane & 31;    // row (A) / column (B) within a 32 x 32 tile
     for (int kt = 0; kt < KT; ++kt) {
         const int cur = kt & 1;
         if (kt + 1 < KT) load_global(kt + 1);
         const uint32_t* wl = reinterpret_cast<const uint32_t*>(smem + cur * (kW2Bytes + kX2Bytes));
         const char* xl = smem + cur * (kW2Bytes + kX2Bytes) + kW2Bytes;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            v4i bx[8];
+        for (int ks = 0; ks < 4; ++ks) {
+            v4i aw[2];
 #pragma unroll
-            for (int mb = 0; mb < 8; ++mb) {
-                const int ml = wm * 128 + mb * 16 + li;
-                const uint4 v = *reinterpret_cast<const uint4*>(xl + ml * kXS2 + ks * 64 + g * 16);
+            for (int nb = 0; nb < 2; ++nb) {
+                const int nl = wn * 64 + nb * 32 + li;
+                const int w = (ks * 2 + g) ^ (((nl >> 3) & 3) << 1);
+                uint32_t wv[4];
+                unpack_word(wl[nl * 8 + w], wv);
+                aw[nb] = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+            }
+            v4i bx[4];
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) {
+                const int ml = wm * 128 + mb * 32 + li;
+                const uint4 v = *reinterpret_cast<const uint4*>(xl + ml * kXS2 + ks * 32 + g * 16);
                 bx[mb] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb) {
-                const int nl = wn * 64 + nb * 16 + li;
-                const int w = (ks * 4 + g) ^ (((nl >> 3) & 1) << 2);
-                const uint32_t p = wl[nl * 8 + w];
-                uint32_t wv[4];
-                unpack_word(p, wv);
-                const v4i aw = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+            for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-                for (int mb = 0; mb < 8; ++mb)
+                for (int mb = 0; mb < 4; ++mb)
                     acc[nb][mb] =
-                        __builtin_amdgcn_mfma_i32_16x16x64_i8(aw, bx[mb], acc[nb][mb], 0, 0, 0);
-            }
+                        __builtin_amdgcn_mfma_i32_32x32x32_i8(aw[nb], bx[mb], acc[nb][mb], 0, 0, 0);
         }
         if (kt + 1 < KT) store_lds(cur ^ 1);
         __syncthreads();
     }
 
-    // epilogue: lane holds n = n_base + 4*g + r for token m = m_base + li
+    // epilogue: lane holds token m = m_base + li and, for q4 = 0..3, the four
+    // consecutive outputs n = n_base + 8 q4 + 4 g + 0..3
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
-        const int ml = m0 + wm * 128 + mb * 16 + li;
+    for (int mb = 0; mb < 4; ++mb) {
+        const int ml = m0 + wm * 128 + mb * 32 + li;
         if (ml >= seg_rows) continue;
         const int64_t orow = (int64_t)(seg_begin + ml);
         const int arow = GATHER ? perm[seg_begin + ml] : (int)orow;
         const float comb = __fmul_rn(act_scale[arow], pb.ws);
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-            const int nbase = n0 + wn * 64 + nb * 16 + 4 * g;
-            const v4i a = acc[nb][mb];
-            const int av[4] = {a.x, a.y, a.z, a.w};
-            const bool full = nbase + 3 < pb.N && (pb.N & 3) == 0;
-            if (ACC_OUT) {
-                if (full) {
-                    *reinterpret_cast<int4*>(acc_out + orow * pb.N + nbase) =
-                        make_int4(av[0], av[1], av[2], av[3]);
-                } else {
-                    for (int r = 0; r < 4; ++r)
-                        if (nbase + r < pb.N) acc_out[orow * pb.N + nbase + r] = av[r];
+        for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int nbase = n0 + wn * 64 + nb * 32 + 8 * q4 + 4 * g;
+                const v16i& a = acc[nb][mb];
+                const int av[4] = {a[4 * q4], a[4 * q4 + 1], a[4 * q4 + 2], a[4 * q4 + 3]};
+                const bool full = nbase + 3 < pb.N && (pb.N & 3) == 0;
+                if (ACC_OUT) {
+                    if (full) {
+                        *reinterpret_cast<int4*>(acc_out + orow * pb.N + nbase) =
+                            make_int4(av[0], av[1], av[2], av[3]);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (nbase + r < pb.N) acc_out[orow * pb.N + nbase + r] = av[r];
+                    }
+                }
+                if (y) {
+                    float o[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int n = min(nbase + r, pb.N - 1);
+                        float v = dequant(av[r], comb, pb.mag, pb.bias, n);
+                        if (SQRELU) {
+                            v = v > 0.0f ? v : 0.0f;
+                            v = __fmul_rn(v, v);
+                        }
+                        o[r] = v;
+                    }
+                    if (full) {
+                        if constexpr (YDT == NSOSX_F32) {
+                            *reinterpret_cast<float4*>(static_cast<float*>(y) + orow * pb.N + nbase) =
+                                make_float4(o[0], o[1], o[2], o[3]);
+                        } else {
+                            const uint32_t lo = f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
+                            const uint32_t hi = f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
+                            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + orow * pb.N + nbase) =
+                                make_uint2(lo, hi);
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (nbase + r < pb.N) store_act<YDT>(y, orow * pb.N + nbase + r, o[r]);
+                    }
                 }
             }
-            if (y) {
-                float o[4];
+        }
+    }
+}
+
+// ===========================================================================
+// Direct-to-LDS int8 MFMA GEMM (M > 128, K % 128 == 0).  Block tile 256 (n)
+// x 128 (m), four waves each owning 64 n x 128 m = 2 x 4 tiles of
+// v_mfma_i32_32x32x32_i8 (128 accumulators, 8 independent chains).  Global
+// memory goes straight into LDS with global_load_lds_dwordx4 (no VGPR
+// staging) through a 3-stage ring of 128-deep K stages (24 KB each, 72 KB in
+// all), so two workgroups share a CU and their barrier phases interleave.
+// K mapping inside a stage: MFMA step ks, lane group g (lane / 32) takes the
+// 16 k values of chunk 4 g + ks, so each lane's weights for the whole stage
+// are one 16-byte packed word group (read once, decoded one word per step)
+// and its activations one 16-byte chunk per step.  Bank spreading (64 banks
+// of 4 bytes; a 16-byte read serves 16 lanes per clock), chosen through
+// which global chunk each lane fetches:
+//   weights     the two 16-byte halves of row r swap when (r / 8) is odd
+//   activations 16-byte chunk c of row r sits in slot c ^ ((r / 2) % 8)
+// Activation rows land in natural byte order; each decoded weight word is
+// byte-transposed to match.  Rows past N or M are fetched from a clamped,
+// in-bounds row; their outputs are never stored.
+// ===========================================================================
+constexpr int kG3BN = 256, kG3BM = 128, kG3BK = 128;
+constexpr int kG3Stages = 3;
+constexpr int kG3WBytes = kG3BN * 32;     // 8 KB
+constexpr int kG3XBytes = kG3BM * 128;    // 16 KB
+constexpr int kG3StageBytes = kG3WBytes + kG3XBytes;
+constexpr int kGemm3Smem = kG3Stages * kG3StageBytes;
+constexpr int kGemm3Threads = 256;
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ lds_void_t* lds_ptr(const char* p) {
+    return (lds_void_t*)((__attribute__((address_space(3))) char*)nullptr +
+                         static_cast<unsigned>(reinterpret_cast<size_t>(p)));
+}
+
+template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU>
+__device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* __restrict__ q,
+                                           const float* __restrict__ act_scale,
+                                           const int32_t* __restrict__ perm, int seg_begin,
+                                           int seg_rows, int n0, int m0, void* y,
+                                           int32_t* acc_out, char* smem) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;        // wave = 64-row slice of n
+    const int W16 = pb.K >> 4;
+    const int KT = pb.K / kG3BK;
+
+    // DMA sources.  Weights: wave-load j (0, 1) of a wave fills LDS rows
+    // 64 wave + 32 j .. +31, lane -> row + lane / 2, slot lane % 2.
+    const char* wsrc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int r = 64 * wave + 32 * j + (lane >> 1);
+        const int half = (lane & 1) ^ ((r >> 3) & 1);
+        const int row = min(n0 + r, pb.N - 1);
+        wsrc[j] = reinterpret_cast<const char*>(pb.packed + (int64_t)row * W16) + half * 16;
+    }
+    // Activations: wave-load i (0..3) of a wave fills LDS rows 32 i + 8 wave .. +7,
+    // lane -> row + lane / 8, slot lane % 8.
+    const char* xsrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 32 * i + 8 * wave + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int m = min(m0 + r, seg_rows - 1);
+        const int src = GATHER ? perm[seg_begin + m] : seg_begin + m;
+        xsrc[i] = reinterpret_cast<const char*>(q + (int64_t)src * pb.K) + c * 16;
+    }
+    auto issue = [&](int kt) {
+        char* st = smem + (kt % kG3Stages) * kG3StageBytes;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            __builtin_amdgcn_global_load_lds(wsrc[j] + kt * 32,
+                                             lds_ptr(st + (64 * wave + 32 * j) * 32), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(xsrc[i] + kt * 128,
+                                             lds_ptr(st + kG3WBytes + (32 * i + 8 * wave) * 128),
+                                             16, 0, 0);
+    };
+
+    v16i acc[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
+
+    issue(0);
+    if (KT > 1) issue(1);
+
+    const int g = lane >> 5;
+    const int li = lane & 31;
+    for (int kt = 0; kt < KT; ++kt) {
+        // this thread's stage-kt DMA is done once at most one stage (6 loads) is pending
+        if (kt + 1 < KT) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + 2 < KT) issue(kt + 2);
+        const char* st = smem + (kt % kG3Stages) * kG3StageBytes;
+        const char* xl = st + kG3WBytes;
+        uint4 wq[2];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int nl = wave * 64 + nb * 32 + li;
+            const int slot = g ^ ((nl >> 3) & 1);
+            wq[nb] = *reinterpret_cast<const uint4*>(st + nl * 32 + slot * 16);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            v4i bx[4];
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) {
+                const int ml = mb * 32 + li;
+                const int slot = (4 * g + ks) ^ ((ml >> 1) & 7);
+                const uint4 v = *reinterpret_cast<const uint4*>(xl + ml * 128 + slot * 16);
+                bx[mb] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            }
+            v4i aw[2];
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const uint32_t words[4] = {wq[nb].x, wq[nb].y, wq[nb].z, wq[nb].w};
+                uint32_t wv[4], wt[4];
+                unpack_word(words[ks], wv);
+                transpose16(wv, wt);                            // unpack order -> natural order
+                aw[nb] = v4i{(int)wt[0], (int)wt[1], (int)wt[2], (int)wt[3]};
+            }
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+                    acc[nb][mb] =
+                        __builtin_amdgcn_mfma_i32_32x32x32_i8(aw[nb], bx[mb], acc[nb][mb], 0, 0, 0);
+        }
+    }
+
+    // epilogue: lane holds token m = m_base + li and, for q4 = 0..3, the four
+    // consecutive outputs n = n_base + 8 q4 + 4 g + 0..3.  A tile that lies
+    // inside N (N % 4 == 0) stores 4 outputs per access at constant offsets from
+    // one row pointer; edge tiles go element by element.
+    const bool full_tile = n0 + kG3BN <= pb.N && (pb.N & 3) == 0;
+    const int nw = n0 + wave * 64 + 4 * g;  // this lane's first output column
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+        const int ml = m0 + mb * 32 + li;
+        if (ml >= seg_rows) continue;
+        const int64_t orow = (int64_t)(seg_begin + ml);
+        const int arow = GATHER ? perm[seg_begin + ml] : (int)orow;
+        const float comb = __fmul_rn(act_scale[arow], pb.ws);
+        if (full_tile) {
+            int32_t* arow_out = ACC_OUT ? acc_out + orow * pb.N + nw : nullptr;
+            char* yrow = y ? static_cast<char*>(y) + (orow * pb.N + nw) * (YDT == NSOSX_F32 ? 4 : 2)
+                           : nullptr;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const int off = nb * 32 + 8 * q4;
+                    const v16i& a = acc[nb][mb];
+                    if (ACC_OUT)
+                        *reinterpret_cast<int4*>(arow_out + off) =
+                            make_int4(a[4 * q4], a[4 * q4 + 1], a[4 * q4 + 2], a[4 * q4 + 3]);
+                    if (y) {
+                        float o[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            float v = dequant(a[4 * q4 + r], comb, pb.mag, pb.bias, nw + off + r);
+                            if (SQRELU) {
+                                v = v > 0.0f ? v : 0.0f;
+                                v = __fmul_rn(v, v);
+                            }
+                            o[r] = v;
+                        }
+                        if constexpr (YDT == NSOSX_F32) {
+                            *reinterpret_cast<float4*>(yrow + off * 4) = make_float4(o[0], o[1], o[2], o[3]);
+                        } else {
+                            *reinterpret_cast<uint2*>(yrow + off * 2) =
+                                make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+                        }
+                    }
+                }
+            }
+            continue;
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int nbase = nw + nb * 32 + 8 * q4;
+                const v16i& a = acc[nb][mb];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int n = min(nbase + r, pb.N - 1);
-                    float v = dequant(av[r], comb, pb.mag, pb.bias, n);
-                    if (SQRELU) {
-                        v = v > 0.0f ? v : 0.0f;
-                        v = __fmul_rn(v, v);
+                    const int n = nbase + r;
+                    if (n >= pb.N) continue;
+                    if (ACC_OUT) acc_out[orow * pb.N + n] = a[4 * q4 + r];
+                    if (y) {
+                        float v = dequant(a[4 * q4 + r], comb, pb.mag, pb.bias, n);
+                        if (SQRELU) {
+                            v = v > 0.0f ? v : 0.0f;
+                            v = __fmul_rn(v, v);
+                        }
+                        store_act<YDT>(y, orow * pb.N + n, v);
                     }
-                    o[r] = v;
-                }
-                if (full) {
-                    if constexpr (YDT == NSOSX_F32) {
-                        *reinterpret_cast<float4*>(static_cast<float*>(y) + orow * pb.N + nbase) =
-                            make_float4(o[0], o[1], o[2], o[3]);
-                    } else {
-                        const uint32_t lo = f32_to_bf16(o[0]) | ((uint32_t)f32_to_bf16(o[1]) << 16);
-                        const uint32_t hi = f32_to_bf16(o[2]) | ((uint32_t)f32_to_bf16(o[3]) << 16);
-                        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + orow * pb.N + nbase) =
-                            make_uint2(lo, hi);
-                    }
-                } else {
-                    for (int r = 0; r < 4; ++r)
-                        if (nbase + r < pb.N) store_act<YDT>(y, orow * pb.N + nbase + r, o[r]);
                 }
             }
         }
@@ -809,6 +1036,39 @@ __global__ __launch_bounds__(kGemm2Threads) void gemm2_kernel(GemmProblem pb, co
     xcd_tile(blockIdx.x, ntn, ntm, nt, mt);
     gemm2_tile<YDT, ACC_OUT, false, false>(pb, q, act_scale, nullptr, 0, M, nt * kBN2, mt * kBM2,
                                            y, acc_out, smem2);
+}
+
+template <int YDT, bool ACC_OUT>
+__global__ __launch_bounds__(kGemm3Threads, 2) void gemm3_kernel(GemmProblem pb,
+                                                                 const int8_t* __restrict__ q,
+                                                                 const float* __restrict__ act_scale,
+                                                                 int M, void* y, int32_t* acc_out) {
+    extern __shared__ __align__(16) char smem3[];
+    const int ntn = (pb.N + kG3BN - 1) / kG3BN;
+    const int ntm = (M + kG3BM - 1) / kG3BM;
+    int nt, mt;
+    xcd_tile(blockIdx.x, ntn, ntm, nt, mt);
+    gemm3_tile<YDT, ACC_OUT, false, false>(pb, q, act_scale, nullptr, 0, M, nt * kG3BN,
+                                           mt * kG3BM, y, acc_out, smem3);
+}
+
+template <int YDT, bool GATHER, bool SQRELU>
+__global__ __launch_bounds__(kGemm3Threads, 2) void grouped_gemm3_kernel(
+    const nsosx_linear_view* views, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ perm, const int8_t* __restrict__ q,
+    const float* __restrict__ act_scale, void* y) {
+    extern __shared__ __align__(16) char smem3[];
+    const int e = blockIdx.z;
+    const int seg_begin = offsets[e];
+    const int seg_rows = offsets[e + 1] - seg_begin;
+    const int m0 = blockIdx.y * kG3BM;
+    if (m0 >= seg_rows) return;
+    const nsosx_linear_view v = views[e];
+    const int n0 = blockIdx.x * kG3BN;
+    if (n0 >= v.outputs) return;
+    GemmProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
+    gemm3_tile<YDT, false, GATHER, SQRELU>(pb, q, act_scale, perm, seg_begin, seg_rows, n0, m0, y,
+                                           nullptr, smem3);
 }
 
 template <int YDT, bool GATHER, bool SQRELU>
@@ -870,6 +1130,16 @@ static void launch_gemm_t(const GemmProblem& pb, const int8_t* q, const float* a
                           void* y, int32_t* acc, hipStream_t st) {
     if (M > kBM) {
         const int tiles = ((pb.N + kBN2 - 1) / kBN2) * ((M + kBM2 - 1) / kBM2);
+        if (pb.K % kG3BK == 0) {
+            const int tiles3 = ((pb.N + kG3BN - 1) / kG3BN) * ((M + kG3BM - 1) / kG3BM);
+            if (acc)
+                hipLaunchKernelGGL((gemm3_kernel<YDT, true>), dim3(tiles3), dim3(kGemm3Threads),
+                                   kGemm3Smem, st, pb, q, as, M, y, acc);
+            else
+                hipLaunchKernelGGL((gemm3_kernel<YDT, false>), dim3(tiles3), dim3(kGemm3Threads),
+                                   kGemm3Smem, st, pb, q, as, M, y, acc);
+            return;
+        }
         if (acc)
             hipLaunchKernelGGL((gemm2_kernel<YDT, true>), dim3(tiles), dim3(kGemm2Threads), kGemm2Smem, st,
                                pb, q, as, M, y, acc);
@@ -1037,11 +1307,15 @@ extern "C" int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, in
     if (!valid_dtype(y_dtype)) return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm: bad dtype");
     if (max_rows_per_expert == 0) return NSOSX_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const dim3 grid((N + kBN2 - 1) / kBN2, (max_rows_per_expert + kBM2 - 1) / kBM2, experts);
-    const dim3 block(kGemm2Threads);
+    const dim3 grid2((N + kBN2 - 1) / kBN2, (max_rows_per_expert + kBM2 - 1) / kBM2, experts);
+    const dim3 grid3((N + kG3BN - 1) / kG3BN, (max_rows_per_expert + kG3BM - 1) / kG3BM, experts);
 #define NSOSX_GGEMM(YDT, G, S)                                                                  \
-    hipLaunchKernelGGL((grouped_gemm2_kernel<YDT, G, S>), grid, block, kGemm2Smem, st, views_dev, \
-                       offsets, perm, q, act_scale, y);
+    if (K % kG3BK == 0)                                                                         \
+        hipLaunchKernelGGL((grouped_gemm3_kernel<YDT, G, S>), grid3, dim3(kGemm3Threads),        \
+                           kGemm3Smem, st, views_dev, offsets, perm, q, act_scale, y);          \
+    else                                                                                        \
+        hipLaunchKernelGGL((grouped_gemm2_kernel<YDT, G, S>), grid2, dim3(kGemm2Threads),        \
+                           kGemm2Smem, st, views_dev, offsets, perm, q, act_scale, y);
     if (y_dtype == NSOSX_F32) {
         if (gather) { if (squared_relu) { NSOSX_GGEMM(NSOSX_F32, true, true) } else { NSOSX_GGEMM(NSOSX_F32, true, false) } }
         else { if (squared_relu) { NSOSX_GGEMM(NSOSX_F32, false, true) } else { NSOSX_GGEMM(NSOSX_F32, false, false) } }
