@@ -242,113 +242,211 @@ struct GemvProblem {
     int K;
 };
 
-// Exact int32 accumulators of the streaming GEMV for K > 4096 rows are summed
-// over chunk rounds before the epilogue: this variant keeps the accumulators
-// of one row step across all rounds (rows outer, chunks inner).
-template <int MT, int YDT, bool ACC_OUT>
-__device__ __forceinline__ void gemv_body_long(const GemvProblem& pb,
+// Decode GEMV.  lpr lanes share a row (a lane takes one 64-weight chunk, 16
+// bytes), so a wave step covers rpw = 64 / lpr rows.  A wave streams blocks of
+// STEPS steps; a lane keeps one partial sum per (step, token row) of the block,
+// and the block's sums are combined by a transpose-reduce over the lpr lanes of
+// a row (each exchange halves the values a lane holds), so a lane ends with
+// complete sums for STEPS / lpr (at least one) of the block's rows.  K > 64*lpr
+// (K > 4096) walks a row in several chunk rounds.
+constexpr int kGemvDepth = 8;   // weight loads in flight per lane
+
+// row steps per block: fewer for more token rows, so the partial sums stay in registers
+template <int MT>
+constexpr int gemv_steps() { return MT <= 2 ? 16 : (MT <= 4 ? 8 : 4); }
+
+// Weight and activation loads of the GEMV are branch-free, so that the
+// compiler counts the loads in flight exactly instead of draining them at every
+// branch.  Out-of-range indices are clamped into the buffers instead: a row
+// past N is computed but never written, and a chunk or word past the row end
+// meets an activation fragment that is zero there.  AL: rows start 16-byte
+// aligned (K % 64 == 0), so a chunk is one 16-byte load; otherwise four dword
+// loads whose word index is clamped to the matrix.
+template <bool AL>
+__device__ __forceinline__ uint4 gemv_load_w(const GemvProblem& pb, int n, int c, int W16) {
+    n = min(n, pb.N - 1);
+    if (AL) {
+        c = min(c, (W16 >> 2) - 1);
+        return load_stream16(pb.packed + (int64_t)n * W16 + c * 4);
+    }
+    const int64_t last = (int64_t)pb.N * W16 - 1;
+    const int64_t base = (int64_t)n * W16 + (int64_t)c * 4;
+    const global_u32* src = (const global_u32*)pb.packed;
+    return make_uint4(src[min(base, last)], src[min(base + 1, last)], src[min(base + 2, last)],
+                      src[min(base + 3, last)]);
+}
+
+// Activation fragment of chunk c (64 values) for token rows 0..MT-1, in the
+// order unpack_word() produces; zero where k >= K.  Rows mi >= M read row M-1
+// (their sums are never written).
+template <int MT>
+__device__ __forceinline__ void gemv_load_x(const int8_t* __restrict__ q, int M, int K, int c,
+                                            uint32_t xa[MT][4][4]) {
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int k = c * 64 + g * 16;
+            const int row = min(mi, M - 1);
+            const uint4 v = *reinterpret_cast<const uint4*>(q + (int64_t)row * K + min(k, K - 16));
+            const uint32_t keep = k < K ? 0xFFFFFFFFu : 0u;
+            const uint32_t d[4] = {v.x & keep, v.y & keep, v.z & keep, v.w & keep};
+            transpose16(d, xa[mi][g]);
+        }
+}
+
+template <int MT>
+__device__ __forceinline__ void gemv_dot(uint4 w, const uint32_t xa[MT][4][4], int acc[MT]) {
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        uint32_t wv[4];
+        unpack_word(ww[g], wv);
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) acc[mi] = sdot4(wv[s], xa[mi][g][s], acc[mi]);
+    }
+}
+
+// Combines a block's partial sums over the lpr lanes of each row and writes the
+// rows.  At offset o, lanes with bit o set keep the upper half of their step
+// values and pass the lower half (the halving levels are unrolled, so every
+// register index is static); offsets left once a lane holds one value are a
+// plain butterfly, and of the lanes holding copies the one with those bits
+// clear writes.
+template <int MT, int STEPS, int YDT, bool ACC_OUT>
+__device__ __forceinline__ void gemv_finish(int (&part)[STEPS][MT], const GemvProblem& pb,
+                                            const float* __restrict__ act_scale, int M, void* y,
+                                            int32_t* acc_out, int lr, int lpr, int sub, int rpw,
+                                            int n_base) {
+    int o = lpr >> 1;
+    int cnt = STEPS;
+    int sidx = 0;
+#pragma unroll
+    for (int L = 0; (STEPS >> (L + 1)) > 0; ++L) {
+        const int half = STEPS >> (L + 1);
+        if (o > 0) {
+            const bool hi = (lr & o) != 0;
+            // bit-mask select: a ternary here is turned into an indexed register read
+            const int hm = hi ? -1 : 0;
+#pragma unroll
+            for (int s = 0; s < half; ++s)
+#pragma unroll
+                for (int mi = 0; mi < MT; ++mi) {
+                    const int lo_v = part[s][mi], hi_v = part[s + half][mi];
+                    const int diff = (lo_v ^ hi_v) & hm;
+                    part[s][mi] = (lo_v ^ diff) + __shfl_xor(hi_v ^ diff, o, kWave);
+                }
+            sidx = (sidx << 1) | (hi ? 1 : 0);
+            cnt = half;
+            o >>= 1;
+        }
+    }
+    const int low_bits = o > 0 ? (lr & ((o << 1) - 1)) : 0;
+    for (; o > 0; o >>= 1)
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi) part[0][mi] += __shfl_xor(part[0][mi], o, kWave);
+    if (low_bits != 0) return;
+    // the lane's values are steps sidx * cnt .. sidx * cnt + cnt - 1 of its sub-row
+#pragma unroll
+    for (int j = 0; j < STEPS; ++j) {
+        if (j < cnt) {
+            const int n = n_base + (sidx * cnt + j) * rpw + sub;
+            if (n < pb.N) {
+#pragma unroll
+                for (int mi = 0; mi < MT; ++mi) {
+                    if (mi < M) {
+                        if (ACC_OUT) acc_out[(int64_t)mi * pb.N + n] = part[j][mi];
+                        if (y) {
+                            const float comb = __fmul_rn(act_scale[mi], pb.ws);
+                            store_act<YDT>(y, (int64_t)mi * pb.N + n,
+                                           dequant(part[j][mi], comb, pb.mag, pb.bias, n));
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// A wave walks its items (row block, chunk round, step) in order and keeps the
+// weight loads of the next D items in flight, across round and block
+// boundaries.  The activation fragment stays in registers while K <= 64 * lpr
+// (one round); longer rows reload it at each round.
+template <int MT, int YDT, bool ACC_OUT, bool AL>
+__device__ __forceinline__ void gemv_body_impl(const GemvProblem& pb,
                                                const int8_t* __restrict__ q,
                                                const float* __restrict__ act_scale, int M,
                                                void* y, int32_t* acc_out, int wave_id,
                                                int num_waves) {
     const int lane = threadIdx.x & 63;
     const int W16 = pb.K >> 4;
-    const int cpr = (W16 + 3) >> 2;
+    const int cpr = (W16 + 3) >> 2;            // 4-word chunks per row
     int lpr = 1;
-    while (lpr < cpr && lpr < 64) lpr <<= 1;
-    const int rpw = 64 / lpr;
+    while (lpr < cpr && lpr < 64) lpr <<= 1;   // lanes per row
+    const int rpw = 64 / lpr;                  // rows per wave step
     const int lr = lane & (lpr - 1);
     const int sub = lane / lpr;
-    const bool aligned16 = (W16 & 3) == 0;
-    const int nsteps = (pb.N + rpw - 1) / rpw;
-    const bool single_round = cpr <= lpr;
+    const int rounds = (cpr + lpr - 1) / lpr;
+    constexpr int STEPS = gemv_steps<MT>();
+    // unaligned rows (rare: K % 64 != 0) keep only two items in flight, as their four
+    // word addresses per item would otherwise raise the register count of the kernel
+    constexpr int DW = AL ? kGemvDepth : 2;
+    constexpr int D = STEPS < DW ? STEPS : DW;
+    const int rows_per_block = STEPS * rpw;
+    const int nblocks = (pb.N + rows_per_block - 1) / rows_per_block;
+    if (wave_id >= nblocks) return;
 
-    // X fragments of the first (often only) chunk round stay in registers
     uint32_t xa[MT][4][4];
-    {
-        const int c = lr;
+    gemv_load_x<MT>(q, M, pb.K, lr, xa);
+    uint4 ring[D];
 #pragma unroll
-        for (int mi = 0; mi < MT; ++mi)
+    for (int d = 0; d < D; ++d)
+        ring[d] = gemv_load_w<AL>(pb, (wave_id * STEPS + d) * rpw + sub, lr, W16);
+    for (int blk = wave_id; blk < nblocks; blk += num_waves) {
+        int part[STEPS][MT];
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                uint32_t d[4] = {0u, 0u, 0u, 0u};
-                const int k = c * 64 + g * 16;
-                if (c < cpr && mi < M && k < pb.K) {
-                    const uint4 v = *reinterpret_cast<const uint4*>(q + (int64_t)mi * pb.K + k);
-                    d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-                }
-                transpose16(d, xa[mi][g]);
+        for (int s = 0; s < STEPS; ++s)
+#pragma unroll
+            for (int mi = 0; mi < MT; ++mi) part[s][mi] = 0;
+        for (int r = 0; r < rounds; ++r) {
+            if (rounds > 1 && (r > 0 || blk != wave_id)) gemv_load_x<MT>(q, M, pb.K, r * lpr + lr, xa);
+            // the item D ahead of step s lies in this round, the next round of this
+            // block, or round 0 of the wave's next block
+            const bool last_round = r + 1 == rounds;
+            const int nb_next = last_round ? blk + num_waves : blk;
+            const int c_next = (last_round ? 0 : r + 1) * lpr + lr;
+            const int c_cur = r * lpr + lr;
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                const uint4 cur = ring[s % D];
+                const int s2 = s + D;
+                if (s2 < STEPS)
+                    ring[s % D] = gemv_load_w<AL>(pb, (blk * STEPS + s2) * rpw + sub, c_cur, W16);
+                else
+                    ring[s % D] = gemv_load_w<AL>(pb, (nb_next * STEPS + s2 - STEPS) * rpw + sub,
+                                                  c_next, W16);
+                gemv_dot<MT>(cur, xa, part[s]);
             }
+        }
+        gemv_finish<MT, STEPS, YDT, ACC_OUT>(part, pb, act_scale, M, y, acc_out, lr, lpr, sub,
+                                             rpw, blk * rows_per_block);
     }
+}
 
-    for (int step = wave_id; step < nsteps; step += num_waves) {
-        const int n = step * rpw + sub;
-        int acc[MT];
-#pragma unroll
-        for (int mi = 0; mi < MT; ++mi) acc[mi] = 0;
-        for (int c = lr; c < cpr; c += lpr) {
-            uint32_t w[4] = {0x55555555u, 0x55555555u, 0x55555555u, 0x55555555u};
-            if (n < pb.N) {
-                const uint32_t* src = pb.packed + (int64_t)n * W16 + c * 4;
-                if (aligned16 && c * 4 + 3 < W16) {
-                    const uint4 v = load_stream16(src);
-                    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (c * 4 + i < W16) w[i] = src[i];
-                }
-            }
-            uint32_t xr[MT][4][4];
-            if (single_round || c == lr) {
-#pragma unroll
-                for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-                    for (int g = 0; g < 4; ++g)
-#pragma unroll
-                        for (int s = 0; s < 4; ++s) xr[mi][g][s] = xa[mi][g][s];
-            } else {
-#pragma unroll
-                for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        uint32_t d[4] = {0u, 0u, 0u, 0u};
-                        const int k = c * 64 + g * 16;
-                        if (mi < M && k < pb.K) {
-                            const uint4 v =
-                                *reinterpret_cast<const uint4*>(q + (int64_t)mi * pb.K + k);
-                            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-                        }
-                        transpose16(d, xr[mi][g]);
-                    }
-            }
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                uint32_t wv[4];
-                unpack_word(w[g], wv);
-#pragma unroll
-                for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) acc[mi] = sdot4(wv[s], xr[mi][g][s], acc[mi]);
-            }
-        }
-#pragma unroll
-        for (int mi = 0; mi < MT; ++mi)
-            for (int o = lpr >> 1; o > 0; o >>= 1) acc[mi] += __shfl_xor(acc[mi], o, kWave);
-        if (lr == 0 && n < pb.N) {
-#pragma unroll
-            for (int mi = 0; mi < MT; ++mi) {
-                if (mi < M) {
-                    if (ACC_OUT) acc_out[(int64_t)mi * pb.N + n] = acc[mi];
-                    if (y) {
-                        const float comb = __fmul_rn(act_scale[mi], pb.ws);
-                        store_act<YDT>(y, (int64_t)mi * pb.N + n,
-                                       dequant(acc[mi], comb, pb.mag, pb.bias, n));
-                    }
-                }
-            }
-        }
-    }
+template <int MT, int YDT, bool ACC_OUT>
+__device__ __forceinline__ void gemv_body_long(const GemvProblem& pb,
+                                               const int8_t* __restrict__ q,
+                                               const float* __restrict__ act_scale, int M,
+                                               void* y, int32_t* acc_out, int wave_id,
+                                               int num_waves) {
+    if ((pb.K & 63) == 0)
+        gemv_body_impl<MT, YDT, ACC_OUT, true>(pb, q, act_scale, M, y, acc_out, wave_id,
+                                               num_waves);
+    else
+        gemv_body_impl<MT, YDT, ACC_OUT, false>(pb, q, act_scale, M, y, acc_out, wave_id,
+                                                num_waves);
 }
 
 template <int MT, int YDT, bool ACC_OUT>
@@ -377,22 +475,27 @@ __global__ __launch_bounds__(256) void grouped_gemv_kernel(const nsosx_linear_vi
                                    nullptr, wave_id, num_waves);
 }
 
-static int gemv_grid(int N, int K) {
+static int gemv_steps_host(int M) { return M <= 2 ? 16 : (M <= 4 ? 8 : 4); }
+
+static int gemv_blocks(int N, int K, int M) {
     const int W16 = K / 16;
     const int cpr = (W16 + 3) / 4;
     int lpr = 1;
     while (lpr < cpr && lpr < 64) lpr <<= 1;
-    const int rpw = 64 / lpr;
-    const int nsteps = (N + rpw - 1) / rpw;
-    // one wave step per wave, up to 8 resident waves per CU on 256 CUs
-    int waves = std::min(nsteps, 256 * 8);
+    const int rows = gemv_steps_host(M) * (64 / lpr);
+    return (N + rows - 1) / rows;
+}
+
+static int gemv_grid(int N, int K, int M) {
+    // one row block per wave, up to 8 resident waves per CU on 256 CUs
+    const int waves = std::min(gemv_blocks(N, K, M), 256 * 8);
     return std::max(1, (waves + 3) / 4);
 }
 
 template <int YDT>
 static void launch_gemv_t(const GemvProblem& pb, const int8_t* q, const float* as, int M,
                           void* y, int32_t* acc, hipStream_t st) {
-    const dim3 grid(gemv_grid(pb.N, pb.K)), block(256);
+    const dim3 grid(gemv_grid(pb.N, pb.K, M)), block(256);
 #define NSOSX_GEMV(MT)                                                                       \
     if (acc)                                                                                 \
         hipLaunchKernelGGL((gemv_kernel<MT, YDT, true>), grid, block, 0, st, pb, q, as, M, y, \
@@ -1277,9 +1380,11 @@ extern "C" int nsosx_grouped_gemv(const nsosx_linear_view* views_dev, int groups
         return fail(NSOSX_ERR_INVALID, "grouped_gemv: groups in [1, 65535], M in [1, 8]");
     if (!valid_dtype(y_dtype)) return fail(NSOSX_ERR_INVALID, "grouped_gemv: bad dtype");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // the grid is sized from the first view's shape read back by the caller's contract:
-    // all views share `inputs`; outputs may differ and each wave strides its own rows
-    const dim3 grid(256 * 2, groups), block(256);
+    // view shapes live on the device, so the grid is sized from the group count alone:
+    // about 2048 workgroups in all (the resident limit at 8 waves per SIMD), and each
+    // wave strides over its view's row blocks
+    const int per_group = std::max(4, std::min(512, 2048 / groups));
+    const dim3 grid(per_group, groups), block(256);
 #define NSOSX_GG(MT)                                                                          \
     if (y_dtype == NSOSX_F32)                                                                 \
         hipLaunchKernelGGL((grouped_gemv_kernel<MT, NSOSX_F32>), grid, block, 0, st, views_dev, \

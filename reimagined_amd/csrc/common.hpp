@@ -115,10 +115,14 @@ __device__ __forceinline__ void transpose16(const uint32_t d[4], uint32_t e[4]) 
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
+typedef __attribute__((address_space(1))) const uint32_t global_u32;
 
 // 16-byte streaming load that is not expected to be reused (weights of a GEMV).
+// The pointer is taken as global memory: a flat load would also count against
+// the LDS/scalar wait counter, so every LDS or shuffle wait would drain it.
 __device__ __forceinline__ uint4 load_stream16(const uint32_t* p) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    const u32x4 v = __builtin_nontemporal_load((global_u32x4*)(p));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 

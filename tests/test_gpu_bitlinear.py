@@ -80,7 +80,9 @@ def _gemm_case(dev, orc, m, n, k, path, mag=False, bias=False, seed=0):
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8])
-@pytest.mark.parametrize("n,k", [(768, 768), (130, 2048), (64, 48), (33, 4096), (40, 8192)])
+@pytest.mark.parametrize("n,k", [(768, 768), (130, 2048), (64, 48), (33, 4096), (40, 8192),
+                                 (1000, 256), (300, 128), (9000, 2048), (70, 12288),
+                                 (37, 1040)])
 def test_gemv_bit_exact(dev, orc, m, n, k):
     _gemm_case(dev, orc, m, n, k, path=0, mag=(m % 2 == 0), bias=(m % 3 == 0))
 
