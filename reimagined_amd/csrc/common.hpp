@@ -60,6 +60,26 @@ __device__ __forceinline__ float load_act(const void* p, int64_t i) {
     }
 }
 
+// Raw storage word of an activation element: kept unconverted in registers, a
+// prefetched value costs no wait until raw_to_f32() is applied where it is used.
+template <int DT> struct raw_word { using type = uint32_t; };
+template <> struct raw_word<NSOSX_BF16> { using type = uint16_t; };
+
+template <int DT>
+__device__ __forceinline__ typename raw_word<DT>::type load_raw(const void* p, int64_t i) {
+    using T = typename raw_word<DT>::type;
+    return ((const __attribute__((address_space(1))) T*)(p))[i];
+}
+
+template <int DT>
+__device__ __forceinline__ float raw_to_f32(typename raw_word<DT>::type u) {
+    if constexpr (DT == NSOSX_F32) {
+        return __uint_as_float(u);
+    } else {
+        return __uint_as_float(static_cast<uint32_t>(u) << 16);
+    }
+}
+
 template <int DT>
 __device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
     if constexpr (DT == NSOSX_F32) {

@@ -285,6 +285,303 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
     }
 }
 
+// ===========================================================================
+// Prefill scan, quad form (N <= 16, conv width <= 4).  A workgroup is one
+// wave: 16 channels x 4 state quads, lane = 4 * channel + quad, each lane
+// holding SPL = N/4 (rounded up) states in registers.  The wave walks its
+// sequence in groups of 4 tokens.  Lane q of a channel forms the
+// per-(token, channel) terms of token r0 + q only: the causal convolution
+// (its window gathered from the quad's and the previous group's raw inputs by
+// DPP), bias + SiLU, delta = softplus(dt) and delta * x; DPP broadcasts then
+// hand every lane all four tokens' terms.  The recurrence runs the four
+// tokens, the 4x4 transpose-reduce leaves lane q with the readout of token
+// r0 + q, and lane q applies the D skip and the SiLU(z) gate and stores it.
+// B and C (shared by all channels of a group) are staged per 32-token chunk
+// in the wave's own LDS slice, converted to float once.  There is no
+// workgroup barrier: the raw inputs of the next group and the B/C rows of the
+// next chunk are loaded into registers one step ahead.
+// ===========================================================================
+constexpr int kQuadTC = 32;       // tokens per B/C chunk
+constexpr int kQuadCh = 16;       // channels per wave
+constexpr int kQuadMaxW = 4;
+
+__device__ __forceinline__ float quad_bcast(float v, int k) {
+    // quad_perm [k, k, k, k]
+    switch (k) {
+        case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x00, 0xF, 0xF, true));
+        case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x55, 0xF, 0xF, true));
+        case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xAA, 0xF, 0xF, true));
+        default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xFF, 0xF, 0xF, true));
+    }
+}
+
+// lane q reads lane (q - d) mod 4 of its quad: quad_perm [(0-d)&3, (1-d)&3, (2-d)&3, (3-d)&3]
+__device__ __forceinline__ float quad_back(float v, int d) {
+    switch (d) {
+        case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x93, 0xF, 0xF, true));
+        case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
+        default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x39, 0xF, 0xF, true));
+    }
+}
+
+// Sequence for this workgroup: the blockIdx.y-th longest (ties by index).
+__device__ __forceinline__ int quad_pick_sequence(const int32_t* cu, int num_seqs, int T,
+                                                  int* s_pick) {
+    if (num_seqs > kOrderMax) return blockIdx.y;
+    for (int i = threadIdx.x; i < num_seqs; i += 64) {
+        const int a = min(max(cu[i], 0), T);
+        const int li = min(max(cu[i + 1], a), T) - a;
+        int rank = 0;
+        for (int k = 0; k < num_seqs; ++k) {
+            const int b = min(max(cu[k], 0), T);
+            const int lk = min(max(cu[k + 1], b), T) - b;
+            rank += (lk > li) || (lk == li && k < i);
+        }
+        if (rank == (int)blockIdx.y) *s_pick = i;
+    }
+    __syncthreads();
+    return *s_pick;
+}
+
+// softplus_fast() without branches: the three regimes are formed and selected.
+__device__ __forceinline__ float softplus_sel(float v) {
+    const float e = exp_native(v);
+    const float u = 1.0f + e;
+    const float mid = __builtin_amdgcn_logf(u) * 0.6931471805599453f * (e * __builtin_amdgcn_rcpf(u - 1.0f));
+    return v > 20.0f ? v : (u == 1.0f ? e : mid);
+}
+
+template <int ADT, int SPL, bool GATE, bool CONV>
+__global__ __launch_bounds__(64) void scan_quad_kernel(
+    const void* __restrict__ x, int64_t x_stride, const void* __restrict__ dt,
+    const float* __restrict__ a_log, int a_per_state, const void* __restrict__ Bm,
+    const void* __restrict__ Cm, const float* __restrict__ Dskip, const void* __restrict__ z,
+    int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int num_seqs, int total_tokens,
+    int H, int P, int N, int G, const float* __restrict__ conv_w, const float* __restrict__ conv_b,
+    int W, const float* __restrict__ init_state, float* __restrict__ final_state,
+    void* __restrict__ y) {
+    using raw_t = typename raw_word<ADT>::type;
+    constexpr int NP = 4 * SPL;                 // padded states per channel
+    constexpr int BCN = NP / 2;                 // states per staging lane (two lanes per row)
+    __shared__ __align__(16) float s_bc[2][kQuadTC][NP];
+    __shared__ int s_pick;
+
+    const int lane = threadIdx.x;
+    const int D = H * P;
+    const int GN = G * N;
+    const int q = lane & 3;
+    const int c = blockIdx.x * kQuadCh + (lane >> 2);
+    const int h = c / P;
+    const int grp = (h * G) / H;
+    const int seq = quad_pick_sequence(cu_seqlens, num_seqs, total_tokens, &s_pick);
+    const int t0 = min(max(cu_seqlens[seq], 0), total_tokens);
+    const int t1 = min(max(cu_seqlens[seq + 1], t0), total_tokens);
+    const int tlast = total_tokens - 1;
+    const float dsk = Dskip[h];
+
+    // conv taps right-aligned in kQuadMaxW slots: a width-W filter is the 4-tap
+    // filter with leading zero taps, and fma(0, x, 0) leaves the sum at +0
+    float cw[kQuadMaxW], cb = 0.0f;
+    if (CONV) {
+#pragma unroll
+        for (int j = 0; j < kQuadMaxW; ++j) {
+            const int jw = j - (kQuadMaxW - W);
+            cw[j] = jw >= 0 ? conv_w[(int64_t)c * W + jw] : 0.0f;
+        }
+        if (conv_b) cb = conv_b[c];
+    }
+    float a2[SPL], st[SPL];
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) {
+        const int n = q * SPL + i;
+        const bool ok = n < N;
+        const float al = a_per_state ? a_log[(int64_t)h * N + min(n, N - 1)] : a_log[h];
+        a2[i] = ok ? a2_from_log(al) : 0.0f;
+        st[i] = (ok && init_state) ? init_state[((int64_t)seq * D + c) * N + n] : 0.0f;
+    }
+
+    // Loads are branch-free: indices past the data are clamped to the last row and
+    // the values masked where they are used, so the compiler keeps the loads in
+    // flight across a whole group (element indices fit in 32 bits; the host checks).
+    // B/C staging role: lanes 0-31 stage B, 32-63 stage C; two lanes per chunk row
+    // (rows srow and srow + 16), each converting half of the row's states.
+    const int sm = lane >> 5;
+    const int srow = (lane & 31) >> 1;
+    const int shalf = lane & 1;
+    const void* smat = sm ? Cm : Bm;
+    const bool bc_vec = (SPL == 4) && N == 16 && (GN % 8) == 0 &&
+                        ((reinterpret_cast<uintptr_t>(Bm) | reinterpret_cast<uintptr_t>(Cm)) & 15) == 0;
+    constexpr int BCW = ADT == NSOSX_F32 ? BCN : (BCN + 1) / 2;  // dwords per lane per row
+    uint32_t bcv[2][BCW > 0 ? BCW : 1];
+    raw_t bcs[2][BCN];
+    int bc_ok = 0;
+    auto prefetch_bc = [&](int tb) {
+        bc_ok = 0;
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+            const int t = tb + srow + 16 * pass;
+            bc_ok |= (t < t1 ? 1 : 0) << pass;
+            const int base = min(t, tlast) * GN + grp * N + shalf * BCN;
+            if (bc_vec) {
+                const global_u32x4* src;
+                if (ADT == NSOSX_F32) {
+                    src = (const global_u32x4*)((const float*)smat + base);
+#pragma unroll
+                    for (int w4 = 0; w4 < BCW / 4; ++w4) {
+                        const u32x4 v = src[w4];
+                        bcv[pass][4 * w4 + 0] = v.x; bcv[pass][4 * w4 + 1] = v.y;
+                        bcv[pass][4 * w4 + 2] = v.z; bcv[pass][4 * w4 + 3] = v.w;
+                    }
+                } else {
+                    src = (const global_u32x4*)((const uint16_t*)smat + base);
+                    const u32x4 v = src[0];
+                    bcv[pass][0] = v.x; bcv[pass][1] = v.y; bcv[pass][2] = v.z; bcv[pass][3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < BCN; ++j) {
+                    const int n = shalf * BCN + j;
+                    bcs[pass][j] = load_raw<ADT>(smat, n < N ? base + j : 0);
+                }
+            }
+        }
+    };
+    auto stage_bc = [&]() {
+#pragma unroll
+        for (int pass = 0; pass < 2; ++pass) {
+            const bool ok = (bc_ok >> pass) & 1;
+            float v[BCN];
+            if (bc_vec) {
+#pragma unroll
+                for (int j = 0; j < BCN; ++j) {
+                    if (ADT == NSOSX_F32) {
+                        v[j] = __uint_as_float(bcv[pass][j]);
+                    } else {
+                        const uint32_t wd = bcv[pass][j >> 1];
+                        v[j] = __uint_as_float((j & 1) ? (wd & 0xFFFF0000u) : (wd << 16));
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < BCN; ++j) {
+                    const int n = shalf * BCN + j;
+                    v[j] = n < N ? raw_to_f32<ADT>(bcs[pass][j]) : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < BCN; ++j) s_bc[sm][srow + 16 * pass][shalf * BCN + j] = ok ? v[j] : 0.0f;
+        }
+    };
+
+    // per-lane token stream: element indices of the next group's token (running,
+    // clamped at use), raw words one group ahead
+    const int xs = static_cast<int>(x_stride), zs = static_cast<int>(z_stride);
+    const int ix_max = tlast * xs + c, idt_max = tlast * H + h, iz_max = tlast * zs + c;
+    int ix = (t0 + q) * xs + c, idt = (t0 + q) * H + h, iz = (t0 + q) * zs + c;
+    int iy = (t0 + q) * D + c;
+    raw_t xr = 0, dtr = 0, zr = 0;
+    auto prefetch_tok = [&]() {
+        xr = load_raw<ADT>(x, min(ix, ix_max));
+        dtr = load_raw<ADT>(dt, min(idt, idt_max));
+        if (GATE) zr = load_raw<ADT>(z, min(iz, iz_max));
+        ix += 4 * xs;
+        idt += 4 * H;
+        iz += 4 * zs;
+    };
+
+    float xprev = 0.0f;  // raw x of this lane's token in the previous group (0 before t0)
+    if (t0 < t1) {
+        prefetch_bc(t0);
+        prefetch_tok();
+    }
+    for (int tb = t0; tb < t1; tb += kQuadTC) {
+        __syncthreads();  // the previous chunk's B/C reads are done
+        stage_bc();
+        if (tb + kQuadTC < t1) prefetch_bc(tb + kQuadTC);
+        __syncthreads();
+        const int tc = min(kQuadTC, t1 - tb);
+        for (int r0 = 0; r0 < tc; r0 += 4) {
+            const int tg = tb + r0 + q;
+            const bool valid = tg < t1;
+            const float xcur = valid ? raw_to_f32<ADT>(xr) : 0.0f;
+            const float dtcur = raw_to_f32<ADT>(dtr);
+            const raw_t zraw = zr;
+            prefetch_tok();
+            // ---- per-(token, channel) terms of token tg ---------------------------
+            float xv;
+            if (CONV) {
+                // tap j multiplies x[tg - 3 + j]: lag d = 3 - j, from this group (lane
+                // q - d) when d <= q, else from the previous group (lane q - d + 4)
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < kQuadMaxW; ++j) {
+                    const int d = kQuadMaxW - 1 - j;
+                    float xl = xcur;
+                    if (d > 0) {
+                        const float fc = quad_back(xcur, d);
+                        const float fp = quad_back(xprev, d);
+                        xl = q >= d ? fc : fp;
+                    }
+                    acc = __fmaf_rn(cw[j], xl, acc);
+                }
+                xv = valid ? silu_fast(acc + cb) : 0.0f;
+            } else {
+                xv = xcur;
+            }
+            xprev = xcur;
+            const float dl = valid ? softplus_sel(dtcur) : 0.0f;
+            const float dx = dl * xv;
+            // ---- recurrence over the group's four tokens --------------------------
+            float part[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float dlk = quad_bcast(dl, k);
+                const float dxk = quad_bcast(dx, k);
+                const int r = r0 + k;  // rows past tc: delta = 0 keeps the state
+                float bq[SPL], cq[SPL];
+#pragma unroll
+                for (int i = 0; i < SPL; ++i) {
+                    bq[i] = s_bc[0][r][q * SPL + i];
+                    cq[i] = s_bc[1][r][q * SPL + i];
+                }
+                float p = 0.0f;
+#pragma unroll
+                for (int i = 0; i < SPL; ++i) {
+                    const float a = __builtin_amdgcn_exp2f(dlk * a2[i]);
+                    st[i] = __fmaf_rn(a, st[i], dxk * bq[i]);
+                    p = __fmaf_rn(st[i], cq[i], p);
+                }
+                part[k] = p;
+            }
+            // ---- 4x4 transpose-reduce: lane q ends with token r0 + q --------------
+            const bool hi2 = (q & 2) != 0;
+            const float s0 = hi2 ? part[0] : part[2];
+            const float s1 = hi2 ? part[1] : part[3];
+            const float k0 = hi2 ? part[2] : part[0];
+            const float k1 = hi2 ? part[3] : part[1];
+            const float m0 = k0 + dpp_xor2(s0);
+            const float m1 = k1 + dpp_xor2(s1);
+            const bool hi1 = (q & 1) != 0;
+            const float send = hi1 ? m0 : m1;
+            const float keep = hi1 ? m1 : m0;
+            const float tot = keep + dpp_xor1(send);
+            if (valid) {
+                float out = __fmaf_rn(dsk, xv, tot);
+                if (GATE) out = out * silu_fast(raw_to_f32<ADT>(zraw));
+                store_act<ADT>(y, iy, out);
+            }
+            iy += 4 * D;
+        }
+    }
+    if (final_state) {
+#pragma unroll
+        for (int i = 0; i < SPL; ++i) {
+            const int n = q * SPL + i;
+            if (n < N) final_state[((int64_t)seq * D + c) * N + n] = st[i];
+        }
+    }
+}
+
 // Any shape: one lane per (sequence, channel), states in a loop, in the
 // reference's own order of operations.
 template <int ADT>
@@ -445,10 +742,40 @@ static int scan_fwd_launch(const void* x, int64_t x_stride, const void* dt, cons
     const bool conv = conv_w != nullptr;
     if (conv && (conv_width <= 0 || conv_width > kMaxConvW))
         return fail(NSOSX_ERR_INVALID, "conv_scan_fwd: conv width must be in [1, 8]");
-    if (conv && per_group % kScanCh != 0)
-        return fail(NSOSX_ERR_INVALID, "conv_scan_fwd: channels per group must be a multiple of 64");
+    if (conv && !(per_group % kScanCh == 0 ||
+                  (N <= 16 && per_group % kQuadCh == 0 && conv_width <= kQuadMaxW)))
+        return fail(NSOSX_ERR_INVALID,
+                    "conv_scan_fwd: channels per group must be a multiple of 64 (or of 16 with "
+                    "N <= 16 and conv width <= 4)");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (per_group % kScanCh == 0) {
+    // the quad kernel indexes rows with 32-bit element offsets
+    const int64_t max_row = std::max<int64_t>(std::max<int64_t>(x_stride, z ? z_stride : 0),
+                                              std::max<int64_t>(Dm, (int64_t)G * N));
+    const bool idx32 = (int64_t)(total_tokens + 8) * max_row < ((int64_t)1 << 31);
+    if (N <= 16 && per_group % kQuadCh == 0 && (!conv || conv_width <= kQuadMaxW) && idx32) {
+        const dim3 grid(Dm / kQuadCh, num_seqs), block(64);
+        const int spl = N <= 4 ? 1 : N <= 8 ? 2 : 4;
+#define NSOSX_QSCAN(ADT, SPL, GATE, CONV)                                                        \
+    hipLaunchKernelGGL((scan_quad_kernel<ADT, SPL, GATE, CONV>), grid, block, 0, st, x, x_stride, \
+                       dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens, num_seqs,       \
+                       total_tokens, H, P, N, G, conv_w, conv_b, conv_width, initial_state,      \
+                       final_state, y);
+#define NSOSX_QSCAN_C(ADT, SPL, GATE) \
+    if (conv) { NSOSX_QSCAN(ADT, SPL, GATE, true) } else { NSOSX_QSCAN(ADT, SPL, GATE, false) }
+#define NSOSX_QSCAN_G(ADT, SPL) \
+    if (z) { NSOSX_QSCAN_C(ADT, SPL, true) } else { NSOSX_QSCAN_C(ADT, SPL, false) }
+#define NSOSX_QSCAN_S(ADT)                          \
+    switch (spl) {                                  \
+        case 1: NSOSX_QSCAN_G(ADT, 1) break;        \
+        case 2: NSOSX_QSCAN_G(ADT, 2) break;        \
+        default: NSOSX_QSCAN_G(ADT, 4) break;       \
+    }
+        if (act_dtype == NSOSX_F32) { NSOSX_QSCAN_S(NSOSX_F32) } else { NSOSX_QSCAN_S(NSOSX_BF16) }
+#undef NSOSX_QSCAN_S
+#undef NSOSX_QSCAN_G
+#undef NSOSX_QSCAN_C
+#undef NSOSX_QSCAN
+    } else if (per_group % kScanCh == 0) {
         const dim3 grid(Dm / kScanCh, num_seqs), block(256);
         const int spl = N <= 4 ? 1 : N <= 8 ? 2 : N <= 16 ? 4 : N <= 32 ? 8 : 16;
 #define NSOSX_SCAN(ADT, SPL, GATE, CONV)                                                        \

@@ -59,6 +59,10 @@ def _run(dev, orc, inp, cu, H, P, N, G, gate=True, init=None, dtype=torch.float3
     (2, 64, 16, 1, False, [40, 7]),               # reference faithful: per-head A, P = 64
     (64, 1, 8, 1, True, [17]),                    # N = 8
     (4, 32, 16, 2, False, [9, 30]),               # G = 2, one group per workgroup
+    (32, 1, 4, 1, True, [9, 22]),                 # N = 4: one state per lane
+    (16, 2, 16, 2, False, [18, 5]),               # 16 channels per group
+    (64, 1, 32, 1, True, [37, 5]),                # N = 32 -> LDS-staged kernel
+    (128, 1, 64, 2, True, [6, 19]),               # N = 64, G = 2 -> LDS-staged kernel
     (6, 1, 5, 1, True, [11, 3]),                  # D = 6, N = 5 -> generic kernel
     (6, 2, 4, 3, False, [8, 2, 5]),               # 4 channels per group -> generic kernel
 ])
@@ -163,12 +167,18 @@ def test_scan_rejects_float_cu_seqlens(dev):
                                torch.tensor([0.0, 4.0], device=dev), 64, 1, 16, 1)
 
 
-@pytest.mark.parametrize("dtype,lengths", [(torch.float32, [5, 64, 1, 33]),
-                                           (torch.bfloat16, [200, 3, 77])])
-def test_conv_scan_fused_matches_oracle(dev, orc, dtype, lengths):
+@pytest.mark.parametrize("dtype,lengths,H,N,W", [
+    (torch.float32, [5, 64, 1, 33], 128, 16, 4),
+    (torch.bfloat16, [200, 3, 77], 128, 16, 4),
+    (torch.float32, [2, 31, 6], 48, 16, 3),      # 48 channels: 16-channel waves only
+    (torch.float32, [1, 9, 40], 64, 8, 2),
+    (torch.float32, [7, 50], 64, 16, 6),        # width 6 -> LDS-staged kernel
+    (torch.float32, [3, 26], 64, 32, 4),        # N = 32 -> LDS-staged kernel
+])
+def test_conv_scan_fused_matches_oracle(dev, orc, dtype, lengths, H, N, W):
     """conv + bias + SiLU fused into the scan == oracle conv, then oracle scan."""
-    rng = np.random.default_rng(len(lengths))
-    H, P, N, G, W = 128, 1, 16, 1, 4
+    rng = np.random.default_rng(len(lengths) + H + W)
+    P, G = 1, 1
     cu = _cu(lengths)
     T = int(cu[-1])
     inp = _inputs(rng, T, H, P, N, G)
