@@ -481,9 +481,9 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
     int iy = (t0 + q) * D + c;
     raw_t xr = 0, dtr = 0, zr = 0;
     auto prefetch_tok = [&]() {
-        xr = load_raw<ADT>(x, min(ix, ix_max));
-        dtr = load_raw<ADT>(dt, min(idt, idt_max));
-        if (GATE) zr = load_raw<ADT>(z, min(iz, iz_max));
+        xr = load_raw<ADT>(x, (uint32_t)min(ix, ix_max));
+        dtr = load_raw<ADT>(dt, (uint32_t)min(idt, idt_max));
+        if (GATE) zr = load_raw<ADT>(z, (uint32_t)min(iz, iz_max));
         ix += 4 * xs;
         idt += 4 * H;
         iz += 4 * zs;
@@ -503,11 +503,22 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
         for (int r0 = 0; r0 < tc; r0 += 4) {
             const int tg = tb + r0 + q;
             const bool valid = tg < t1;
+            // B/C of the group's four rows first: the reads overlap the staging math
+            // (rows past tc were staged as zero; delta = 0 keeps the state there)
+            float bq[4][SPL], cq[4][SPL];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int i = 0; i < SPL; ++i) {
+                    bq[k][i] = s_bc[0][r0 + k][q * SPL + i];
+                    cq[k][i] = s_bc[1][r0 + k][q * SPL + i];
+                }
             const float xcur = valid ? raw_to_f32<ADT>(xr) : 0.0f;
             const float dtcur = raw_to_f32<ADT>(dtr);
             const raw_t zraw = zr;
             prefetch_tok();
-            // ---- per-(token, channel) terms of token tg ---------------------------
+            // ---- per-(token, channel) terms of token tg (formed unconditionally and
+            // masked, so the group has no divergent branch) -------------------------
             float xv;
             if (CONV) {
                 // tap j multiplies x[tg - 3 + j]: lag d = 3 - j, from this group (lane
@@ -524,32 +535,31 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
                     }
                     acc = __fmaf_rn(cw[j], xl, acc);
                 }
-                xv = valid ? silu_fast(acc + cb) : 0.0f;
+                const float sx = silu_fast(acc + cb);
+                xv = valid ? sx : 0.0f;
             } else {
                 xv = xcur;
             }
             xprev = xcur;
-            const float dl = valid ? softplus_sel(dtcur) : 0.0f;
+            const float sp = softplus_sel(dtcur);
+            const float dl = valid ? sp : 0.0f;
             const float dx = dl * xv;
-            // ---- recurrence over the group's four tokens --------------------------
+            // ---- recurrence over the group's four tokens: all decays first --------
+            // (each broadcast is folded into its multiply as a DPP operand)
+            float a[4][SPL];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int i = 0; i < SPL; ++i)
+                    a[k][i] = __builtin_amdgcn_exp2f(quad_bcast(dl, k) * a2[i]);
             float part[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const float dlk = quad_bcast(dl, k);
-                const float dxk = quad_bcast(dx, k);
-                const int r = r0 + k;  // rows past tc: delta = 0 keeps the state
-                float bq[SPL], cq[SPL];
-#pragma unroll
-                for (int i = 0; i < SPL; ++i) {
-                    bq[i] = s_bc[0][r][q * SPL + i];
-                    cq[i] = s_bc[1][r][q * SPL + i];
-                }
                 float p = 0.0f;
 #pragma unroll
                 for (int i = 0; i < SPL; ++i) {
-                    const float a = __builtin_amdgcn_exp2f(dlk * a2[i]);
-                    st[i] = __fmaf_rn(a, st[i], dxk * bq[i]);
-                    p = __fmaf_rn(st[i], cq[i], p);
+                    st[i] = __fmaf_rn(a[k][i], st[i], quad_bcast(dx, k) * bq[k][i]);
+                    p = __fmaf_rn(st[i], cq[k][i], p);
                 }
                 part[k] = p;
             }
@@ -568,7 +578,7 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
             if (valid) {
                 float out = __fmaf_rn(dsk, xv, tot);
                 if (GATE) out = out * silu_fast(raw_to_f32<ADT>(zraw));
-                store_act<ADT>(y, iy, out);
+                store_act<ADT>(y, (uint32_t)iy, out);
             }
             iy += 4 * D;
         }
