@@ -238,6 +238,35 @@ int nsosx_moe_combine(const void* expert_out, int in_dtype, const int32_t* slot_
                       const int32_t* selected, const float* weights, int rows, int experts, int k,
                       int dim, void* out, int out_dtype, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Row norms of the hybrid block and the decode conv ring.
+ * ------------------------------------------------------------------------- */
+
+/* Gated RMSNorm epilogue RMSNorm(y * SiLU(z)) * gamma (src/mamba2.cpp:2677-2680,
+ * launch_mamba_gated_rmsnorm src/cuda/mamba_kernels.cu:3421-3445); with z NULL
+ * it is Tensor::rmsnorm (src/tensor.cpp:3455-3492) times gamma; gamma NULL is
+ * a unit weight.  y, z: [rows, dim] (act_dtype); out: [rows, dim] (out_dtype).
+ * The sum of squares is reduced in fp32 across the row in tree order. */
+int nsosx_rmsnorm_gated(const void* y, const void* z, const float* gamma, int rows, int dim,
+                        float eps, int act_dtype, void* out, int out_dtype, void* stream);
+
+/* Residual add and the next block norm of JambaBlock::forward
+ * (src/jamba.cpp:3253, 3286-3290, 3316): residual_out = x + delta (act_dtype);
+ * when norm_out is not NULL, norm_out = rmsnorm(residual_out, eps) * gamma
+ * (gamma NULL = unit).  All buffers [rows, dim]. */
+int nsosx_add_rmsnorm(const void* x, const void* delta, const float* gamma, int rows, int dim,
+                      float eps, int act_dtype, void* residual_out, void* norm_out, void* stream);
+
+/* Decode conv ring step, the role of launch_mamba2_faithful_conv_step
+ * (src/cuda/mamba_kernels.cu:3332-3374; CPU src/mamba2.cpp:4072-4090):
+ *   v = bias[c] + sum_{j<W} w[c,j] * (j < W-1 ? ring[r][j][c] : x[r,c])
+ *   out[r,c] = apply_silu ? silu(v) : v; ring[r] shifts one slot and takes x[r,c].
+ * x: [rows, channels] with row stride x_stride; ring: f32 [rows, W-1, channels]
+ * (unused when W == 1); weight f32 [channels, W]; bias f32 [channels] or NULL. */
+int nsosx_conv_step(const void* x, int x_dtype, int64_t x_stride, int rows, int channels,
+                    const float* weight, const float* bias, int width, float* ring,
+                    int apply_silu, void* out, int out_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -291,6 +291,60 @@ void orc_conv1d_causal(const float* in, const float* weight, const float* bias,
     }
 }
 
+/* Decode conv ring step, CPU streaming path of forward_faithful_step:
+ *   v = bias[c]; v += w[c,j] * (j < W-1 ? ring[r][j][c] : x[r,c]) for j < W;
+ *   out = silu(v); ring shifts one slot and takes x[r,c].
+ * The reference writes `value += w * src` under -mfma, contracted to fma.
+ * ring: [rows, W-1, channels].  OXN/nsos/src/mamba2.cpp:4072-4090 */
+void orc_conv_step(const float* x, int rows, int channels, const float* weight,
+                   const float* bias, int width, float* ring, int apply_silu, float* out) {
+    const int taps = width - 1;
+    for (int r = 0; r < rows; ++r) {
+        float* rg = ring ? ring + (int64_t)r * taps * channels : NULL;
+        for (int c = 0; c < channels; ++c) {
+            const float cur = x[(int64_t)r * channels + c];
+            float v = bias ? bias[c] : 0.0f;
+            for (int j = 0; j < width; ++j) {
+                const float src = j < taps ? rg[(int64_t)j * channels + c] : cur;
+                v = fmaf(weight[(int64_t)c * width + j], src, v);
+            }
+            out[(int64_t)r * channels + c] = apply_silu ? orc_silu(v) : v;
+            for (int s2 = 0; s2 + 1 < taps; ++s2)
+                rg[(int64_t)s2 * channels + c] = rg[(int64_t)(s2 + 1) * channels + c];
+            if (taps > 0) rg[(int64_t)(taps - 1) * channels + c] = cur;
+        }
+    }
+}
+
+/* Gated RMSNorm epilogue, norm_before_gate = false:
+ *   g = y * silu(z)                  Tensor::silu_gate, tensor.cpp:3323-3343
+ *   inv = 1 / sqrt(sum g^2 / K + eps), sum in index order
+ *                                    Tensor::rmsnorm, tensor.cpp:3455-3492
+ *   out = (g * inv) * gamma          Tensor::mul, mamba2.cpp:2677-2680
+ * z NULL: plain rmsnorm; gamma NULL: unit weight. */
+void orc_rmsnorm_gated(const float* y, const float* z, const float* gamma, int rows, int cols,
+                       float eps, float* out) {
+    for (int r = 0; r < rows; ++r) {
+        const float* yr = y + (int64_t)r * cols;
+        const float* zr = z ? z + (int64_t)r * cols : NULL;
+        float* dst = out + (int64_t)r * cols;
+        for (int j = 0; j < cols; ++j) dst[j] = zr ? yr[j] * orc_silu(zr[j]) : yr[j];
+        /* the same sum as orc_rmsnorm: rounded squares added in order, fma tail */
+        const int body = cols & ~3;
+        float sum_sq = 0.0f;
+        for (int j = 0; j < body; ++j) {
+            const float sq = dst[j] * dst[j];
+            sum_sq = sum_sq + sq;
+        }
+        for (int j = body; j < cols; ++j) sum_sq = fmaf(dst[j], dst[j], sum_sq);
+        const float inv = 1.0f / sqrtf(sum_sq / (float)(cols > 1 ? cols : 1) + eps);
+        for (int j = 0; j < cols; ++j) {
+            dst[j] = dst[j] * inv;
+            if (gamma) dst[j] = dst[j] * gamma[j];
+        }
+    }
+}
+
 /* One token of the faithful recurrence for channel chan = h*P + p:
  *   out = D[h]*x; for n: h_n = decay*h_n + delta*B[g,n]*x; out += h_n*C[g,n]
  * with A_log per head (the reference) or per (head, state) (the Mamba-1

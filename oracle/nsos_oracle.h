@@ -41,6 +41,10 @@ void orc_bitlinear_forward(const float* x, int M, int K, int N, const uint8_t* p
 
 /* ---- elementwise ---------------------------------------------------------- */
 float orc_silu(float v);
+void orc_conv_step(const float* x, int rows, int channels, const float* weight,
+                   const float* bias, int width, float* ring, int apply_silu, float* out);
+void orc_rmsnorm_gated(const float* y, const float* z, const float* gamma, int rows, int cols,
+                       float eps, float* out);
 float orc_softplus(float v);
 void orc_squared_relu(const float* x, int64_t n, float* out);
 

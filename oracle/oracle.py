@@ -64,6 +64,8 @@ def _load() -> ctypes.CDLL:
                                       _i32p, _i, _i, _i, _i, _i, _vp, _f32p, _vp, _i]),
         "orc_scan_step": (None, [_f32p, _f32p, _f32p, _i, _f32p, _f32p, _f32p, _vp,
                                  _i, _i, _i, _i, _i, _f32p, _f32p, _i]),
+        "orc_conv_step": (None, [_f32p, _i, _i, _f32p, _vp, _i, _vp, _i, _f32p]),
+        "orc_rmsnorm_gated": (None, [_f32p, _vp, _vp, _i, _i, _f, _f32p]),
         "orc_softmax_rows": (None, [_f32p, _i, _i, _f32p]),
         "orc_topk_mask": (None, [_f32p, _i, _i, _i, _vp]),
         "orc_moe_dispatch": (None, [_f32p, _i, _i, _i, _i32p, _i32p, _i32p]),
@@ -257,6 +259,28 @@ def conv1d_causal(x, weight, cu_seqlens, bias=None, silu_act: bool = True) -> np
     out = np.zeros_like(x)
     _lib.orc_conv1d_causal(x, weight, _ptr(b), cu, cu.size - 1, x.shape[1], weight.shape[1],
                            int(silu_act), out)
+    return out
+
+
+def conv_step(x, weight, bias, ring, silu_act: bool = True):
+    """Decode conv ring step -> (out [R, C], new ring [R, W-1, C]); `ring` is not touched."""
+    x = _f32(x)
+    weight = _f32(weight)
+    b = None if bias is None else _f32(bias)
+    rg = None if ring is None else _f32(ring).copy()
+    out = np.empty_like(x)
+    _lib.orc_conv_step(x, x.shape[0], x.shape[1], weight, _ptr(b), weight.shape[1], _ptr(rg),
+                       int(silu_act), out)
+    return out, rg
+
+
+def rmsnorm_gated(y, z=None, gamma=None, eps: float = 1e-5) -> np.ndarray:
+    """RMSNorm(y * silu(z)) * gamma (z None: rmsnorm(y) * gamma; gamma None: unit)."""
+    y = _f32(y)
+    zz = None if z is None else _f32(z)
+    g = None if gamma is None else _f32(gamma)
+    out = np.empty_like(y)
+    _lib.orc_rmsnorm_gated(y, _ptr(zz), _ptr(g), y.shape[0], y.shape[1], eps, out)
     return out
 
 

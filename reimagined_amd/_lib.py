@@ -44,6 +44,9 @@ SIGNATURES = {
     "nsosx_grouped_ternary_gemm": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _vp,
                                         _i, _vp]),
     "nsosx_moe_combine": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
+    "nsosx_rmsnorm_gated": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp, _i, _vp]),
+    "nsosx_add_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp, _vp, _vp]),
+    "nsosx_conv_step": (_i, [_vp, _i, _i64, _i, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _vp]),
 }
 
 STATUS = {0: "OK", 1: "INVALID", 2: "OVERFLOW", 3: "RESERVED", 4: "LAUNCH"}

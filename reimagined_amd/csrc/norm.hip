@@ -1,0 +1,200 @@
+// Row norms around the hybrid block and the decode conv ring on gfx950.
+//
+// Reference semantics (OXN/nsos/ of vitorGgC569/reimagined):
+//   Tensor::rmsnorm        src/tensor.cpp:3455-3492   inv = 1/sqrt(sum x^2 / K + eps), x * inv
+//   Tensor::silu_gate      src/tensor.cpp:3323-3343   y * silu(z), silu split on the sign (3261-3282)
+//   gated RMSNorm epilogue src/mamba2.cpp:2677-2680   RMSNorm(y * SiLU(z)) * gamma
+//                          (GPU twin mamba_gated_rmsnorm_kernel, src/cuda/mamba_kernels.cu:3421-3445)
+//   block composition      src/jamba.cpp:3158-3375    r = x + core; rmsnorm(r) [* gamma]
+//   decode conv ring       src/mamba2.cpp:4072-4090   (GPU twin mamba2_faithful_conv_step_kernel,
+//                          src/cuda/mamba_kernels.cu:3332-3358)
+//
+// The row sum of squares is a wave tree reduction in fp32 (as the reference's
+// GPU kernels reduce); the CPU reference sums in index order, so outputs agree
+// to float rounding of that sum, not bit for bit.
+#include "common.hpp"
+
+#include <cmath>
+
+namespace nsosx {
+
+__device__ __forceinline__ float silu_exact(float v) {
+    const float sig = v >= 0.0f ? 1.0f / (1.0f + expf(-v)) : expf(v) / (1.0f + expf(v));
+    return v * sig;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+// ===========================================================================
+// out = (g * inv) * gamma with g = y * silu(z) (GATED) or g = y, one wave per
+// row, two passes over the row (the second recomputes g).
+// ===========================================================================
+template <int DT, int ODT, bool GATED>
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const void* __restrict__ y,
+                                                           const void* __restrict__ z,
+                                                           const float* __restrict__ gamma,
+                                                           int rows, int dim, float eps,
+                                                           void* __restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int64_t base = (int64_t)row * dim;
+    auto value = [&](int j) {
+        const float v = load_act<DT>(y, base + j);
+        return GATED ? v * silu_exact(load_act<DT>(z, base + j)) : v;
+    };
+    float sum = 0.0f;
+    for (int j = lane; j < dim; j += kWave) {
+        const float g = value(j);
+        sum = __fmaf_rn(g, g, sum);
+    }
+    sum = wave_sum(sum);
+    const float inv = 1.0f / sqrtf(sum / static_cast<float>(dim) + eps);
+    for (int j = lane; j < dim; j += kWave) {
+        float o = value(j) * inv;
+        if (gamma) o = o * gamma[j];
+        store_act<ODT>(out, base + j, o);
+    }
+}
+
+// ===========================================================================
+// residual = x + delta (stored in the activation dtype); when norm_out is
+// given, norm_out = rmsnorm(residual as stored) [* gamma].  One wave per row.
+// ===========================================================================
+template <int DT>
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const void* __restrict__ x,
+                                                          const void* __restrict__ delta,
+                                                          const float* __restrict__ gamma,
+                                                          int rows, int dim, float eps,
+                                                          void* __restrict__ residual,
+                                                          void* __restrict__ norm_out) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int64_t base = (int64_t)row * dim;
+    float sum = 0.0f;
+    for (int j = lane; j < dim; j += kWave) {
+        store_act<DT>(residual, base + j,
+                      load_act<DT>(x, base + j) + load_act<DT>(delta, base + j));
+    }
+    if (!norm_out) return;
+    // each lane re-reads only what it wrote itself: no cross-lane ordering needed
+    for (int j = lane; j < dim; j += kWave) {
+        const float r = load_act<DT>(residual, base + j);
+        sum = __fmaf_rn(r, r, sum);
+    }
+    sum = wave_sum(sum);
+    const float inv = 1.0f / sqrtf(sum / static_cast<float>(dim) + eps);
+    for (int j = lane; j < dim; j += kWave) {
+        float o = load_act<DT>(residual, base + j) * inv;
+        if (gamma) o = o * gamma[j];
+        store_act<DT>(norm_out, base + j, o);
+    }
+}
+
+// ===========================================================================
+// Decode conv ring: per (row, channel) value = bias; value += w[j] * src_j for
+// j < W, src_j = ring[row][j][c] for j < W - 1 and the new input for the last
+// tap; out = silu(value) (or value); the ring shifts one slot and takes the
+// new input.  ring: f32 [rows, W-1, C].  Thread = (row, channel).
+// ===========================================================================
+template <int DT, int ODT>
+__global__ __launch_bounds__(256) void conv_step_kernel(const void* __restrict__ x,
+                                                        int64_t x_stride, int rows, int C,
+                                                        const float* __restrict__ w,
+                                                        const float* __restrict__ bias, int W,
+                                                        float* __restrict__ ring, int silu,
+                                                        void* __restrict__ out) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    const int r = blockIdx.y;
+    if (c >= C || r >= rows) return;
+    const int taps = W - 1;
+    float* rg = ring + (int64_t)r * taps * C + c;
+    const float cur = load_act<DT>(x, (int64_t)r * x_stride + c);
+    float v = bias ? bias[c] : 0.0f;
+    for (int j = 0; j < W; ++j) {
+        const float src = j < taps ? rg[(int64_t)j * C] : cur;
+        v = __fmaf_rn(w[(int64_t)c * W + j], src, v);
+    }
+    store_act<ODT>(out, (int64_t)r * C + c, silu ? silu_exact(v) : v);
+    for (int s = 0; s + 1 < taps; ++s) rg[(int64_t)s * C] = rg[(int64_t)(s + 1) * C];
+    if (taps > 0) rg[(int64_t)(taps - 1) * C] = cur;
+}
+
+}  // namespace nsosx
+
+using namespace nsosx;
+
+extern "C" int nsosx_rmsnorm_gated(const void* y, const void* z, const float* gamma, int rows,
+                                   int dim, float eps, int act_dtype, void* out, int out_dtype,
+                                   void* stream) {
+    if (!y || !out) return fail(NSOSX_ERR_INVALID, "rmsnorm_gated: null pointer");
+    if (rows < 0 || dim <= 0 || !(eps > 0.0f) || !std::isfinite(eps))
+        return fail(NSOSX_ERR_INVALID, "rmsnorm_gated: need rows >= 0, dim > 0, finite eps > 0");
+    if (!valid_dtype(act_dtype) || !valid_dtype(out_dtype))
+        return fail(NSOSX_ERR_INVALID, "rmsnorm_gated: bad dtype");
+    if (rows == 0) return NSOSX_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid((rows + 3) / 4), block(256);
+#define NSOSX_RN(D, O)                                                                          \
+    if (z) hipLaunchKernelGGL((rmsnorm_rows_kernel<D, O, true>), grid, block, 0, st, y, z,       \
+                              gamma, rows, dim, eps, out);                                       \
+    else hipLaunchKernelGGL((rmsnorm_rows_kernel<D, O, false>), grid, block, 0, st, y, z, gamma, \
+                            rows, dim, eps, out);
+    if (act_dtype == NSOSX_F32) {
+        if (out_dtype == NSOSX_F32) { NSOSX_RN(NSOSX_F32, NSOSX_F32) } else { NSOSX_RN(NSOSX_F32, NSOSX_BF16) }
+    } else {
+        if (out_dtype == NSOSX_F32) { NSOSX_RN(NSOSX_BF16, NSOSX_F32) } else { NSOSX_RN(NSOSX_BF16, NSOSX_BF16) }
+    }
+#undef NSOSX_RN
+    return check_launch("rmsnorm_gated");
+}
+
+extern "C" int nsosx_add_rmsnorm(const void* x, const void* delta, const float* gamma, int rows,
+                                 int dim, float eps, int act_dtype, void* residual_out,
+                                 void* norm_out, void* stream) {
+    if (!x || !delta || !residual_out) return fail(NSOSX_ERR_INVALID, "add_rmsnorm: null pointer");
+    if (rows < 0 || dim <= 0 || (norm_out && (!(eps > 0.0f) || !std::isfinite(eps))))
+        return fail(NSOSX_ERR_INVALID, "add_rmsnorm: need rows >= 0, dim > 0, finite eps > 0");
+    if (!valid_dtype(act_dtype)) return fail(NSOSX_ERR_INVALID, "add_rmsnorm: bad dtype");
+    if (rows == 0) return NSOSX_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid((rows + 3) / 4), block(256);
+    if (act_dtype == NSOSX_F32)
+        hipLaunchKernelGGL((add_rmsnorm_kernel<NSOSX_F32>), grid, block, 0, st, x, delta, gamma,
+                           rows, dim, eps, residual_out, norm_out);
+    else
+        hipLaunchKernelGGL((add_rmsnorm_kernel<NSOSX_BF16>), grid, block, 0, st, x, delta, gamma,
+                           rows, dim, eps, residual_out, norm_out);
+    return check_launch("add_rmsnorm");
+}
+
+extern "C" int nsosx_conv_step(const void* x, int x_dtype, int64_t x_stride, int rows,
+                               int channels, const float* weight, const float* bias, int width,
+                               float* ring, int apply_silu, void* out, int out_dtype,
+                               void* stream) {
+    if (!x || !weight || !out || (width > 1 && !ring))
+        return fail(NSOSX_ERR_INVALID, "conv_step: null pointer");
+    if (rows < 0 || rows > 65535 || channels <= 0 || width <= 0 || width > 64 ||
+        x_stride < channels)
+        return fail(NSOSX_ERR_INVALID, "conv_step: bad shape");
+    if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype))
+        return fail(NSOSX_ERR_INVALID, "conv_step: bad dtype");
+    if (rows == 0) return NSOSX_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid((channels + 255) / 256, rows), block(256);
+#define NSOSX_CS(I, O)                                                                         \
+    hipLaunchKernelGGL((conv_step_kernel<I, O>), grid, block, 0, st, x, x_stride, rows, channels, \
+                       weight, bias, width, ring, apply_silu, out);
+    if (x_dtype == NSOSX_F32) {
+        if (out_dtype == NSOSX_F32) { NSOSX_CS(NSOSX_F32, NSOSX_F32) } else { NSOSX_CS(NSOSX_F32, NSOSX_BF16) }
+    } else {
+        if (out_dtype == NSOSX_F32) { NSOSX_CS(NSOSX_BF16, NSOSX_F32) } else { NSOSX_CS(NSOSX_BF16, NSOSX_BF16) }
+    }
+#undef NSOSX_CS
+    return check_launch("conv_step");
+}

@@ -8,6 +8,8 @@
   MoEFFN             MoERouter::forward from logits + JambaBlock::forward_moe
                      (src/jamba.cpp:3692-3973, 8140-8319): device routing,
                      grouped ternary GEMMs, squared ReLU, weighted combine
+  HybridBlock        JambaBlock::forward (src/jamba.cpp:3158-3375) for a Mamba
+                     core and an MoE feed-forward: block norms, residual adds
 
 Workspaces are allocated once per shape and reused, so a forward enqueues
 kernels only.  Citations are into OXN/nsos/ of vitorGgC569/reimagined.
@@ -219,3 +221,43 @@ class MoEFFN:
              _DT[out.dtype], st)
         return {"out": out, **{n: b[n] for n in ("weights", "selected", "counts", "offsets",
                                                  "perm", "slot_of", "h", "o")}}
+
+
+class HybridBlock:
+    """JambaBlock::forward with a Mamba core and an MoE feed-forward (src/jamba.cpp:3158-3375):
+
+        h   = rmsnorm(x, 1e-6) * core_gamma        (3175-3179)
+        r   = x + mamba(h)                          (3253)
+        f   = rmsnorm(r, 1e-6) * ff_gamma           (3286-3290)
+        out = r + moe(f)                            (3305-3316)
+
+    gammas None are the non-learnable norms.  The router logits are supplied by the
+    caller, or, with `gate_w`, come from a ternary gate BitLinear [experts, d_model]
+    over f (MoERouter's gate projection, src/jamba.cpp:8140-8319).
+    """
+
+    def __init__(self, mamba_params: dict, w_up: list, w_down: list, device="cuda", k: int = 2,
+                 core_gamma=None, ff_gamma=None, gate_w=None, core_eps: float = 1e-6,
+                 ff_eps: float = 1e-6):
+        self.mamba = HybridMambaLayer(mamba_params, device)
+        self.moe = MoEFFN(w_up, w_down, device, k=k)
+        f32 = dict(dtype=torch.float32, device=device)
+        self.core_gamma = None if core_gamma is None else torch.as_tensor(core_gamma, **f32)
+        self.ff_gamma = None if ff_gamma is None else torch.as_tensor(ff_gamma, **f32)
+        self.gate = None if gate_w is None else BitLinear(gate_w, device)
+        self.core_eps, self.ff_eps = core_eps, ff_eps
+
+    def forward(self, x, dt, B, C, cu_seqlens, logits=None, final_state=None) -> dict:
+        """x [T, d_model] (f32 or bf16); the remaining scan inputs as HybridMambaLayer."""
+        ops._dev(cu_seqlens, "cu_seqlens", torch.int32)
+        if logits is None and self.gate is None:
+            raise ValueError("HybridBlock: pass router logits or build the block with gate_w")
+        t, d = x.shape
+        h = ops.rmsnorm_gated(x, None, self.core_gamma, eps=self.core_eps)
+        core = self.mamba.forward(h, dt, B, C, cu_seqlens, final_state=final_state)
+        r, f = ops.add_rmsnorm(x, core, self.ff_gamma, eps=self.ff_eps)
+        if logits is None:
+            logits = self.gate.forward(f, out_dtype=torch.float32)
+        ff = self.moe.forward(f, logits, out_dtype=x.dtype)["out"]
+        out, _ = ops.add_rmsnorm(r, ff, want_norm=False)
+        return {"out": out, "residual": r, "core": core, "ff": ff, "logits": logits}

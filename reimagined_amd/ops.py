@@ -326,3 +326,62 @@ def moe_combine(expert_out, slot_of, selected, weights, out_dtype=torch.float32)
     call("nsosx_moe_combine", _p(expert_out), _dt(expert_out), _p(slot_of), _p(selected),
          _p(weights), rows, e, k, dim, _p(out), _DT[out_dtype], _stream())
     return out
+
+
+# ---- row norms of the hybrid block and the decode conv ring -----------------
+
+def rmsnorm_gated(y: torch.Tensor, z=None, gamma=None, eps: float = 1e-5,
+                  out_dtype=None) -> torch.Tensor:
+    """RMSNorm(y * SiLU(z)) * gamma (src/mamba2.cpp:2677-2680); z None: rmsnorm(y) * gamma."""
+    _dev(y, "y")
+    if y.dim() != 2:
+        raise ValueError("rmsnorm_gated: y must be [rows, dim]")
+    if z is not None:
+        _dev(z, "z", y.dtype)
+        if z.shape != y.shape:
+            raise ValueError("rmsnorm_gated: z must match y")
+    _opt(gamma, "gamma")
+    if gamma is not None and gamma.numel() != y.shape[1]:
+        raise ValueError("rmsnorm_gated: gamma must have dim elements")
+    out = torch.empty(y.shape, dtype=out_dtype or y.dtype, device=y.device)
+    call("nsosx_rmsnorm_gated", _p(y), _p(z), _p(gamma), y.shape[0], y.shape[1], eps, _dt(y),
+         _p(out), _dt(out), _stream())
+    return out
+
+
+def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor, gamma=None, eps: float = 1e-6,
+                want_norm: bool = True):
+    """residual = x + delta; norm = rmsnorm(residual) * gamma (src/jamba.cpp:3253, 3286-3290).
+
+    Returns (residual, norm) with norm None when want_norm is False."""
+    _dev(x, "x")
+    _dev(delta, "delta", x.dtype)
+    if x.dim() != 2 or delta.shape != x.shape:
+        raise ValueError("add_rmsnorm: x and delta must be the same [rows, dim]")
+    _opt(gamma, "gamma")
+    res = torch.empty_like(x)
+    norm = torch.empty_like(x) if want_norm else None
+    call("nsosx_add_rmsnorm", _p(x), _p(delta), _p(gamma), x.shape[0], x.shape[1], eps, _dt(x),
+         _p(res), _p(norm), _stream())
+    return res, norm
+
+
+def conv_step(x: torch.Tensor, weight: torch.Tensor, bias, ring, apply_silu: bool = True,
+              out_dtype=None) -> torch.Tensor:
+    """Decode conv ring step in place on `ring` [R, W-1, C] (src/mamba2.cpp:4072-4090) -> out."""
+    if not x.is_cuda or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("conv_step: x must be a device [rows, channels] with unit channel stride")
+    _dev(weight, "weight", torch.float32)
+    _opt(bias, "bias")
+    r, c = x.shape
+    w = weight.shape[1]
+    if weight.shape[0] != c:
+        raise ValueError("conv_step: weight must be [channels, W]")
+    if w > 1:
+        _dev(ring, "ring", torch.float32)
+        if tuple(ring.shape) != (r, w - 1, c):
+            raise ValueError("conv_step: ring must be [rows, W-1, channels]")
+    out = torch.empty((r, c), dtype=out_dtype or x.dtype, device=x.device)
+    call("nsosx_conv_step", _p(x), _dt(x), x.stride(0), r, c, _p(weight), _p(bias), w,
+         _p(ring) if w > 1 else None, int(apply_silu), _p(out), _dt(out), _stream())
+    return out
