@@ -324,10 +324,25 @@ __device__ __forceinline__ float quad_back(float v, int d) {
     }
 }
 
-// Sequence for this workgroup: the blockIdx.y-th longest (ties by index).
+// Workgroup -> (sequence rank, channel block).  Consecutive workgroup ids go
+// round-robin to the 8 XCDs, each with its own L2; this map hands every run of
+// 4 channel blocks (4 x 16 channels: one 128-byte line of a bf16 activation
+// row) to one XCD, so a line is fetched into one L2 instead of four, while
+// the ranks still advance in dispatch order (longest sequences first).
+__device__ __forceinline__ void quad_work_item(int& rank, int& cblk) {
+    const int nbx = gridDim.x;
+    const int total = nbx * gridDim.y;
+    const int L = blockIdx.y * nbx + blockIdx.x;
+    int lam = L;
+    if (L < (total / 32) * 32) lam = (L / 32) * 32 + (L % 8) * 4 + (L / 8) % 4;
+    rank = lam / nbx;
+    cblk = lam % nbx;
+}
+
+// Sequence of the given rank: the rank-th longest (ties by index).
 __device__ __forceinline__ int quad_pick_sequence(const int32_t* cu, int num_seqs, int T,
-                                                  int* s_pick) {
-    if (num_seqs > kOrderMax) return blockIdx.y;
+                                                  int target, int* s_pick) {
+    if (num_seqs > kOrderMax) return target;
     for (int i = threadIdx.x; i < num_seqs; i += 64) {
         const int a = min(max(cu[i], 0), T);
         const int li = min(max(cu[i + 1], a), T) - a;
@@ -337,7 +352,7 @@ __device__ __forceinline__ int quad_pick_sequence(const int32_t* cu, int num_seq
             const int lk = min(max(cu[k + 1], b), T) - b;
             rank += (lk > li) || (lk == li && k < i);
         }
-        if (rank == (int)blockIdx.y) *s_pick = i;
+        if (rank == target) *s_pick = i;
     }
     __syncthreads();
     return *s_pick;
@@ -370,10 +385,12 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
     const int D = H * P;
     const int GN = G * N;
     const int q = lane & 3;
-    const int c = blockIdx.x * kQuadCh + (lane >> 2);
+    int rank, cblk;
+    quad_work_item(rank, cblk);
+    const int c = cblk * kQuadCh + (lane >> 2);
     const int h = c / P;
     const int grp = (h * G) / H;
-    const int seq = quad_pick_sequence(cu_seqlens, num_seqs, total_tokens, &s_pick);
+    const int seq = quad_pick_sequence(cu_seqlens, num_seqs, total_tokens, rank, &s_pick);
     const int t0 = min(max(cu_seqlens[seq], 0), total_tokens);
     const int t1 = min(max(cu_seqlens[seq + 1], t0), total_tokens);
     const int tlast = total_tokens - 1;
