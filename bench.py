@@ -118,17 +118,43 @@ def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=3
     name = max((k for k in stages if k in work), key=lambda k: stages[k])
     bound, amount = work[name]
     sec = stages[name] / 1e3
+    traffic = pmc_traffic(name)
     if bound == "mfma":
         achieved = amount / sec / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None,
-                "kernel": name, "note": "int8 ops (TOPS) against the dense int8 MFMA peak"}
+                "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
+                "traffic": traffic, "kernel": name,
+                "note": "int8 ops (TOPS) against the dense int8 MFMA peak"}
     else:
         achieved = amount / sec / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": name}
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": name, "algorithmic_bytes": int(amount)}
     return roof, work
+
+
+PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                           "hybrid_layer_c4_pmc_traffic.md")
+
+
+def pmc_traffic(stage: str):
+    """HBM bytes per launch of a layer stage's kernel, from the committed rocprofv3 PMC summary.
+
+    The summary's table rows read `| stage | kernel | FETCH KiB | WRITE KiB | bytes |`, the
+    bytes column already scaled by the copy-kernel calibration stated in that file.  None when
+    the summary or the stage's row is absent."""
+    try:
+        text = open(PMC_SUMMARY).read()
+    except OSError:
+        return None
+    for line in text.splitlines():
+        cells = [c.strip().strip("`") for c in line.strip().strip("|").split("|")]
+        if len(cells) == 5 and cells[0] == stage:
+            try:
+                return int(cells[4].replace(",", ""))
+            except ValueError:
+                return None
+    return None
 
 
 def bench_prefill_gemm(torch, dev, reps=20):
@@ -255,6 +281,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--pmc-calibration", action="store_true",
+                    help="end with a plain 256 MiB device copy, the known-size kernel that "
+                         "FETCH_SIZE / WRITE_SIZE counters are scaled by")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the hot path's kernels run on one MI355X; "
@@ -309,6 +338,11 @@ def main():
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
+    if args.pmc_calibration:
+        a = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
 
 
 if __name__ == "__main__":
