@@ -942,107 +942,58 @@ __device__ __forceinline__ lds_void_t* lds_ptr(const char* p) {
                          static_cast<unsigned>(reinterpret_cast<size_t>(p)));
 }
 
-template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU>
-__device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* __restrict__ q,
-                                           const float* __restrict__ act_scale,
-                                           const int32_t* __restrict__ perm, int seg_begin,
-                                           int seg_rows, int n0, int m0, void* y,
-                                           int32_t* acc_out, char* smem) {
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;        // wave = 64-row slice of n
-    const int W16 = pb.K >> 4;
-    const int KT = pb.K / kG3BK;
-
-    // DMA sources.  Weights: wave-load j (0, 1) of a wave fills LDS rows
-    // 64 wave + 32 j .. +31, lane -> row + lane / 2, slot lane % 2.
-    const char* wsrc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int r = 64 * wave + 32 * j + (lane >> 1);
-        const int half = (lane & 1) ^ ((r >> 3) & 1);
-        const int row = min(n0 + r, pb.N - 1);
-        wsrc[j] = reinterpret_cast<const char*>(pb.packed + (int64_t)row * W16) + half * 16;
-    }
-    // Activations: wave-load i (0..3) of a wave fills LDS rows 32 i + 8 wave .. +7,
-    // lane -> row + lane / 8, slot lane % 8.
-    const char* xsrc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = 32 * i + 8 * wave + (lane >> 3);
-        const int c = (lane & 7) ^ ((r >> 1) & 7);
-        const int m = min(m0 + r, seg_rows - 1);
-        const int src = GATHER ? perm[seg_begin + m] : seg_begin + m;
-        xsrc[i] = reinterpret_cast<const char*>(q + (int64_t)src * pb.K) + c * 16;
-    }
-    auto issue = [&](int kt) {
-        char* st = smem + (kt % kG3Stages) * kG3StageBytes;
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            __builtin_amdgcn_global_load_lds(wsrc[j] + kt * 32,
-                                             lds_ptr(st + (64 * wave + 32 * j) * 32), 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            __builtin_amdgcn_global_load_lds(xsrc[i] + kt * 128,
-                                             lds_ptr(st + kG3WBytes + (32 * i + 8 * wave) * 128),
-                                             16, 0, 0);
-    };
-
-    v16i acc[2][4];
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
-
-    issue(0);
-    if (KT > 1) issue(1);
-
+// One 128-deep K stage of the 256 x 128 block from LDS stage `st`: each lane
+// reads its two 16-byte weight word groups once, then per MFMA step ks decodes
+// one word per n-tile and reads one 16-byte activation chunk per m-tile.
+__device__ __forceinline__ void gemm3_stage(const char* st, int wave, int lane, v16i (&acc)[2][4]) {
     const int g = lane >> 5;
     const int li = lane & 31;
-    for (int kt = 0; kt < KT; ++kt) {
-        // this thread's stage-kt DMA is done once at most one stage (6 loads) is pending
-        if (kt + 1 < KT) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        if (kt + 2 < KT) issue(kt + 2);
-        const char* st = smem + (kt % kG3Stages) * kG3StageBytes;
-        const char* xl = st + kG3WBytes;
-        uint4 wq[2];
+    const char* xl = st + kG3WBytes;
+    uint4 wq[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const int nl = wave * 64 + nb * 32 + li;
+        const int slot = g ^ ((nl >> 3) & 1);
+        wq[nb] = *reinterpret_cast<const uint4*>(st + nl * 32 + slot * 16);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        v4i bx[4];
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const int ml = mb * 32 + li;
+            const int slot = (4 * g + ks) ^ ((ml >> 1) & 7);
+            const uint4 v = *reinterpret_cast<const uint4*>(xl + ml * 128 + slot * 16);
+            bx[mb] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+        }
+        v4i aw[2];
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            const int nl = wave * 64 + nb * 32 + li;
-            const int slot = g ^ ((nl >> 3) & 1);
-            wq[nb] = *reinterpret_cast<const uint4*>(st + nl * 32 + slot * 16);
+            const uint32_t words[4] = {wq[nb].x, wq[nb].y, wq[nb].z, wq[nb].w};
+            uint32_t wv[4], wt[4];
+            unpack_word(words[ks], wv);
+            transpose16(wv, wt);                            // unpack order -> natural order
+            aw[nb] = v4i{(int)wt[0], (int)wt[1], (int)wt[2], (int)wt[3]};
         }
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            v4i bx[4];
+        for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                const int ml = mb * 32 + li;
-                const int slot = (4 * g + ks) ^ ((ml >> 1) & 7);
-                const uint4 v = *reinterpret_cast<const uint4*>(xl + ml * 128 + slot * 16);
-                bx[mb] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-            }
-            v4i aw[2];
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                const uint32_t words[4] = {wq[nb].x, wq[nb].y, wq[nb].z, wq[nb].w};
-                uint32_t wv[4], wt[4];
-                unpack_word(words[ks], wv);
-                transpose16(wv, wt);                            // unpack order -> natural order
-                aw[nb] = v4i{(int)wt[0], (int)wt[1], (int)wt[2], (int)wt[3]};
-            }
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-                for (int mb = 0; mb < 4; ++mb)
-                    acc[nb][mb] =
-                        __builtin_amdgcn_mfma_i32_32x32x32_i8(aw[nb], bx[mb], acc[nb][mb], 0, 0, 0);
-        }
+            for (int mb = 0; mb < 4; ++mb)
+                acc[nb][mb] =
+                    __builtin_amdgcn_mfma_i32_32x32x32_i8(aw[nb], bx[mb], acc[nb][mb], 0, 0, 0);
     }
+}
 
+template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU>
+__device__ __forceinline__ void gemm3_epilogue(const GemmProblem& pb,
+                                               const float* __restrict__ act_scale,
+                                               const int32_t* __restrict__ perm, int seg_begin,
+                                               int seg_rows, int n0, int m0, void* y,
+                                               int32_t* acc_out, const v16i (&acc)[2][4]) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 5;
+    const int li = lane & 31;
     // epilogue: lane holds token m = m_base + li and, for q4 = 0..3, the four
     // consecutive outputs n = n_base + 8 q4 + 4 g + 0..3.  A tile that lies
     // inside N (N % 4 == 0) stores 4 outputs per access at constant offsets from
@@ -1114,6 +1065,75 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
             }
         }
     }
+}
+
+template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU>
+__device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* __restrict__ q,
+                                           const float* __restrict__ act_scale,
+                                           const int32_t* __restrict__ perm, int seg_begin,
+                                           int seg_rows, int n0, int m0, void* y,
+                                           int32_t* acc_out, char* smem) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;        // wave = 64-row slice of n
+    const int W16 = pb.K >> 4;
+    const int KT = pb.K / kG3BK;
+
+    // DMA sources.  Weights: wave-load j (0, 1) of a wave fills LDS rows
+    // 64 wave + 32 j .. +31, lane -> row + lane / 2, slot lane % 2.
+    const char* wsrc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int r = 64 * wave + 32 * j + (lane >> 1);
+        const int half = (lane & 1) ^ ((r >> 3) & 1);
+        const int row = min(n0 + r, pb.N - 1);
+        wsrc[j] = reinterpret_cast<const char*>(pb.packed + (int64_t)row * W16) + half * 16;
+    }
+    // Activations: wave-load i (0..3) of a wave fills LDS rows 32 i + 8 wave .. +7,
+    // lane -> row + lane / 8, slot lane % 8.
+    const char* xsrc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 32 * i + 8 * wave + (lane >> 3);
+        const int c = (lane & 7) ^ ((r >> 1) & 7);
+        const int m = min(m0 + r, seg_rows - 1);
+        const int src = GATHER ? perm[seg_begin + m] : seg_begin + m;
+        xsrc[i] = reinterpret_cast<const char*>(q + (int64_t)src * pb.K) + c * 16;
+    }
+    auto issue = [&](int kt) {
+        char* st = smem + (kt % kG3Stages) * kG3StageBytes;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            __builtin_amdgcn_global_load_lds(wsrc[j] + kt * 32,
+                                             lds_ptr(st + (64 * wave + 32 * j) * 32), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(xsrc[i] + kt * 128,
+                                             lds_ptr(st + kG3WBytes + (32 * i + 8 * wave) * 128),
+                                             16, 0, 0);
+    };
+
+    v16i acc[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
+
+    issue(0);
+    if (KT > 1) issue(1);
+
+    for (int kt = 0; kt < KT; ++kt) {
+        // this thread's stage-kt DMA is done once at most one stage (6 loads) is pending
+        if (kt + 1 < KT) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (kt + 2 < KT) issue(kt + 2);
+        gemm3_stage(smem + (kt % kG3Stages) * kG3StageBytes, wave, lane, acc);
+    }
+
+    gemm3_epilogue<YDT, ACC_OUT, GATHER, SQRELU>(pb, act_scale, perm, seg_begin, seg_rows, n0, m0,
+                                                 y, acc_out, acc);
 }
 
 // Linear workgroup id -> (n tile, m tile).  Consecutive ids go round-robin to

@@ -93,6 +93,13 @@ def test_mfma_gemm_bit_exact(dev, orc, m, n, k):
     _gemm_case(dev, orc, m, n, k, path=1, mag=True, bias=(n % 2 == 0))
 
 
+@pytest.mark.parametrize("m,n,k", [(1000, 700, 512), (129, 256, 256), (513, 1024, 384),
+                                   (2000, 96, 1024)])
+def test_mfma_gemm_more_shapes_bit_exact(dev, orc, m, n, k):
+    """Direct-to-LDS GEMM: edge tiles in n and m, the shortest ring (K = 256), odd stage counts."""
+    _gemm_case(dev, orc, m, n, k, path=1, mag=(m % 2 == 0), bias=True)
+
+
 def test_gemm_dispatch_and_extremes(dev, orc):
     # |acc| = 127 * K at the extremes: int32 accumulation must not saturate or wrap
     k, n = 4096, 64
