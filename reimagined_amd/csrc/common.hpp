@@ -80,6 +80,36 @@ __device__ __forceinline__ float raw_to_f32(typename raw_word<DT>::type u) {
     }
 }
 
+// Raw buffer access (buffer_load / buffer_store with a 32-bit byte offset from a
+// resource that carries the base and the extent): a load past the extent
+// returns 0 and a store past it is dropped, so running offsets need no clamps.
+// Word 3 of the resource (0x00020000) is the untyped 32-bit data format of the
+// gfx9 family.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+template <int DT>
+__device__ __forceinline__ typename raw_word<DT>::type buf_load_raw(__amdgpu_buffer_rsrc_t r,
+                                                                    uint32_t byte_off) {
+    if constexpr (DT == NSOSX_F32) {
+        return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0);
+    } else {
+        return __builtin_amdgcn_raw_buffer_load_b16(r, byte_off, 0, 0);
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void buf_store_act(__amdgpu_buffer_rsrc_t r, uint32_t byte_off,
+                                              float v) {
+    if constexpr (DT == NSOSX_F32) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, byte_off, 0, 0);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), r, byte_off, 0, 0);
+    }
+}
+
 template <int DT>
 __device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
     if constexpr (DT == NSOSX_F32) {

@@ -490,20 +490,26 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
         }
     };
 
-    // per-lane token stream: element indices of the next group's token (running,
-    // clamped at use), raw words one group ahead
-    const int xs = static_cast<int>(x_stride), zs = static_cast<int>(z_stride);
-    const int ix_max = tlast * xs + c, idt_max = tlast * H + h, iz_max = tlast * zs + c;
-    int ix = (t0 + q) * xs + c, idt = (t0 + q) * H + h, iz = (t0 + q) * zs + c;
-    int iy = (t0 + q) * D + c;
+    // per-lane token stream through buffer resources: byte offsets of the next group's
+    // token (running; past the data the hardware returns 0), raw words one group ahead
+    constexpr uint32_t ES = ADT == NSOSX_F32 ? 4 : 2;
+    const uint32_t xs = static_cast<uint32_t>(x_stride) * ES, zs = static_cast<uint32_t>(z_stride) * ES;
+    const uint32_t Tn = static_cast<uint32_t>(total_tokens);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (Tn - 1) * xs + D * ES);
+    const __amdgpu_buffer_rsrc_t rdt = make_rsrc(dt, Tn * H * ES);
+    const __amdgpu_buffer_rsrc_t rz = make_rsrc(GATE ? z : x, GATE ? (Tn - 1) * zs + D * ES : 0);
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(y, Tn * D * ES);
+    const uint32_t tq = static_cast<uint32_t>(t0 + q);
+    uint32_t ox = tq * xs + c * ES, odt = (tq * H + h) * ES, oz = tq * zs + c * ES;
+    uint32_t oy = (tq * D + c) * ES;
     raw_t xr = 0, dtr = 0, zr = 0;
     auto prefetch_tok = [&]() {
-        xr = load_raw<ADT>(x, (uint32_t)min(ix, ix_max));
-        dtr = load_raw<ADT>(dt, (uint32_t)min(idt, idt_max));
-        if (GATE) zr = load_raw<ADT>(z, (uint32_t)min(iz, iz_max));
-        ix += 4 * xs;
-        idt += 4 * H;
-        iz += 4 * zs;
+        xr = buf_load_raw<ADT>(rx, ox);
+        dtr = buf_load_raw<ADT>(rdt, odt);
+        if (GATE) zr = buf_load_raw<ADT>(rz, oz);
+        ox += 4 * xs;
+        odt += 4 * H * ES;
+        oz += 4 * zs;
     };
 
     float xprev = 0.0f;  // raw x of this lane's token in the previous group (0 before t0)
@@ -530,7 +536,8 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
                     bq[k][i] = s_bc[0][r0 + k][q * SPL + i];
                     cq[k][i] = s_bc[1][r0 + k][q * SPL + i];
                 }
-            const float xcur = valid ? raw_to_f32<ADT>(xr) : 0.0f;
+            // tokens past the sequence feed only later tokens past it: no mask needed on x
+            const float xcur = raw_to_f32<ADT>(xr);
             const float dtcur = raw_to_f32<ADT>(dtr);
             const raw_t zraw = zr;
             prefetch_tok();
@@ -552,8 +559,7 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
                     }
                     acc = __fmaf_rn(cw[j], xl, acc);
                 }
-                const float sx = silu_fast(acc + cb);
-                xv = valid ? sx : 0.0f;
+                xv = silu_fast(acc + cb);  // finite; an invalid token's dl = 0 cancels it
             } else {
                 xv = xcur;
             }
@@ -595,9 +601,9 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
             if (valid) {
                 float out = __fmaf_rn(dsk, xv, tot);
                 if (GATE) out = out * silu_fast(raw_to_f32<ADT>(zraw));
-                store_act<ADT>(y, (uint32_t)iy, out);
+                buf_store_act<ADT>(ry, oy, out);
             }
-            iy += 4 * D;
+            oy += 4 * D * ES;
         }
     }
     if (final_state) {
@@ -775,10 +781,11 @@ static int scan_fwd_launch(const void* x, int64_t x_stride, const void* dt, cons
                     "conv_scan_fwd: channels per group must be a multiple of 64 (or of 16 with "
                     "N <= 16 and conv width <= 4)");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // the quad kernel indexes rows with 32-bit element offsets
+    // the quad kernel addresses rows with 32-bit byte offsets (buffer resources)
     const int64_t max_row = std::max<int64_t>(std::max<int64_t>(x_stride, z ? z_stride : 0),
                                               std::max<int64_t>(Dm, (int64_t)G * N));
-    const bool idx32 = (int64_t)(total_tokens + 8) * max_row < ((int64_t)1 << 31);
+    const int64_t esz = act_dtype == NSOSX_F32 ? 4 : 2;
+    const bool idx32 = (int64_t)(total_tokens + 8) * max_row * esz < ((int64_t)1 << 31);
     if (N <= 16 && per_group % kQuadCh == 0 && (!conv || conv_width <= kQuadMaxW) && idx32) {
         const dim3 grid(Dm / kQuadCh, num_seqs), block(64);
         const int spl = N <= 4 ? 1 : N <= 8 ? 2 : 4;
