@@ -720,6 +720,108 @@ __global__ __launch_bounds__(256) void scan_step_kernel(
 }
 
 // ===========================================================================
+// Decode step, row-blocked: a workgroup is 64 channels x 4 state quads and
+// walks kStepRows rows, so each lane forms its decay exponents A2 (a double exp
+// each) once for all those rows.  Per row a lane moves its SPL states with
+// vector loads and stores (N = 4 * SPL contiguous floats per channel), the
+// per-token terms use the same native softplus / SiLU as the prefill quad
+// kernel, and the four lanes of a channel meet with two DPP steps.  The loads of
+// all kStepRows rows are issued before the first row is computed.
+// ===========================================================================
+constexpr int kStepRows = 4;
+
+template <int SPL>
+__device__ __forceinline__ void load_states(const float* p, float v[SPL]) {
+    if constexpr (SPL == 1) {
+        v[0] = p[0];
+    } else if constexpr (SPL == 2) {
+        const float2 a = *reinterpret_cast<const float2*>(p);
+        v[0] = a.x; v[1] = a.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < SPL; i += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(p + i);
+            v[i] = a.x; v[i + 1] = a.y; v[i + 2] = a.z; v[i + 3] = a.w;
+        }
+    }
+}
+
+template <int SPL>
+__device__ __forceinline__ void store_states(float* p, const float v[SPL]) {
+    if constexpr (SPL == 1) {
+        p[0] = v[0];
+    } else if constexpr (SPL == 2) {
+        *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < SPL; i += 4)
+            *reinterpret_cast<float4*>(p + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+    }
+}
+
+template <int ADT, int SPL, bool GATE>
+__global__ __launch_bounds__(256) void scan_step_rows_kernel(
+    const void* __restrict__ x, const void* __restrict__ dt, const float* __restrict__ a_log,
+    int a_per_state, const void* __restrict__ Bm, const void* __restrict__ Cm,
+    const float* __restrict__ Dskip, const void* __restrict__ z, int rows, int H, int P, int N,
+    int G, float* __restrict__ state, void* __restrict__ y) {
+    const int D = H * P;
+    const int GN = G * N;
+    const int q = threadIdx.x & 3;
+    const int c = blockIdx.x * 64 + (threadIdx.x >> 2);
+    if (c >= D) return;  // whole quads leave together
+    const int h = c / P;
+    const int grp = (h * G) / H;
+    const int r0 = blockIdx.y * kStepRows;
+    float a2[SPL];
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) {
+        const int n = q * SPL + i;
+        a2[i] = a2_from_log(a_per_state ? a_log[(int64_t)h * N + n] : a_log[h]);
+    }
+    const float dsk = Dskip[h];
+    float sv[kStepRows][SPL], bq[kStepRows][SPL], cq[kStepRows][SPL];
+    float xv[kStepRows], dtv[kStepRows], zv[kStepRows];
+#pragma unroll
+    for (int j = 0; j < kStepRows; ++j) {
+        const int r = min(r0 + j, rows - 1);  // rows past the end repeat the last (never stored)
+        load_states<SPL>(state + ((int64_t)r * D + c) * N + q * SPL, sv[j]);
+        xv[j] = load_act<ADT>(x, (int64_t)r * D + c);
+        dtv[j] = load_act<ADT>(dt, (int64_t)r * H + h);
+        zv[j] = GATE ? load_act<ADT>(z, (int64_t)r * D + c) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < SPL; ++i) {
+            const int64_t off = (int64_t)r * GN + grp * N + q * SPL + i;
+            bq[j][i] = load_act<ADT>(Bm, off);
+            cq[j][i] = load_act<ADT>(Cm, off);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kStepRows; ++j) {
+        const int r = r0 + j;
+        const float dl = softplus_sel(dtv[j]);
+        const float dx = dl * xv[j];
+        float p = 0.0f;
+#pragma unroll
+        for (int i = 0; i < SPL; ++i) {
+            const float a = __builtin_amdgcn_exp2f(dl * a2[i]);
+            sv[j][i] = __fmaf_rn(a, sv[j][i], dx * bq[j][i]);
+            p = __fmaf_rn(sv[j][i], cq[j][i], p);
+        }
+        p += dpp_xor2(p);
+        p += dpp_xor1(p);
+        if (r < rows) {
+            store_states<SPL>(state + ((int64_t)r * D + c) * N + q * SPL, sv[j]);
+            if (q == 0) {
+                float out = __fmaf_rn(dsk, xv[j], p);
+                if (GATE) out = out * silu_fast(zv[j]);
+                store_act<ADT>(y, (int64_t)r * D + c, out);
+            }
+        }
+    }
+}
+
+// ===========================================================================
 // Depthwise causal convolution + bias + SiLU, restarted per sequence.
 // Thread = (token, channel); the sequence start comes from a binary search
 // of cu_seqlens.
@@ -888,6 +990,29 @@ extern "C" int nsosx_selective_scan_step(const void* x, const void* dt, const fl
     if (reinterpret_cast<uintptr_t>(state) % 16)
         return fail(NSOSX_ERR_INVALID, "selective_scan_step: state must be 16-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (N % 4 == 0 && (N / 4 == 1 || N / 4 == 2 || N / 4 == 4 || N / 4 == 8 || N / 4 == 16) &&
+        rows <= 65535 * kStepRows) {
+        // states of a channel split evenly over the quad: the row-blocked kernel
+        const dim3 grid((H * P + 63) / 64, (rows + kStepRows - 1) / kStepRows), block(256);
+#define NSOSX_STEPR(ADT, SPL, GATE)                                                            \
+    hipLaunchKernelGGL((scan_step_rows_kernel<ADT, SPL, GATE>), grid, block, 0, st, x, dt, A_log, \
+                       a_per_state, B, C, D, z, rows, H, P, N, G, state, y);
+#define NSOSX_STEPR_G(ADT, SPL) \
+    if (z) { NSOSX_STEPR(ADT, SPL, true) } else { NSOSX_STEPR(ADT, SPL, false) }
+#define NSOSX_STEPR_S(ADT)                          \
+    switch (N / 4) {                                \
+        case 1: NSOSX_STEPR_G(ADT, 1) break;        \
+        case 2: NSOSX_STEPR_G(ADT, 2) break;        \
+        case 4: NSOSX_STEPR_G(ADT, 4) break;        \
+        case 8: NSOSX_STEPR_G(ADT, 8) break;        \
+        default: NSOSX_STEPR_G(ADT, 16) break;      \
+    }
+        if (act_dtype == NSOSX_F32) { NSOSX_STEPR_S(NSOSX_F32) } else { NSOSX_STEPR_S(NSOSX_BF16) }
+#undef NSOSX_STEPR_S
+#undef NSOSX_STEPR_G
+#undef NSOSX_STEPR
+        return check_launch("selective_scan_step");
+    }
     const int64_t lanes = (int64_t)rows * H * P * 4;
     const dim3 grid((unsigned)((lanes + 255) / 256)), block(256);
     const int spl = N <= 4 ? 1 : N <= 8 ? 2 : N <= 16 ? 4 : N <= 32 ? 8 : 16;

@@ -121,7 +121,9 @@ def test_scan_bf16_io(dev, orc):
 
 
 @pytest.mark.parametrize("H,P,N,G,per_state", [(256, 1, 16, 1, True), (4, 64, 16, 1, False),
-                                               (8, 3, 5, 2, True)])
+                                               (8, 3, 5, 2, True), (100, 1, 8, 1, True),
+                                               (64, 2, 32, 2, True), (96, 1, 64, 1, True),
+                                               (40, 1, 4, 1, True)])
 def test_step_matches_oracle_and_prefill(dev, orc, H, P, N, G, per_state):
     rng = np.random.default_rng(21 + N)
     R = 33
