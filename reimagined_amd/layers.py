@@ -261,3 +261,114 @@ class HybridBlock:
         ff = self.moe.forward(f, logits, out_dtype=x.dtype)["out"]
         out, _ = ops.add_rmsnorm(r, ff, want_norm=False)
         return {"out": out, "residual": r, "core": core, "ff": ff, "logits": logits}
+
+
+class Mamba2Block:
+    """Faithful Mamba-2 block on the packed path (Mamba2SSD::forward_faithful,
+    src/mamba2.cpp:2360-2681; streaming step forward_faithful_step, 3947-4126):
+
+        x, z, B, C, dt = five BitLinear projections of u (one RMS_PERI + int8
+                         quantization shared by five ternary GEMMs)
+        x, B, C        = SiLU(causal conv + bias) per sequence (x's conv is fused into
+                         the scan's staging; B and C go through the conv kernel)
+        y              = faithful scan: per-head A_log [H], P = d_head, G groups, D skip
+        out            = out_proj(RMSNorm(y * SiLU(z), eps) * gamma)
+
+    params: w_x [inner, d], w_z [inner, d], w_B [G*N, d], w_C [G*N, d], w_dt [H, d],
+    w_out [d, inner], conv_w [inner + 2*G*N, K], conv_b [inner + 2*G*N], a_log [H],
+    d_skip [H], norm_w [inner]; shape keys H, P, N, G and optional eps (1e-5).
+    Activations run in `dtype` (f32 by default, the reference's).
+    """
+
+    def __init__(self, params: dict, device="cuda", rms_input: bool = True, dtype=torch.float32):
+        self.H, self.P, self.N, self.G = (int(params[k]) for k in ("H", "P", "N", "G"))
+        self.inner = self.H * self.P
+        self.gs = self.G * self.N
+        self.eps = float(params.get("eps", 1e-5))
+        self.dtype = dtype
+        self.proj = [BitLinear(params[k], device, rms_input=rms_input)
+                     for k in ("w_x", "w_z", "w_B", "w_C", "w_dt")]
+        self.out_proj = BitLinear(params["w_out"], device, rms_input=rms_input)
+        self.d_model = self.proj[0].in_features
+        f32 = dict(dtype=torch.float32, device=device)
+        cw = torch.as_tensor(params["conv_w"], **f32)
+        cb = torch.as_tensor(params["conv_b"], **f32)
+        self.K = cw.shape[1]
+        i, g = self.inner, self.gs
+        self.conv_w = [cw[:i].contiguous(), cw[i:i + g].contiguous(), cw[i + g:].contiguous()]
+        self.conv_b = [cb[:i].contiguous(), cb[i:i + g].contiguous(), cb[i + g:].contiguous()]
+        self.a_log = torch.as_tensor(params["a_log"], **f32)
+        self.d_skip = torch.as_tensor(params["d_skip"], **f32)
+        self.norm_w = torch.as_tensor(params["norm_w"], **f32)
+        self.views = ops.LinearViewArray([p.view_entry() for p in self.proj], device)
+        self._ws = {}
+
+    def _project(self, u: torch.Tensor) -> list:
+        """One quantization, five ternary GEMMs (GEMV for <= 8 rows)."""
+        m = u.shape[0]
+        q, s, r = self.proj[0].workspace(m, u.device)
+        st = _stream()
+        call("nsosx_quantize_act_i8", _p(u), ops._dt(u), m, self.d_model, 8, 1, _p(q), _p(s),
+             _p(r), st)
+        outs = []
+        for p in self.proj:
+            y = torch.empty((m, p.out_features), dtype=self.dtype, device=u.device)
+            call("nsosx_ternary_gemm", _p(q), _p(s), _p(p.packed), p.weight_scale, m,
+                 p.in_features, p.out_features, _p(p.magnitude), _p(p.bias), _p(y),
+                 _DT[self.dtype], None, st)
+            outs.append(y)
+        return outs
+
+    def forward(self, u: torch.Tensor, cu_seqlens: torch.Tensor, initial_state=None,
+                final_state=None) -> dict:
+        """u [T, d_model] over the packed ragged batch cu_seqlens (int32 [S+1])."""
+        ops._dev(cu_seqlens, "cu_seqlens", torch.int32)
+        xv, z, Bv, Cv, dt = self._project(u)
+        Bc = ops.conv1d_causal(Bv, self.conv_w[1], cu_seqlens, self.conv_b[1], True)
+        Cc = ops.conv1d_causal(Cv, self.conv_w[2], cu_seqlens, self.conv_b[2], True)
+        y, fin = ops.conv_scan_fwd(xv, self.conv_w[0], self.conv_b[0], dt, self.a_log, Bc, Cc,
+                                   self.d_skip, None, cu_seqlens, self.H, self.P, self.N, self.G,
+                                   initial_state=initial_state, want_final=True)
+        if final_state is not None:
+            final_state.copy_(fin)
+        normed = ops.rmsnorm_gated(y, z, self.norm_w, eps=self.eps)
+        out = self.out_proj.forward(normed, out_dtype=self.dtype)
+        return {"out": out, "x": xv, "z": z, "B": Bc, "C": Cc, "dt": dt, "y": y,
+                "normed": normed, "final_state": fin}
+
+    def new_decode_state(self, rows: int, device) -> dict:
+        """Zero recurrent state [R, inner, N] and conv rings [R, K-1, channels]."""
+        f32 = dict(dtype=torch.float32, device=device)
+        taps = max(self.K - 1, 1)
+        return {"state": torch.zeros((rows, self.inner, self.N), **f32),
+                "ring": [torch.zeros((rows, taps, c), **f32)
+                         for c in (self.inner, self.gs, self.gs)]}
+
+    def step(self, u: torch.Tensor, dec: dict) -> torch.Tensor:
+        """One decode token per row: u [R, d_model]; updates dec's state and rings in place."""
+        xv, z, Bv, Cv, dt = self._project(u)
+        rings = dec["ring"] if self.K > 1 else [None] * 3
+        xc = ops.conv_step(xv, self.conv_w[0], self.conv_b[0], rings[0])
+        Bc = ops.conv_step(Bv, self.conv_w[1], self.conv_b[1], rings[1])
+        Cc = ops.conv_step(Cv, self.conv_w[2], self.conv_b[2], rings[2])
+        y = ops.selective_scan_step(xc, dt, self.a_log, Bc, Cc, self.d_skip, None, dec["state"],
+                                    self.H, self.P, self.N, self.G)
+        normed = ops.rmsnorm_gated(y, z, self.norm_w, eps=self.eps)
+        return self.out_proj.forward(normed, out_dtype=self.dtype)
+
+    def capture_step(self, u_static: torch.Tensor, dec: dict):
+        """Records one decode step into a HIP graph (torch.cuda.CUDAGraph on ROCm).
+
+        Returns (graph, out): graph.replay() reruns the step on the current contents of
+        u_static and dec, writing `out`.  The step launches only kernels (no copies or
+        memsets) on the capturing stream, so the graph holds kernel nodes only."""
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self.step(u_static, {"state": dec["state"].clone(),
+                                 "ring": [r.clone() for r in dec["ring"]]})  # warm the pools
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = self.step(u_static, dec)
+        return g, out
