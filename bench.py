@@ -101,6 +101,44 @@ def bench_layer(torch, dev, steps, warmup):
     return T, wall, stages, params, inp
 
 
+def bench_mamba2_decode(torch, dev, rows=1, reps=50):
+    """Faithful Mamba-2 decode step (d_model 1024, 32 heads x 64, N 16, conv 4), eager vs one
+    HIP-graph replay per step: 11 kernels per token, so the step is launch-bound."""
+    from reimagined_amd.layers import Mamba2Block
+    rng = np.random.default_rng(41)
+    d, H, P, N, G, K = 1024, 32, 64, 16, 1, 4
+    inner, gs = H * P, G * N
+    w = lambda n, k: rng.standard_normal((n, k)).astype(np.float32)
+    params = {"w_x": w(inner, d), "w_z": w(inner, d), "w_B": w(gs, d), "w_C": w(gs, d),
+              "w_dt": w(H, d), "w_out": w(d, inner),
+              "conv_w": (rng.standard_normal((inner + 2 * gs, K)) * 0.5).astype(np.float32),
+              "conv_b": np.zeros(inner + 2 * gs, np.float32),
+              "a_log": rng.standard_normal(H).astype(np.float32),
+              "d_skip": np.ones(H, np.float32), "norm_w": np.ones(inner, np.float32),
+              "H": H, "P": P, "N": N, "G": G}
+    blk = Mamba2Block(params, dev)
+    dec = blk.new_decode_state(rows, dev)
+    u = torch.randn((rows, d), device=dev)
+    for _ in range(3):
+        blk.step(u, dec)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        blk.step(u, dec)
+    torch.cuda.synchronize()
+    eager_us = (time.perf_counter() - t0) / reps * 1e6
+    g, _ = blk.capture_step(u, dec)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    graph_us = (time.perf_counter() - t0) / reps * 1e6
+    return {"rows": rows, "eager_us_per_step": round(eager_us, 1),
+            "graph_us_per_step": round(graph_us, 1), "kernels_per_step": 11}
+
+
 def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=32):
     """Algorithmic work of each layer kernel per launch (bytes or int8 ops)."""
     work = {
@@ -307,6 +345,8 @@ def main():
         _log(f"decode gemv {extra['decode_gemv_c3_m1']}")
         extra["decode_step_c5"] = bench_decode_step(torch, dev)
         _log(f"decode step {extra['decode_step_c5']}")
+        extra["mamba2_decode_step"] = bench_mamba2_decode(torch, dev)
+        _log(f"mamba2 decode step {extra['mamba2_decode_step']}")
         sc = stages.get("conv_scan")
         if sc:
             _, work = layer_roofline(T, {"conv_scan": sc})

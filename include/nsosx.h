@@ -131,8 +131,10 @@ typedef struct nsosx_linear_view {
  * role of launch_grouped_decode_projections (include/cuda/kernels.cuh:27-29).
  * Group g multiplies q + g*q_stride (int8 [M, inputs]) with views[g] and
  * writes y + g*y_stride elements ([M, outputs], y_dtype); act_scale + g *
- * scale_stride holds the group's M scales.  M <= 8.  views_dev: device array
- * of `groups` descriptors (the caller uploads it once and reuses it). */
+ * scale_stride holds the group's M scales (zero strides share one input
+ * across the groups, as the decode projections of one token do).  M <= 8.
+ * views_dev: device array of `groups` descriptors (the caller uploads it once
+ * and reuses it). */
 int nsosx_grouped_gemv(const nsosx_linear_view* views_dev, int groups, const int8_t* q,
                        int64_t q_stride, const float* act_scale, int64_t scale_stride, int M,
                        void* y, int64_t y_stride, int y_dtype, void* stream);

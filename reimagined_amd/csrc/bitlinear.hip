@@ -72,6 +72,34 @@ __global__ __launch_bounds__(64) void rms_inv_kernel(const void* __restrict__ x,
     inv[row] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
 }
 
+// Few rows (decode): a workgroup per row stages the row in LDS with coalesced
+// 16-byte loads, then one lane takes the in-order sum from LDS, so the row's
+// load latency is paid once instead of once per four loads.  K <= 8192.
+constexpr int kRmsSmallMaxK = 8192;
+
+template <int DT>
+__global__ __launch_bounds__(256) void rms_inv_small_kernel(const void* __restrict__ x, int K,
+                                                            float eps, float* __restrict__ inv) {
+    __shared__ __align__(16) float s_row[kRmsSmallMaxK];
+    const int row = blockIdx.x;
+    const int64_t base = (int64_t)row * K;
+    for (int k = threadIdx.x; k < K; k += 256) s_row[k] = load_act<DT>(x, base + k);
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    const int body = K & ~3;
+    float sum = 0.0f;
+    for (int k = 0; k < body; k += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(s_row + k);
+        sum = __fadd_rn(sum, __fmul_rn(v.x, v.x));
+        sum = __fadd_rn(sum, __fmul_rn(v.y, v.y));
+        sum = __fadd_rn(sum, __fmul_rn(v.z, v.z));
+        sum = __fadd_rn(sum, __fmul_rn(v.w, v.w));
+    }
+    for (int k = body; k < K; ++k) sum = __fmaf_rn(s_row[k], s_row[k], sum);
+    const float mean = __fdiv_rn(sum, static_cast<float>(K > 1 ? K : 1));
+    inv[row] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
+}
+
 // ===========================================================================
 // Per-row absmax quantization, one wave per row.
 //   m = max|x|; s = q_max / (m + 1e-8f); act_scale = (m + 1e-8f) / q_max;
@@ -195,7 +223,10 @@ static int launch_quantize(const void* x, int M, int K, int bits, int rms_input,
                            float* act_scale, float* rms_ws, hipStream_t st) {
     const float qm = q_max_for_bits(bits);
     const int elem = DT == NSOSX_F32 ? 4 : 2;
-    if (rms_input) {
+    if (rms_input && M <= 1024 && K <= kRmsSmallMaxK) {
+        hipLaunchKernelGGL((rms_inv_small_kernel<DT>), dim3(M), dim3(256), 0, st, x, K, 1e-6f,
+                           rms_ws);
+    } else if (rms_input) {
         const bool rvec = ((int64_t)K * elem) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
         if (rvec)
             hipLaunchKernelGGL((rms_inv_kernel<DT, true>), dim3((M + 63) / 64), dim3(64), 0, st, x,

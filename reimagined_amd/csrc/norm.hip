@@ -47,17 +47,37 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const void* __restric
         const float v = load_act<DT>(y, base + j);
         return GATED ? v * silu_exact(load_act<DT>(z, base + j)) : v;
     };
+    // four strided elements per lane per step: four independent loads in flight
     float sum = 0.0f;
-    for (int j = lane; j < dim; j += kWave) {
-        const float g = value(j);
+    int j0 = lane;
+    for (; j0 + 3 * kWave < dim; j0 += 4 * kWave) {
+        float g[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) g[u] = value(j0 + u * kWave);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sum = __fmaf_rn(g[u], g[u], sum);
+    }
+    for (; j0 < dim; j0 += kWave) {
+        const float g = value(j0);
         sum = __fmaf_rn(g, g, sum);
     }
     sum = wave_sum(sum);
     const float inv = 1.0f / sqrtf(sum / static_cast<float>(dim) + eps);
-    for (int j = lane; j < dim; j += kWave) {
-        float o = value(j) * inv;
-        if (gamma) o = o * gamma[j];
-        store_act<ODT>(out, base + j, o);
+    j0 = lane;
+    for (; j0 + 3 * kWave < dim; j0 += 4 * kWave) {
+        float o[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) o[u] = value(j0 + u * kWave) * inv;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (gamma) o[u] = o[u] * gamma[j0 + u * kWave];
+            store_act<ODT>(out, base + j0 + u * kWave, o[u]);
+        }
+    }
+    for (; j0 < dim; j0 += kWave) {
+        float o = value(j0) * inv;
+        if (gamma) o = o * gamma[j0];
+        store_act<ODT>(out, base + j0, o);
     }
 }
 

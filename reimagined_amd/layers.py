@@ -304,12 +304,21 @@ class Mamba2Block:
         self._ws = {}
 
     def _project(self, u: torch.Tensor) -> list:
-        """One quantization, five ternary GEMMs (GEMV for <= 8 rows)."""
+        """One quantization, then the five ternary projections: one grouped GEMV launch
+        for <= 8 rows (launch_grouped_decode_projections' role), else five GEMMs."""
         m = u.shape[0]
         q, s, r = self.proj[0].workspace(m, u.device)
         st = _stream()
         call("nsosx_quantize_act_i8", _p(u), ops._dt(u), m, self.d_model, 8, 1, _p(q), _p(s),
              _p(r), st)
+        if m <= 8:
+            widest = max(p.out_features for p in self.proj)
+            y = torch.empty((len(self.proj), m * widest), dtype=self.dtype, device=u.device)
+            # every group reads the same codes and scales: zero strides
+            call("nsosx_grouped_gemv", self.views.ptr, len(self.proj), _p(q), 0, _p(s), 0, m,
+                 _p(y), m * widest, _DT[self.dtype], st)
+            return [y[g, :m * p.out_features].view(m, p.out_features)
+                    for g, p in enumerate(self.proj)]
         outs = []
         for p in self.proj:
             y = torch.empty((m, p.out_features), dtype=self.dtype, device=u.device)

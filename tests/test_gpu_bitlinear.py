@@ -35,7 +35,8 @@ def test_quantize_matches_reference_golden(dev, orc):
             np.testing.assert_array_equal(s.cpu().numpy(), g[f"{name}__b{bits}__scales"])
 
 
-@pytest.mark.parametrize("m,k", [(1, 16), (5, 1003), (33, 768), (7, 4096), (3, 8200), (64, 2048)])
+@pytest.mark.parametrize("m,k", [(1, 16), (5, 1003), (33, 768), (7, 4096), (3, 8200), (64, 2048),
+                                 (1500, 1024), (1100, 1003)])
 @pytest.mark.parametrize("rms", [False, True])
 def test_quantize_random_f32(dev, orc, m, k, rms):
     rng = np.random.default_rng(m * 1000 + k)
@@ -48,9 +49,10 @@ def test_quantize_random_f32(dev, orc, m, k, rms):
 
 
 @pytest.mark.parametrize("rms", [False, True])
-def test_quantize_bf16_input(dev, orc, rms):
+@pytest.mark.parametrize("m", [37, 1200])
+def test_quantize_bf16_input(dev, orc, rms, m):
     rng = np.random.default_rng(3)
-    x = rng.standard_normal((37, 1024)).astype(np.float32)
+    x = rng.standard_normal((m, 1024)).astype(np.float32)
     xb = torch.from_numpy(x).to(torch.bfloat16)
     q, s = ops.quantize_activations_bitnet(xb.to(dev), 8, rms_input=rms)
     xf = xb.float().numpy()
