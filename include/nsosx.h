@@ -58,6 +58,40 @@ const char* nsosx_version(void);
  * w: float [N, K] host; packed: uint32 [N*K/16] host. */
 int nsosx_pack_ternary(const float* w, int N, int K, uint32_t* packed, float* weight_scale);
 
+/* Edge linear pack ("DGE1" v3 with the "EGI3" SHA-256 trailer, or legacy v2),
+ * the reference's on-disk BitLinear format: JambaModel::load_edge_linear_pack
+ * (src/jamba.cpp:1447-1620, field order 1345-1389, validation 556-616).  One
+ * descriptor per layer; every vector is a byte offset into the caller's
+ * buffer (zero-copy), the packed words in the format the GEMM/GEMV read. */
+typedef struct nsosx_edge_layer {
+    int32_t in_features;
+    int32_t out_features;
+    int32_t use_bias;
+    int32_t sensitive;        /* 1: the layer also carries fp32 weights */
+    float weight_scale;
+    uint64_t packed_words;    /* ceil(in * out / 16) */
+    uint64_t packed_offset;   /* uint32 [packed_words] */
+    uint64_t magnitude_offset;/* f32 [out] */
+    uint64_t bias_offset;     /* f32 [out] when use_bias */
+    uint64_t alpha_offset;    /* f32 [in] (flat_alpha) */
+    uint64_t beta_offset;     /* f32 [in] (flat_beta) */
+    uint64_t sensitive_offset;/* f32 [out * in] when sensitive */
+} nsosx_edge_layer;
+
+/* Host parse + validation of a pack held in memory: magic, version, the v3
+ * trailer (magic, payload length, SHA-256 of the payload), exact vector
+ * lengths, finite values, positive finite weight_scale, no reserved code 3
+ * (NSOSX_ERR_RESERVED), no trailing payload.  With more layers than
+ * max_layers it returns NSOSX_ERR_OVERFLOW and the count in *num_layers (so
+ * layers may be NULL with max_layers 0 to query it). */
+int nsosx_edge_pack_parse(const uint8_t* data, uint64_t size, nsosx_edge_layer* layers,
+                          int max_layers, int* num_layers, uint32_t* version);
+
+/* SHA-256 (FIPS 180-4) of a host buffer as 64 lowercase hex digits plus NUL,
+ * the digest the edge pack trailer carries (integrity::sha256_file_prefix,
+ * src/sha256.cpp:221). */
+int nsosx_sha256_hex(const uint8_t* data, uint64_t size, char* hex_out);
+
 /* BitNetAdapter::unpack_weights_microsoft_style_to_i8
  * (src/bitnet_adapter.cpp:590-606): codes int8 [n] host. */
 int nsosx_unpack_ternary(const uint32_t* packed, int64_t n, int8_t* codes);

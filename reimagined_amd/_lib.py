@@ -47,6 +47,8 @@ SIGNATURES = {
     "nsosx_rmsnorm_gated": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp, _i, _vp]),
     "nsosx_add_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp, _vp, _vp]),
     "nsosx_conv_step": (_i, [_vp, _i, _i64, _i, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _vp]),
+    "nsosx_edge_pack_parse": (_i, [_vp, ctypes.c_uint64, _vp, _i, _vp, _vp]),
+    "nsosx_sha256_hex": (_i, [_vp, ctypes.c_uint64, _vp]),
 }
 
 STATUS = {0: "OK", 1: "INVALID", 2: "OVERFLOW", 3: "RESERVED", 4: "LAUNCH"}
