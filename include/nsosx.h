@@ -269,10 +269,27 @@ int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, int experts,
 /* Weighted combine in ascending expert order (src/jamba.cpp:3947-3969):
  * out[r] = sum over the row's selected experts, lowest id first, of
  * expert_out[slot] * weights[r, e], starting from 0.
- * expert_out [slots, dim] (in_dtype), out [rows, dim] (out_dtype). */
+ * expert_out [slots, dim] (in_dtype), out [rows, dim] (out_dtype).
+ * slot_of NULL: the slot of (row r, choice i) is r * k + i. */
 int nsosx_moe_combine(const void* expert_out, int in_dtype, const int32_t* slot_of,
                       const int32_t* selected, const float* weights, int rows, int experts, int k,
                       int dim, void* out, int out_dtype, void* stream);
+
+/* Sparse MoE decode, the role of launch_moe_sparse_decode
+ * (src/cuda/moe_kernels.cu:786-795) with forward_moe's semantics
+ * (src/jamba.cpp:3865-3972): for each row and each of its k routed experts
+ * (selected [rows, k], weights [rows, experts] from nsosx_moe_route), the
+ * expert's up BitLinear -> squared ReLU -> down BitLinear as grouped GEMVs
+ * over (row, expert) pairs, then the ascending-expert weighted combine.  x:
+ * [rows, dim] (x_dtype); out [rows, dim] (out_dtype); rows * k <= 65535.
+ * workspace: device, nsosx_moe_sparse_decode_workspace(rows, k, dim, hidden)
+ * bytes. */
+int64_t nsosx_moe_sparse_decode_workspace(int rows, int k, int dim, int hidden);
+int nsosx_moe_sparse_decode(const nsosx_linear_view* up_views,
+                            const nsosx_linear_view* down_views, int experts, int k,
+                            const int32_t* selected, const float* weights, const void* x,
+                            int x_dtype, int rows, int dim, int hidden, int rms_input,
+                            void* workspace, void* out, int out_dtype, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Row norms of the hybrid block and the decode conv ring.

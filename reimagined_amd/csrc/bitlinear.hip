@@ -346,7 +346,7 @@ __device__ __forceinline__ void gemv_dot(uint4 w, const uint32_t xa[MT][4][4], i
 // register index is static); offsets left once a lane holds one value are a
 // plain butterfly, and of the lanes holding copies the one with those bits
 // clear writes.
-template <int MT, int STEPS, int YDT, bool ACC_OUT>
+template <int MT, int STEPS, int YDT, bool ACC_OUT, bool SQRELU = false>
 __device__ __forceinline__ void gemv_finish(int (&part)[STEPS][MT], const GemvProblem& pb,
                                             const float* __restrict__ act_scale, int M, void* y,
                                             int32_t* acc_out, int lr, int lpr, int sub, int rpw,
@@ -391,8 +391,12 @@ __device__ __forceinline__ void gemv_finish(int (&part)[STEPS][MT], const GemvPr
                         if (ACC_OUT) acc_out[(int64_t)mi * pb.N + n] = part[j][mi];
                         if (y) {
                             const float comb = __fmul_rn(act_scale[mi], pb.ws);
-                            store_act<YDT>(y, (int64_t)mi * pb.N + n,
-                                           dequant(part[j][mi], comb, pb.mag, pb.bias, n));
+                            float v = dequant(part[j][mi], comb, pb.mag, pb.bias, n);
+                            if (SQRELU) {
+                                v = v > 0.0f ? v : 0.0f;
+                                v = __fmul_rn(v, v);
+                            }
+                            store_act<YDT>(y, (int64_t)mi * pb.N + n, v);
                         }
                     }
                 }
@@ -405,7 +409,7 @@ __device__ __forceinline__ void gemv_finish(int (&part)[STEPS][MT], const GemvPr
 // weight loads of the next D items in flight, across round and block
 // boundaries.  The activation fragment stays in registers while K <= 64 * lpr
 // (one round); longer rows reload it at each round.
-template <int MT, int YDT, bool ACC_OUT, bool AL>
+template <int MT, int YDT, bool ACC_OUT, bool AL, bool SQRELU = false>
 __device__ __forceinline__ void gemv_body_impl(const GemvProblem& pb,
                                                const int8_t* __restrict__ q,
                                                const float* __restrict__ act_scale, int M,
@@ -461,23 +465,23 @@ __device__ __forceinline__ void gemv_body_impl(const GemvProblem& pb,
                 gemv_dot<MT>(cur, xa, part[s]);
             }
         }
-        gemv_finish<MT, STEPS, YDT, ACC_OUT>(part, pb, act_scale, M, y, acc_out, lr, lpr, sub,
+        gemv_finish<MT, STEPS, YDT, ACC_OUT, SQRELU>(part, pb, act_scale, M, y, acc_out, lr, lpr, sub,
                                              rpw, blk * rows_per_block);
     }
 }
 
-template <int MT, int YDT, bool ACC_OUT>
+template <int MT, int YDT, bool ACC_OUT, bool SQRELU = false>
 __device__ __forceinline__ void gemv_body_long(const GemvProblem& pb,
                                                const int8_t* __restrict__ q,
                                                const float* __restrict__ act_scale, int M,
                                                void* y, int32_t* acc_out, int wave_id,
                                                int num_waves) {
     if ((pb.K & 63) == 0)
-        gemv_body_impl<MT, YDT, ACC_OUT, true>(pb, q, act_scale, M, y, acc_out, wave_id,
-                                               num_waves);
+        gemv_body_impl<MT, YDT, ACC_OUT, true, SQRELU>(pb, q, act_scale, M, y, acc_out, wave_id,
+                                                       num_waves);
     else
-        gemv_body_impl<MT, YDT, ACC_OUT, false>(pb, q, act_scale, M, y, acc_out, wave_id,
-                                                num_waves);
+        gemv_body_impl<MT, YDT, ACC_OUT, false, SQRELU>(pb, q, act_scale, M, y, acc_out, wave_id,
+                                                        num_waves);
 }
 
 template <int MT, int YDT, bool ACC_OUT>
@@ -489,21 +493,26 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvProblem pb, const int8_t*
     gemv_body_long<MT, YDT, ACC_OUT>(pb, q, act_scale, M, y, acc_out, wave_id, num_waves);
 }
 
-template <int MT, int YDT>
+// Group g multiplies views[view_sel ? view_sel[g] : g] with activation rows
+// q + (g / q_div) * q_stride (q_div > 1: consecutive groups share one input,
+// e.g. the k experts a decode token is routed to).
+template <int MT, int YDT, bool SQRELU>
 __global__ __launch_bounds__(256) void grouped_gemv_kernel(const nsosx_linear_view* views,
+                                                           const int32_t* __restrict__ view_sel,
                                                            const int8_t* __restrict__ q,
-                                                           int64_t q_stride,
+                                                           int64_t q_stride, int q_div,
                                                            const float* __restrict__ act_scale,
                                                            int64_t scale_stride, int M, void* y,
                                                            int64_t y_stride) {
     const int g = blockIdx.y;
-    const nsosx_linear_view v = views[g];
+    const nsosx_linear_view v = views[view_sel ? view_sel[g] : g];
     GemvProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
     const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int num_waves = gridDim.x * 4;
+    const int gi = g / q_div;
     char* yb = static_cast<char*>(y) + g * y_stride * (YDT == NSOSX_F32 ? 4 : 2);
-    gemv_body_long<MT, YDT, false>(pb, q + g * q_stride, act_scale + g * scale_stride, M, yb,
-                                   nullptr, wave_id, num_waves);
+    gemv_body_long<MT, YDT, false, SQRELU>(pb, q + gi * q_stride, act_scale + gi * scale_stride,
+                                           M, yb, nullptr, wave_id, num_waves);
 }
 
 static int gemv_steps_host(int M) { return M <= 2 ? 16 : (M <= 4 ? 8 : 4); }
@@ -1438,11 +1447,13 @@ extern "C" int nsosx_grouped_gemv(const nsosx_linear_view* views_dev, int groups
     const dim3 grid(per_group, groups), block(256);
 #define NSOSX_GG(MT)                                                                          \
     if (y_dtype == NSOSX_F32)                                                                 \
-        hipLaunchKernelGGL((grouped_gemv_kernel<MT, NSOSX_F32>), grid, block, 0, st, views_dev, \
-                           q, q_stride, act_scale, scale_stride, M, y, y_stride);            \
+        hipLaunchKernelGGL((grouped_gemv_kernel<MT, NSOSX_F32, false>), grid, block, 0, st,    \
+                           views_dev, nullptr, q, q_stride, 1, act_scale, scale_stride, M, y,  \
+                           y_stride);                                                         \
     else                                                                                      \
-        hipLaunchKernelGGL((grouped_gemv_kernel<MT, NSOSX_BF16>), grid, block, 0, st,        \
-                           views_dev, q, q_stride, act_scale, scale_stride, M, y, y_stride);
+        hipLaunchKernelGGL((grouped_gemv_kernel<MT, NSOSX_BF16, false>), grid, block, 0, st,   \
+                           views_dev, nullptr, q, q_stride, 1, act_scale, scale_stride, M, y,  \
+                           y_stride);
     if (M == 1) { NSOSX_GG(1) }
     else if (M == 2) { NSOSX_GG(2) }
     else if (M <= 4) { NSOSX_GG(4) }
@@ -1497,4 +1508,84 @@ extern "C" int nsosx_find_reserved_code(const uint32_t* packed, int64_t n_codes,
     }
     hipLaunchKernelGGL(finish_reserved_kernel, dim3(1), dim3(1), 0, st, fb);
     return check_launch("find_reserved_code");
+}
+
+// ===========================================================================
+// Sparse MoE decode (launch_moe_sparse_decode, src/cuda/moe_kernels.cu:786-795;
+// CPU semantics JambaBlock::forward_moe, src/jamba.cpp:3865-3972): for every
+// decode row and each of its k routed experts, up BitLinear -> squared ReLU ->
+// down BitLinear as grouped GEMVs over (row, expert) pairs, then the weighted
+// combine in ascending expert order.  The row is quantized once for all of its
+// experts.  Workspace layout (256-byte aligned sections): q1 int8 [rows, dim],
+// s1, r1 f32 [rows], h f32 [rows*k, hidden], q2 int8 [rows*k, hidden],
+// s2, r2 f32 [rows*k], o f32 [rows*k, dim].
+// ===========================================================================
+namespace {
+struct SparseWs {
+    int8_t* q1; float* s1; float* r1; float* h; int8_t* q2; float* s2; float* r2; float* o;
+    int64_t bytes;
+};
+SparseWs sparse_layout(char* base, int rows, int k, int dim, int hidden) {
+    int64_t off = 0;
+    auto take = [&](int64_t n) {
+        const int64_t at = off;
+        off += (n + 255) & ~int64_t(255);
+        return base ? base + at : nullptr;
+    };
+    const int64_t slots = (int64_t)rows * k;
+    SparseWs w;
+    w.q1 = reinterpret_cast<int8_t*>(take((int64_t)rows * dim));
+    w.s1 = reinterpret_cast<float*>(take(4LL * rows));
+    w.r1 = reinterpret_cast<float*>(take(4LL * rows));
+    w.h = reinterpret_cast<float*>(take(4 * slots * hidden));
+    w.q2 = reinterpret_cast<int8_t*>(take(slots * hidden));
+    w.s2 = reinterpret_cast<float*>(take(4 * slots));
+    w.r2 = reinterpret_cast<float*>(take(4 * slots));
+    w.o = reinterpret_cast<float*>(take(4 * slots * dim));
+    w.bytes = off;
+    return w;
+}
+}  // namespace
+
+extern "C" int64_t nsosx_moe_sparse_decode_workspace(int rows, int k, int dim, int hidden) {
+    if (rows <= 0 || k <= 0 || dim <= 0 || hidden <= 0) return -1;
+    return sparse_layout(nullptr, rows, k, dim, hidden).bytes;
+}
+
+extern "C" int nsosx_moe_sparse_decode(const nsosx_linear_view* up_views,
+                                       const nsosx_linear_view* down_views, int experts, int k,
+                                       const int32_t* selected, const float* weights,
+                                       const void* x, int x_dtype, int rows, int dim, int hidden,
+                                       int rms_input, void* workspace, void* out, int out_dtype,
+                                       void* stream) {
+    if (!up_views || !down_views || !selected || !weights || !x || !workspace || !out)
+        return fail(NSOSX_ERR_INVALID, "moe_sparse_decode: null pointer");
+    if (rows <= 0 || experts <= 0 || k <= 0 || k > 8 || k > experts || dim <= 0 || hidden <= 0 ||
+        (int64_t)rows * k > 65535)
+        return fail(NSOSX_ERR_INVALID, "moe_sparse_decode: bad shape (rows * k <= 65535)");
+    if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype))
+        return fail(NSOSX_ERR_INVALID, "moe_sparse_decode: bad dtype");
+    const SparseWs w = sparse_layout(static_cast<char*>(workspace), rows, k, dim, hidden);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int rc = nsosx_quantize_act_i8(x, x_dtype, rows, dim, 8, rms_input, w.q1, w.s1, w.r1, stream);
+    if (rc) return rc;
+    const int slots = rows * k;
+    const dim3 block(256);
+    const dim3 grid_up(std::max(1, std::min(512, 2048 / slots)), slots);
+    // up: group g = (row g / k, expert selected[g]); the k groups of a row share its codes
+    hipLaunchKernelGGL((grouped_gemv_kernel<1, NSOSX_F32, true>), grid_up, block, 0, st, up_views,
+                       selected, w.q1, (int64_t)dim, k, w.s1, (int64_t)1, 1, w.h, (int64_t)hidden);
+    rc = check_launch("moe_sparse_decode");
+    if (rc) return rc;
+    rc = nsosx_quantize_act_i8(w.h, NSOSX_F32, slots, hidden, 8, rms_input, w.q2, w.s2, w.r2,
+                               stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL((grouped_gemv_kernel<1, NSOSX_F32, false>), grid_up, block, 0, st,
+                       down_views, selected, w.q2, (int64_t)hidden, 1, w.s2, (int64_t)1, 1, w.o,
+                       (int64_t)dim);
+    rc = check_launch("moe_sparse_decode");
+    if (rc) return rc;
+    // slot of (row r, choice i) is r * k + i: the combine's identity map
+    return nsosx_moe_combine(w.o, NSOSX_F32, nullptr, selected, weights, rows, experts, k, dim,
+                             out, out_dtype, stream);
 }

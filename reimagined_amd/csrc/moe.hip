@@ -156,7 +156,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ e
     const int kk = k < 8 ? k : 8;
     for (int i = 0; i < kk; ++i) {
         es[i] = selected[(int64_t)r * k + i];
-        ss[i] = slot_of[(int64_t)r * k + i];
+        ss[i] = slot_of ? slot_of[(int64_t)r * k + i] : r * k + i;
     }
     // insertion sort by expert id (k is tiny)
     for (int i = 1; i < kk; ++i) {
@@ -209,7 +209,7 @@ extern "C" int nsosx_moe_combine(const void* expert_out, int in_dtype, const int
                                  const int32_t* selected, const float* weights, int rows,
                                  int experts, int k, int dim, void* out, int out_dtype,
                                  void* stream) {
-    if (!expert_out || !slot_of || !selected || !weights || !out)
+    if (!expert_out || !selected || !weights || !out)
         return fail(NSOSX_ERR_INVALID, "moe_combine: null pointer");
     if (rows <= 0 || rows > 65535 * 256 || experts <= 0 || experts > kMaxExperts || k <= 0 ||
         k > 8 || k > experts || dim <= 0)

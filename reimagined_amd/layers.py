@@ -222,6 +222,27 @@ class MoEFFN:
         return {"out": out, **{n: b[n] for n in ("weights", "selected", "counts", "offsets",
                                                  "perm", "slot_of", "h", "o")}}
 
+    def decode(self, x: torch.Tensor, logits: torch.Tensor, out_dtype=None) -> dict:
+        """Sparse decode for a few rows (launch_moe_sparse_decode's role): routing on the
+        device, then grouped GEMVs over the (row, routed expert) pairs and the combine."""
+        rows = x.shape[0]
+        b = self._buffers(rows, x.device)
+        e, k = self.experts, self.k
+        st = _stream()
+        call("nsosx_moe_route", _p(logits), rows, e, k, _p(b["weights"]), _p(b["selected"]),
+             _p(b["counts"]), _p(b["offsets"]), _p(b["perm"]), _p(b["slot_of"]),
+             _p(b["route_ws"]), st)
+        nbytes = int(ops.lib().nsosx_moe_sparse_decode_workspace(rows, k, self.d_model,
+                                                                 self.d_ff))
+        ws = b.get("sparse_ws")
+        if ws is None or ws.numel() < nbytes:
+            ws = b["sparse_ws"] = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        out = torch.empty((rows, self.d_model), dtype=out_dtype or x.dtype, device=x.device)
+        call("nsosx_moe_sparse_decode", self.up_views.ptr, self.down_views.ptr, e, k,
+             _p(b["selected"]), _p(b["weights"]), _p(x), ops._dt(x), rows, self.d_model,
+             self.d_ff, int(self.rms_input), _p(ws), _p(out), _DT[out.dtype], st)
+        return {"out": out, "weights": b["weights"], "selected": b["selected"], "workspace": ws}
+
 
 class HybridBlock:
     """JambaBlock::forward with a Mamba core and an MoE feed-forward (src/jamba.cpp:3158-3375):
