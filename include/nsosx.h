@@ -247,6 +247,8 @@ int nsosx_selective_scan_step(const void* x, const void* dt, const float* A_log,
  *   slot_of int32 [rows, k]: slot_of[r, i] is the slot of selected[r, i]
  *   (rank order), so perm[slot_of[r, i]] == r.
  *   workspace: int32, nsosx_moe_route_workspace(rows, E) elements.
+ * counts, offsets, perm, slot_of and workspace all NULL: selection only
+ * (weights and selected, one launch), what the sparse decode consumes.
  * E <= 64, k <= E. */
 int64_t nsosx_moe_route_workspace(int rows, int experts);
 int nsosx_moe_route(const float* logits, int rows, int experts, int k, float* weights,

@@ -187,7 +187,11 @@ extern "C" int64_t nsosx_moe_route_workspace(int rows, int experts) {
 extern "C" int nsosx_moe_route(const float* logits, int rows, int experts, int k, float* weights,
                                int32_t* selected, int32_t* counts, int32_t* offsets, int32_t* perm,
                                int32_t* slot_of, int32_t* workspace, void* stream) {
-    if (!logits || !weights || !selected || !counts || !offsets || !perm || !slot_of || !workspace)
+    // counts/offsets/perm/slot_of/workspace all NULL: selection only (the sparse decode
+    // reads selected and weights and needs no expert-major permutation)
+    const bool select_only = !counts && !offsets && !perm && !slot_of && !workspace;
+    if (!logits || !weights || !selected ||
+        (!select_only && (!counts || !offsets || !perm || !slot_of || !workspace)))
         return fail(NSOSX_ERR_INVALID, "moe_route: null pointer");
     if (rows <= 0 || experts <= 0 || experts > kMaxExperts || k <= 0 || k > experts || k > 8)
         return fail(NSOSX_ERR_INVALID, "moe_route: need rows > 0, 0 < k <= min(E, 8), E <= 64");
@@ -196,6 +200,7 @@ extern "C" int nsosx_moe_route(const float* logits, int rows, int experts, int k
     const int nblocks = (rows + kRouteBlock - 1) / kRouteBlock;
     hipLaunchKernelGGL(route_rows_kernel, dim3((rows + 255) / 256), dim3(256), 0, st, logits, rows,
                        experts, k, weights, selected);
+    if (select_only) return check_launch("moe_route");
     hipLaunchKernelGGL(route_count_kernel, dim3(nblocks), dim3(kRouteBlock), 0, st, selected, rows,
                        experts, k, workspace);
     hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(64), 0, st, workspace, nblocks, experts,

@@ -304,6 +304,7 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
 constexpr int kQuadTC = 32;       // tokens per B/C chunk
 constexpr int kQuadCh = 16;       // channels per wave
 constexpr int kQuadMaxW = 4;
+constexpr int kQuadRedStride = 20;  // floats per channel row of the readout transpose
 
 __device__ __forceinline__ float quad_bcast(float v, int k) {
     // quad_perm [k, k, k, k]
@@ -379,18 +380,25 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
     constexpr int NP = 4 * SPL;                 // padded states per channel
     constexpr int BCN = NP / 2;                 // states per staging lane (two lanes per row)
     __shared__ __align__(16) float s_bc[2][kQuadTC][NP];
+    __shared__ __align__(16) float s_red[kQuadCh * kQuadRedStride];
     __shared__ int s_pick;
 
     const int lane = threadIdx.x;
     const int D = H * P;
     const int GN = G * N;
     const int q = lane & 3;
+    // readout transpose slots: channel row of kQuadRedStride floats, state lane j's
+    // partial of token k at 4 j + k (row stride padded against bank conflicts)
+    const int red_w = (lane >> 2) * kQuadRedStride + 4 * q;
+    const int red_r = (lane >> 2) * kQuadRedStride + q;
     int rank, cblk;
     quad_work_item(rank, cblk);
     const int c = cblk * kQuadCh + (lane >> 2);
     const int h = c / P;
     const int grp = (h * G) / H;
-    const int seq = quad_pick_sequence(cu_seqlens, num_seqs, total_tokens, rank, &s_pick);
+    // uniform across the wave: keeps the token bases in scalar registers
+    const int seq = __builtin_amdgcn_readfirstlane(
+        quad_pick_sequence(cu_seqlens, num_seqs, total_tokens, rank, &s_pick));
     const int t0 = min(max(cu_seqlens[seq], 0), total_tokens);
     const int t1 = min(max(cu_seqlens[seq + 1], t0), total_tokens);
     const int tlast = total_tokens - 1;
@@ -494,22 +502,26 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
     // token (running; past the data the hardware returns 0), raw words one group ahead
     constexpr uint32_t ES = ADT == NSOSX_F32 ? 4 : 2;
     const uint32_t xs = static_cast<uint32_t>(x_stride) * ES, zs = static_cast<uint32_t>(z_stride) * ES;
+    // Each group's resources start at the group's first token (scalar arithmetic:
+    // the group base is uniform) and keep the true end of the data as their
+    // extent, so the lane offsets stay constant and reads past the end return 0.
     const uint32_t Tn = static_cast<uint32_t>(total_tokens);
-    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (Tn - 1) * xs + D * ES);
-    const __amdgpu_buffer_rsrc_t rdt = make_rsrc(dt, Tn * H * ES);
-    const __amdgpu_buffer_rsrc_t rz = make_rsrc(GATE ? z : x, GATE ? (Tn - 1) * zs + D * ES : 0);
-    const __amdgpu_buffer_rsrc_t ry = make_rsrc(y, Tn * D * ES);
-    const uint32_t tq = static_cast<uint32_t>(t0 + q);
-    uint32_t ox = tq * xs + c * ES, odt = (tq * H + h) * ES, oz = tq * zs + c * ES;
-    uint32_t oy = (tq * D + c) * ES;
+    const uint32_t ex = (Tn - 1) * xs + D * ES, edt = Tn * H * ES, ey = Tn * D * ES;
+    const uint32_t ez = GATE ? (Tn - 1) * zs + D * ES : 0;
+    const uint32_t lx = q * xs + c * ES, ldt = (q * H + h) * ES, lz = q * zs + c * ES;
+    const uint32_t ly = (q * D + c) * ES;
+    auto group_rsrc = [](const void* base, uint32_t extent, uint32_t off) {
+        // extents are below 2^31 (the host checks), so the signed max stays scalar
+        const int left = max(static_cast<int>(extent) - static_cast<int>(off), 0);
+        return make_rsrc(static_cast<const char*>(base) + off, static_cast<uint32_t>(left));
+    };
+    uint32_t tnext = static_cast<uint32_t>(t0);  // first token of the group to prefetch
     raw_t xr = 0, dtr = 0, zr = 0;
     auto prefetch_tok = [&]() {
-        xr = buf_load_raw<ADT>(rx, ox);
-        dtr = buf_load_raw<ADT>(rdt, odt);
-        if (GATE) zr = buf_load_raw<ADT>(rz, oz);
-        ox += 4 * xs;
-        odt += 4 * H * ES;
-        oz += 4 * zs;
+        xr = buf_load_raw<ADT>(group_rsrc(x, ex, tnext * xs), lx);
+        dtr = buf_load_raw<ADT>(group_rsrc(dt, edt, tnext * H * ES), ldt);
+        if (GATE) zr = buf_load_raw<ADT>(group_rsrc(z, ez, tnext * zs), lz);
+        tnext += 4;
     };
 
     float xprev = 0.0f;  // raw x of this lane's token in the previous group (0 before t0)
@@ -524,8 +536,8 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
         __syncthreads();
         const int tc = min(kQuadTC, t1 - tb);
         for (int r0 = 0; r0 < tc; r0 += 4) {
-            const int tg = tb + r0 + q;
-            const bool valid = tg < t1;
+            const int tgrp = tb + r0;  // first token of the group (uniform)
+            const bool valid = q < t1 - tgrp;
             // B/C of the group's four rows first: the reads overlap the staging math
             // (rows past tc were staged as zero; delta = 0 keeps the state there)
             float bq[4][SPL], cq[4][SPL];
@@ -545,19 +557,17 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
             // masked, so the group has no divergent branch) -------------------------
             float xv;
             if (CONV) {
-                // tap j multiplies x[tg - 3 + j]: lag d = 3 - j, from this group (lane
-                // q - d) when d <= q, else from the previous group (lane q - d + 4)
+                // tap j multiplies x[tg - 3 + j]: lag d = 3 - j, read from lane
+                // p = (q - d) mod 4, which is this group's token when q >= d and the
+                // previous group's when q < d.  The source lane picks what it hands
+                // out (its current x when p < 4 - d, else its previous one), so the
+                // reader's lag shift folds into the multiply-add as a DPP operand.
                 float acc = 0.0f;
 #pragma unroll
                 for (int j = 0; j < kQuadMaxW; ++j) {
                     const int d = kQuadMaxW - 1 - j;
-                    float xl = xcur;
-                    if (d > 0) {
-                        const float fc = quad_back(xcur, d);
-                        const float fp = quad_back(xprev, d);
-                        xl = q >= d ? fc : fp;
-                    }
-                    acc = __fmaf_rn(cw[j], xl, acc);
+                    const float src = d == 0 ? xcur : (q < 4 - d ? xcur : xprev);
+                    acc = __fmaf_rn(d == 0 ? src : quad_back(src, d), cw[j], acc);
                 }
                 xv = silu_fast(acc + cb);  // finite; an invalid token's dl = 0 cancels it
             } else {
@@ -586,24 +596,16 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
                 }
                 part[k] = p;
             }
-            // ---- 4x4 transpose-reduce: lane q ends with token r0 + q --------------
-            const bool hi2 = (q & 2) != 0;
-            const float s0 = hi2 ? part[0] : part[2];
-            const float s1 = hi2 ? part[1] : part[3];
-            const float k0 = hi2 ? part[2] : part[0];
-            const float k1 = hi2 ? part[3] : part[1];
-            const float m0 = k0 + dpp_xor2(s0);
-            const float m1 = k1 + dpp_xor2(s1);
-            const bool hi1 = (q & 1) != 0;
-            const float send = hi1 ? m0 : m1;
-            const float keep = hi1 ? m1 : m0;
-            const float tot = keep + dpp_xor1(send);
+            // ---- 4x4 transpose through the wave's LDS slice: lane q sums token
+            // r0 + q over the channel's four state lanes (LDS operations of one wave
+            // complete in order, so the reads see this group's writes) ------------
+            *reinterpret_cast<float4*>(&s_red[red_w]) = make_float4(part[0], part[1], part[2], part[3]);
+            const float tot = ((s_red[red_r] + s_red[red_r + 4]) + s_red[red_r + 8]) + s_red[red_r + 12];
             if (valid) {
                 float out = __fmaf_rn(dsk, xv, tot);
                 if (GATE) out = out * silu_fast(raw_to_f32<ADT>(zraw));
-                buf_store_act<ADT>(ry, oy, out);
+                buf_store_act<ADT>(group_rsrc(y, ey, static_cast<uint32_t>(tgrp) * D * ES), ly, out);
             }
-            oy += 4 * D * ES;
         }
     }
     if (final_state) {

@@ -230,8 +230,7 @@ class MoEFFN:
         e, k = self.experts, self.k
         st = _stream()
         call("nsosx_moe_route", _p(logits), rows, e, k, _p(b["weights"]), _p(b["selected"]),
-             _p(b["counts"]), _p(b["offsets"]), _p(b["perm"]), _p(b["slot_of"]),
-             _p(b["route_ws"]), st)
+             None, None, None, None, None, st)
         nbytes = int(ops.lib().nsosx_moe_sparse_decode_workspace(rows, k, self.d_model,
                                                                  self.d_ff))
         ws = b.get("sparse_ws")

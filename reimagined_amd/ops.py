@@ -276,19 +276,26 @@ def selective_scan_step(x, dt, a_log, B, C, D, z, state, H, P, N, G):
 
 # ---- MoE ------------------------------------------------------------------------
 
-def moe_route(logits: torch.Tensor, k: int = 2) -> dict:
-    """MoERouter::forward from logits + forward_moe's ordered dispatch, on the device."""
+def moe_route(logits: torch.Tensor, k: int = 2, select_only: bool = False) -> dict:
+    """MoERouter::forward from logits + forward_moe's ordered dispatch, on the device.
+    select_only: weights and selected only (one launch), as the sparse decode needs."""
     _dev(logits, "logits", torch.float32)
     rows, e = logits.shape
     dev = logits.device
     out = {
         "weights": torch.empty((rows, e), dtype=torch.float32, device=dev),
         "selected": torch.empty((rows, k), dtype=torch.int32, device=dev),
+    }
+    if select_only:
+        call("nsosx_moe_route", _p(logits), rows, e, k, _p(out["weights"]), _p(out["selected"]),
+             None, None, None, None, None, _stream())
+        return out
+    out.update({
         "counts": torch.empty(e, dtype=torch.int32, device=dev),
         "offsets": torch.empty(e + 1, dtype=torch.int32, device=dev),
         "perm": torch.empty(rows * k, dtype=torch.int32, device=dev),
         "slot_of": torch.empty((rows, k), dtype=torch.int32, device=dev),
-    }
+    })
     ws = torch.empty(max(1, int(lib().nsosx_moe_route_workspace(rows, e))), dtype=torch.int32,
                      device=dev)
     call("nsosx_moe_route", _p(logits), rows, e, k, _p(out["weights"]), _p(out["selected"]),

@@ -39,6 +39,28 @@ def test_route_matches_oracle(dev, orc, rows, E, k):
         np.testing.assert_array_equal(seg, sel[:, i])
 
 
+@pytest.mark.parametrize("rows,E,k", [(1, 8, 2), (37, 16, 4)])
+def test_route_select_only_matches_full(dev, rows, E, k):
+    rng = np.random.default_rng(rows * 3 + E)
+    logits = torch.from_numpy(rng.standard_normal((rows, E)).astype(np.float32)).to(dev)
+    full = ops.moe_route(logits, k)
+    sel = ops.moe_route(logits, k, select_only=True)
+    assert set(sel) == {"weights", "selected"}
+    torch.testing.assert_close(sel["selected"], full["selected"], rtol=0, atol=0)
+    torch.testing.assert_close(sel["weights"], full["weights"], rtol=0, atol=0)
+
+
+def test_route_partial_null_outputs_rejected(dev):
+    logits = torch.zeros((4, 8), dtype=torch.float32, device=dev)
+    w = torch.empty((4, 8), dtype=torch.float32, device=dev)
+    s = torch.empty((4, 2), dtype=torch.int32, device=dev)
+    counts = torch.empty(8, dtype=torch.int32, device=dev)
+    rc = ops.lib().nsosx_moe_route(logits.data_ptr(), 4, 8, 2, w.data_ptr(),
+                                   s.data_ptr(), counts.data_ptr(), None, None, None, None, None)
+    assert rc != 0
+    assert b"null pointer" in ops.lib().nsosx_last_error()
+
+
 def test_route_ties_prefer_lower_index(dev, orc):
     logits = np.zeros((4, 8), np.float32)
     logits[1, [2, 5]] = 1.0
