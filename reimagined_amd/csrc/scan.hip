@@ -525,6 +525,16 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
     };
 
     float xprev = 0.0f;  // raw x of this lane's token in the previous group (0 before t0)
+    // the group whose readout is pending: its validity, conv output, raw gate and base token
+    bool pv_valid = false;
+    float pv_xv = 0.0f;
+    raw_t pv_z = 0;
+    int pv_t = 0;
+    auto finish_readout = [&](float tot) {
+        float out = __fmaf_rn(dsk, pv_xv, tot);
+        if (GATE) out = out * silu_fast(raw_to_f32<ADT>(pv_z));
+        buf_store_act<ADT>(group_rsrc(y, ey, static_cast<uint32_t>(pv_t) * D * ES), ly, out);
+    };
     if (t0 < t1) {
         prefetch_bc(t0);
         prefetch_tok();
@@ -548,6 +558,9 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
                     bq[k][i] = s_bc[0][r0 + k][q * SPL + i];
                     cq[k][i] = s_bc[1][r0 + k][q * SPL + i];
                 }
+            // the previous group's readout partials (written at the end of that group)
+            const float rd0 = s_red[red_r], rd1 = s_red[red_r + 4];
+            const float rd2 = s_red[red_r + 8], rd3 = s_red[red_r + 12];
             // tokens past the sequence feed only later tokens past it: no mask needed on x
             const float xcur = raw_to_f32<ADT>(xr);
             const float dtcur = raw_to_f32<ADT>(dtr);
@@ -596,18 +609,21 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
                 }
                 part[k] = p;
             }
-            // ---- 4x4 transpose through the wave's LDS slice: lane q sums token
-            // r0 + q over the channel's four state lanes (LDS operations of one wave
-            // complete in order, so the reads see this group's writes) ------------
+            // ---- 4x4 transpose through the wave's LDS slice, one group behind:
+            // lane q sums token q of the previous group over the channel's four state
+            // lanes (its partials were read at the top of this group), then this
+            // group's partials are written (LDS operations of one wave complete in
+            // order, so the next group's reads see them) -------------------------
+            if (pv_valid) finish_readout(((rd0 + rd1) + rd2) + rd3);
             *reinterpret_cast<float4*>(&s_red[red_w]) = make_float4(part[0], part[1], part[2], part[3]);
-            const float tot = ((s_red[red_r] + s_red[red_r + 4]) + s_red[red_r + 8]) + s_red[red_r + 12];
-            if (valid) {
-                float out = __fmaf_rn(dsk, xv, tot);
-                if (GATE) out = out * silu_fast(raw_to_f32<ADT>(zraw));
-                buf_store_act<ADT>(group_rsrc(y, ey, static_cast<uint32_t>(tgrp) * D * ES), ly, out);
-            }
+            pv_valid = valid;
+            pv_xv = xv;
+            pv_z = zraw;
+            pv_t = tgrp;
         }
     }
+    if (pv_valid)
+        finish_readout(((s_red[red_r] + s_red[red_r + 4]) + s_red[red_r + 8]) + s_red[red_r + 12]);
     if (final_state) {
 #pragma unroll
         for (int i = 0; i < SPL; ++i) {
