@@ -259,6 +259,41 @@ def bench_decode_gemv(torch, dev, m=1, sets=128, reps=5):
             "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def bench_decode_gemv_sweep(torch, dev, ms=(1, 2, 4, 8, 16, 32), reps=10):
+    """Config 3's decode GEMV at M = 1..32 through the dispatching entry point, on one tall
+    weight matrix of 128 config-3 weight sets stacked in N (N = 128 * 8192, K = 2048; 537 MB,
+    so every launch streams the weights from HBM)."""
+    from reimagined_amd._lib import call
+    from reimagined_amd.ops import _p, _stream
+    K, N = 2048, 128 * 8192
+    packed = torch.randint(-2**31, 2**31 - 1, (N * K // 16,), dtype=torch.int32, device=dev)
+    packed = (packed ^ ((packed & (packed >> 1) & 0x55555555) << 1)).contiguous()
+    rng = np.random.default_rng(32)
+    out = {}
+    for m in ms:
+        q = torch.from_numpy(rng.integers(-127, 128, size=(m, K)).astype(np.int8)).to(dev)
+        s = torch.full((m,), 0.01, dtype=torch.float32, device=dev)
+        y = torch.empty((m, N), dtype=torch.bfloat16, device=dev)
+
+        def run():
+            call("nsosx_ternary_gemm", _p(q), _p(s), _p(packed), 1.0, m, K, N, None, None, _p(y),
+                 1, None, _stream())
+        run()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            run()
+        b.record()
+        torch.cuda.synchronize()
+        t = a.elapsed_time(b) / reps
+        bytes_ = N * K / 4 + m * K + m * N * 2
+        gbs = bytes_ / (t / 1e3) / 1e9
+        out[f"m{m}"] = {"ms": round(t, 4), "gbs": round(gbs, 1),
+                        "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    del packed
+    return out
+
+
 def bench_decode_step(torch, dev, reps=8):
     from reimagined_amd import ops, workloads
     _, dec = workloads.config5(rows=16, experts=2, d_model=64, d_ff=64)
@@ -343,6 +378,8 @@ def main():
         _log(f"prefill gemm {extra['prefill_gemm_c3']}")
         extra["decode_gemv_c3_m1"] = bench_decode_gemv(torch, dev, m=1)
         _log(f"decode gemv {extra['decode_gemv_c3_m1']}")
+        extra["decode_gemv_c3_sweep"] = bench_decode_gemv_sweep(torch, dev)
+        _log(f"decode gemv sweep {extra['decode_gemv_c3_sweep']}")
         extra["decode_step_c5"] = bench_decode_step(torch, dev)
         _log(f"decode step {extra['decode_step_c5']}")
         extra["mamba2_decode_step"] = bench_mamba2_decode(torch, dev)

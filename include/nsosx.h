@@ -125,7 +125,10 @@ int nsosx_quantize_act_i8(const void* x, int x_dtype, int M, int K, int bits, in
  *              then * magnitude[n] and + bias[n] (one fma when both are given)
  * Replaces launch_bitnet_gemm / launch_bitnet_gemv_scaled /
  * launch_bitnet_apply_act_scales_kernel (include/cuda/kernels.cuh:106-110).
- * M <= 8 runs the packed-weight streaming GEMV, larger M the int8 MFMA GEMM.
+ * M = 1, 2 run the packed-weight streaming GEMV; 3 <= M <= 32 with K in
+ * {1024, 2048, 4096} (ceil(M/16) * K <= 4096) the skinny MFMA kernel (one
+ * decoded word feeds 16 tokens); other M <= 8 the GEMV; larger M the int8 MFMA
+ * GEMM.
  *   y: [M, N] f32 or bf16 (y_dtype), may be NULL when acc_out is given.
  *   acc_out: int32 [M, N] or NULL (exposes the accumulators).
  *   magnitude, bias: f32 [N] or NULL. */
@@ -134,7 +137,9 @@ int nsosx_ternary_gemm(const int8_t* q, const float* act_scale, const uint32_t* 
                        const float* bias, void* y, int y_dtype, int32_t* acc_out, void* stream);
 
 /* Same contract, forcing one kernel: path 0 = streaming GEMV (M <= 8),
- * path 1 = MFMA GEMM (any M).  For tests and measurement. */
+ * path 1 = MFMA GEMM (any M), path 2 = skinny MFMA (2 <= M <= 32, K in
+ * {1024, 2048, 4096}, ceil(M/16) * K <= 4096, M * N < 2^29).  For tests and
+ * measurement. */
 int nsosx_ternary_gemm_path(const int8_t* q, const float* act_scale, const uint32_t* packed,
                             float weight_scale, int M, int K, int N, const float* magnitude,
                             const float* bias, void* y, int y_dtype, int32_t* acc_out,

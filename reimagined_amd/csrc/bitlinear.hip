@@ -1319,6 +1319,224 @@ static void launch_gemm_t(const GemmProblem& pb, const int8_t* q, const float* a
 }
 
 // ===========================================================================
+// Skinny GEMM for decode batches (2 <= M <= 32 token rows) on
+// v_mfma_i32_16x16x64_i8.  A tile is 16 weight rows x 16 tokens; lane (g, li) =
+// (lane / 16, lane % 16) feeds row li of the tile with the g-th quarter of the
+// row's packed words, one word (16 codes) per MFMA step, so its words for
+// consecutive steps are consecutive in memory and four steps come in one
+// 16-byte load.  The decoded word goes to the MFMA in unpack order; the
+// activation fragments (token li, the same 16 k) are byte-transposed into that
+// order once per workgroup and held in LDS (16 bytes per lane per step and m
+// tile, M_pad x K bytes).  A wave walks its tiles as a flat stream of 16-byte
+// items with kSkDepth loads in flight across tile boundaries; the dot costs one
+// decode per word whatever M is, so the kernel stays HBM-bound where the VALU
+// GEMV's per-row dot products do not.  Needs K % 256 == 0 and MT * K <= 4096.
+// MFMA 16x16x64 lane layout: A row = lane % 16 and B column = lane % 16, k group
+// lane / 16 (16 consecutive k); accumulator r is C[4 (lane / 16) + r][lane % 16].
+// ===========================================================================
+constexpr int kSkDepth = 8;
+constexpr int kSkMaxLds = 64 * 1024;
+
+// K = 256 * LT with LT (16-byte loads per lane per tile) in {4, 8, 16}; the
+// outputs are addressed with 32-bit byte offsets below the 2^31 drop offset
+static bool skinny_ok(int M, int K, int N) {
+    const int mt = (M + 15) / 16;
+    return M >= 2 && M <= 32 && (K == 1024 || K == 2048 || K == 4096) &&
+           (int64_t)mt * K * 16 <= kSkMaxLds && (int64_t)M * N * 4 < ((int64_t)1 << 31);
+}
+
+// The steady state is straight-line code (the tile loop's back edge is its only
+// branch), so the compiler keeps exact counts of the loads in flight: loads
+// past the last tile are clamped into the matrix, and stores of rows past N or
+// tokens past M go to an offset past the output's buffer extent, where the
+// hardware drops them.
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+
+template <int MT, int LT, int YDT, bool ACC_OUT, bool SQRELU, bool VEC4>
+__device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t* __restrict__ q,
+                                            const float* __restrict__ act_scale, int M, void* y,
+                                            int32_t* acc_out, int wave_id, int num_waves,
+                                            char* lds) {
+    constexpr int Q = 4 * LT;                       // words per lane per tile (MFMA steps)
+    constexpr int D = LT < kSkDepth ? LT : kSkDepth; // loads in flight per lane
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int g = lane >> 4, li = lane & 15;
+    const int W16 = pb.K >> 4;
+    // activation fragments: fragment (s, mt) of lane l at ((s * MT + mt) * 64 + l) * 16;
+    // step s covers k = 64 s .. 64 s + 63, k group g its 16 k from 64 s + 16 g
+    constexpr int nfrag = Q * MT * 64;
+    for (int f = tid; f < nfrag; f += 256) {
+        const int l = f & 63;
+        const int smt = f >> 6;
+        const int mt = smt % MT, st = smt / MT;
+        const int m = mt * 16 + (l & 15);
+        const int k0 = 16 * (4 * st + (l >> 4));
+        uint32_t d[4] = {0u, 0u, 0u, 0u};
+        if (m < M) {
+            const uint4 v = *reinterpret_cast<const uint4*>(q + (int64_t)m * pb.K + k0);
+            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+        }
+        uint32_t e[4];
+        transpose16(d, e);
+        *reinterpret_cast<uint4*>(lds + f * 16) = make_uint4(e[0], e[1], e[2], e[3]);
+    }
+    __syncthreads();
+    const int tiles = (pb.N + 15) >> 4;
+    if (wave_id >= tiles) return;
+    const int my_tiles = (tiles - 1 - wave_id) / num_waves + 1;
+    // Load j of a tile: the four lanes (g = 0..3) of row li read its 64 bytes
+    // 64 j .. 64 j + 63 (words 16 j + 4 g .. +3), so a wave load covers 16 row
+    // segments of 64 bytes.  Lane (g, li) then holds k group u of steps 4 j + g;
+    // a 4 x 4 transpose across the four 16-lane rows (v_permlane32_swap, then
+    // v_permlane16_swap) turns that into k group g of steps 4 j + u.
+    auto row_src = [&](int ti) {
+        const int tile = wave_id + min(ti, my_tiles - 1) * num_waves;
+        const int n = min(tile * 16 + li, pb.N - 1);
+        return pb.packed + (int64_t)n * W16 + 4 * g;
+    };
+    constexpr uint32_t ES = YDT == NSOSX_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t ry =
+        make_rsrc(y, y ? static_cast<uint32_t>(M * pb.N) * ES : 0u);
+    const __amdgpu_buffer_rsrc_t racc =
+        make_rsrc(acc_out, ACC_OUT ? static_cast<uint32_t>(M * pb.N) * 4u : 0u);
+    float comb[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+        comb[mt] = __fmul_rn(act_scale[min(mt * 16 + li, M - 1)], pb.ws);
+
+    const uint32_t* src = row_src(0);
+    uint4 ring[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) ring[d] = load_stream16(src + 16 * d);
+    const char* frag = lds + lane * 16;
+    for (int ti = 0; ti < my_tiles; ++ti) {
+        // two m tiles' fragments (2 KB per lane at K = 2048) would not fit in registers
+        // beside the ring: keep them in LDS, re-read per tile
+        if constexpr (MT > 1) asm volatile("" : "+v"(frag));
+        const uint32_t* nsrc = row_src(ti + 1);
+        v4i acc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < LT; ++j) {
+            const uint4 w = ring[j % D];
+            // the item D ahead: this tile's load j + D, or the next tile's
+            ring[j % D] = j + D < LT ? load_stream16(src + 16 * (j + D))
+                                     : load_stream16(nsrc + 16 * (j + D - LT));
+            // 4 x 4 transpose (16-lane row g, slot u) -> (row u, slot g)
+            const auto p02 = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
+            const auto p13 = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
+            const auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+            const auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+            const uint32_t words[4] = {p01[0], p01[1], p23[0], p23[1]};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                uint32_t wv[4];
+                unpack_word(words[u], wv);
+                const v4i aw = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const uint4 v =
+                        *reinterpret_cast<const uint4*>(frag + ((4 * j + u) * MT + mt) * 1024);
+                    acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        aw, v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w}, acc[mt], 0, 0, 0);
+                }
+            }
+        }
+        // lane holds outputs n = tile * 16 + 4 g + r of token mt * 16 + li
+        const int nb = (wave_id + ti * num_waves) * 16 + 4 * g;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int m = mt * 16 + li;
+            const int av[4] = {acc[mt].x, acc[mt].y, acc[mt].z, acc[mt].w};
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                v[r] = dequant(av[r], comb[mt], pb.mag, pb.bias, min(nb + r, pb.N - 1));
+                if (SQRELU) {
+                    v[r] = v[r] > 0.0f ? v[r] : 0.0f;
+                    v[r] = __fmul_rn(v[r], v[r]);
+                }
+            }
+            const uint32_t e = static_cast<uint32_t>(m * pb.N + nb);
+            if (VEC4) {
+                // N % 4 == 0: the lane's four outputs are one aligned vector, inside N
+                // exactly when its first one is
+                const bool ok = m < M && nb < pb.N;
+                if (ACC_OUT)
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        v4i{av[0], av[1], av[2], av[3]}, racc, ok ? e * 4u : 0x80000000u, 0, 0);
+                if (y) {
+                    const uint32_t off = ok ? e * ES : 0x80000000u;
+                    if constexpr (YDT == NSOSX_F32)
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            v4i{(int)__float_as_uint(v[0]), (int)__float_as_uint(v[1]),
+                                (int)__float_as_uint(v[2]), (int)__float_as_uint(v[3])},
+                            ry, off, 0, 0);
+                    else
+                        __builtin_amdgcn_raw_buffer_store_b64(
+                            v2u{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, ry, off, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bool ok = m < M && nb + r < pb.N;
+                    const uint32_t er = e + r;
+                    if (ACC_OUT)
+                        __builtin_amdgcn_raw_buffer_store_b32(av[r], racc,
+                                                              ok ? er * 4u : 0x80000000u, 0, 0);
+                    if (y) buf_store_act<YDT>(ry, ok ? er * ES : 0x80000000u, v[r]);
+                }
+            }
+        }
+        src = nsrc;
+    }
+}
+
+template <int MT, int LT, int YDT, bool ACC_OUT>
+__global__ __launch_bounds__(256) void skinny_kernel(GemvProblem pb, const int8_t* __restrict__ q,
+                                                     const float* __restrict__ act_scale, int M,
+                                                     void* y, int32_t* acc_out) {
+    extern __shared__ __align__(16) char lds_sk[];
+    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if ((pb.N & 3) == 0)
+        skinny_body<MT, LT, YDT, ACC_OUT, false, true>(pb, q, act_scale, M, y, acc_out, wave_id,
+                                                       gridDim.x * 4, lds_sk);
+    else
+        skinny_body<MT, LT, YDT, ACC_OUT, false, false>(pb, q, act_scale, M, y, acc_out, wave_id,
+                                                        gridDim.x * 4, lds_sk);
+}
+
+template <int MT, int YDT>
+static void launch_skinny_lt(const GemvProblem& pb, const int8_t* q, const float* as, int M,
+                             void* y, int32_t* acc, dim3 grid, size_t lds, hipStream_t st) {
+#define NSOSX_SK(LT)                                                                            \
+    if (acc)                                                                                    \
+        hipLaunchKernelGGL((skinny_kernel<MT, LT, YDT, true>), grid, dim3(256), lds, st, pb, q, as, \
+                           M, y, acc);                                                          \
+    else                                                                                        \
+        hipLaunchKernelGGL((skinny_kernel<MT, LT, YDT, false>), grid, dim3(256), lds, st, pb, q,    \
+                           as, M, y, acc);
+    if (pb.K == 1024) { NSOSX_SK(4) }
+    else if (pb.K == 2048) { NSOSX_SK(8) }
+    else { NSOSX_SK(16) }
+#undef NSOSX_SK
+}
+
+template <int YDT>
+static void launch_skinny_t(const GemvProblem& pb, const int8_t* q, const float* as, int M,
+                            void* y, int32_t* acc, hipStream_t st) {
+    const int tiles = (pb.N + 15) / 16;
+    // about 8 waves per CU in all; the LDS fragments (up to 64 KB) allow 2 workgroups
+    const int wgs = std::max(1, std::min((tiles + 3) / 4, 512));
+    const int mt = (M + 15) / 16;
+    const size_t lds = (size_t)mt * pb.K * 16;
+    if (mt == 1) launch_skinny_lt<1, YDT>(pb, q, as, M, y, acc, dim3(wgs), lds, st);
+    else launch_skinny_lt<2, YDT>(pb, q, as, M, y, acc, dim3(wgs), lds, st);
+}
+
+// ===========================================================================
 // Reserved-code scan (import check).
 // ===========================================================================
 __global__ void find_reserved_kernel(const uint32_t* __restrict__ packed, int64_t n_codes,
@@ -1386,6 +1604,13 @@ static int check_gemm_args(const int8_t* q, const float* as, const uint32_t* pac
     return NSOSX_OK;
 }
 
+// M = 1, 2: the VALU GEMV; 3 <= M <= 32 where the skinny MFMA path takes the
+// shape; other M <= 8: the GEMV; else the MFMA GEMM.
+static int ternary_gemm_auto_path(int M, int K, int N) {
+    if (M >= 3 && skinny_ok(M, K, N)) return 2;
+    return M <= 8 ? 0 : 1;
+}
+
 extern "C" int nsosx_ternary_gemm_path(const int8_t* q, const float* act_scale,
                                        const uint32_t* packed, float weight_scale, int M, int K,
                                        int N, const float* magnitude, const float* bias, void* y,
@@ -1393,9 +1618,17 @@ extern "C" int nsosx_ternary_gemm_path(const int8_t* q, const float* act_scale,
     int rc = check_gemm_args(q, act_scale, packed, weight_scale, M, K, N, y, y_dtype, acc_out);
     if (rc) return rc;
     if (path == 0 && M > 8) return fail(NSOSX_ERR_INVALID, "ternary_gemm: GEMV path needs M <= 8");
-    if (path != 0 && path != 1) return fail(NSOSX_ERR_INVALID, "ternary_gemm: bad path");
+    if (path < 0 || path > 2) return fail(NSOSX_ERR_INVALID, "ternary_gemm: bad path");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (path == 0) {
+    if (path == 2) {
+        if (!skinny_ok(M, K, N))
+            return fail(NSOSX_ERR_INVALID,
+                        "ternary_gemm: skinny path needs 2 <= M <= 32, K in {1024, 2048, 4096}, "
+                        "ceil(M / 16) * K <= 4096, M * N < 2^29");
+        GemvProblem pb{packed, magnitude, bias, weight_scale, N, K};
+        if (y_dtype == NSOSX_F32) launch_skinny_t<NSOSX_F32>(pb, q, act_scale, M, y, acc_out, st);
+        else launch_skinny_t<NSOSX_BF16>(pb, q, act_scale, M, y, acc_out, st);
+    } else if (path == 0) {
         GemvProblem pb{packed, magnitude, bias, weight_scale, N, K};
         if (y_dtype == NSOSX_F32) launch_gemv_t<NSOSX_F32>(pb, q, act_scale, M, y, acc_out, st);
         else launch_gemv_t<NSOSX_BF16>(pb, q, act_scale, M, y, acc_out, st);
@@ -1412,7 +1645,7 @@ extern "C" int nsosx_ternary_gemm(const int8_t* q, const float* act_scale, const
                                   const float* bias, void* y, int y_dtype, int32_t* acc_out,
                                   void* stream) {
     return nsosx_ternary_gemm_path(q, act_scale, packed, weight_scale, M, K, N, magnitude, bias, y,
-                                   y_dtype, acc_out, M <= 8 ? 0 : 1, stream);
+                                   y_dtype, acc_out, ternary_gemm_auto_path(M, K, N), stream);
 }
 
 extern "C" int nsosx_bitlinear_forward(const void* x, int x_dtype, const uint32_t* packed,

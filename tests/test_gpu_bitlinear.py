@@ -102,6 +102,25 @@ def test_mfma_gemm_more_shapes_bit_exact(dev, orc, m, n, k):
     _gemm_case(dev, orc, m, n, k, path=1, mag=(m % 2 == 0), bias=True)
 
 
+@pytest.mark.parametrize("m", [2, 3, 5, 8, 16, 17, 32])
+@pytest.mark.parametrize("n,k", [(768, 1024), (130, 2048), (9000, 1024), (37, 2048), (64, 4096),
+                                 (1, 1024)])
+def test_skinny_mfma_bit_exact(dev, orc, m, n, k):
+    """Decode-batch MFMA path: edge tiles in n, one and two m tiles, every K it accepts."""
+    if (m + 15) // 16 * k > 4096:
+        pytest.skip("outside the skinny path's LDS budget (ceil(M/16) * K <= 4096)")
+    _gemm_case(dev, orc, m, n, k, path=2, mag=(m % 2 == 1), bias=(n % 2 == 0))
+
+
+@pytest.mark.parametrize("m,k", [(4, 768), (4, 1040), (1, 1024), (33, 1024), (17, 4096)])
+def test_skinny_rejects_unsupported_shapes(dev, m, k):
+    q = torch.zeros((m, k), dtype=torch.int8, device=dev)
+    s = torch.ones(m, dtype=torch.float32, device=dev)
+    pk = torch.zeros(64 * k // 16, dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError, match="skinny"):
+        ops.ternary_gemm(q, s, pk, 1.0, 64, path=2)
+
+
 def test_gemm_dispatch_and_extremes(dev, orc):
     # |acc| = 127 * K at the extremes: int32 accumulation must not saturate or wrap
     k, n = 4096, 64
@@ -111,8 +130,8 @@ def test_gemm_dispatch_and_extremes(dev, orc):
     codes[1::2] = -1
     packed = orc.pack_codes(codes).view(np.uint32)
     s = np.ones(9, np.float32)
-    for path in (0, 1):
-        m = 8 if path == 0 else 9
+    for path in (0, 1, 2):
+        m = {0: 8, 1: 9, 2: 9}[path]
         y, acc = ops.ternary_gemm(torch.from_numpy(q[:m]).to(dev), torch.from_numpy(s[:m]).to(dev),
                                   torch.from_numpy(packed.view(np.int32)).to(dev), 1.0, n,
                                   want_acc=True, path=path)
