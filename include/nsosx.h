@@ -125,7 +125,7 @@ int nsosx_quantize_act_i8(const void* x, int x_dtype, int M, int K, int bits, in
  *              then * magnitude[n] and + bias[n] (one fma when both are given)
  * Replaces launch_bitnet_gemm / launch_bitnet_gemv_scaled /
  * launch_bitnet_apply_act_scales_kernel (include/cuda/kernels.cuh:106-110).
- * M = 1, 2 run the packed-weight streaming GEMV; 3 <= M <= 32 with K in
+ * M = 1 runs the packed-weight streaming GEMV; 2 <= M <= 32 with K in
  * {1024, 2048, 4096} (ceil(M/16) * K <= 4096) the skinny MFMA kernel (one
  * decoded word feeds 16 tokens); other M <= 8 the GEMV; larger M the int8 MFMA
  * GEMM.

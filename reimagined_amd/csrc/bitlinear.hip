@@ -493,9 +493,18 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvProblem pb, const int8_t*
     gemv_body_long<MT, YDT, ACC_OUT>(pb, q, act_scale, M, y, acc_out, wave_id, num_waves);
 }
 
+// A group of a grouped GEMV with M >= 2 rows that the skinny MFMA body takes:
+// K = 1024 or 2048 (its fragments fit the launch's 64 KB of LDS) and whole
+// 4-output vectors (N % 4 == 0, 16-byte aligned rows).
+__device__ __forceinline__ bool skinny_group(const nsosx_linear_view& v, const void* yb) {
+    return (v.inputs == 1024 || v.inputs == 2048) && (v.outputs & 3) == 0 &&
+           (reinterpret_cast<uintptr_t>(yb) & 15) == 0;
+}
+
 // Group g multiplies views[view_sel ? view_sel[g] : g] with activation rows
 // q + (g / q_div) * q_stride (q_div > 1: consecutive groups share one input,
-// e.g. the k experts a decode token is routed to).
+// e.g. the k experts a decode token is routed to).  skip_skinny: groups that
+// grouped_skinny_kernel takes are left to it.
 template <int MT, int YDT, bool SQRELU>
 __global__ __launch_bounds__(256) void grouped_gemv_kernel(const nsosx_linear_view* views,
                                                            const int32_t* __restrict__ view_sel,
@@ -503,14 +512,15 @@ __global__ __launch_bounds__(256) void grouped_gemv_kernel(const nsosx_linear_vi
                                                            int64_t q_stride, int q_div,
                                                            const float* __restrict__ act_scale,
                                                            int64_t scale_stride, int M, void* y,
-                                                           int64_t y_stride) {
+                                                           int64_t y_stride, int skip_skinny) {
     const int g = blockIdx.y;
     const nsosx_linear_view v = views[view_sel ? view_sel[g] : g];
+    char* yb = static_cast<char*>(y) + g * y_stride * (YDT == NSOSX_F32 ? 4 : 2);
+    if (skip_skinny && skinny_group(v, yb)) return;
     GemvProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
     const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int num_waves = gridDim.x * 4;
     const int gi = g / q_div;
-    char* yb = static_cast<char*>(y) + g * y_stride * (YDT == NSOSX_F32 ? 4 : 2);
     gemv_body_long<MT, YDT, false, SQRELU>(pb, q + gi * q_stride, act_scale + gi * scale_stride,
                                            M, yb, nullptr, wave_id, num_waves);
 }
@@ -1320,22 +1330,22 @@ static void launch_gemm_t(const GemmProblem& pb, const int8_t* q, const float* a
 
 // ===========================================================================
 // Skinny GEMM for decode batches (2 <= M <= 32 token rows) on
-// v_mfma_i32_16x16x64_i8.  A tile is 16 weight rows x 16 tokens; lane (g, li) =
-// (lane / 16, lane % 16) feeds row li of the tile with the g-th quarter of the
-// row's packed words, one word (16 codes) per MFMA step, so its words for
-// consecutive steps are consecutive in memory and four steps come in one
-// 16-byte load.  The decoded word goes to the MFMA in unpack order; the
-// activation fragments (token li, the same 16 k) are byte-transposed into that
-// order once per workgroup and held in LDS (16 bytes per lane per step and m
-// tile, M_pad x K bytes).  A wave walks its tiles as a flat stream of 16-byte
-// items with kSkDepth loads in flight across tile boundaries; the dot costs one
-// decode per word whatever M is, so the kernel stays HBM-bound where the VALU
-// GEMV's per-row dot products do not.  Needs K % 256 == 0 and MT * K <= 4096.
+// v_mfma_i32_16x16x64_i8.  A tile is 16 weight rows x 16 tokens (one or two m
+// tiles); MFMA step s covers k = 64 s .. 64 s + 63, and lane (g, li) =
+// (lane / 16, lane % 16) feeds row li of the tile with k group g of the step:
+// one packed word (16 codes) per step, decoded in registers and used in unpack
+// order.  The activation fragments (token li, the same 16 k) are byte-transposed
+// into that order once per workgroup (16 bytes per lane per step and m tile,
+// M_pad x K bytes of LDS); the first m tile's stay in registers up to K = 2048.
+// A wave streams its tiles with the next tile's loads in flight; the dot costs
+// one decode per word whatever M is, so the kernel stays HBM-bound where the
+// VALU GEMV's per-row dot products do not.  Needs K in {1024, 2048, 4096} and
+// ceil(M / 16) * K <= 4096.
 // MFMA 16x16x64 lane layout: A row = lane % 16 and B column = lane % 16, k group
 // lane / 16 (16 consecutive k); accumulator r is C[4 (lane / 16) + r][lane % 16].
 // ===========================================================================
-constexpr int kSkDepth = 8;
 constexpr int kSkMaxLds = 64 * 1024;
+constexpr size_t kGroupedSkinnyLds = 2 * 2048 * 16;  // one m tile at K <= 2048
 
 // K = 256 * LT with LT (16-byte loads per lane per tile) in {4, 8, 16}; the
 // outputs are addressed with 32-bit byte offsets below the 2^31 drop offset
@@ -1358,7 +1368,6 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
                                             int32_t* acc_out, int wave_id, int num_waves,
                                             char* lds) {
     constexpr int Q = 4 * LT;                       // words per lane per tile (MFMA steps)
-    constexpr int D = LT < kSkDepth ? LT : kSkDepth; // loads in flight per lane
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int g = lane >> 4, li = lane & 15;
@@ -1385,15 +1394,23 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
     const int tiles = (pb.N + 15) >> 4;
     if (wave_id >= tiles) return;
     const int my_tiles = (tiles - 1 - wave_id) / num_waves + 1;
-    // Load j of a tile: the four lanes (g = 0..3) of row li read its 64 bytes
-    // 64 j .. 64 j + 63 (words 16 j + 4 g .. +3), so a wave load covers 16 row
-    // segments of 64 bytes.  Lane (g, li) then holds k group u of steps 4 j + g;
-    // a 4 x 4 transpose across the four 16-lane rows (v_permlane32_swap, then
+    // A tile's 16 rows are one contiguous block of 16 * K / 4 bytes.  The wave
+    // reads it in LT loads of 1 KB (lane l: bytes 1024 j + 16 l), so every load
+    // instruction covers eight whole 128-byte lines, and passes it through its own
+    // LDS slice: 16-byte chunk c of row r sits at chunk c ^ (r % 16) of the row
+    // (conflict-free both ways).  Read j of lane (g, li) is row li's 64 bytes
+    // 64 j + 16 g (words 16 j + 4 g .. +3), i.e. k group u of steps 4 j + g; a
+    // 4 x 4 transpose across the four 16-lane rows (v_permlane32_swap, then
     // v_permlane16_swap) turns that into k group g of steps 4 j + u.
-    auto row_src = [&](int ti) {
+    constexpr int RB = 64 * LT;                     // bytes per weight row
+    char* stage = lds + MT * pb.K * 16 + (tid >> 6) * 16 * RB;
+    const int64_t last_word = (int64_t)pb.N * W16 - 4;
+    auto tile_src = [&](int ti) {
         const int tile = wave_id + min(ti, my_tiles - 1) * num_waves;
-        const int n = min(tile * 16 + li, pb.N - 1);
-        return pb.packed + (int64_t)n * W16 + 4 * g;
+        return (int64_t)tile * 16 * W16 + 4 * lane;
+    };
+    auto load_piece = [&](int64_t base, int j) {
+        return load_stream16(pb.packed + min(base + 256 * j, last_word));
     };
     constexpr uint32_t ES = YDT == NSOSX_F32 ? 4 : 2;
     const __amdgpu_buffer_rsrc_t ry =
@@ -1405,25 +1422,43 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
     for (int mt = 0; mt < MT; ++mt)
         comb[mt] = __fmul_rn(act_scale[min(mt * 16 + li, M - 1)], pb.ws);
 
-    const uint32_t* src = row_src(0);
-    uint4 ring[D];
+    uint4 ring[LT];
+    {
+        const int64_t b0 = tile_src(0);
 #pragma unroll
-    for (int d = 0; d < D; ++d) ring[d] = load_stream16(src + 16 * d);
+        for (int j = 0; j < LT; ++j) ring[j] = load_piece(b0, j);
+    }
     const char* frag = lds + lane * 16;
+    // the first m tile's fragments up to K = 2048 (512 bytes per lane) stay in
+    // registers for the whole stream; the rest are re-read from LDS per tile
+    constexpr bool kHold = LT <= 8;
+    uint4 held[kHold ? 4 * LT : 1];
+    if constexpr (kHold) {
+#pragma unroll
+        for (int st = 0; st < 4 * LT; ++st)
+            held[st] = *reinterpret_cast<const uint4*>(frag + st * MT * 1024);
+    }
     for (int ti = 0; ti < my_tiles; ++ti) {
-        // two m tiles' fragments (2 KB per lane at K = 2048) would not fit in registers
-        // beside the ring: keep them in LDS, re-read per tile
-        if constexpr (MT > 1) asm volatile("" : "+v"(frag));
-        const uint32_t* nsrc = row_src(ti + 1);
+        // this tile to the wave's LDS slice (in order with the reads below), then
+        // the next tile's loads into the ring
+#pragma unroll
+        for (int j = 0; j < LT; ++j) {
+            const int b = 1024 * j + 16 * lane;
+            const int r = b / RB, c = (b % RB) >> 4;
+            *reinterpret_cast<uint4*>(stage + r * RB + ((c ^ (r & 15)) << 4)) = ring[j];
+        }
+        {
+            const int64_t nb0 = tile_src(ti + 1);
+#pragma unroll
+            for (int j = 0; j < LT; ++j) ring[j] = load_piece(nb0, j);
+        }
         v4i acc[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < LT; ++j) {
-            const uint4 w = ring[j % D];
-            // the item D ahead: this tile's load j + D, or the next tile's
-            ring[j % D] = j + D < LT ? load_stream16(src + 16 * (j + D))
-                                     : load_stream16(nsrc + 16 * (j + D - LT));
+            const uint4 w = *reinterpret_cast<const uint4*>(
+                stage + li * RB + (((4 * j + g) ^ li) << 4));
             // 4 x 4 transpose (16-lane row g, slot u) -> (row u, slot g)
             const auto p02 = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
             const auto p13 = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
@@ -1438,7 +1473,9 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const uint4 v =
-                        *reinterpret_cast<const uint4*>(frag + ((4 * j + u) * MT + mt) * 1024);
+                        kHold && mt == 0
+                            ? held[(4 * j + u) % (kHold ? 4 * LT : 1)]
+                            : *reinterpret_cast<const uint4*>(frag + ((4 * j + u) * MT + mt) * 1024);
                     acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                         aw, v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w}, acc[mt], 0, 0, 0);
                 }
@@ -1490,8 +1527,37 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
                 }
             }
         }
-        src = nsrc;
     }
+}
+
+// Grouped decode GEMV for M >= 2 token rows, the groups skinny_group() accepts
+// (the launch reserves 64 KB of LDS); the others are left to a grouped_gemv_kernel
+// launch over the same groups.  The decision is uniform per workgroup.
+template <int YDT, bool SQRELU>
+__global__ __launch_bounds__(256) void grouped_skinny_kernel(const nsosx_linear_view* views,
+                                                             const int32_t* __restrict__ view_sel,
+                                                             const int8_t* __restrict__ q,
+                                                             int64_t q_stride, int q_div,
+                                                             const float* __restrict__ act_scale,
+                                                             int64_t scale_stride, int M, void* y,
+                                                             int64_t y_stride) {
+    extern __shared__ __align__(16) char lds_gsk[];
+    const int g = blockIdx.y;
+    const nsosx_linear_view v = views[view_sel ? view_sel[g] : g];
+    char* yb = static_cast<char*>(y) + g * y_stride * (YDT == NSOSX_F32 ? 4 : 2);
+    if (!skinny_group(v, yb)) return;
+    GemvProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
+    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int num_waves = gridDim.x * 4;
+    const int gi = g / q_div;
+    const int8_t* qg = q + gi * q_stride;
+    const float* sg = act_scale + gi * scale_stride;
+    if (pb.K == 1024)
+        skinny_body<1, 4, YDT, false, SQRELU, true>(pb, qg, sg, M, yb, nullptr, wave_id, num_waves,
+                                                     lds_gsk);
+    else
+        skinny_body<1, 8, YDT, false, SQRELU, true>(pb, qg, sg, M, yb, nullptr, wave_id, num_waves,
+                                                     lds_gsk);
 }
 
 template <int MT, int LT, int YDT, bool ACC_OUT>
@@ -1531,7 +1597,8 @@ static void launch_skinny_t(const GemvProblem& pb, const int8_t* q, const float*
     // about 8 waves per CU in all; the LDS fragments (up to 64 KB) allow 2 workgroups
     const int wgs = std::max(1, std::min((tiles + 3) / 4, 512));
     const int mt = (M + 15) / 16;
-    const size_t lds = (size_t)mt * pb.K * 16;
+    // activation fragments + one tile per wave (16 rows of K / 4 bytes)
+    const size_t lds = (size_t)(mt + 1) * pb.K * 16;
     if (mt == 1) launch_skinny_lt<1, YDT>(pb, q, as, M, y, acc, dim3(wgs), lds, st);
     else launch_skinny_lt<2, YDT>(pb, q, as, M, y, acc, dim3(wgs), lds, st);
 }
@@ -1604,10 +1671,10 @@ static int check_gemm_args(const int8_t* q, const float* as, const uint32_t* pac
     return NSOSX_OK;
 }
 
-// M = 1, 2: the VALU GEMV; 3 <= M <= 32 where the skinny MFMA path takes the
+// M = 1: the VALU GEMV; 2 <= M <= 32 where the skinny MFMA path takes the
 // shape; other M <= 8: the GEMV; else the MFMA GEMM.
 static int ternary_gemm_auto_path(int M, int K, int N) {
-    if (M >= 3 && skinny_ok(M, K, N)) return 2;
+    if (skinny_ok(M, K, N)) return 2;
     return M <= 8 ? 0 : 1;
 }
 
@@ -1678,19 +1745,35 @@ extern "C" int nsosx_grouped_gemv(const nsosx_linear_view* views_dev, int groups
     // wave strides over its view's row blocks
     const int per_group = std::max(4, std::min(512, 2048 / groups));
     const dim3 grid(per_group, groups), block(256);
-#define NSOSX_GG(MT)                                                                          \
+#define NSOSX_GG(MT, SKIP)                                                                    \
     if (y_dtype == NSOSX_F32)                                                                 \
         hipLaunchKernelGGL((grouped_gemv_kernel<MT, NSOSX_F32, false>), grid, block, 0, st,    \
                            views_dev, nullptr, q, q_stride, 1, act_scale, scale_stride, M, y,  \
-                           y_stride);                                                         \
+                           y_stride, SKIP);                                                   \
     else                                                                                      \
         hipLaunchKernelGGL((grouped_gemv_kernel<MT, NSOSX_BF16, false>), grid, block, 0, st,   \
                            views_dev, nullptr, q, q_stride, 1, act_scale, scale_stride, M, y,  \
-                           y_stride);
-    if (M == 1) { NSOSX_GG(1) }
-    else if (M == 2) { NSOSX_GG(2) }
-    else if (M <= 4) { NSOSX_GG(4) }
-    else { NSOSX_GG(8) }
+                           y_stride, SKIP);
+    // M >= 2: the skinny MFMA launch takes the groups it accepts (its stores address y
+    // with 32-bit offsets), then the VALU GEMV launch the rest
+    const int skip = M >= 2 && (int64_t)groups * y_stride * 4 < ((int64_t)1 << 31);
+    if (skip) {
+        // about 512 workgroups in all (2 per CU at 64 KB of LDS), so each wave
+        // streams several tiles past its workgroup's fragment staging
+        const dim3 gsk(std::max(2, std::min(512, 512 / groups)), groups);
+        if (y_dtype == NSOSX_F32)
+            hipLaunchKernelGGL((grouped_skinny_kernel<NSOSX_F32, false>), gsk, block,
+                               kGroupedSkinnyLds, st, views_dev, nullptr, q, q_stride, 1,
+                               act_scale, scale_stride, M, y, y_stride);
+        else
+            hipLaunchKernelGGL((grouped_skinny_kernel<NSOSX_BF16, false>), gsk, block,
+                               kGroupedSkinnyLds, st, views_dev, nullptr, q, q_stride, 1,
+                               act_scale, scale_stride, M, y, y_stride);
+    }
+    if (M == 1) { NSOSX_GG(1, 0) }
+    else if (M == 2) { NSOSX_GG(2, skip) }
+    else if (M <= 4) { NSOSX_GG(4, skip) }
+    else { NSOSX_GG(8, skip) }
 #undef NSOSX_GG
     return check_launch("grouped_gemv");
 }
@@ -1807,7 +1890,8 @@ extern "C" int nsosx_moe_sparse_decode(const nsosx_linear_view* up_views,
     const dim3 grid_up(std::max(1, std::min(512, 2048 / slots)), slots);
     // up: group g = (row g / k, expert selected[g]); the k groups of a row share its codes
     hipLaunchKernelGGL((grouped_gemv_kernel<1, NSOSX_F32, true>), grid_up, block, 0, st, up_views,
-                       selected, w.q1, (int64_t)dim, k, w.s1, (int64_t)1, 1, w.h, (int64_t)hidden);
+                       selected, w.q1, (int64_t)dim, k, w.s1, (int64_t)1, 1, w.h, (int64_t)hidden,
+                       0);
     rc = check_launch("moe_sparse_decode");
     if (rc) return rc;
     rc = nsosx_quantize_act_i8(w.h, NSOSX_F32, slots, hidden, 8, rms_input, w.q2, w.s2, w.r2,
@@ -1815,7 +1899,7 @@ extern "C" int nsosx_moe_sparse_decode(const nsosx_linear_view* up_views,
     if (rc) return rc;
     hipLaunchKernelGGL((grouped_gemv_kernel<1, NSOSX_F32, false>), grid_up, block, 0, st,
                        down_views, selected, w.q2, (int64_t)hidden, 1, w.s2, (int64_t)1, 1, w.o,
-                       (int64_t)dim);
+                       (int64_t)dim, 0);
     rc = check_launch("moe_sparse_decode");
     if (rc) return rc;
     // slot of (row r, choice i) is r * k + i: the combine's identity map

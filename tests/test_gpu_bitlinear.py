@@ -195,6 +195,40 @@ def test_grouped_gemv_matches_per_group(dev, orc):
     np.testing.assert_array_equal(y.cpu().numpy(), np.stack(wants))
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 8])
+def test_grouped_gemv_mixed_shapes(dev, orc, m):
+    """Groups of different K and N in one launch: K = 1024 / 2048 with N % 4 == 0 take the
+    skinny MFMA body for M >= 2, the others (K = 768, N = 130) the VALU GEMV body."""
+    from reimagined_amd._lib import call
+    rng = np.random.default_rng(90 + m)
+    shapes = [(1024, 256), (2048, 520), (768, 128), (1024, 130), (2048, 64)]
+    kmax, nmax = max(k for k, _ in shapes), max(n for _, n in shapes)
+    qbuf = np.zeros((len(shapes), m * kmax), np.int8)
+    sbuf = np.zeros((len(shapes), m), np.float32)
+    entries, wants = [], []
+    for g, (k, n) in enumerate(shapes):
+        w = _weights(rng, n, k)
+        packed, ws, codes = orc.pack_weights(w)
+        q, s = orc.quantize_act(rng.standard_normal((m, k)).astype(np.float32), 8)
+        bias = rng.standard_normal(n).astype(np.float32) if g % 2 else None
+        wants.append(orc.dequant(orc.gemm_i8(q, codes), s, ws, None, bias))
+        entries.append((torch.from_numpy(packed.view(np.int32)).to(dev), ws, k, n, None,
+                        None if bias is None else torch.from_numpy(bias).to(dev)))
+        qbuf[g, :m * k] = q.reshape(-1)
+        sbuf[g] = s
+    views = ops.LinearViewArray(entries, dev)
+    qd, sd = torch.from_numpy(qbuf).to(dev), torch.from_numpy(sbuf).to(dev)
+    for dt in (torch.float32, torch.bfloat16):
+        y = torch.full((len(shapes), m * nmax), 7.0, dtype=dt, device=dev)
+        call("nsosx_grouped_gemv", views.ptr, len(shapes), qd.data_ptr(), m * kmax, sd.data_ptr(),
+             m, m, y.data_ptr(), m * nmax, 0 if dt == torch.float32 else 1, None)
+        got = y.float().cpu().numpy()
+        for g, (k, n) in enumerate(shapes):
+            want = wants[g] if dt == torch.float32 else _bf16_round(wants[g])
+            np.testing.assert_array_equal(got[g, :m * n].reshape(m, n), want)
+            assert np.all(got[g, m * n:] == 7.0)  # nothing written past the group's rows
+
+
 def test_rejects_bad_arguments(dev):
     q = torch.zeros((2, 24), dtype=torch.int8, device=dev)
     s = torch.ones(2, device=dev)
