@@ -758,8 +758,9 @@ __device__ __forceinline__ void load_states(const float* p, float v[SPL]) {
     } else {
 #pragma unroll
         for (int i = 0; i < SPL; i += 4) {
-            const float4 a = *reinterpret_cast<const float4*>(p + i);
-            v[i] = a.x; v[i + 1] = a.y; v[i + 2] = a.z; v[i + 3] = a.w;
+            const u32x4 a = __builtin_nontemporal_load((global_u32x4*)(p + i));
+            v[i] = __uint_as_float(a.x); v[i + 1] = __uint_as_float(a.y);
+            v[i + 2] = __uint_as_float(a.z); v[i + 3] = __uint_as_float(a.w);
         }
     }
 }
@@ -773,11 +774,14 @@ __device__ __forceinline__ void store_states(float* p, const float v[SPL]) {
     } else {
 #pragma unroll
         for (int i = 0; i < SPL; i += 4)
-            *reinterpret_cast<float4*>(p + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+            __builtin_nontemporal_store(
+                u32x4{__float_as_uint(v[i]), __float_as_uint(v[i + 1]), __float_as_uint(v[i + 2]),
+                      __float_as_uint(v[i + 3])},
+                (__attribute__((address_space(1))) u32x4*)(p + i));
     }
 }
 
-template <int ADT, int SPL, bool GATE>
+template <int ADT, int SPL, bool GATE, bool VBC>
 __global__ __launch_bounds__(256) void scan_step_rows_kernel(
     const void* __restrict__ x, const void* __restrict__ dt, const float* __restrict__ a_log,
     int a_per_state, const void* __restrict__ Bm, const void* __restrict__ Cm,
@@ -807,11 +811,22 @@ __global__ __launch_bounds__(256) void scan_step_rows_kernel(
         xv[j] = load_act<ADT>(x, (int64_t)r * D + c);
         dtv[j] = load_act<ADT>(dt, (int64_t)r * H + h);
         zv[j] = GATE ? load_act<ADT>(z, (int64_t)r * D + c) : 0.0f;
+        const int64_t boff = (int64_t)r * GN + grp * N + q * SPL;
+        if constexpr (VBC && SPL == 4 && ADT == NSOSX_BF16) {
+            // four consecutive bf16 states (N = 16, 8-byte aligned B and C): one 8-byte
+            // load each
+            const uint2 b2 = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(Bm) + boff);
+            const uint2 c2 = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(Cm) + boff);
+            bq[j][0] = __uint_as_float(b2.x << 16); bq[j][1] = __uint_as_float(b2.x & 0xFFFF0000u);
+            bq[j][2] = __uint_as_float(b2.y << 16); bq[j][3] = __uint_as_float(b2.y & 0xFFFF0000u);
+            cq[j][0] = __uint_as_float(c2.x << 16); cq[j][1] = __uint_as_float(c2.x & 0xFFFF0000u);
+            cq[j][2] = __uint_as_float(c2.y << 16); cq[j][3] = __uint_as_float(c2.y & 0xFFFF0000u);
+        } else {
 #pragma unroll
-        for (int i = 0; i < SPL; ++i) {
-            const int64_t off = (int64_t)r * GN + grp * N + q * SPL + i;
-            bq[j][i] = load_act<ADT>(Bm, off);
-            cq[j][i] = load_act<ADT>(Cm, off);
+            for (int i = 0; i < SPL; ++i) {
+                bq[j][i] = load_act<ADT>(Bm, boff + i);
+                cq[j][i] = load_act<ADT>(Cm, boff + i);
+            }
         }
     }
 #pragma unroll
@@ -1012,11 +1027,18 @@ extern "C" int nsosx_selective_scan_step(const void* x, const void* dt, const fl
         rows <= 65535 * kStepRows) {
         // states of a channel split evenly over the quad: the row-blocked kernel
         const dim3 grid((H * P + 63) / 64, (rows + kStepRows - 1) / kStepRows), block(256);
-#define NSOSX_STEPR(ADT, SPL, GATE)                                                            \
-    hipLaunchKernelGGL((scan_step_rows_kernel<ADT, SPL, GATE>), grid, block, 0, st, x, dt, A_log, \
+        // B and C of a quad in one 8-byte load when N = 16 and they are 8-byte aligned (chosen
+        // here: a branch on the alignment inside the kernel would drain its loads)
+        const bool vbc = ((reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) & 7) == 0;
+#define NSOSX_STEPR(ADT, SPL, GATE, V)                                                             \
+    hipLaunchKernelGGL((scan_step_rows_kernel<ADT, SPL, GATE, V>), grid, block, 0, st, x, dt, A_log, \
                        a_per_state, B, C, D, z, rows, H, P, N, G, state, y);
-#define NSOSX_STEPR_G(ADT, SPL) \
-    if (z) { NSOSX_STEPR(ADT, SPL, true) } else { NSOSX_STEPR(ADT, SPL, false) }
+#define NSOSX_STEPR_G(ADT, SPL)                                                   \
+    if (SPL == 4 && vbc) {                                                       \
+        if (z) { NSOSX_STEPR(ADT, SPL, true, true) } else { NSOSX_STEPR(ADT, SPL, false, true) } \
+    } else {                                                                     \
+        if (z) { NSOSX_STEPR(ADT, SPL, true, false) } else { NSOSX_STEPR(ADT, SPL, false, false) } \
+    }
 #define NSOSX_STEPR_S(ADT)                          \
     switch (N / 4) {                                \
         case 1: NSOSX_STEPR_G(ADT, 1) break;        \
