@@ -137,6 +137,87 @@ __device__ __forceinline__ uint32_t pack4_i8(float a, float b, float c, float d)
 
 __device__ __forceinline__ float clamp127(float c) { return fminf(fmaxf(c, -127.0f), 127.0f); }
 
+// ===========================================================================
+// Few rows with RMS_PERI (decode): the RMS pass and the quantization in one
+// launch.  A workgroup per row keeps the row in registers (8 elements per
+// thread and 2048-element chunk, K % 8 == 0, K <= 4096) and in LDS as floats;
+// lane 0 takes the in-order sum from LDS, the workgroup the absmax of x * inv
+// and the codes, with the operations of rms_inv_small_kernel and
+// quantize_rows_vec_kernel<DT, true> (so the same bits).
+// ===========================================================================
+constexpr int kQSmallMaxK = 4096;
+
+template <int DT>
+__global__ __launch_bounds__(256) void quantize_small_rms_kernel(const void* __restrict__ x,
+                                                                 int K, float q_max, float eps,
+                                                                 float* __restrict__ rms_inv,
+                                                                 int8_t* __restrict__ q,
+                                                                 float* __restrict__ act_scale) {
+    __shared__ __align__(16) float s_row[kQSmallMaxK];
+    __shared__ float s_red[5];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t base = (int64_t)row * K;
+    float v[2][8];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int e0 = (c * 256 + tid) * 8;
+        if (e0 < K) {
+            load8<DT>(x, base + e0, v[c]);
+            *reinterpret_cast<float4*>(s_row + e0) = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
+            *reinterpret_cast<float4*>(s_row + e0 + 4) = make_float4(v[c][4], v[c][5], v[c][6], v[c][7]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[c][j] = 0.0f;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int k = 0; k < K; k += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(s_row + k);
+            sum = __fadd_rn(sum, __fmul_rn(a.x, a.x));
+            sum = __fadd_rn(sum, __fmul_rn(a.y, a.y));
+            sum = __fadd_rn(sum, __fmul_rn(a.z, a.z));
+            sum = __fadd_rn(sum, __fmul_rn(a.w, a.w));
+        }
+        const float mean = __fdiv_rn(sum, static_cast<float>(K));
+        const float inv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
+        s_red[4] = inv;
+        rms_inv[row] = inv;
+    }
+    __syncthreads();
+    const float inv = s_red[4];
+    float m = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[c][j] = __fmul_rn(v[c][j], inv);
+            m = fmaxf(m, fabsf(v[c][j]));
+        }
+    m = wave_max(m);
+    if ((tid & 63) == 0) s_red[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    const float denom = __fadd_rn(m, 1e-8f);
+    const float sc = __fdiv_rn(q_max, denom);
+    if (tid == 0) act_scale[row] = __fdiv_rn(denom, q_max);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int e0 = (c * 256 + tid) * 8;
+        if (e0 < K) {
+            float code[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) code[j] = clamp127(rintf(__fmul_rn(v[c][j], sc)));
+            uint2 out;
+            out.x = pack4_i8(code[0], code[1], code[2], code[3]);
+            out.y = pack4_i8(code[4], code[5], code[6], code[7]);
+            *reinterpret_cast<uint2*>(q + base + e0) = out;
+        }
+    }
+}
+
 template <int DT, bool RMS>
 __global__ __launch_bounds__(256) void quantize_rows_vec_kernel(
     const void* __restrict__ x, int M, int K, float q_max, const float* __restrict__ rms_inv,
@@ -223,6 +304,12 @@ static int launch_quantize(const void* x, int M, int K, int bits, int rms_input,
                            float* act_scale, float* rms_ws, hipStream_t st) {
     const float qm = q_max_for_bits(bits);
     const int elem = DT == NSOSX_F32 ? 4 : 2;
+    if (rms_input && M <= 1024 && K % 8 == 0 && K <= kQSmallMaxK &&
+        reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 8 == 0) {
+        hipLaunchKernelGGL((quantize_small_rms_kernel<DT>), dim3(M), dim3(256), 0, st, x, K, qm,
+                           1e-6f, rms_ws, q, act_scale);
+        return check_launch("quantize_act");
+    }
     if (rms_input && M <= 1024 && K <= kRmsSmallMaxK) {
         hipLaunchKernelGGL((rms_inv_small_kernel<DT>), dim3(M), dim3(256), 0, st, x, K, 1e-6f,
                            rms_ws);
