@@ -77,6 +77,39 @@ def test_scan_matches_oracle(dev, orc, H, P, N, G, per_state, lengths):
     np.testing.assert_allclose(fin, wfin, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("count,hi", [(40, 12), (1100, 3)])
+def test_scan_many_sequences_with_empty_ones(dev, orc, count, hi):
+    """Empty sequences (equal cu_seqlens entries) and more sequences than the longest-first
+    ordering covers (1100 > 1024): every non-empty sequence still matches the oracle and an
+    empty one's final state is its (zero) initial state."""
+    rng = np.random.default_rng(count)
+    H, P, N, G = 32, 1, 16, 1
+    lengths = rng.integers(0, hi + 1, size=count)
+    lengths[::7] = 0
+    cu = _cu(lengths)
+    inp = _inputs(rng, int(cu[-1]), H, P, N, G)
+    y, fin = _run(dev, orc, inp, cu, H, P, N, G)
+    wy, wfin = orc.selective_scan(inp["x"], inp["dt"], inp["a_log"], inp["B"], inp["C"], inp["D"],
+                                  inp["z"], cu, H, P, N, G)
+    np.testing.assert_allclose(y, wy, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(fin, wfin, rtol=RTOL, atol=ATOL)
+    assert np.all(fin[lengths == 0] == 0.0)
+
+
+def test_scan_long_sequence_chunk_edges(dev, orc):
+    """Lengths around the 32-token staging chunk and the 4-token group (the pipelined readout
+    flushes the last group after the loop)."""
+    rng = np.random.default_rng(77)
+    H, P, N, G = 64, 1, 16, 1
+    cu = _cu([31, 32, 33, 1001, 2, 4, 96])
+    inp = _inputs(rng, int(cu[-1]), H, P, N, G)
+    y, fin = _run(dev, orc, inp, cu, H, P, N, G)
+    wy, wfin = orc.selective_scan(inp["x"], inp["dt"], inp["a_log"], inp["B"], inp["C"], inp["D"],
+                                  inp["z"], cu, H, P, N, G)
+    np.testing.assert_allclose(y, wy, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(fin, wfin, rtol=RTOL, atol=ATOL)
+
+
 def test_scan_initial_state_and_no_gate(dev, orc):
     rng = np.random.default_rng(4)
     H, P, N, G = 128, 1, 16, 1
