@@ -327,6 +327,42 @@ int nsosx_conv_step(const void* x, int x_dtype, int64_t x_stride, int rows, int 
                     const float* weight, const float* bias, int width, float* ring,
                     int apply_silu, void* out, int out_dtype, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Quantization-aware training: fake-quant forward and the STE weight-gradient
+ * clip, bit-exact with the CPU path.  All tensors f32 on the device.
+ * ------------------------------------------------------------------------- */
+
+/* qat_fake_quant_ternary (src/bitnet_gpu_dispatch.cpp:193-217;
+ * launch_fake_quant_ternary_kernel include/cuda/kernels.cuh:506):
+ *   v = w * (1 / (scale + 1e-8f)); out = (v > 0.5 ? 1 : v < -0.5 ? -1 : 0) * scale.
+ * scale finite and > 0. */
+int nsosx_qat_fake_quant_ternary(const float* w, int64_t n, float scale, float* out,
+                                 void* stream);
+
+/* qat_fake_quant_ternary_absmean (src/bitnet_gpu_dispatch.cpp:219-245;
+ * launch_fake_quant_ternary_absmean_kernel kernels.cuh:510): scale =
+ * float(sum |w| / n, summed in double) + 1e-8f written to scale_out (device,
+ * one float), then the fake-quant above with that scale; no host sync.
+ * workspace: device, nsosx_qat_absmean_workspace(n) bytes. */
+int64_t nsosx_qat_absmean_workspace(int64_t n);
+int nsosx_qat_fake_quant_ternary_absmean(const float* w, int64_t n, float* out,
+                                         float* scale_out, void* workspace, void* stream);
+
+/* qat_fake_quant_activations (src/bitnet_gpu_dispatch.cpp:247-282;
+ * launch_fake_quant_activations_kernel kernels.cuh:518), per row of x [M, K]:
+ * denom = max|x| + 1e-8f; v = clamp(x * (q_max / denom), -q_max, q_max);
+ * out = round_half_away(v) * (denom / q_max); q_max = 2^(bits-1) - 1 (1 for
+ * bits = 2); precision_bits in [2, 8]. */
+int nsosx_qat_fake_quant_activations(const float* x, int M, int K, int precision_bits,
+                                     float* out, void* stream);
+
+/* qat_ste_clip_weight_grad / _device_scale (src/bitnet_gpu_dispatch.cpp:284-325;
+ * launch_ste_clip_weight_grad(_device_scale)_kernel kernels.cuh:522-527):
+ * dW[i] = 0 where |w[i] * (1 / (scale + 1e-8f))| > 1.  The scale is scale_dev[0]
+ * when scale_dev is not NULL (device), else `scale` (finite, > 0). */
+int nsosx_qat_ste_clip_weight_grad(float* dW, const float* w, int64_t n, float scale,
+                                   const float* scale_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

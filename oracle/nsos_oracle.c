@@ -529,3 +529,55 @@ void orc_moe_combine(const float* expert_out, const int32_t* perm, const int32_t
         }
     }
 }
+
+/* ---- quantization-aware training ------------------------------------------
+ * qat_fake_quant_ternary: inv = 1 / (scale + 1e-8f); v = w * inv;
+ * out = (v > 0.5 ? 1 : v < -0.5 ? -1 : 0) * scale.
+ * OXN/nsos/src/bitnet_gpu_dispatch.cpp:193-217 (CPU branch 209-216) */
+void orc_qat_fake_quant_ternary(const float* w, int64_t n, float scale, float* out) {
+    const float inv = 1.0f / (scale + 1e-8f);
+    for (int64_t i = 0; i < n; ++i) {
+        const float v = w[i] * inv;
+        const float t = (v > 0.5f) ? 1.0f : ((v < -0.5f) ? -1.0f : 0.0f);
+        out[i] = t * scale;
+    }
+}
+
+/* qat_fake_quant_ternary_absmean: scale = tensor_abs_mean(w) + 1e-8f
+ * (double sum, src/tensor.cpp:2095-2101), then the ternary fake-quant.
+ * OXN/nsos/src/bitnet_gpu_dispatch.cpp:238-244 */
+float orc_qat_fake_quant_ternary_absmean(const float* w, int64_t n, float* out) {
+    const float scale = orc_absmean(w, n) + 1e-8f;
+    orc_qat_fake_quant_ternary(w, n, scale, out);
+    return scale;
+}
+
+/* qat_fake_quant_activations, per row: denom = max|x| + 1e-8f;
+ * scale = q_max / denom; inv_scale = denom / q_max;
+ * out = round(min(max(x * scale, -q_max), q_max)) * inv_scale (std::round).
+ * OXN/nsos/src/bitnet_gpu_dispatch.cpp:262-281 */
+void orc_qat_fake_quant_activations(const float* x, int M, int K, int bits, float* out) {
+    const float q_max = bits <= 2 ? 1.0f : (float)((1 << (bits - 1)) - 1);
+    for (int r = 0; r < M; ++r) {
+        const float* row = x + (int64_t)r * K;
+        float* orow = out + (int64_t)r * K;
+        float mx = 0.0f;
+        for (int j = 0; j < K; ++j) mx = fmaxf(mx, fabsf(row[j]));
+        const float denom = mx + 1e-8f;
+        const float scale = q_max / denom;
+        const float inv_scale = denom / q_max;
+        for (int j = 0; j < K; ++j) {
+            float v = row[j] * scale;
+            v = fminf(fmaxf(v, -q_max), q_max);
+            orow[j] = roundf(v) * inv_scale;
+        }
+    }
+}
+
+/* qat_ste_clip_weight_grad: dW[i] = 0 where |w[i] * (1 / (scale + 1e-8f))| > 1.
+ * OXN/nsos/src/bitnet_gpu_dispatch.cpp:300-307 */
+void orc_qat_ste_clip(float* dW, const float* w, int64_t n, float scale) {
+    const float inv = 1.0f / (scale + 1e-8f);
+    for (int64_t i = 0; i < n; ++i)
+        if (fabsf(w[i] * inv) > 1.0f) dW[i] = 0.0f;
+}

@@ -45,6 +45,13 @@ void orc_conv_step(const float* x, int rows, int channels, const float* weight,
                    const float* bias, int width, float* ring, int apply_silu, float* out);
 void orc_rmsnorm_gated(const float* y, const float* z, const float* gamma, int rows, int cols,
                        float eps, float* out);
+
+/* Quantization-aware training: fake-quant forward and the STE clip
+ * (OXN/nsos/src/bitnet_gpu_dispatch.cpp:193-325). */
+void orc_qat_fake_quant_ternary(const float* w, int64_t n, float scale, float* out);
+float orc_qat_fake_quant_ternary_absmean(const float* w, int64_t n, float* out);
+void orc_qat_fake_quant_activations(const float* x, int M, int K, int bits, float* out);
+void orc_qat_ste_clip(float* dW, const float* w, int64_t n, float scale);
 float orc_softplus(float v);
 void orc_squared_relu(const float* x, int64_t n, float* out);
 

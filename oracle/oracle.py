@@ -66,6 +66,10 @@ def _load() -> ctypes.CDLL:
                                  _i, _i, _i, _i, _i, _f32p, _f32p, _i]),
         "orc_conv_step": (None, [_f32p, _i, _i, _f32p, _vp, _i, _vp, _i, _f32p]),
         "orc_rmsnorm_gated": (None, [_f32p, _vp, _vp, _i, _i, _f, _f32p]),
+        "orc_qat_fake_quant_ternary": (None, [_f32p, _i64, _f, _f32p]),
+        "orc_qat_fake_quant_ternary_absmean": (_f, [_f32p, _i64, _f32p]),
+        "orc_qat_fake_quant_activations": (None, [_f32p, _i, _i, _i, _f32p]),
+        "orc_qat_ste_clip": (None, [_f32p, _f32p, _i64, _f]),
         "orc_softmax_rows": (None, [_f32p, _i, _i, _f32p]),
         "orc_topk_mask": (None, [_f32p, _i, _i, _i, _vp]),
         "orc_moe_dispatch": (None, [_f32p, _i, _i, _i, _i32p, _i32p, _i32p]),
@@ -385,3 +389,38 @@ def ref_row_sum_i8(row) -> int:
     lib.ref_row_sum_i8.argtypes = [_i8p, _i]
     row = np.ascontiguousarray(row, dtype=np.int8)
     return int(lib.ref_row_sum_i8(row, row.size))
+
+
+# ---- quantization-aware training -----------------------------------------------
+
+def qat_fake_quant_ternary(w, scale):
+    """qat_fake_quant_ternary (src/bitnet_gpu_dispatch.cpp:193-217)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(w)
+    _lib.orc_qat_fake_quant_ternary(w.ravel(), w.size, float(scale), out.ravel())
+    return out
+
+
+def qat_fake_quant_ternary_absmean(w):
+    """qat_fake_quant_ternary_absmean (src/bitnet_gpu_dispatch.cpp:219-245) -> (out, scale)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(w)
+    scale = _lib.orc_qat_fake_quant_ternary_absmean(w.ravel(), w.size, out.ravel())
+    return out, np.float32(scale)
+
+
+def qat_fake_quant_activations(x, bits=8):
+    """qat_fake_quant_activations (src/bitnet_gpu_dispatch.cpp:247-282), rows = last dim."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    k = x.shape[-1]
+    out = np.empty_like(x)
+    _lib.orc_qat_fake_quant_activations(x.ravel(), x.size // k, k, int(bits), out.ravel())
+    return out
+
+
+def qat_ste_clip(dW, w, scale):
+    """qat_ste_clip_weight_grad (src/bitnet_gpu_dispatch.cpp:284-308) on a copy of dW."""
+    out = np.array(dW, dtype=np.float32, copy=True)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    _lib.orc_qat_ste_clip(out.ravel(), w.ravel(), w.size, float(scale))
+    return out

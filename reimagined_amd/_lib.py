@@ -48,6 +48,11 @@ SIGNATURES = {
     "nsosx_add_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp, _vp, _vp]),
     "nsosx_conv_step": (_i, [_vp, _i, _i64, _i, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _vp]),
     "nsosx_edge_pack_parse": (_i, [_vp, ctypes.c_uint64, _vp, _i, _vp, _vp]),
+    "nsosx_qat_fake_quant_ternary": (_i, [_vp, _i64, ctypes.c_float, _vp, _vp]),
+    "nsosx_qat_absmean_workspace": (_i64, [_i64]),
+    "nsosx_qat_fake_quant_ternary_absmean": (_i, [_vp, _i64, _vp, _vp, _vp, _vp]),
+    "nsosx_qat_fake_quant_activations": (_i, [_vp, _i, _i, _i, _vp, _vp]),
+    "nsosx_qat_ste_clip_weight_grad": (_i, [_vp, _vp, _i64, ctypes.c_float, _vp, _vp]),
     "nsosx_moe_sparse_decode_workspace": (_i64, [_i, _i, _i, _i]),
     "nsosx_moe_sparse_decode": (_i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp,
                                      _vp, _i, _vp]),

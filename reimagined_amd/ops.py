@@ -392,3 +392,53 @@ def conv_step(x: torch.Tensor, weight: torch.Tensor, bias, ring, apply_silu: boo
     call("nsosx_conv_step", _p(x), _dt(x), x.stride(0), r, c, _p(weight), _p(bias), w,
          _p(ring) if w > 1 else None, int(apply_silu), _p(out), _dt(out), _stream())
     return out
+
+
+# ---- quantization-aware training (fake quant + STE clip) -------------------------
+
+def qat_fake_quant_ternary(w: torch.Tensor, scale: float) -> torch.Tensor:
+    """qat_fake_quant_ternary (src/bitnet_gpu_dispatch.cpp:193-217): ternary(w / scale) * scale."""
+    _dev(w, "w", torch.float32)
+    out = torch.empty_like(w)
+    call("nsosx_qat_fake_quant_ternary", _p(w), w.numel(), float(scale), _p(out), _stream())
+    return out
+
+
+def qat_fake_quant_ternary_absmean(w: torch.Tensor):
+    """qat_fake_quant_ternary_absmean (src/bitnet_gpu_dispatch.cpp:219-245) -> (out, scale [1])
+    with the absmean scale computed and kept on the device."""
+    _dev(w, "w", torch.float32)
+    out = torch.empty_like(w)
+    scale = torch.empty(1, dtype=torch.float32, device=w.device)
+    ws = torch.empty(int(lib().nsosx_qat_absmean_workspace(w.numel())), dtype=torch.uint8,
+                     device=w.device)
+    call("nsosx_qat_fake_quant_ternary_absmean", _p(w), w.numel(), _p(out), _p(scale), _p(ws),
+         _stream())
+    return out, scale
+
+
+def qat_fake_quant_activations(x: torch.Tensor, precision_bits: int = 8) -> torch.Tensor:
+    """qat_fake_quant_activations (src/bitnet_gpu_dispatch.cpp:247-282): per-row absmax
+    quantize-dequantize of the last dimension."""
+    _dev(x, "x", torch.float32)
+    k = x.shape[-1] if x.dim() else 0
+    m = x.numel() // k if k else 0
+    out = torch.empty_like(x)
+    call("nsosx_qat_fake_quant_activations", _p(x), m, k, int(precision_bits), _p(out), _stream())
+    return out
+
+
+def qat_ste_clip_weight_grad(dW: torch.Tensor, w: torch.Tensor, scale) -> torch.Tensor:
+    """qat_ste_clip_weight_grad(_device_scale) (src/bitnet_gpu_dispatch.cpp:284-325), in place
+    on dW; `scale` is a float or a device tensor [1]."""
+    _dev(dW, "dW", torch.float32)
+    _dev(w, "w", torch.float32)
+    if dW.shape != w.shape:
+        raise ValueError("qat_ste_clip_weight_grad requires identical shapes")
+    if isinstance(scale, torch.Tensor):
+        _dev(scale, "scale", torch.float32)
+        call("nsosx_qat_ste_clip_weight_grad", _p(dW), _p(w), w.numel(), 0.0, _p(scale), _stream())
+    else:
+        call("nsosx_qat_ste_clip_weight_grad", _p(dW), _p(w), w.numel(), float(scale), None,
+             _stream())
+    return dW
