@@ -72,6 +72,73 @@ __global__ __launch_bounds__(64) void rms_inv_kernel(const void* __restrict__ x,
     inv[row] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
 }
 
+// Many rows, rows of a multiple of kRmsDepth tiles: the same in-order sums,
+// lane = row, with the rows coming in through LDS.  A one-wave workgroup owns
+// 64 rows and streams them in column tiles of kRmsTileBytes per row: a tile is
+// read with 1 KB loads (whole 128-byte lines, where lane-per-row loads touch 64
+// lines per instruction), kRmsDepth tiles in flight in registers, and passed
+// through a double-buffered LDS slice from which each lane sums its own row.
+// LDS operations of one wave complete in order, so no barrier is needed.
+constexpr int kRmsTileBytes = 128;                    // bytes of a row per tile
+constexpr int kRmsRowPitch = kRmsTileBytes + 16;      // padded LDS row (bank spread)
+constexpr int kRmsDepth = 4;                          // tiles in flight
+
+template <int DT>
+__global__ __launch_bounds__(64) void rms_inv_tiled_kernel(const void* __restrict__ x, int M,
+                                                           int K, float eps,
+                                                           float* __restrict__ inv) {
+    __shared__ __align__(16) char s_tile[2][64 * kRmsRowPitch];
+    constexpr int ES = DT == NSOSX_F32 ? 4 : 2;
+    constexpr int PER = 16 / ES;                      // elements per 16 bytes
+    constexpr int TE = kRmsTileBytes / ES;            // elements of a row per tile
+    const int lane = threadIdx.x;
+    const int row0 = blockIdx.x * 64;
+    const int64_t row_bytes = (int64_t)K * ES;
+    const char* xb = static_cast<const char*>(x);
+    const int tiles = K / TE;
+    // load j (0..7) of a tile: row 8 j + lane / 8, 16-byte piece lane % 8; rows past M
+    // re-read the last row and tiles past the end the last tile (never used)
+    const char* src[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        src[j] = xb + min(row0 + 8 * j + (lane >> 3), M - 1) * row_bytes + (lane & 7) * 16;
+    uint4 buf[kRmsDepth][8];
+    auto load_tile = [&](int t, uint4 (&b)[8]) {
+        const int64_t off = (int64_t)min(t, tiles - 1) * kRmsTileBytes;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) b[j] = load_stream16(reinterpret_cast<const uint32_t*>(src[j] + off));
+    };
+#pragma unroll
+    for (int d = 0; d < kRmsDepth; ++d) load_tile(d, buf[d]);
+    float sum = 0.0f;
+    for (int t0 = 0; t0 < tiles; t0 += kRmsDepth) {
+        // tiles is a multiple of kRmsDepth (host check): straight-line code, so the
+        // loads stay in flight across tiles
+#pragma unroll
+        for (int d = 0; d < kRmsDepth; ++d) {
+            const int t = t0 + d;
+            char* slot = s_tile[d & 1];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                *reinterpret_cast<uint4*>(slot + (8 * j + (lane >> 3)) * kRmsRowPitch +
+                                          (lane & 7) * 16) = buf[d][j];
+            load_tile(t + kRmsDepth, buf[d]);
+            const char* my = slot + lane * kRmsRowPitch;
+#pragma unroll
+            for (int p = 0; p < kRmsTileBytes / 16; ++p) {
+                float v[PER];
+                load16_f32<DT>(my + p * 16, v);
+#pragma unroll
+                for (int j = 0; j < PER; ++j) sum = __fadd_rn(sum, __fmul_rn(v[j], v[j]));
+            }
+        }
+    }
+    const int row = row0 + lane;
+    if (row >= M) return;
+    const float mean = __fdiv_rn(sum, static_cast<float>(K));
+    inv[row] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
+}
+
 // Few rows (decode): a workgroup per row stages the row in LDS with coalesced
 // 16-byte loads, then one lane takes the in-order sum from LDS, so the row's
 // load latency is paid once instead of once per four loads.  K <= 8192.
@@ -313,6 +380,10 @@ static int launch_quantize(const void* x, int M, int K, int bits, int rms_input,
     if (rms_input && M <= 1024 && K <= kRmsSmallMaxK) {
         hipLaunchKernelGGL((rms_inv_small_kernel<DT>), dim3(M), dim3(256), 0, st, x, K, 1e-6f,
                            rms_ws);
+    } else if (rms_input && ((int64_t)K * elem) % (kRmsTileBytes * kRmsDepth) == 0 &&
+               reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+        hipLaunchKernelGGL((rms_inv_tiled_kernel<DT>), dim3((M + 63) / 64), dim3(64), 0, st, x, M,
+                           K, 1e-6f, rms_ws);
     } else if (rms_input) {
         const bool rvec = ((int64_t)K * elem) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
         if (rvec)
