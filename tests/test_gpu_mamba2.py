@@ -1,4 +1,4 @@
-"""Faithful Mamba-2 block on the GPU against the oracle's composition,
+"""Faithful Mamba-2 block (Mamba2SSD::forward_faithful and its decode step) on the GPU against the oracle's composition,
 stage by stage on the GPU's own upstream tensors (src/mamba2.cpp:2360-2681):
 the five projections and out_proj bit-exact, conv / scan / gated norm within the fp32
 bounds of their own tests (1e-4 rel, 1e-5 abs; norm 1e-5 / 1e-6).  The decode step equals
