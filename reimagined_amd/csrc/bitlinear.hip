@@ -150,17 +150,23 @@ __global__ __launch_bounds__(256) void rms_inv_small_kernel(const void* __restri
     __shared__ __align__(16) float s_row[kRmsSmallMaxK];
     const int row = blockIdx.x;
     const int64_t base = (int64_t)row * K;
-    for (int k = threadIdx.x; k < K; k += 256) s_row[k] = load_act<DT>(x, base + k);
+    const int body = K & ~3;
+    // body elements as their rounded squares (the lane walking the row only adds),
+    // the K % 4 tail as values for the fused multiply-adds
+    for (int k = threadIdx.x; k < K; k += 256) {
+        const float v = load_act<DT>(x, base + k);
+        s_row[k] = k < body ? __fmul_rn(v, v) : v;
+    }
     __syncthreads();
     if (threadIdx.x != 0) return;
-    const int body = K & ~3;
     float sum = 0.0f;
+#pragma unroll 8
     for (int k = 0; k < body; k += 4) {
         const float4 v = *reinterpret_cast<const float4*>(s_row + k);
-        sum = __fadd_rn(sum, __fmul_rn(v.x, v.x));
-        sum = __fadd_rn(sum, __fmul_rn(v.y, v.y));
-        sum = __fadd_rn(sum, __fmul_rn(v.z, v.z));
-        sum = __fadd_rn(sum, __fmul_rn(v.w, v.w));
+        sum = __fadd_rn(sum, v.x);
+        sum = __fadd_rn(sum, v.y);
+        sum = __fadd_rn(sum, v.z);
+        sum = __fadd_rn(sum, v.w);
     }
     for (int k = body; k < K; ++k) sum = __fmaf_rn(s_row[k], s_row[k], sum);
     const float mean = __fdiv_rn(sum, static_cast<float>(K > 1 ? K : 1));
@@ -226,13 +232,18 @@ __global__ __launch_bounds__(256) void quantize_small_rms_kernel(const void* __r
     const int tid = threadIdx.x;
     const int64_t base = (int64_t)row * K;
     float v[2][8];
+    // the squares (each rounded on its own, as in the in-order sum) go to LDS, so the
+    // one lane that walks the row only adds: a chain of K dependent adds
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
         const int e0 = (c * 256 + tid) * 8;
         if (e0 < K) {
             load8<DT>(x, base + e0, v[c]);
-            *reinterpret_cast<float4*>(s_row + e0) = make_float4(v[c][0], v[c][1], v[c][2], v[c][3]);
-            *reinterpret_cast<float4*>(s_row + e0 + 4) = make_float4(v[c][4], v[c][5], v[c][6], v[c][7]);
+            float q[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) q[j] = __fmul_rn(v[c][j], v[c][j]);
+            *reinterpret_cast<float4*>(s_row + e0) = make_float4(q[0], q[1], q[2], q[3]);
+            *reinterpret_cast<float4*>(s_row + e0 + 4) = make_float4(q[4], q[5], q[6], q[7]);
         } else {
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[c][j] = 0.0f;
@@ -241,12 +252,13 @@ __global__ __launch_bounds__(256) void quantize_small_rms_kernel(const void* __r
     __syncthreads();
     if (tid == 0) {
         float sum = 0.0f;
+#pragma unroll 8
         for (int k = 0; k < K; k += 4) {
             const float4 a = *reinterpret_cast<const float4*>(s_row + k);
-            sum = __fadd_rn(sum, __fmul_rn(a.x, a.x));
-            sum = __fadd_rn(sum, __fmul_rn(a.y, a.y));
-            sum = __fadd_rn(sum, __fmul_rn(a.z, a.z));
-            sum = __fadd_rn(sum, __fmul_rn(a.w, a.w));
+            sum = __fadd_rn(sum, a.x);
+            sum = __fadd_rn(sum, a.y);
+            sum = __fadd_rn(sum, a.z);
+            sum = __fadd_rn(sum, a.w);
         }
         const float mean = __fdiv_rn(sum, static_cast<float>(K));
         const float inv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
