@@ -707,8 +707,8 @@ static int gemv_blocks(int N, int K, int M) {
 }
 
 static int gemv_grid(int N, int K, int M) {
-    // one row block per wave, up to 8 resident waves per CU on 256 CUs
-    const int waves = std::min(gemv_blocks(N, K, M), 256 * 8);
+    // one row block per wave, up to four rounds of 8 resident waves per CU on 256 CUs
+    const int waves = std::min(gemv_blocks(N, K, M), 256 * 8 * 4);
     return std::max(1, (waves + 3) / 4);
 }
 
@@ -1910,10 +1910,12 @@ extern "C" int nsosx_grouped_gemv(const nsosx_linear_view* views_dev, int groups
         return fail(NSOSX_ERR_INVALID, "grouped_gemv: groups in [1, 65535], M in [1, 8]");
     if (!valid_dtype(y_dtype)) return fail(NSOSX_ERR_INVALID, "grouped_gemv: bad dtype");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // view shapes live on the device, so the grid is sized from the group count alone:
-    // about 2048 workgroups in all (the resident limit at 8 waves per SIMD), and each
-    // wave strides over its view's row blocks
-    const int per_group = std::max(4, std::min(512, 2048 / groups));
+    // view shapes live on the device, so the grid is sized from the group count alone,
+    // each wave striding over its view's row blocks: at M = 1 about 8192 workgroups in
+    // all (four rounds of the resident limit at 8 waves per SIMD: short waves balance
+    // better than long ones), at M >= 2 about 2048 (most groups usually leave this
+    // launch to the skinny one)
+    const int per_group = std::max(4, std::min(512, (M == 1 ? 8192 : 2048) / groups));
     const dim3 grid(per_group, groups), block(256);
 #define NSOSX_GG(MT, SKIP)                                                                    \
     if (y_dtype == NSOSX_F32)                                                                 \
