@@ -1287,6 +1287,82 @@ __device__ __forceinline__ void gemm3_epilogue(const GemmProblem& pb,
     }
 }
 
+// bf16 epilogue of a tile that lies inside N (N % 8 == 0).  The accumulator
+// layout scatters a store instruction over 32 rows at 8 bytes per lane; here
+// each wave instead dequantizes its 64 n x 128 m block into a private 16 KB
+// slice of the idle stage ring as 128 rows of 64 bf16 (128 bytes), then stores
+// whole row segments: one instruction writes 8 rows, 16 bytes per lane, each
+// row one aligned 128-byte line.  In a slice, 16-byte chunk c of row r sits in
+// slot c ^ ((r / 2) % 8), so neither the 8-byte writes (32 rows, one chunk)
+// nor the 16-byte reads (8 rows, 8 chunks) conflict on the 64 banks.
+// Magnitude, bias and every output pointer must be 16-byte aligned.
+template <bool GATHER, bool SQRELU>
+__device__ __forceinline__ void gemm3_epilogue_rows(const GemmProblem& pb,
+                                                    const float* __restrict__ act_scale,
+                                                    const int32_t* __restrict__ perm, int seg_begin,
+                                                    int seg_rows, int n0, int m0, uint16_t* y,
+                                                    const v16i (&acc)[2][4], char* smem) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 5;
+    const int li = lane & 31;
+    const int nw = n0 + wave * 64 + 4 * g;  // this lane's first output column
+    const bool has_mag = pb.mag != nullptr;
+    const bool has_bias = pb.bias != nullptr;
+    float comb[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+        const int ml = min(m0 + mb * 32 + li, seg_rows - 1);  // rows past the segment are never stored
+        const int arow = GATHER ? perm[seg_begin + ml] : seg_begin + ml;
+        comb[mb] = __fmul_rn(act_scale[arow], pb.ws);
+    }
+    __syncthreads();  // every wave is done reading the stage ring
+    char* slice = smem + wave * (kG3BM * 128);
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const int n = nw + nb * 32 + 8 * q4;
+            const float4 mg = has_mag ? *reinterpret_cast<const float4*>(pb.mag + n) : float4{};
+            const float4 bs = has_bias ? *reinterpret_cast<const float4*>(pb.bias + n) : float4{};
+            const float mv[4] = {mg.x, mg.y, mg.z, mg.w};
+            const float bv[4] = {bs.x, bs.y, bs.z, bs.w};
+            const int c = nb * 4 + q4;
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb) {
+                const v16i& a = acc[nb][mb];
+                float o[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float v = __fmul_rn(static_cast<float>(a[4 * q4 + r]), comb[mb]);
+                    if (has_mag && has_bias) v = __fmaf_rn(v, mv[r], bv[r]);
+                    else if (has_mag) v = __fmul_rn(v, mv[r]);
+                    else if (has_bias) v = __fadd_rn(v, bv[r]);
+                    if (SQRELU) {
+                        v = v > 0.0f ? v : 0.0f;
+                        v = __fmul_rn(v, v);
+                    }
+                    o[r] = v;
+                }
+                const int row = mb * 32 + li;
+                *reinterpret_cast<uint2*>(slice + row * 128 + g * 8 + ((c ^ ((row >> 1) & 7)) << 4)) =
+                    make_uint2(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]));
+            }
+        }
+    // The wave reads back what its own lanes wrote: LDS operations of one wave
+    // complete in order, and the wait keeps the compiler from hoisting the reads.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const int c = lane & 7;
+    uint16_t* ycol = y + n0 + wave * 64 + c * 8;
+#pragma unroll
+    for (int i = 0; i < kG3BM / 8; ++i) {
+        const int row = i * 8 + (lane >> 3);
+        const uint4 v = *reinterpret_cast<const uint4*>(slice + row * 128 + ((c ^ ((row >> 1) & 7)) << 4));
+        if (m0 + row < seg_rows)
+            *reinterpret_cast<uint4*>(ycol + (int64_t)(seg_begin + m0 + row) * pb.N) = v;
+    }
+}
+
 template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU>
 __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* __restrict__ q,
                                            const float* __restrict__ act_scale,
@@ -1352,6 +1428,15 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
         gemm3_stage(smem + (kt % kG3Stages) * kG3StageBytes, wave, lane, acc);
     }
 
+    if constexpr (YDT == NSOSX_BF16 && !ACC_OUT) {
+        if (y && n0 + kG3BN <= pb.N && (pb.N & 7) == 0 &&
+            ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(pb.mag) |
+              reinterpret_cast<uintptr_t>(pb.bias)) & 15) == 0) {
+            gemm3_epilogue_rows<GATHER, SQRELU>(pb, act_scale, perm, seg_begin, seg_rows, n0, m0,
+                                                static_cast<uint16_t*>(y), acc, smem);
+            return;
+        }
+    }
     gemm3_epilogue<YDT, ACC_OUT, GATHER, SQRELU>(pb, act_scale, perm, seg_begin, seg_rows, n0, m0,
                                                  y, acc_out, acc);
 }
