@@ -343,6 +343,89 @@ __global__ __launch_bounds__(256) void quantize_rows_vec_kernel(
     }
 }
 
+// Many rows with K = CH x 512: a wave quantizes RPW = 8 / CH rows and issues
+// all RPW x CH chunk loads (8 elements per lane each) before it uses any, so a
+// wave keeps 8 KB of bf16 in flight where one row per wave kept 1-2 KB (the
+// row-per-wave kernel is latency-bound at ~3.9 TB/s).  The float operations
+// are those of quantize_rows_vec_kernel (x * inv is formed again for the codes,
+// the same product), so the same bits.
+template <int DT, bool RMS, int CH>
+__global__ __launch_bounds__(256) void quantize_rows_multi_kernel(
+    const void* __restrict__ x, int M, float q_max, const float* __restrict__ rms_inv,
+    int8_t* __restrict__ q, float* __restrict__ act_scale) {
+    constexpr int RPW = 8 / CH;
+    constexpr int K = CH * kWave * 8;
+    constexpr int ES = DT == NSOSX_F32 ? 4 : 2;  // bytes per element
+    constexpr int NW = ES / 2;                   // 16-byte words per 8-element chunk
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+    if (row0 >= M) return;
+    uint4 raw[RPW][CH][NW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = min(row0 + r, M - 1);  // rows past M re-read row M - 1 and are not stored
+        const char* src = static_cast<const char*>(x) + ((int64_t)row * K + lane * 8) * ES;
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+                raw[r][c][w] = *reinterpret_cast<const uint4*>(src + c * (kWave * 8 * ES) + w * 16);
+    }
+    auto unpack = [&](const uint4 (&u)[NW], float v[8]) {
+        if constexpr (DT == NSOSX_F32) {
+            const uint32_t w[8] = {u[0].x, u[0].y, u[0].z, u[0].w, u[NW - 1].x, u[NW - 1].y,
+                                   u[NW - 1].z, u[NW - 1].w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(w[j]);
+        } else {
+            const uint32_t w[4] = {u[0].x, u[0].y, u[0].z, u[0].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v[2 * i] = __uint_as_float(w[i] << 16);
+                v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+            }
+        }
+    };
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const int row = row0 + r;
+        const float inv = RMS ? rms_inv[min(row, M - 1)] : 1.0f;
+        float m = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            float v[8];
+            unpack(raw[r][c], v);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(RMS ? __fmul_rn(v[j], inv) : v[j]));
+        }
+        m = wave_max(m);
+        if (row >= M) break;
+        const float denom = __fadd_rn(m, 1e-8f);
+        const float sc = __fdiv_rn(q_max, denom);
+        if (lane == 0) act_scale[row] = __fdiv_rn(denom, q_max);
+        int8_t* dst = q + (int64_t)row * K + lane * 8;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            float v[8], code[8];
+            unpack(raw[r][c], v);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                code[j] = clamp127(rintf(__fmul_rn(RMS ? __fmul_rn(v[j], inv) : v[j], sc)));
+            *reinterpret_cast<uint2*>(dst + c * kWave * 8) =
+                make_uint2(pack4_i8(code[0], code[1], code[2], code[3]),
+                           pack4_i8(code[4], code[5], code[6], code[7]));
+        }
+    }
+}
+
+template <int DT, bool RMS, int CH>
+static void launch_quantize_multi(const void* x, int M, float qm, const float* rms_ws, int8_t* q,
+                                  float* act_scale, hipStream_t st) {
+    const int rows_per_wg = 4 * (8 / CH);
+    hipLaunchKernelGGL((quantize_rows_multi_kernel<DT, RMS, CH>), dim3((M + rows_per_wg - 1) / rows_per_wg),
+                       dim3(256), 0, st, x, M, qm, rms_ws, q, act_scale);
+}
+
 // Any K: element-wise loads, the ties-to-even body / half-away tail split.
 template <int DT, bool RMS>
 __global__ __launch_bounds__(256) void quantize_rows_generic_kernel(
@@ -404,6 +487,18 @@ static int launch_quantize(const void* x, int M, int K, int bits, int rms_input,
         else
             hipLaunchKernelGGL((rms_inv_kernel<DT, false>), dim3((M + 63) / 64), dim3(64), 0, st,
                                x, M, K, 1e-6f, rms_ws);
+    }
+    if ((K == 512 || K == 1024 || K == 2048 || K == 4096) && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(q) % 8 == 0) {
+#define NSOSX_QMULTI(CH)                                                                   \
+    (rms_input ? launch_quantize_multi<DT, true, CH>(x, M, qm, rms_ws, q, act_scale, st)   \
+               : launch_quantize_multi<DT, false, CH>(x, M, qm, rms_ws, q, act_scale, st))
+        if (K == 512) NSOSX_QMULTI(1);
+        else if (K == 1024) NSOSX_QMULTI(2);
+        else if (K == 2048) NSOSX_QMULTI(4);
+        else NSOSX_QMULTI(8);
+#undef NSOSX_QMULTI
+        return check_launch("quantize_act");
     }
     const bool vec = (K % 8 == 0) && K <= 4096 && (reinterpret_cast<uintptr_t>(x) % 16 == 0) &&
                      (reinterpret_cast<uintptr_t>(q) % 8 == 0) && ((int64_t)K * elem) % 16 == 0;

@@ -36,7 +36,7 @@ def test_quantize_matches_reference_golden(dev, orc):
 
 
 @pytest.mark.parametrize("m,k", [(1, 16), (5, 1003), (33, 768), (7, 4096), (3, 8200), (64, 2048),
-                                 (1500, 1024), (1100, 1003)])
+                                 (1500, 1024), (1100, 1003), (1029, 512), (1030, 4096), (1027, 2048)])
 @pytest.mark.parametrize("rms", [False, True])
 def test_quantize_random_f32(dev, orc, m, k, rms):
     rng = np.random.default_rng(m * 1000 + k)
@@ -49,10 +49,12 @@ def test_quantize_random_f32(dev, orc, m, k, rms):
 
 
 @pytest.mark.parametrize("rms", [False, True])
-@pytest.mark.parametrize("m", [37, 1200])
-def test_quantize_bf16_input(dev, orc, rms, m):
+@pytest.mark.parametrize("m,k", [(37, 1024), (1200, 1024), (1201, 2048), (1029, 512), (1026, 4096)])
+def test_quantize_bf16_input(dev, orc, rms, m, k):
+    """bf16 rows; M > 1024 with K = 512 / 1024 / 2048 / 4096 takes the several-rows-per-wave
+    kernel, including row counts that leave a wave with rows past M."""
     rng = np.random.default_rng(3)
-    x = rng.standard_normal((m, 1024)).astype(np.float32)
+    x = (rng.standard_normal((m, k)) * rng.uniform(0.5, 8.0, (m, 1))).astype(np.float32)
     xb = torch.from_numpy(x).to(torch.bfloat16)
     q, s = ops.quantize_activations_bitnet(xb.to(dev), 8, rms_input=rms)
     xf = xb.float().numpy()
