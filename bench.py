@@ -226,6 +226,38 @@ def bench_prefill_gemm(torch, dev, reps=20):
             "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
 
 
+def bench_moe_c5(torch, dev, reps=10):
+    """Config 5's MoE FFN prefill: 8192 bf16 tokens, 8 experts (gate_up 1024->4096, squared ReLU,
+    down 4096->1024), top-2.  One forward = device routing, RMS + quantize, the grouped up GEMM
+    (gathered rows, squared-ReLU epilogue, bf16 hidden), RMS + quantize of the 16384 hidden rows,
+    the grouped down GEMM and the combine.  TOPS counts the 2 x 16384 x 2 x 4096 x 1024 int8 ops
+    of the two grouped GEMMs over the whole forward's time (a lower bound on the GEMMs' own
+    rate)."""
+    from reimagined_amd import workloads
+    from reimagined_amd.layers import MoEFFN
+    moe, _ = workloads.config5(rows=8192, decode_rows=1, d_inner=64)
+    layer = MoEFFN(moe["w_up"], moe["w_down"], dev, k=2, rms_input=True,
+                   hidden_dtype=torch.bfloat16)
+    x = _bf16(torch, moe["x"], dev)
+    logits = _f32(torch, moe["logits"], dev)
+    for _ in range(3):
+        layer.forward(x, logits)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        layer.forward(x, logits)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    rows, d, f = 8192, 1024, 4096
+    ops_ = 2.0 * (rows * 2) * (2 * f * d)
+    tops = ops_ / (ms / 1e3) / 1e12
+    return {"tokens": rows, "experts": 8, "k": 2, "ms": round(ms, 4),
+            "tops_whole_forward": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+            "tokens_per_s": round(rows / (ms / 1e3), 1)}
+
+
 def bench_decode_gemv(torch, dev, m=1, sets=128, reps=5):
     """Grouped GEMV over `sets` distinct copies of the config-3 weight shape (> MALL)."""
     from reimagined_amd import ops
@@ -384,6 +416,8 @@ def main():
         _log(f"decode gemv {extra['decode_gemv_c3_m1']}")
         extra["decode_gemv_c3_sweep"] = bench_decode_gemv_sweep(torch, dev)
         _log(f"decode gemv sweep {extra['decode_gemv_c3_sweep']}")
+        extra["moe_c5"] = bench_moe_c5(torch, dev)
+        _log(f"moe c5 {extra['moe_c5']}")
         extra["decode_step_c5"] = bench_decode_step(torch, dev)
         _log(f"decode step {extra['decode_step_c5']}")
         extra["mamba2_decode_step"] = bench_mamba2_decode(torch, dev)

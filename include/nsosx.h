@@ -277,7 +277,8 @@ int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, int experts,
  * out[r] = sum over the row's selected experts, lowest id first, of
  * expert_out[slot] * weights[r, e], starting from 0.
  * expert_out [slots, dim] (in_dtype), out [rows, dim] (out_dtype).
- * slot_of NULL: the slot of (row r, choice i) is r * k + i. */
+ * slot_of NULL: the slot of (row r, choice i) is r * k + i.  rows <= 65535 unless
+ * dim % 4 == 0 and expert_out / out are 16-byte aligned (8 with both bf16). */
 int nsosx_moe_combine(const void* expert_out, int in_dtype, const int32_t* slot_of,
                       const int32_t* selected, const float* weights, int rows, int experts, int k,
                       int dim, void* out, int out_dtype, void* stream);

@@ -115,6 +115,28 @@ def test_moe_ffn_matches_oracle(dev, orc, hidden_dtype):
     np.testing.assert_allclose(got, want_w, rtol=1e-4, atol=1e-5 * np.abs(want_w).max())
 
 
+@pytest.mark.parametrize("in_dt,out_dt", [(torch.float32, torch.float32),
+                                           (torch.bfloat16, torch.float32),
+                                           (torch.float32, torch.bfloat16),
+                                           (torch.bfloat16, torch.bfloat16)])
+@pytest.mark.parametrize("rows,E,k,dim", [(300, 8, 2, 1024), (77, 8, 3, 1022), (1, 4, 1, 8),
+                                          (70000, 8, 2, 64)])
+def test_moe_combine_matches_oracle(dev, orc, in_dt, out_dt, rows, E, k, dim):
+    """The weighted combine alone, both input and output dtypes, the row-per-wave vector form
+    (dim % 4 == 0) and the element-wise one (dim = 1022), over the device routing: bit-exact
+    with the oracle's ascending-expert sum (a bf16 output is that sum rounded to nearest even).
+    70000 rows exceed the element-wise form's 65535-row grid limit."""
+    rng = np.random.default_rng(rows * 7 + dim + k)
+    logits = rng.standard_normal((rows, E)).astype(np.float32)
+    r = ops.moe_route(torch.from_numpy(logits).to(dev), k)
+    o = torch.from_numpy(rng.standard_normal((rows * k, dim)).astype(np.float32)).to(in_dt)
+    got = ops.moe_combine(o.to(dev), r["slot_of"], r["selected"], r["weights"], out_dtype=out_dt)
+    want = orc.moe_combine(o.float().numpy(), r["perm"].cpu().numpy(), r["offsets"].cpu().numpy(),
+                           r["weights"].cpu().numpy())
+    want_t = torch.from_numpy(want).to(out_dt)
+    assert torch.equal(got.cpu(), want_t)
+
+
 @pytest.mark.parametrize("rows", [1, 5, 32])
 def test_moe_sparse_decode_matches_oracle(dev, orc, rows):
     """Decode rows through (row, routed expert) grouped GEMVs: bit-exact against the oracle's
