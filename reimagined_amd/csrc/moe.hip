@@ -19,40 +19,56 @@ constexpr int kRouteBlock = 256;  // rows per dispatch block
 // operations: running max, exp(x - max), an in-order float sum, one
 // multiply by 1/max(sum, 1e-8f).  Top-k is a selection under the strict
 // order (value desc, index asc); renormalisation sums the selected values in
-// rank order and multiplies by 1/max(sum, 1e-9f).
+// rank order and multiplies by 1/max(sum, 1e-9f).  EMAX (>= E) bounds every
+// loop at compile time, so the row's probabilities stay in registers (a
+// runtime-indexed array of 64 lives in scratch memory); experts past E are
+// masked out.
+template <int EMAX>
 __global__ __launch_bounds__(256) void route_rows_kernel(const float* __restrict__ logits, int rows,
                                                          int E, int k, float* __restrict__ weights,
                                                          int32_t* __restrict__ selected) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= rows) return;
     const float* src = logits + (int64_t)r * E;
-    float p[kMaxExperts];
-    float mx = src[0];
-    for (int j = 1; j < E; ++j) mx = src[j] > mx ? src[j] : mx;
+    float p[EMAX];
+#pragma unroll
+    for (int j = 0; j < EMAX; ++j) p[j] = j < E ? src[j] : 0.0f;
+    float mx = p[0];
+#pragma unroll
+    for (int j = 1; j < EMAX; ++j)
+        if (j < E) mx = p[j] > mx ? p[j] : mx;
     float sum = 0.0f;
-    for (int j = 0; j < E; ++j) {
-        p[j] = expf(src[j] - mx);
-        sum = sum + p[j];
-    }
+#pragma unroll
+    for (int j = 0; j < EMAX; ++j)
+        if (j < E) {
+            p[j] = expf(p[j] - mx);
+            sum = sum + p[j];
+        }
     const float inv = 1.0f / (sum > 1e-8f ? sum : 1e-8f);
-    for (int j = 0; j < E; ++j) p[j] = p[j] * inv;
+#pragma unroll
+    for (int j = 0; j < EMAX; ++j) p[j] = p[j] * inv;
     uint64_t taken = 0;
-    int sel[kMaxExperts];
     float ssum = 0.0f;
     for (int i = 0; i < k; ++i) {
         int best = -1;
-        for (int j = 0; j < E; ++j) {
-            if ((taken >> j) & 1ull) continue;
-            if (best < 0 || p[j] > p[best]) best = j;  // ties keep the lower index
+        float bv = 0.0f;
+#pragma unroll
+        for (int j = 0; j < EMAX; ++j) {
+            const bool free = j < E && !((taken >> j) & 1ull);
+            if (free && (best < 0 || p[j] > bv)) {  // ties keep the lower index
+                best = j;
+                bv = p[j];
+            }
         }
         taken |= 1ull << best;
-        sel[i] = best;
-        ssum = ssum + p[best];
+        selected[(int64_t)r * k + i] = best;
+        ssum = ssum + bv;
     }
     const float inv2 = 1.0f / (ssum > 1e-9f ? ssum : 1e-9f);
     float* w = weights + (int64_t)r * E;
-    for (int j = 0; j < E; ++j) w[j] = ((taken >> j) & 1ull) ? p[j] * inv2 : 0.0f;
-    for (int i = 0; i < k; ++i) selected[(int64_t)r * k + i] = sel[i];
+#pragma unroll
+    for (int j = 0; j < EMAX; ++j)
+        if (j < E) w[j] = ((taken >> j) & 1ull) ? p[j] * inv2 : 0.0f;
 }
 
 // Per dispatch block of 256 rows: how many of its rows selected each expert.
@@ -253,8 +269,16 @@ extern "C" int nsosx_moe_route(const float* logits, int rows, int experts, int k
     if ((int64_t)rows * k > 2147483647LL) return fail(NSOSX_ERR_OVERFLOW, "moe_route: rows*k too large");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int nblocks = (rows + kRouteBlock - 1) / kRouteBlock;
-    hipLaunchKernelGGL(route_rows_kernel, dim3((rows + 255) / 256), dim3(256), 0, st, logits, rows,
-                       experts, k, weights, selected);
+    const dim3 rgrid((rows + 255) / 256), rblock(256);
+    if (experts <= 8)
+        hipLaunchKernelGGL(route_rows_kernel<8>, rgrid, rblock, 0, st, logits, rows, experts, k,
+                           weights, selected);
+    else if (experts <= 16)
+        hipLaunchKernelGGL(route_rows_kernel<16>, rgrid, rblock, 0, st, logits, rows, experts, k,
+                           weights, selected);
+    else
+        hipLaunchKernelGGL(route_rows_kernel<kMaxExperts>, rgrid, rblock, 0, st, logits, rows,
+                           experts, k, weights, selected);
     if (select_only) return check_launch("moe_route");
     hipLaunchKernelGGL(route_count_kernel, dim3(nblocks), dim3(kRouteBlock), 0, st, selected, rows,
                        experts, k, workspace);
