@@ -1579,15 +1579,19 @@ template <int YDT, bool GATHER, bool SQRELU>
 __global__ __launch_bounds__(kGemm3Threads, 2) void grouped_gemm3_kernel(
     const nsosx_linear_view* views, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ perm, const int8_t* __restrict__ q,
-    const float* __restrict__ act_scale, void* y) {
+    const float* __restrict__ act_scale, void* y, int ntn, int ntm, int experts) {
     extern __shared__ __align__(16) char smem3[];
-    const int e = blockIdx.z;
+    // 1-D grid over (n tile, m tile, expert), n fastest; xcd_tile() hands each XCD a
+    // contiguous run, so the n tiles of one (expert, m tile) share its rows in one L2
+    int nt, rest;
+    xcd_tile(blockIdx.x, ntn, ntm * experts, nt, rest);
+    const int e = rest / ntm;
     const int seg_begin = offsets[e];
     const int seg_rows = offsets[e + 1] - seg_begin;
-    const int m0 = blockIdx.y * kG3BM;
+    const int m0 = (rest % ntm) * kG3BM;
     if (m0 >= seg_rows) return;
     const nsosx_linear_view v = views[e];
-    const int n0 = blockIdx.x * kG3BN;
+    const int n0 = nt * kG3BN;
     if (n0 >= v.outputs) return;
     GemmProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
     gemm3_tile<YDT, false, GATHER, SQRELU>(pb, q, act_scale, perm, seg_begin, seg_rows, n0, m0, y,
@@ -2143,11 +2147,15 @@ extern "C" int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, in
     if (max_rows_per_expert == 0) return NSOSX_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const dim3 grid2((N + kBN2 - 1) / kBN2, (max_rows_per_expert + kBM2 - 1) / kBM2, experts);
-    const dim3 grid3((N + kG3BN - 1) / kG3BN, (max_rows_per_expert + kG3BM - 1) / kG3BM, experts);
+    const int ntn3 = (N + kG3BN - 1) / kG3BN, ntm3 = (max_rows_per_expert + kG3BM - 1) / kG3BM;
+    if ((int64_t)ntn3 * ntm3 * experts > 0x7fffffff)
+        return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm: too many tiles for one launch");
+    const dim3 grid3(ntn3 * ntm3 * experts);
 #define NSOSX_GGEMM(YDT, G, S)                                                                  \
     if (K % kG3BK == 0)                                                                         \
         hipLaunchKernelGGL((grouped_gemm3_kernel<YDT, G, S>), grid3, dim3(kGemm3Threads),        \
-                           kGemm3Smem, st, views_dev, offsets, perm, q, act_scale, y);          \
+                           kGemm3Smem, st, views_dev, offsets, perm, q, act_scale, y, ntn3,     \
+                           ntm3, experts);                                                      \
     else                                                                                        \
         hipLaunchKernelGGL((grouped_gemm2_kernel<YDT, G, S>), grid2, dim3(kGemm2Threads),        \
                            kGemm2Smem, st, views_dev, offsets, perm, q, act_scale, y);
