@@ -139,6 +139,106 @@ __global__ __launch_bounds__(64) void rms_inv_tiled_kernel(const void* __restric
     inv[row] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
 }
 
+// The same sums for few, long rows, where the tiled kernel's one wave per 64
+// rows leaves most SIMDs idle and runs the whole row's convert / square / add
+// chain alone.  Here two producer waves (rows 0-31 and 32-63 of the group)
+// load the column tiles (1 KB loads, kRmsDepth tiles in flight), convert and
+// square them, and write the rounded squares to a double-buffered LDS tile in
+// row order; a third wave (lane = row) adds them in order, one tile behind,
+// with one barrier per tile.  Same operations in the same order, so the same
+// bits as rms_inv_tiled_kernel.
+constexpr int kRmsPcPitch = 64 + 4;  // floats per LDS row (one tile of 64 squares + pad)
+
+template <int DT>
+__global__ __launch_bounds__(192) void rms_inv_pc_kernel(const void* __restrict__ x, int M, int K,
+                                                         float eps, float* __restrict__ inv) {
+    constexpr int ES = DT == NSOSX_F32 ? 4 : 2;
+    constexpr int PER = 16 / ES;            // elements per 16-byte piece
+    constexpr int TE = kRmsTileBytes / ES;  // elements of a row per tile
+    __shared__ __align__(16) float s_sq[2][64 * kRmsPcPitch];
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int row0 = blockIdx.x * 64;
+    const int tiles = K / TE;
+    const int64_t row_bytes = (int64_t)K * ES;
+    if (wave < 2) {
+        // load j (0..3) of a tile: row 32 wave + 8 j + lane / 8, 16-byte piece lane % 8;
+        // rows past M re-read the last row and tiles past the end the last tile
+        const char* src[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            src[j] = static_cast<const char*>(x) +
+                     min(row0 + 32 * wave + 8 * j + (lane >> 3), M - 1) * row_bytes + (lane & 7) * 16;
+        uint4 buf[kRmsDepth][4];
+        auto load_tile = [&](int t, uint4 (&b)[4]) {
+            const int64_t off = (int64_t)min(t, tiles - 1) * kRmsTileBytes;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = load_stream16(reinterpret_cast<const uint32_t*>(src[j] + off));
+        };
+#pragma unroll
+        for (int d = 0; d < kRmsDepth; ++d) load_tile(d, buf[d]);
+        for (int t0 = 0; t0 <= tiles; t0 += kRmsDepth) {
+#pragma unroll
+            for (int d = 0; d < kRmsDepth; ++d) {
+                const int t = t0 + d;
+                if (t < tiles) {
+                    float* dst = s_sq[t & 1];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint4 a = buf[d][j];
+                        float v[PER];
+                        if constexpr (DT == NSOSX_F32) {
+                            v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+                            v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+                        } else {
+                            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                v[2 * i] = __uint_as_float(w[i] << 16);
+                                v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+                            }
+                        }
+                        float* q = dst + (32 * wave + 8 * j + (lane >> 3)) * kRmsPcPitch + (lane & 7) * PER;
+#pragma unroll
+                        for (int i = 0; i < PER; i += 4)
+                            *reinterpret_cast<float4*>(q + i) =
+                                make_float4(__fmul_rn(v[i], v[i]), __fmul_rn(v[i + 1], v[i + 1]),
+                                            __fmul_rn(v[i + 2], v[i + 2]), __fmul_rn(v[i + 3], v[i + 3]));
+                    }
+                    load_tile(t + kRmsDepth, buf[d]);
+                }
+                __syncthreads();
+            }
+        }
+    } else {
+        float sum = 0.0f;
+        const int off = lane * kRmsPcPitch;
+        for (int t0 = 0; t0 <= tiles; t0 += kRmsDepth) {
+#pragma unroll
+            for (int d = 0; d < kRmsDepth; ++d) {
+                const int t = t0 + d;
+                if (t >= 1 && t <= tiles) {
+                    const float* my = s_sq[(t - 1) & 1] + off;
+#pragma unroll
+                    for (int i = 0; i < TE; i += 4) {
+                        const float4 v = *reinterpret_cast<const float4*>(my + i);
+                        sum = __fadd_rn(sum, v.x);
+                        sum = __fadd_rn(sum, v.y);
+                        sum = __fadd_rn(sum, v.z);
+                        sum = __fadd_rn(sum, v.w);
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        const int row = row0 + lane;
+        if (row < M) {
+            const float mean = __fdiv_rn(sum, static_cast<float>(K));
+            inv[row] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
+        }
+    }
+}
+
 // Few rows (decode): a workgroup per row stages the row in LDS with coalesced
 // 16-byte loads, then one lane takes the in-order sum from LDS, so the row's
 // load latency is paid once instead of once per four loads.  K <= 8192.
@@ -477,8 +577,14 @@ static int launch_quantize(const void* x, int M, int K, int bits, int rms_input,
                            rms_ws);
     } else if (rms_input && ((int64_t)K * elem) % (kRmsTileBytes * kRmsDepth) == 0 &&
                reinterpret_cast<uintptr_t>(x) % 16 == 0) {
-        hipLaunchKernelGGL((rms_inv_tiled_kernel<DT>), dim3((M + 63) / 64), dim3(64), 0, st, x, M,
-                           K, 1e-6f, rms_ws);
+        // rows of 8 KB and more in fewer than 512 groups of 64 (config 5's 16384 hidden rows of
+        // 4096: 44 -> 34 us); the one-wave form is as fast or faster elsewhere
+        if ((M + 63) / 64 < 512 && (int64_t)K * elem >= 8192)
+            hipLaunchKernelGGL((rms_inv_pc_kernel<DT>), dim3((M + 63) / 64), dim3(192), 0, st, x, M,
+                               K, 1e-6f, rms_ws);
+        else
+            hipLaunchKernelGGL((rms_inv_tiled_kernel<DT>), dim3((M + 63) / 64), dim3(64), 0, st, x,
+                               M, K, 1e-6f, rms_ws);
     } else if (rms_input) {
         const bool rvec = ((int64_t)K * elem) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
         if (rvec)
