@@ -139,9 +139,9 @@ __global__ __launch_bounds__(64) void rms_inv_tiled_kernel(const void* __restric
     inv[row] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
 }
 
-// The same sums for few, long rows, where the tiled kernel's one wave per 64
-// rows leaves most SIMDs idle and runs the whole row's convert / square / add
-// chain alone.  Here two producer waves (rows 0-31 and 32-63 of the group)
+// The same sums for fewer rows, where the tiled kernel's one wave per 64 rows
+// leaves most SIMDs idle and runs the whole row's convert / square / add chain
+// alone.  Here two producer waves (rows 0-31 and 32-63 of the group)
 // load the column tiles (1 KB loads, kRmsDepth tiles in flight), convert and
 // square them, and write the rounded squares to a double-buffered LDS tile in
 // row order; a third wave (lane = row) adds them in order, one tile behind,
@@ -177,60 +177,59 @@ __global__ __launch_bounds__(192) void rms_inv_pc_kernel(const void* __restrict_
         };
 #pragma unroll
         for (int d = 0; d < kRmsDepth; ++d) load_tile(d, buf[d]);
-        for (int t0 = 0; t0 <= tiles; t0 += kRmsDepth) {
+        // tiles is a multiple of kRmsDepth (host check): straight-line steady state, the
+        // loads past the end clamped to the last tile
+        for (int t0 = 0; t0 < tiles; t0 += kRmsDepth) {
 #pragma unroll
             for (int d = 0; d < kRmsDepth; ++d) {
                 const int t = t0 + d;
-                if (t < tiles) {
-                    float* dst = s_sq[t & 1];
+                float* dst = s_sq[t & 1];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint4 a = buf[d][j];
-                        float v[PER];
-                        if constexpr (DT == NSOSX_F32) {
-                            v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
-                            v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
-                        } else {
-                            const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+                for (int j = 0; j < 4; ++j) {
+                    const uint4 a = buf[d][j];
+                    float v[PER];
+                    if constexpr (DT == NSOSX_F32) {
+                        v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
+                        v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+                    } else {
+                        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-                            for (int i = 0; i < 4; ++i) {
-                                v[2 * i] = __uint_as_float(w[i] << 16);
-                                v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-                            }
+                        for (int i = 0; i < 4; ++i) {
+                            v[2 * i] = __uint_as_float(w[i] << 16);
+                            v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
                         }
-                        float* q = dst + (32 * wave + 8 * j + (lane >> 3)) * kRmsPcPitch + (lane & 7) * PER;
-#pragma unroll
-                        for (int i = 0; i < PER; i += 4)
-                            *reinterpret_cast<float4*>(q + i) =
-                                make_float4(__fmul_rn(v[i], v[i]), __fmul_rn(v[i + 1], v[i + 1]),
-                                            __fmul_rn(v[i + 2], v[i + 2]), __fmul_rn(v[i + 3], v[i + 3]));
                     }
-                    load_tile(t + kRmsDepth, buf[d]);
+                    float* q = dst + (32 * wave + 8 * j + (lane >> 3)) * kRmsPcPitch + (lane & 7) * PER;
+#pragma unroll
+                    for (int i = 0; i < PER; i += 4)
+                        *reinterpret_cast<float4*>(q + i) =
+                            make_float4(__fmul_rn(v[i], v[i]), __fmul_rn(v[i + 1], v[i + 1]),
+                                        __fmul_rn(v[i + 2], v[i + 2]), __fmul_rn(v[i + 3], v[i + 3]));
                 }
+                load_tile(t + kRmsDepth, buf[d]);
                 __syncthreads();
             }
         }
     } else {
+        // one tile behind the producers: tile t - 1 during their tile t, the last after the loop
         float sum = 0.0f;
         const int off = lane * kRmsPcPitch;
-        for (int t0 = 0; t0 <= tiles; t0 += kRmsDepth) {
+        auto add_tile = [&](int t) {
+            const float* my = s_sq[t & 1] + off;
 #pragma unroll
-            for (int d = 0; d < kRmsDepth; ++d) {
-                const int t = t0 + d;
-                if (t >= 1 && t <= tiles) {
-                    const float* my = s_sq[(t - 1) & 1] + off;
-#pragma unroll
-                    for (int i = 0; i < TE; i += 4) {
-                        const float4 v = *reinterpret_cast<const float4*>(my + i);
-                        sum = __fadd_rn(sum, v.x);
-                        sum = __fadd_rn(sum, v.y);
-                        sum = __fadd_rn(sum, v.z);
-                        sum = __fadd_rn(sum, v.w);
-                    }
-                }
-                __syncthreads();
+            for (int i = 0; i < TE; i += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(my + i);
+                sum = __fadd_rn(sum, v.x);
+                sum = __fadd_rn(sum, v.y);
+                sum = __fadd_rn(sum, v.z);
+                sum = __fadd_rn(sum, v.w);
             }
+        };
+        for (int t = 0; t < tiles; ++t) {
+            if (t > 0) add_tile(t - 1);
+            __syncthreads();
         }
+        add_tile(tiles - 1);
         const int row = row0 + lane;
         if (row < M) {
             const float mean = __fdiv_rn(sum, static_cast<float>(K));
@@ -577,9 +576,10 @@ static int launch_quantize(const void* x, int M, int K, int bits, int rms_input,
                            rms_ws);
     } else if (rms_input && ((int64_t)K * elem) % (kRmsTileBytes * kRmsDepth) == 0 &&
                reinterpret_cast<uintptr_t>(x) % 16 == 0) {
-        // rows of 8 KB and more in fewer than 512 groups of 64 (config 5's 16384 hidden rows of
-        // 4096: 44 -> 34 us); the one-wave form is as fast or faster elsewhere
-        if ((M + 63) / 64 < 512 && (int64_t)K * elem >= 8192)
+        // fewer than 512 groups of 64 rows: the three-wave form (config 5's 16384 hidden rows of
+        // 4096 in 33 us, its 8192 input rows of 1024 in 5 us less); with more groups the one-wave
+        // form streams faster (config 4: 40796 rows of 1024 / 2048, 3 / 6 us less)
+        if ((M + 63) / 64 < 512)
             hipLaunchKernelGGL((rms_inv_pc_kernel<DT>), dim3((M + 63) / 64), dim3(192), 0, st, x, M,
                                K, 1e-6f, rms_ws);
         else
