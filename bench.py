@@ -170,6 +170,14 @@ def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=3
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "kernel": name, "algorithmic_bytes": int(amount)}
+        if name in ("conv_scan", "scan"):
+            # 16 exp + 64 VALU ops per (token, channel) are irreducible (one exp per state and
+            # four FMA-class ops); at T*d_inner pairs this issue time exceeds the HBM time
+            pairs = T * d_inner
+            issue_s = pairs * d_state * (2 + 4) * 4 / 64 / 1024 / 2.4e9
+            roof["note"] = ("VALU/transcendental-issue bound, not HBM: the recurrence alone needs "
+                            f"{issue_s * 1e3:.3f} ms of issue at 2.4 GHz (exp = 2 FMA slots) "
+                            f"against {amount / HBM_PEAK_GBS / 1e6:.3f} ms of HBM time")
     return roof, work
 
 
