@@ -142,12 +142,13 @@ __global__ __launch_bounds__(64) void rms_inv_tiled_kernel(const void* __restric
 // The same sums for fewer rows, where the tiled kernel's one wave per 64 rows
 // leaves most SIMDs idle and runs the whole row's convert / square / add chain
 // alone.  Here two producer waves (rows 0-31 and 32-63 of the group)
-// load the column tiles (1 KB loads, kRmsDepth tiles in flight), convert and
+// load the column tiles (1 KB loads, kRmsPcDepth tiles in flight), convert and
 // square them, and write the rounded squares to a double-buffered LDS tile in
 // row order; a third wave (lane = row) adds them in order, one tile behind,
 // with one barrier per tile.  Same operations in the same order, so the same
 // bits as rms_inv_tiled_kernel.
 constexpr int kRmsPcPitch = 64 + 4;  // floats per LDS row (one tile of 64 squares + pad)
+constexpr int kRmsPcDepth = 8;       // tiles in flight per producer wave
 
 template <int DT>
 __global__ __launch_bounds__(192) void rms_inv_pc_kernel(const void* __restrict__ x, int M, int K,
@@ -169,19 +170,19 @@ __global__ __launch_bounds__(192) void rms_inv_pc_kernel(const void* __restrict_
         for (int j = 0; j < 4; ++j)
             src[j] = static_cast<const char*>(x) +
                      min(row0 + 32 * wave + 8 * j + (lane >> 3), M - 1) * row_bytes + (lane & 7) * 16;
-        uint4 buf[kRmsDepth][4];
+        uint4 buf[kRmsPcDepth][4];
         auto load_tile = [&](int t, uint4 (&b)[4]) {
             const int64_t off = (int64_t)min(t, tiles - 1) * kRmsTileBytes;
 #pragma unroll
             for (int j = 0; j < 4; ++j) b[j] = load_stream16(reinterpret_cast<const uint32_t*>(src[j] + off));
         };
 #pragma unroll
-        for (int d = 0; d < kRmsDepth; ++d) load_tile(d, buf[d]);
-        // tiles is a multiple of kRmsDepth (host check): straight-line steady state, the
+        for (int d = 0; d < kRmsPcDepth; ++d) load_tile(d, buf[d]);
+        // tiles is a multiple of kRmsPcDepth (host check): straight-line steady state, the
         // loads past the end clamped to the last tile
-        for (int t0 = 0; t0 < tiles; t0 += kRmsDepth) {
+        for (int t0 = 0; t0 < tiles; t0 += kRmsPcDepth) {
 #pragma unroll
-            for (int d = 0; d < kRmsDepth; ++d) {
+            for (int d = 0; d < kRmsPcDepth; ++d) {
                 const int t = t0 + d;
                 float* dst = s_sq[t & 1];
 #pragma unroll
@@ -206,7 +207,7 @@ __global__ __launch_bounds__(192) void rms_inv_pc_kernel(const void* __restrict_
                             make_float4(__fmul_rn(v[i], v[i]), __fmul_rn(v[i + 1], v[i + 1]),
                                         __fmul_rn(v[i + 2], v[i + 2]), __fmul_rn(v[i + 3], v[i + 3]));
                 }
-                load_tile(t + kRmsDepth, buf[d]);
+                load_tile(t + kRmsPcDepth, buf[d]);
                 __syncthreads();
             }
         }
@@ -579,7 +580,7 @@ static int launch_quantize(const void* x, int M, int K, int bits, int rms_input,
         // fewer than 512 groups of 64 rows: the three-wave form (config 5's 16384 hidden rows of
         // 4096 in 33 us, its 8192 input rows of 1024 in 5 us less); with more groups the one-wave
         // form streams faster (config 4: 40796 rows of 1024 / 2048, 3 / 6 us less)
-        if ((M + 63) / 64 < 512)
+        if ((M + 63) / 64 < 512 && ((int64_t)K * elem) % (kRmsTileBytes * kRmsPcDepth) == 0)
             hipLaunchKernelGGL((rms_inv_pc_kernel<DT>), dim3((M + 63) / 64), dim3(192), 0, st, x, M,
                                K, 1e-6f, rms_ws);
         else

@@ -49,10 +49,12 @@ def test_quantize_random_f32(dev, orc, m, k, rms):
 
 
 @pytest.mark.parametrize("rms", [False, True])
-@pytest.mark.parametrize("m,k", [(37, 1024), (1200, 1024), (1201, 2048), (1029, 512), (1026, 4096)])
+@pytest.mark.parametrize("m,k", [(37, 1024), (1200, 1024), (1201, 2048), (1029, 512), (1026, 4096),
+                                 (32769, 1024)])
 def test_quantize_bf16_input(dev, orc, rms, m, k):
     """bf16 rows; M > 1024 with K = 512 / 1024 / 2048 / 4096 takes the several-rows-per-wave
-    kernel, including row counts that leave a wave with rows past M."""
+    kernel, including row counts that leave a wave with rows past M.  The RMS pass is the
+    three-wave form below 512 groups of 64 rows and the one-wave tiled form from 32705 rows."""
     rng = np.random.default_rng(3)
     x = (rng.standard_normal((m, k)) * rng.uniform(0.5, 8.0, (m, 1))).astype(np.float32)
     xb = torch.from_numpy(x).to(torch.bfloat16)
