@@ -167,3 +167,42 @@ def test_moe_sparse_decode_matches_oracle(dev, orc, rows):
     np.testing.assert_array_equal(res["out"].cpu().numpy(), want)
     w_orc, sel_orc = orc.topk_mask(orc.softmax_rows(logits), k)
     np.testing.assert_array_equal(sel, sel_orc)
+
+
+def test_moe_ffn_full_size_sampled(dev, orc):
+    """Config 5's MoE prefill at full size (8192 bf16 tokens, 8 experts of 1024 -> 4096 -> 1024,
+    top-2, bf16 hidden), the shapes the bench times: the permutation bit-exact, and for
+    sampled slots the up projection (bf16 of the oracle's squared-ReLU output) and the down
+    projection (on the GPU's hidden row) bit-exact, and sampled combined rows bit-exact with
+    the oracle's ascending-expert sum over the GPU's expert outputs."""
+    from reimagined_amd import workloads
+    moe_p, _ = workloads.config5(rows=8192, decode_rows=1, d_inner=64)
+    E, k = 8, 2
+    moe = MoEFFN(moe_p["w_up"], moe_p["w_down"], dev, k=k, rms_input=True,
+                 hidden_dtype=torch.bfloat16)
+    xb = torch.from_numpy(moe_p["x"]).to(torch.bfloat16)
+    logits = moe_p["logits"]
+    res = moe.forward(xb.to(dev), torch.from_numpy(logits).to(dev), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _, _, _, offsets, perm = _route_oracle(orc, logits, k)
+    np.testing.assert_array_equal(res["perm"].cpu().numpy(), perm)
+    np.testing.assert_array_equal(res["offsets"].cpu().numpy(), offsets)
+    h = res["h"]
+    o = res["o"]
+    xf = xb.float().numpy()
+    rng = np.random.default_rng(505)
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        slots = np.unique(np.concatenate([rng.choice(np.arange(lo, hi), 12, replace=False),
+                                          [lo, hi - 1]]))
+        pu, wsu, _ = orc.pack_weights(moe_p["w_up"][e])
+        pd, wsd, _ = orc.pack_weights(moe_p["w_down"][e])
+        hu = orc.squared_relu(orc.bitlinear_forward(xf[perm[slots]], pu, wsu, 4096, rms_input=True))
+        ts = torch.from_numpy(slots).to(dev)
+        h_gpu = h[ts].float().cpu().numpy()
+        np.testing.assert_array_equal(h_gpu, torch.from_numpy(hu).to(torch.bfloat16).float().numpy())
+        od = orc.bitlinear_forward(h_gpu, pd, wsd, 1024, rms_input=True)
+        np.testing.assert_array_equal(o[ts].cpu().numpy(), od)
+    rows = np.unique(rng.choice(8192, 64, replace=False))
+    want = orc.moe_combine(o.cpu().numpy(), perm, offsets, res["weights"].cpu().numpy())
+    np.testing.assert_array_equal(res["out"].cpu().numpy()[rows], want[rows])
