@@ -244,3 +244,26 @@ def test_rejects_bad_arguments(dev):
         ops.ternary_gemm(q, s, pk, 0.0, 4)  # weight_scale must be > 0
     with pytest.raises(ValueError):
         ops.ternary_gemm(q, s, pk, 1.0, 4, path=0, want_y=False)  # no output
+
+
+def test_config3_full_size_sampled(dev, orc):
+    """Config 3 at full size through the dispatching entry point: the 4096 x 2048 x 8192 prefill
+    GEMM (bf16 out, the bench's launch) bit-exact on sampled rows, and the decode GEMV / skinny
+    paths on the same 8192 x 2048 weights at M = 1, 2, 16 and 32 bit-exact in full."""
+    from reimagined_amd import workloads
+    c3 = workloads.config3()
+    packed, ws, codes = orc.pack_weights(c3["w"])
+    q, s = orc.quantize_act(c3["x"], 8)
+    pk = torch.from_numpy(packed.view(np.int32)).to(dev)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    y = ops.ternary_gemm(t(q), t(s), pk, ws, 8192, None, None, torch.bfloat16)
+    rng = np.random.default_rng(33)
+    rows = np.unique(np.concatenate([rng.choice(4096, 48, replace=False), [0, 4095]]))
+    y_want = orc.dequant(orc.gemm_i8(q[rows], codes), s[rows], ws, None, None)
+    np.testing.assert_array_equal(y[t(rows)].float().cpu().numpy(), _bf16_round(y_want))
+    for m in (1, 2, 16, 32):
+        yd, acc = ops.ternary_gemm(t(q[:m]), t(s[:m]), pk, ws, 8192, None, None, torch.float32,
+                                   want_acc=True)
+        acc_want = orc.gemm_i8(q[:m], codes)
+        np.testing.assert_array_equal(acc.cpu().numpy(), acc_want)
+        np.testing.assert_array_equal(yd.cpu().numpy(), orc.dequant(acc_want, s[:m], ws, None, None))
