@@ -176,6 +176,38 @@ def test_step_matches_oracle_and_prefill(dev, orc, H, P, N, G, per_state):
     np.testing.assert_allclose(state.cpu().numpy(), fp, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("R,offset_bc", [(256, 0), (37, 0), (37, 1)])
+def test_step_bf16_config5(dev, orc, R, offset_bc):
+    """Config 5's decode step: bf16 x, dt, z, B, C against an fp32 state [R, 2048, 16]
+    (R = 256 is the bench's launch; 37 rows leave a partial row block; B and C one element
+    off 8-byte alignment take the two-byte loads).  The oracle runs in fp32 on the same
+    bf16-rounded inputs; y within the bf16 bound, the state within the fp32 bound."""
+    rng = np.random.default_rng(500 + R + offset_bc)
+    H, P, N, G = 2048, 1, 16, 1
+    inp = _inputs(rng, R, H, P, N, G, True)
+    rb = {k: (torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+              if k in ("x", "dt", "B", "C", "z") else v) for k, v in inp.items()}
+    st0 = rng.normal(0, 0.1, (R, H * P, N)).astype(np.float32)
+    state = _t(dev, st0)
+    bf = lambda k: _t(dev, inp[k], torch.bfloat16)
+    if offset_bc:
+        # B and C as [R, N] views one element into a larger buffer
+        def shifted(k):
+            big = torch.zeros(R * N + 1, dtype=torch.bfloat16, device=dev)
+            big[1:] = _t(dev, inp[k], torch.bfloat16).reshape(-1)
+            return big[1:].view(R, N)
+        Bt, Ct = shifted("B"), shifted("C")
+    else:
+        Bt, Ct = bf("B"), bf("C")
+    y = ops.selective_scan_step(bf("x"), bf("dt"), _t(dev, inp["a_log"]), Bt, Ct,
+                                _t(dev, inp["D"]), bf("z"), state, H, P, N, G)
+    wy, wst = orc.scan_step(rb["x"], rb["dt"], rb["a_log"], rb["B"], rb["C"], rb["D"], rb["z"],
+                            st0, H, P, N, G)
+    scale = np.abs(wy).max()
+    np.testing.assert_allclose(y.float().cpu().numpy(), wy, rtol=2e-2, atol=2e-2 * scale / 64)
+    np.testing.assert_allclose(state.cpu().numpy(), wst, rtol=RTOL, atol=ATOL)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_conv1d_matches_oracle(dev, orc, dtype):
     rng = np.random.default_rng(2)
