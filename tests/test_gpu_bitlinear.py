@@ -267,3 +267,33 @@ def test_config3_full_size_sampled(dev, orc):
         acc_want = orc.gemm_i8(q[:m], codes)
         np.testing.assert_array_equal(acc.cpu().numpy(), acc_want)
         np.testing.assert_array_equal(yd.cpu().numpy(), orc.dequant(acc_want, s[:m], ws, None, None))
+
+
+@pytest.mark.parametrize("shift_y,shift_affine", [(0, 1), (1, 0), (4, 4)])
+def test_gemm_epilogue_alignment(dev, orc, shift_y, shift_affine):
+    """The MFMA GEMM's row-store epilogue needs 16-byte aligned output, magnitude and bias;
+    outputs and affine vectors that start a few elements into their buffers take the
+    accumulator-order stores instead, with the same bits (bf16 output, magnitude and bias)."""
+    from reimagined_amd._lib import call
+    from reimagined_amd.ops import _p, _stream
+    rng = np.random.default_rng(71 + shift_y * 3 + shift_affine)
+    m, n, k = 300, 768, 512
+    w = _weights(rng, n, k)
+    packed, ws, codes = orc.pack_weights(w)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    q, s = orc.quantize_act(x, 8)
+    mg = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    bs = rng.standard_normal(n).astype(np.float32)
+    y_want = _bf16_round(orc.dequant(orc.gemm_i8(q, codes), s, ws, mg, bs))
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    mg_buf = torch.zeros(n + shift_affine, dtype=torch.float32, device=dev)
+    bs_buf = torch.zeros(n + shift_affine, dtype=torch.float32, device=dev)
+    mg_buf[shift_affine:] = t(mg)
+    bs_buf[shift_affine:] = t(bs)
+    y_buf = torch.zeros(m * n + shift_y, dtype=torch.bfloat16, device=dev)
+    y = y_buf[shift_y:].view(m, n)
+    pk = torch.from_numpy(packed.view(np.int32)).to(dev)
+    qd, sd = t(q), t(s)  # held until the kernel has run: a freed temporary is reused at once
+    call("nsosx_ternary_gemm_path", _p(qd), _p(sd), _p(pk), ws, m, k, n,
+         _p(mg_buf[shift_affine:]), _p(bs_buf[shift_affine:]), _p(y), 1, None, 1, _stream())
+    np.testing.assert_array_equal(y.float().cpu().numpy(), y_want)
