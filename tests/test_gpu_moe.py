@@ -206,3 +206,53 @@ def test_moe_ffn_full_size_sampled(dev, orc):
     rows = np.unique(rng.choice(8192, 64, replace=False))
     want = orc.moe_combine(o.cpu().numpy(), perm, offsets, res["weights"].cpu().numpy())
     np.testing.assert_array_equal(res["out"].cpu().numpy()[rows], want[rows])
+
+
+@pytest.mark.parametrize("gather,sqrelu,out_dtype", [(True, True, torch.bfloat16),
+                                                     (False, False, torch.float32),
+                                                     (True, False, torch.float32),
+                                                     (False, True, torch.bfloat16)])
+def test_grouped_gemm_segments(dev, orc, gather, sqrelu, out_dtype):
+    """The grouped ternary GEMM over constructed expert segments: empty experts, a single row,
+    segments across one and several 128-row tiles, N with an edge tile (520) and K = 384
+    (three ring stages), with magnitude and bias; each segment bit-exact against the oracle's
+    dequantized product (squared ReLU, bf16 RNE where asked)."""
+    rng = np.random.default_rng(11 + 2 * gather + sqrelu)
+    counts = [0, 1, 129, 0, 300, 64, 257]
+    E, K, N = len(counts), 384, 520
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    slots = int(offsets[-1])
+    rows = slots + 17
+    q = rng.integers(-127, 128, size=(rows, K), dtype=np.int8)
+    s = rng.uniform(0.001, 0.02, rows).astype(np.float32)
+    perm = rng.permutation(rows)[:slots].astype(np.int32) if gather else np.arange(slots, dtype=np.int32)
+    ws_, packs, codes, mags, biases = [], [], [], [], []
+    entries = []
+    for e in range(E):
+        pk, wsc, cd = orc.pack_weights(rng.standard_normal((N, K)).astype(np.float32))
+        mg = rng.uniform(0.5, 1.5, N).astype(np.float32)
+        bs = rng.standard_normal(N).astype(np.float32)
+        pk_t = torch.from_numpy(pk.view(np.int32)).to(dev)
+        entries.append((pk_t, wsc, K, N, torch.from_numpy(mg).to(dev), torch.from_numpy(bs).to(dev)))
+        ws_.append(wsc); codes.append(cd); mags.append(mg); biases.append(bs)
+    views = ops.LinearViewArray(entries, dev)
+    qd, sd = torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev)
+    offd, permd = torch.from_numpy(offsets).to(dev), torch.from_numpy(perm).to(dev)
+    if gather:
+        y = ops.grouped_ternary_gemm(views, offd, permd, qd, sd, N, max(counts), sqrelu, True,
+                                     out_dtype)
+    else:
+        y = ops.grouped_ternary_gemm(views, offd, None, qd[:slots], sd[:slots], N, max(counts),
+                                     sqrelu, False, out_dtype)
+    got = y.float().cpu().numpy()
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi == lo:
+            continue
+        src = perm[lo:hi]
+        want = orc.dequant(orc.gemm_i8(q[src], codes[e]), s[src], ws_[e], mags[e], biases[e])
+        if sqrelu:
+            want = orc.squared_relu(want)
+        if out_dtype == torch.bfloat16:
+            want = torch.from_numpy(want).to(torch.bfloat16).float().numpy()
+        np.testing.assert_array_equal(got[lo:hi], want, err_msg=f"expert {e}")
