@@ -292,9 +292,10 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
 // sequence in groups of 4 tokens.  Lane q of a channel forms the
 // per-(token, channel) terms of token r0 + q only: the causal convolution
 // (its window gathered from the quad's and the previous group's raw inputs by
-// DPP), bias + SiLU, delta = softplus(dt) and delta * x; DPP broadcasts then
-// hand every lane all four tokens' terms.  The recurrence runs the four
-// tokens, the 4x4 transpose-reduce leaves lane q with the readout of token
+// DPP), bias + SiLU, delta = softplus(dt) and delta * x; a 32-byte exchange
+// through the wave's LDS slice then hands every lane all four tokens' delta and
+// delta * x (two reads instead of eight VALU broadcasts).  The recurrence runs
+// the four tokens, the 4x4 transpose-reduce leaves lane q with the readout of token
 // r0 + q, and lane q applies the D skip and the SiLU(z) gate and stores it.
 // B and C (shared by all channels of a group) are staged per 32-token chunk
 // in the wave's own LDS slice, converted to float once.  There is no
@@ -305,16 +306,6 @@ constexpr int kQuadTC = 32;       // tokens per B/C chunk
 constexpr int kQuadCh = 16;       // channels per wave
 constexpr int kQuadMaxW = 4;
 constexpr int kQuadRedStride = 20;  // floats per channel row of the readout transpose
-
-__device__ __forceinline__ float quad_bcast(float v, int k) {
-    // quad_perm [k, k, k, k]
-    switch (k) {
-        case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x00, 0xF, 0xF, true));
-        case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x55, 0xF, 0xF, true));
-        case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xAA, 0xF, 0xF, true));
-        default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xFF, 0xF, 0xF, true));
-    }
-}
 
 // lane q reads lane (q - d) mod 4 of its quad: quad_perm [(0-d)&3, (1-d)&3, (2-d)&3, (3-d)&3]
 __device__ __forceinline__ float quad_back(float v, int d) {
@@ -381,6 +372,7 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
     constexpr int BCN = NP / 2;                 // states per staging lane (two lanes per row)
     __shared__ __align__(16) float s_bc[2][kQuadTC][NP];
     __shared__ __align__(16) float s_red[kQuadCh * kQuadRedStride];
+    __shared__ __align__(16) float2 s_dx[kQuadCh][4];  // {delta, delta * x} of the group's 4 tokens
     __shared__ int s_pick;
 
     const int lane = threadIdx.x;
@@ -590,21 +582,27 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
             const float sp = softplus_sel(dtcur);
             const float dl = valid ? sp : 0.0f;
             const float dx = dl * xv;
+            // the quad's four tokens through the wave's LDS slice (LDS operations of one
+            // wave complete in order): two reads instead of eight VALU broadcasts
+            s_dx[lane >> 2][q] = make_float2(dl, dx);
+            const float4 t01 = *reinterpret_cast<const float4*>(&s_dx[lane >> 2][0]);
+            const float4 t23 = *reinterpret_cast<const float4*>(&s_dx[lane >> 2][2]);
+            const float dlk[4] = {t01.x, t01.z, t23.x, t23.z};
+            const float dxk[4] = {t01.y, t01.w, t23.y, t23.w};
             // ---- recurrence over the group's four tokens: all decays first --------
-            // (each broadcast is folded into its multiply as a DPP operand)
             float a[4][SPL];
 #pragma unroll
             for (int k = 0; k < 4; ++k)
 #pragma unroll
                 for (int i = 0; i < SPL; ++i)
-                    a[k][i] = __builtin_amdgcn_exp2f(quad_bcast(dl, k) * a2[i]);
+                    a[k][i] = __builtin_amdgcn_exp2f(dlk[k] * a2[i]);
             float part[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 float p = 0.0f;
 #pragma unroll
                 for (int i = 0; i < SPL; ++i) {
-                    st[i] = __fmaf_rn(a[k][i], st[i], quad_bcast(dx, k) * bq[k][i]);
+                    st[i] = __fmaf_rn(a[k][i], st[i], dxk[k] * bq[k][i]);
                     p = __fmaf_rn(st[i], cq[k][i], p);
                 }
                 part[k] = p;
