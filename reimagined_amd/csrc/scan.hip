@@ -291,8 +291,8 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
 // holding SPL = N/4 (rounded up) states in registers.  The wave walks its
 // sequence in groups of 4 tokens.  Lane q of a channel forms the
 // per-(token, channel) terms of token r0 + q only: the causal convolution
-// (its window gathered from the quad's and the previous group's raw inputs by
-// DPP), bias + SiLU, delta = softplus(dt) and delta * x; a 32-byte exchange
+// (its window read from an 8-slot LDS row holding the previous and this
+// group's raw inputs), bias + SiLU, delta = softplus(dt) and delta * x; a 32-byte exchange
 // through the wave's LDS slice then hands every lane all four tokens' delta and
 // delta * x (two reads instead of eight VALU broadcasts).  The recurrence runs
 // the four tokens, the 4x4 transpose-reduce leaves lane q with the readout of token
@@ -306,15 +306,6 @@ constexpr int kQuadTC = 32;       // tokens per B/C chunk
 constexpr int kQuadCh = 16;       // channels per wave
 constexpr int kQuadMaxW = 4;
 constexpr int kQuadRedStride = 20;  // floats per channel row of the readout transpose
-
-// lane q reads lane (q - d) mod 4 of its quad: quad_perm [(0-d)&3, (1-d)&3, (2-d)&3, (3-d)&3]
-__device__ __forceinline__ float quad_back(float v, int d) {
-    switch (d) {
-        case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x93, 0xF, 0xF, true));
-        case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));
-        default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x39, 0xF, 0xF, true));
-    }
-}
 
 // Workgroup -> (sequence rank, channel block).  Consecutive workgroup ids go
 // round-robin to the 8 XCDs, each with its own L2; this map hands every run of
@@ -373,6 +364,7 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
     __shared__ __align__(16) float s_bc[2][kQuadTC][NP];
     __shared__ __align__(16) float s_red[kQuadCh * kQuadRedStride];
     __shared__ __align__(16) float2 s_dx[kQuadCh][4];  // {delta, delta * x} of the group's 4 tokens
+    __shared__ float s_xw[kQuadCh][8];  // conv window: raw x of the previous and this group
     __shared__ int s_pick;
 
     const int lane = threadIdx.x;
@@ -516,7 +508,7 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
         tnext += 4;
     };
 
-    float xprev = 0.0f;  // raw x of this lane's token in the previous group (0 before t0)
+    if (CONV) s_xw[lane >> 2][q] = 0.0f;  // the window before t0 is zero
     // the group whose readout is pending: its validity, conv output, raw gate and base token
     bool pv_valid = false;
     float pv_xv = 0.0f;
@@ -562,23 +554,23 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
             // masked, so the group has no divergent branch) -------------------------
             float xv;
             if (CONV) {
-                // tap j multiplies x[tg - 3 + j]: lag d = 3 - j, read from lane
-                // p = (q - d) mod 4, which is this group's token when q >= d and the
-                // previous group's when q < d.  The source lane picks what it hands
-                // out (its current x when p < 4 - d, else its previous one), so the
-                // reader's lag shift folds into the multiply-add as a DPP operand.
+                // the channel's row holds the previous group's raw x in slots 0-3 and
+                // this group's in 4-7, so tap j (x[tg - 3 + j]) of token tg = r0 + q is
+                // slot q + 1 + j.  LDS operations of one wave complete in order; the
+                // compiler barriers keep the other lanes' slots from being read before
+                // this group's write or overwritten before the reads.
+                float* row = s_xw[lane >> 2];
+                row[4 + q] = xcur;
+                asm volatile("" ::: "memory");
                 float acc = 0.0f;
 #pragma unroll
-                for (int j = 0; j < kQuadMaxW; ++j) {
-                    const int d = kQuadMaxW - 1 - j;
-                    const float src = d == 0 ? xcur : (q < 4 - d ? xcur : xprev);
-                    acc = __fmaf_rn(d == 0 ? src : quad_back(src, d), cw[j], acc);
-                }
+                for (int j = 0; j < kQuadMaxW; ++j) acc = __fmaf_rn(row[q + 1 + j], cw[j], acc);
+                asm volatile("" ::: "memory");
+                row[q] = xcur;  // the next group's previous x
                 xv = silu_fast(acc + cb);  // finite; an invalid token's dl = 0 cancels it
             } else {
                 xv = xcur;
             }
-            xprev = xcur;
             const float sp = softplus_sel(dtcur);
             const float dl = valid ? sp : 0.0f;
             const float dx = dl * xv;
