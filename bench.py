@@ -141,6 +141,41 @@ def bench_mamba2_decode(torch, dev, rows=1, reps=50):
             "graph_us_per_step": round(graph_us, 1), "kernels_per_step": 9}
 
 
+def bench_mamba2_prefill(torch, dev, reps=5):
+    """Faithful Mamba-2 block forward (d_model 1024, 32 heads x 64, N 16, one A per head, conv 4,
+    f32 activations as in the reference) over config 4's 32 ragged sequences (T = 40796): the
+    five projections, B/C conv, fused conv + scan, gated norm and out_proj."""
+    from reimagined_amd import workloads
+    from reimagined_amd.layers import Mamba2Block
+    rng = np.random.default_rng(42)
+    d, H, P, N, G, K = 1024, 32, 64, 16, 1, 4
+    inner, gs = H * P, G * N
+    w = lambda n, k: rng.standard_normal((n, k)).astype(np.float32)
+    params = {"w_x": w(inner, d), "w_z": w(inner, d), "w_B": w(gs, d), "w_C": w(gs, d),
+              "w_dt": w(H, d), "w_out": w(d, inner),
+              "conv_w": (rng.standard_normal((inner + 2 * gs, K)) * 0.5).astype(np.float32),
+              "conv_b": np.zeros(inner + 2 * gs, np.float32),
+              "a_log": rng.standard_normal(H).astype(np.float32),
+              "d_skip": np.ones(H, np.float32), "norm_w": np.ones(inner, np.float32),
+              "H": H, "P": P, "N": N, "G": G}
+    blk = Mamba2Block(params, dev)
+    _, inp = workloads.config4()
+    cu = torch.from_numpy(inp["cu_seqlens"]).to(dev)
+    T = int(inp["cu_seqlens"][-1])
+    u = torch.randn((T, d), device=dev)
+    for _ in range(2):
+        blk.forward(u, cu)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        blk.forward(u, cu)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    return {"tokens": T, "ms": round(ms, 4), "tokens_per_s": round(T / (ms / 1e3), 1)}
+
+
 def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=32):
     """Algorithmic work of each layer kernel per launch (bytes or int8 ops)."""
     work = {
@@ -428,6 +463,8 @@ def main():
         _log(f"moe c5 {extra['moe_c5']}")
         extra["decode_step_c5"] = bench_decode_step(torch, dev)
         _log(f"decode step {extra['decode_step_c5']}")
+        extra["mamba2_prefill"] = bench_mamba2_prefill(torch, dev)
+        _log(f"mamba2 prefill {extra['mamba2_prefill']}")
         extra["mamba2_decode_step"] = bench_mamba2_decode(torch, dev)
         _log(f"mamba2 decode step {extra['mamba2_decode_step']}")
         sc = stages.get("conv_scan")

@@ -349,7 +349,7 @@ __device__ __forceinline__ float softplus_sel(float v) {
     return v > 20.0f ? v : (u == 1.0f ? e : mid);
 }
 
-template <int ADT, int SPL, bool GATE, bool CONV>
+template <int ADT, int SPL, bool GATE, bool CONV, bool PH = false>
 __global__ __launch_bounds__(64) void scan_quad_kernel(
     const void* __restrict__ x, int64_t x_stride, const void* __restrict__ dt,
     const float* __restrict__ a_log, int a_per_state, const void* __restrict__ Bm,
@@ -582,12 +582,23 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
             const float dlk[4] = {t01.x, t01.z, t23.x, t23.z};
             const float dxk[4] = {t01.y, t01.w, t23.y, t23.w};
             // ---- recurrence over the group's four tokens: all decays first --------
+            // (PH, one A per head: every state of the channel decays alike, one exp per
+            // token; padded states carry B = C = 0, so their shared decay is harmless)
             float a[4][SPL];
+            if constexpr (!PH) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
+                for (int k = 0; k < 4; ++k)
 #pragma unroll
-                for (int i = 0; i < SPL; ++i)
-                    a[k][i] = __builtin_amdgcn_exp2f(dlk[k] * a2[i]);
+                    for (int i = 0; i < SPL; ++i)
+                        a[k][i] = __builtin_amdgcn_exp2f(dlk[k] * a2[i]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float ak = __builtin_amdgcn_exp2f(dlk[k] * a2[0]);
+#pragma unroll
+                    for (int i = 0; i < SPL; ++i) a[k][i] = ak;
+                }
+            }
             float part[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -914,11 +925,19 @@ static int scan_fwd_launch(const void* x, int64_t x_stride, const void* dt, cons
     if (N <= 16 && per_group % kQuadCh == 0 && (!conv || conv_width <= kQuadMaxW) && idx32) {
         const dim3 grid(Dm / kQuadCh, num_seqs), block(64);
         const int spl = N <= 4 ? 1 : N <= 8 ? 2 : 4;
-#define NSOSX_QSCAN(ADT, SPL, GATE, CONV)                                                        \
-    hipLaunchKernelGGL((scan_quad_kernel<ADT, SPL, GATE, CONV>), grid, block, 0, st, x, x_stride, \
-                       dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens, num_seqs,       \
-                       total_tokens, H, P, N, G, conv_w, conv_b, conv_width, initial_state,      \
-                       final_state, y);
+        // one A per head with N = 16 (the faithful Mamba-2 block): one decay exp per token
+        const bool ph = !a_per_state && spl == 4;
+#define NSOSX_QSCAN(ADT, SPL, GATE, CONV)                                                          \
+    if (SPL == 4 && ph)                                                                            \
+        hipLaunchKernelGGL((scan_quad_kernel<ADT, SPL, GATE, CONV, SPL == 4>), grid, block, 0, st, \
+                           x, x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens,  \
+                           num_seqs, total_tokens, H, P, N, G, conv_w, conv_b, conv_width,         \
+                           initial_state, final_state, y);                                         \
+    else                                                                                           \
+        hipLaunchKernelGGL((scan_quad_kernel<ADT, SPL, GATE, CONV, false>), grid, block, 0, st, x, \
+                           x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens,     \
+                           num_seqs, total_tokens, H, P, N, G, conv_w, conv_b, conv_width,         \
+                           initial_state, final_state, y);
 #define NSOSX_QSCAN_C(ADT, SPL, GATE) \
     if (conv) { NSOSX_QSCAN(ADT, SPL, GATE, true) } else { NSOSX_QSCAN(ADT, SPL, GATE, false) }
 #define NSOSX_QSCAN_G(ADT, SPL) \
