@@ -132,6 +132,12 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_reg_kernel(const void* __res
     float g[CH][8];
 #pragma unroll
     for (int c = 0; c < CH; ++c) load8v<DT>(y, base + (c * 64 + lane) * 8, g[c]);
+    // gamma is fetched with the row, so the output pass waits on no further load
+    float gm[CH][8];
+    if (gamma) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) load8v<NSOSX_F32>(gamma, (c * 64 + lane) * 8, gm[c]);
+    }
     if (GATED) {
         float zv[CH][8];
 #pragma unroll
@@ -155,7 +161,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_reg_kernel(const void* __res
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             o[k] = g[c][k] * inv;
-            if (gamma) o[k] = o[k] * gamma[e0 + k];
+            if (gamma) o[k] = o[k] * gm[c][k];
         }
         store8v<ODT>(out, base + e0, o);
     }
@@ -242,7 +248,7 @@ extern "C" int nsosx_rmsnorm_gated(const void* y, const void* z, const float* ga
     const dim3 grid((rows + 3) / 4), block(256);
     const bool reg = dim % 512 == 0 && dim <= 4096 &&
                      ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(z) |
-                       reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+                       reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(gamma)) & 15) == 0;
     if (reg) {
 #define NSOSX_RNR(D, O, GT, CH)                                                                  \
     hipLaunchKernelGGL((rmsnorm_rows_reg_kernel<D, O, GT, CH>), grid, block, 0, st, y, z, gamma, \
