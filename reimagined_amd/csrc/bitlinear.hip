@@ -461,9 +461,11 @@ __global__ __launch_bounds__(256) void quantize_rows_multi_kernel(
     const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
     if (row0 >= M) return;
     uint4 raw[RPW][CH][NW];
+    float invs[RPW];  // fetched with the rows: no load waits between one row's codes and the next
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         const int row = min(row0 + r, M - 1);  // rows past M re-read row M - 1 and are not stored
+        invs[r] = RMS ? rms_inv[row] : 1.0f;
         const char* src = static_cast<const char*>(x) + ((int64_t)row * K + lane * 8) * ES;
 #pragma unroll
         for (int c = 0; c < CH; ++c)
@@ -489,7 +491,7 @@ __global__ __launch_bounds__(256) void quantize_rows_multi_kernel(
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
         const int row = row0 + r;
-        const float inv = RMS ? rms_inv[min(row, M - 1)] : 1.0f;
+        const float inv = invs[r];
         float m = 0.0f;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
