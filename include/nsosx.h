@@ -102,6 +102,11 @@ int nsosx_unpack_ternary(const uint32_t* packed, int64_t n, int8_t* codes);
 int nsosx_find_reserved_code(const uint32_t* packed, int64_t n_codes, int64_t* first_bad,
                              void* stream);
 
+/* compute_weight_row_sums (src/bitlinear.cpp:36-73), on the device over the
+ * packed words: sums[n] = sum_k w[n, k] (int32) with w decoded by the table
+ * above.  packed: device [N * K / 16]; sums: device int32 [N]; K % 16 == 0. */
+int nsosx_weight_row_sums(const uint32_t* packed, int N, int K, int32_t* sums, void* stream);
+
 /* ---------------------------------------------------------------------------
  * BitLinear activations and ternary GEMM.
  * ------------------------------------------------------------------------- */
@@ -122,7 +127,7 @@ int nsosx_quantize_act_i8(const void* x, int x_dtype, int M, int K, int bits, in
  * (src/bitnet_adapter.cpp:520-568, src/bitnet_adapter_avx2.cpp:52-158):
  *   acc[m,n] = sum_k q[m,k] * w[n,k]                       (exact int32)
  *   y[m,n]   = float(acc) * (act_scale[m] * weight_scale)
- *              then * magnitude[n] and + bias[n] (one fma when both are given)
+ *              then * magnitude[n], then + bias[n] (each rounded, no fma)
  * Replaces launch_bitnet_gemm / launch_bitnet_gemv_scaled /
  * launch_bitnet_apply_act_scales_kernel (include/cuda/kernels.cuh:106-110).
  * M = 1 runs the packed-weight streaming GEMV; 2 <= M <= 32 with K in
@@ -254,7 +259,8 @@ int nsosx_selective_scan_step(const void* x, const void* dt, const float* A_log,
  *   workspace: int32, nsosx_moe_route_workspace(rows, E) elements.
  * counts, offsets, perm, slot_of and workspace all NULL: selection only
  * (weights and selected, one launch), what the sparse decode consumes.
- * E <= 64, k <= E. */
+ * E <= 64, k <= min(E, 8) (the reference allows any k <= E; routing wider than
+ * top-8 is not supported here). */
 int64_t nsosx_moe_route_workspace(int rows, int experts);
 int nsosx_moe_route(const float* logits, int rows, int experts, int k, float* weights,
                     int32_t* selected, int32_t* counts, int32_t* offsets, int32_t* perm,

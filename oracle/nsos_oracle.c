@@ -10,14 +10,18 @@
  * with -ffp-contract=off and spells every fusion the reference's code
  * generation performs as an explicit fmaf(), so the oracle's bits do not
  * depend on this file's compiler flags:
- *   - output affine  value*magnitude + bias        -> fmaf (bitnet_adapter_avx2.cpp:150-156)
+ *   - output affine  value*magnitude, then + bias  -> two roundings: the multiply
+ *                    and the add sit in separate branches of apply_output_affine
+ *                    (bitnet_adapter_avx2.cpp:36-47), which gcc does not contract
  *   - scan update    decay*state + (delta*B)*x      -> fmaf (mamba2.cpp:2654-2662)
  *   - scan readout   out += state*C                 -> fmaf (mamba2.cpp:2662)
  *   - causal conv    acc += w*in                    -> fmaf (mamba2.cpp:1068-1071)
  *   - RMSNorm        sum_sq += v*v: the -O3 body reduces rounded squares in
  *                    order, the <4-element remainder is fused (tensor.cpp:3480-3484)
- * Those fusion choices were read from gcc 11.4's assembly of restated
- * snippets of those loops; they are a property of that compiler.
+ * Those fusion choices are a property of gcc 11.4 with the reference's flags.
+ * The output affine, the RMSNorm sum and the BitLinear forward are pinned
+ * bit for bit against the reference's own build of those files (oracle/_ref,
+ * fixtures in tests/golden/); the scan's are pinned by float64 closed forms.
  */
 #include "nsos_oracle.h"
 
@@ -171,7 +175,7 @@ void orc_gemm_i8(const int8_t* q, const int8_t* w, int M, int K, int N, int32_t*
 }
 
 /* Dequantizing epilogue: y = float(acc) * (act_scale*ws), then *magnitude,
- * then +bias (fused as one fma when both are present).
+ * then +bias, each rounded (the reference build does not fuse them).
  * OXN/nsos/src/bitnet_adapter_avx2.cpp:93,150-156 and apply_output_affine :37-48 */
 void orc_dequant(const int32_t* acc, const float* act_scale, float weight_scale,
                  const float* magnitude, const float* bias, int M, int N, float* y) {
@@ -179,9 +183,8 @@ void orc_dequant(const int32_t* acc, const float* act_scale, float weight_scale,
         const float combined = act_scale[m] * weight_scale;
         for (int n = 0; n < N; ++n) {
             float v = (float)acc[(int64_t)m * N + n] * combined;
-            if (magnitude && bias) v = fmaf(v, magnitude[n], bias[n]);
-            else if (magnitude) v = v * magnitude[n];
-            else if (bias) v = v + bias[n];
+            if (magnitude) v = v * magnitude[n];
+            if (bias) v = v + bias[n];
             y[(int64_t)m * N + n] = v;
         }
     }
@@ -474,13 +477,16 @@ void orc_topk_mask(float* weights, int rows, int experts, int k, int32_t* select
             rank[i] = rank[best];
             rank[best] = t;
         }
-        float sum = 0.0f;
-        for (int i = 0; i < k; ++i) sum = sum + w[rank[i]];
-        const float inv = 1.0f / (sum > 1e-9f ? sum : 1e-9f);
-        for (int e = 0; e < experts; ++e) {
-            int keep = 0;
-            for (int i = 0; i < k; ++i) keep |= rank[i] == e;
-            w[e] = keep ? w[e] * inv : 0.0f;
+        /* the mask and renormalisation run only when k < experts (jamba.cpp:8268) */
+        if (k < experts) {
+            float sum = 0.0f;
+            for (int i = 0; i < k; ++i) sum = sum + w[rank[i]];
+            const float inv = 1.0f / (sum > 1e-9f ? sum : 1e-9f);
+            for (int e = 0; e < experts; ++e) {
+                int keep = 0;
+                for (int i = 0; i < k; ++i) keep |= rank[i] == e;
+                w[e] = keep ? w[e] * inv : 0.0f;
+            }
         }
         if (selected)
             for (int i = 0; i < k; ++i) selected[(int64_t)r * k + i] = rank[i];
@@ -580,4 +586,142 @@ void orc_qat_ste_clip(float* dW, const float* w, int64_t n, float scale) {
     const float inv = 1.0f / (scale + 1e-8f);
     for (int64_t i = 0; i < n; ++i)
         if (fabsf(w[i] * inv) > 1.0f) dW[i] = 0.0f;
+}
+
+/* ========================================================================
+ * BitLinear float (quantization-sensitive) path and the packed STE backward
+ * ====================================================================== */
+
+/* Tensor::rmsnorm_backward (OXN/nsos/src/tensor.cpp:3997-4056) per row:
+ *   sum_sq += x*x; dot += g*y  in index order: gcc -O3 -mavx -mfma forms the
+ *   products of the first K - K%4 elements as rounded vector products (summed
+ *   in order) and fuses the last K%4 into fma, as in Tensor::rmsnorm;
+ *   dot /= K; inv_rms = 1/sqrt(sum_sq/K + eps); dx = (g - y*dot) * inv_rms with
+ *   g - y*dot fused.  Pinned bit for bit against the reference build's output
+ *   (tests/golden/tensor_ref.npz and oracle/_ref). */
+void orc_rmsnorm_backward(const float* x, const float* g, const float* y, int rows, int cols,
+                          float eps, float* dx) {
+#pragma omp parallel for
+    for (int r = 0; r < rows; ++r) {
+        const int64_t base = (int64_t)r * cols;
+        float sum_sq = 0.0f, dot = 0.0f;
+        const int body = cols & ~3;
+        for (int j = 0; j < body; ++j) {
+            const float sq = x[base + j] * x[base + j];
+            const float gy = g[base + j] * y[base + j];
+            sum_sq = sum_sq + sq;
+            dot = dot + gy;
+        }
+        for (int j = body; j < cols; ++j) {
+            sum_sq = fmaf(x[base + j], x[base + j], sum_sq);
+            dot = fmaf(g[base + j], y[base + j], dot);
+        }
+        const float k = (float)(cols > 1 ? cols : 1);
+        dot = dot / k;
+        const float inv_rms = 1.0f / sqrtf(sum_sq / k + eps);
+        for (int j = 0; j < cols; ++j)
+            dx[base + j] = fmaf(-y[base + j], dot, g[base + j]) * inv_rms;
+    }
+}
+
+/* The float reference path BitLinear keeps for quantization-sensitive layers
+ * (OXN/nsos/src/bitlinear.cpp:465-518): optional RMS_PERI input norm, then
+ * x @ W^T, then *magnitude and +bias, each rounded.  The float matmul's
+ * summation order belongs to the reference's matmul_nt; this restatement
+ * accumulates in double (a tolerance oracle, checked against the reference
+ * build's outputs in tests/golden/bitlinear_ref.npz). */
+void orc_linear_f32(const float* x, int M, int K, int N, const float* w, int rms_input,
+                    const float* magnitude, const float* bias, float* y) {
+    float* xn = NULL;
+    const float* src = x;
+    if (rms_input) {
+        xn = (float*)malloc(sizeof(float) * (size_t)M * (size_t)K);
+        orc_rmsnorm(x, M, K, 1e-6f, xn);
+        src = xn;
+    }
+#pragma omp parallel for
+    for (int m = 0; m < M; ++m) {
+        for (int n = 0; n < N; ++n) {
+            double acc = 0.0;
+            for (int k = 0; k < K; ++k)
+                acc += (double)src[(int64_t)m * K + k] * (double)w[(int64_t)n * K + k];
+            float v = (float)acc;
+            if (magnitude) v = v * magnitude[n];
+            if (bias) v = v + bias[n];
+            y[(int64_t)m * N + n] = v;
+        }
+    }
+    free(xn);
+}
+
+/* BitLinear::backward on the packed path: the straight-through estimator of
+ * OXN/nsos/src/bitlinear.cpp:1191-1357, given what the forward saved.
+ *   x         the layer input [M, K] (pre-norm)
+ *   q, as     the int8 codes and act_scale the forward multiplied
+ *   w         latent fp32 weights [N, K] (for the clip); codes their ternary
+ *   grad      dL/dy [M, N]
+ *   pre[i,j]  = float(acc) * (as[i] * ws)                (gemm without affine)
+ *   dmag[j]   = sum_i grad[i,j] * pre[i,j]               (magnitude != NULL)
+ *   dbias[j]  = sum_i grad[i,j]                          (dbias != NULL)
+ *   gp        = grad * magnitude (or grad in exact-linear mode)
+ *   dW[j,k]   = sum_i gp[i,j] * (q[i,k] * as[i]); 0 where |w / (ws + 1e-8f)| > 1
+ *   d_act     = gp @ (codes * ws)
+ *   dx        = rms_input ? rmsnorm_backward(x, d_act, rmsnorm(x)) : d_act
+ * Sums accumulate in double: a tolerance oracle pinned by the reference build's
+ * outputs (tests/golden/bitlinear_ref.npz). */
+void orc_bitlinear_ste_backward(const float* x, const int8_t* q, const float* as,
+                                const float* w, const int8_t* codes, float ws, int M, int K,
+                                int N, int rms_input, const float* magnitude, const float* grad,
+                                float* dx, float* dW, float* dmag, float* dbias) {
+    float* gp = (float*)malloc(sizeof(float) * (size_t)M * (size_t)N);
+    float* dact = (float*)malloc(sizeof(float) * (size_t)M * (size_t)K);
+    for (int j = 0; j < N; ++j) {
+        double sm = 0.0, sb = 0.0;
+        for (int i = 0; i < M; ++i) {
+            const float g = grad[(int64_t)i * N + j];
+            if (magnitude) {
+                int64_t acc = 0;
+                for (int k = 0; k < K; ++k)
+                    acc += (int64_t)q[(int64_t)i * K + k] * codes[(int64_t)j * K + k];
+                const float pre = (float)acc * (as[i] * ws);
+                sm += (double)(g * pre);
+                gp[(int64_t)i * N + j] = g * magnitude[j];
+            } else {
+                gp[(int64_t)i * N + j] = g;
+            }
+            sb += (double)g;
+        }
+        if (dmag) dmag[j] = (float)sm;
+        if (dbias) dbias[j] = (float)sb;
+    }
+    const float clip = ws + 1e-8f;
+#pragma omp parallel for
+    for (int j = 0; j < N; ++j) {
+        for (int k = 0; k < K; ++k) {
+            double acc = 0.0;
+            for (int i = 0; i < M; ++i)
+                acc += (double)gp[(int64_t)i * N + j] * (double)((float)q[(int64_t)i * K + k] * as[i]);
+            const float wv = w[(int64_t)j * K + k];
+            dW[(int64_t)j * K + k] = fabsf(wv / clip) > 1.0f ? 0.0f : (float)acc;
+        }
+    }
+#pragma omp parallel for
+    for (int i = 0; i < M; ++i) {
+        for (int k = 0; k < K; ++k) {
+            double acc = 0.0;
+            for (int j = 0; j < N; ++j)
+                acc += (double)gp[(int64_t)i * N + j] * (double)((float)codes[(int64_t)j * K + k] * ws);
+            dact[(int64_t)i * K + k] = (float)acc;
+        }
+    }
+    if (rms_input) {
+        float* xn = (float*)malloc(sizeof(float) * (size_t)M * (size_t)K);
+        orc_rmsnorm(x, M, K, 1e-6f, xn);
+        orc_rmsnorm_backward(x, dact, xn, M, K, 1e-6f, dx);
+        free(xn);
+    } else {
+        memcpy(dx, dact, sizeof(float) * (size_t)M * (size_t)K);
+    }
+    free(dact);
+    free(gp);
 }

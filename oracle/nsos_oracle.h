@@ -71,6 +71,16 @@ void orc_scan_step(const float* x, const float* dt, const float* a_log, int a_pe
                    int rows, int H, int P, int N, int G, float* state, float* y,
                    int gate_silu);
 
+/* ---- BitLinear float path and packed STE backward ------------------------- */
+void orc_rmsnorm_backward(const float* x, const float* g, const float* y, int rows, int cols,
+                          float eps, float* dx);
+void orc_linear_f32(const float* x, int M, int K, int N, const float* w, int rms_input,
+                    const float* magnitude, const float* bias, float* y);
+void orc_bitlinear_ste_backward(const float* x, const int8_t* q, const float* as,
+                                const float* w, const int8_t* codes, float ws, int M, int K,
+                                int N, int rms_input, const float* magnitude, const float* grad,
+                                float* dx, float* dW, float* dmag, float* dbias);
+
 /* ---- MoE routing / dispatch ---------------------------------------------- */
 void orc_softmax_rows(const float* logits, int rows, int cols, float* probs);
 void orc_topk_mask(float* weights, int rows, int experts, int k, int32_t* selected);

@@ -70,6 +70,10 @@ def _load() -> ctypes.CDLL:
         "orc_qat_fake_quant_ternary_absmean": (_f, [_f32p, _i64, _f32p]),
         "orc_qat_fake_quant_activations": (None, [_f32p, _i, _i, _i, _f32p]),
         "orc_qat_ste_clip": (None, [_f32p, _f32p, _i64, _f]),
+        "orc_rmsnorm_backward": (None, [_f32p, _f32p, _f32p, _i, _i, _f, _f32p]),
+        "orc_linear_f32": (None, [_f32p, _i, _i, _i, _f32p, _i, _vp, _vp, _f32p]),
+        "orc_bitlinear_ste_backward": (None, [_f32p, _i8p, _f32p, _f32p, _i8p, _f, _i, _i, _i,
+                                              _i, _vp, _f32p, _f32p, _f32p, _vp, _vp]),
         "orc_softmax_rows": (None, [_f32p, _i, _i, _f32p]),
         "orc_topk_mask": (None, [_f32p, _i, _i, _i, _vp]),
         "orc_moe_dispatch": (None, [_f32p, _i, _i, _i, _i32p, _i32p, _i32p]),
@@ -361,6 +365,55 @@ def moe_combine(expert_out, perm, offsets, weights) -> np.ndarray:
     rows, e = w.shape
     out = np.empty((rows, expert_out.shape[1]), np.float32)
     _lib.orc_moe_combine(expert_out, perm, offsets, w, rows, e, expert_out.shape[1], out)
+    return out
+
+
+# ---- float (quantization-sensitive) path and the packed STE backward -----------
+
+def rmsnorm_backward(x, grad, x_norm, eps: float = 1e-6) -> np.ndarray:
+    """Tensor::rmsnorm_backward (src/tensor.cpp:3997-4056)."""
+    x, grad, x_norm = _f32(x), _f32(grad), _f32(x_norm)
+    out = np.empty_like(x)
+    _lib.orc_rmsnorm_backward(x, grad, x_norm, x.shape[0], x.shape[1], eps, out)
+    return out
+
+
+def linear_f32(x, w, rms_input: bool = False, magnitude=None, bias=None) -> np.ndarray:
+    """BitLinear's float reference path (src/bitlinear.cpp:465-518): [rmsnorm] x @ W^T
+    (double accumulation), then *magnitude, +bias."""
+    x, w = _f32(x), _f32(w)
+    m, k = x.shape
+    n = w.shape[0]
+    mag = None if magnitude is None else _f32(magnitude)
+    b = None if bias is None else _f32(bias)
+    y = np.empty((m, n), np.float32)
+    _lib.orc_linear_f32(x, m, k, n, w, int(rms_input), _ptr(mag), _ptr(b), y)
+    return y
+
+
+def bitlinear_ste_backward(x, w, grad, rms_input: bool = True, magnitude=None,
+                           use_bias: bool = False, bits: int = 8) -> dict:
+    """BitLinear forward (packed path) then its STE backward (src/bitlinear.cpp:1191-1357).
+
+    Returns dx, dW, dmag (with magnitude), dbias (use_bias), plus the forward's q / as /
+    codes / weight_scale."""
+    x, w, grad = _f32(x), _f32(w), _f32(grad)
+    m, k = x.shape
+    n = w.shape[0]
+    packed, ws, codes = pack_weights(w)
+    src = rmsnorm(x) if rms_input else x
+    q, s = quantize_act(src, bits)
+    mag = None if magnitude is None else _f32(magnitude)
+    out = {"dx": np.empty((m, k), np.float32), "dW": np.empty((n, k), np.float32),
+           "q": q, "act_scale": s, "codes": codes, "weight_scale": ws, "packed": packed}
+    dmag = np.empty(n, np.float32) if mag is not None else None
+    dbias = np.empty(n, np.float32) if use_bias else None
+    _lib.orc_bitlinear_ste_backward(x, q, s, w, codes, ws, m, k, n, int(rms_input), _ptr(mag),
+                                    grad, out["dx"], out["dW"], _ptr(dmag), _ptr(dbias))
+    if dmag is not None:
+        out["dmag"] = dmag
+    if dbias is not None:
+        out["dbias"] = dbias
     return out
 
 

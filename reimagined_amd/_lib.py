@@ -24,6 +24,7 @@ SIGNATURES = {
     "nsosx_pack_ternary": (_i, [_vp, _i, _i, _vp, _vp]),
     "nsosx_unpack_ternary": (_i, [_vp, _i64, _vp]),
     "nsosx_find_reserved_code": (_i, [_vp, _i64, _vp, _vp]),
+    "nsosx_weight_row_sums": (_i, [_vp, _i, _i, _vp, _vp]),
     "nsosx_quantize_act_i8": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "nsosx_ternary_gemm": (_i, [_vp, _vp, _vp, _f, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp]),
     "nsosx_ternary_gemm_path": (_i, [_vp, _vp, _vp, _f, _i, _i, _i, _vp, _vp, _vp, _i, _vp,

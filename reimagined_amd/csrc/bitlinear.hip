@@ -1539,9 +1539,8 @@ __device__ __forceinline__ void gemm3_epilogue_rows(const GemmProblem& pb,
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     float v = __fmul_rn(static_cast<float>(a[4 * q4 + r]), comb[mb]);
-                    if (has_mag && has_bias) v = __fmaf_rn(v, mv[r], bv[r]);
-                    else if (has_mag) v = __fmul_rn(v, mv[r]);
-                    else if (has_bias) v = __fadd_rn(v, bv[r]);
+                    if (has_mag) v = __fmul_rn(v, mv[r]);
+                    if (has_bias) v = __fadd_rn(v, bv[r]);
                     if (SQRELU) {
                         v = v > 0.0f ? v : 0.0f;
                         v = __fmul_rn(v, v);

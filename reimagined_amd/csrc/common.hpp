@@ -180,13 +180,14 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
 }
 
-// ---- dequantizing epilogue (bitnet_adapter_avx2.cpp:93,150-156) ----------
+// ---- dequantizing epilogue (bitnet_adapter_avx2.cpp:36-47,93,150-156) -----
+// The reference's apply_output_affine multiplies and adds in separate branches,
+// so its build rounds twice (no fma) even under -mfma; so does this.
 __device__ __forceinline__ float dequant(int acc, float combined, const float* mag,
                                          const float* bias, int n) {
     float v = __fmul_rn(static_cast<float>(acc), combined);
-    if (mag && bias) return __fmaf_rn(v, mag[n], bias[n]);
-    if (mag) return __fmul_rn(v, mag[n]);
-    if (bias) return __fadd_rn(v, bias[n]);
+    if (mag) v = __fmul_rn(v, mag[n]);
+    if (bias) v = __fadd_rn(v, bias[n]);
     return v;
 }
 

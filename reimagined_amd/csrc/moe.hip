@@ -64,11 +64,14 @@ __global__ __launch_bounds__(256) void route_rows_kernel(const float* __restrict
         selected[(int64_t)r * k + i] = best;
         ssum = ssum + bv;
     }
+    // k == E keeps the raw softmax: the reference masks and renormalises only when
+    // top_k < num_experts (src/jamba.cpp:8268)
     const float inv2 = 1.0f / (ssum > 1e-9f ? ssum : 1e-9f);
+    const bool renorm = k < E;
     float* w = weights + (int64_t)r * E;
 #pragma unroll
     for (int j = 0; j < EMAX; ++j)
-        if (j < E) w[j] = ((taken >> j) & 1ull) ? p[j] * inv2 : 0.0f;
+        if (j < E) w[j] = ((taken >> j) & 1ull) ? (renorm ? p[j] * inv2 : p[j]) : 0.0f;
 }
 
 // Per dispatch block of 256 rows: how many of its rows selected each expert.

@@ -81,6 +81,16 @@ def find_reserved_code(packed: torch.Tensor, n_codes: int) -> int:
     return int(out.item())
 
 
+def weight_row_sums(packed: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """compute_weight_row_sums (src/bitlinear.cpp:36-73) on the device -> int32 [N]."""
+    _dev(packed, "packed")
+    if k <= 0 or k % 16 or packed.numel() != n * k // 16:
+        raise ValueError("weight_row_sums: packed must hold N*K/16 words with K % 16 == 0")
+    out = torch.empty(n, dtype=torch.int32, device=packed.device)
+    call("nsosx_weight_row_sums", _p(packed), n, k, _p(out), _stream())
+    return out
+
+
 # ---- BitLinear ------------------------------------------------------------------
 
 def quantize_activations_bitnet(x: torch.Tensor, bits: int = 8, rms_input: bool = False):
@@ -189,6 +199,35 @@ def grouped_gemv(views: LinearViewArray, q: torch.Tensor, act_scale: torch.Tenso
 
 # ---- Mamba ----------------------------------------------------------------------
 
+def _shape(t, want: tuple, name: str, fn: str) -> None:
+    if t is not None and tuple(t.shape) != tuple(want):
+        raise ValueError(f"{fn}: {name} must have shape {tuple(want)}, got {tuple(t.shape)}")
+
+
+def _check_scan_shapes(fn, x, dt, a_log, B, C, D, z, H, P, N, G, t_rows=None):
+    """Host-side shape checks of the scan inputs: the C ABI takes raw pointers, so an
+    undersized buffer would be read or written out of bounds on the device."""
+    if min(H, P, N, G) <= 0 or H % G:
+        raise ValueError(f"{fn}: need positive H, P, N, G with G dividing H")
+    if x.dim() != 2 or x.shape[1] != H * P:
+        raise ValueError(f"{fn}: x must be [T, H*P] = [T, {H * P}], got {tuple(x.shape)}")
+    t = x.shape[0] if t_rows is None else t_rows
+    _shape(dt, (t, H), "dt", fn)
+    _shape(B, (t, G * N), "B", fn)
+    _shape(C, (t, G * N), "C", fn)
+    _shape(z, (t, H * P), "z", fn)
+    if D.numel() != H:
+        raise ValueError(f"{fn}: D must hold H = {H} values, got {D.numel()}")
+    if a_log.numel() not in (H, H * N):
+        raise ValueError(f"{fn}: a_log must hold H or H*N values, got {a_log.numel()}")
+
+
+def _check_cu_seqlens(fn, cu_seqlens):
+    """Offsets outside [0, T] are clamped by the kernels; the count must be S+1 >= 2."""
+    if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
+        raise ValueError(f"{fn}: cu_seqlens must be a 1-D int32 tensor of S+1 >= 2 offsets")
+
+
 def conv1d_causal(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tensor, bias=None,
                   silu: bool = True, out_dtype=None) -> torch.Tensor:
     """Depthwise causal conv + bias + SiLU per sequence (src/mamba2.cpp:1056-1076, 2437-2446).
@@ -212,8 +251,13 @@ def conv1d_causal(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tenso
 def selective_scan_fwd(x, dt, a_log, B, C, D, z, cu_seqlens, H, P, N, G, initial_state=None,
                        want_final: bool = True):
     """Packed ragged faithful scan (src/mamba2.cpp:2602-2675) -> (y [T, H*P], final [S, H*P, N])."""
+    _check_scan_shapes("selective_scan_fwd", x, dt, a_log, B, C, D, z, H, P, N, G)
+    _check_cu_seqlens("selective_scan_fwd", cu_seqlens)
     t = x.shape[0]
     s = cu_seqlens.numel() - 1
+    _shape(initial_state, (s, H * P, N), "initial_state", "selective_scan_fwd")
+    if not x.is_cuda:
+        raise ValueError("x must be a device tensor")
     if x.stride(1) != 1 or (z is not None and z.stride(1) != 1):
         raise ValueError("selective_scan_fwd: x and z need unit stride in the channel dim")
     for name, v in (("dt", dt), ("B", B), ("C", C)):
@@ -236,8 +280,18 @@ def selective_scan_fwd(x, dt, a_log, B, C, D, z, cu_seqlens, H, P, N, G, initial
 def conv_scan_fwd(x_raw, conv_w, conv_b, dt, a_log, B, C, D, z, cu_seqlens, H, P, N, G,
                   initial_state=None, want_final: bool = True):
     """Causal conv + bias + SiLU fused into the scan's staging -> (y, final state)."""
+    _check_scan_shapes("conv_scan_fwd", x_raw, dt, a_log, B, C, D, z, H, P, N, G)
+    _check_cu_seqlens("conv_scan_fwd", cu_seqlens)
     t = x_raw.shape[0]
     s = cu_seqlens.numel() - 1
+    _shape(initial_state, (s, H * P, N), "initial_state", "conv_scan_fwd")
+    if conv_w.dim() != 2 or conv_w.shape[0] != H * P or not 1 <= conv_w.shape[1] <= 8:
+        raise ValueError(f"conv_scan_fwd: conv_w must be [H*P, W] = [{H * P}, 1..8], "
+                         f"got {tuple(conv_w.shape)}")
+    if conv_b is not None and conv_b.numel() != H * P:
+        raise ValueError(f"conv_scan_fwd: conv_b must hold H*P = {H * P} values")
+    if not x_raw.is_cuda:
+        raise ValueError("x_raw must be a device tensor")
     if x_raw.stride(1) != 1 or (z is not None and z.stride(1) != 1):
         raise ValueError("conv_scan_fwd: x and z need unit stride in the channel dim")
     for name, v in (("dt", dt), ("B", B), ("C", C)):
@@ -261,9 +315,13 @@ def conv_scan_fwd(x_raw, conv_w, conv_b, dt, a_log, B, C, D, z, cu_seqlens, H, P
 
 def selective_scan_step(x, dt, a_log, B, C, D, z, state, H, P, N, G):
     """Decode step in place on `state` [R, H*P, N] (src/mamba2.cpp:4038-4125) -> y [R, H*P]."""
+    _check_scan_shapes("selective_scan_step", x, dt, a_log, B, C, D, z, H, P, N, G)
     r = x.shape[0]
+    _shape(state, (r, H * P, N), "state", "selective_scan_step")
     for name, v in (("x", x), ("dt", dt), ("B", B), ("C", C)):
         _dev(v, name, x.dtype)
+    if z is not None:
+        _dev(z, "z", x.dtype)
     _dev(a_log, "a_log", torch.float32)
     _dev(D, "D", torch.float32)
     _dev(state, "state", torch.float32)

@@ -1,10 +1,20 @@
-"""Writes the golden activation-quantization vectors from the reference's own code.
+"""Writes golden vectors from the reference's own compiled code.
 
 Runs only in a container where the reference tree is mounted: it builds
-oracle/_ref/libnsos_ref.so from OXN/nsos/src/bitlinear_quantize_avx2.cpp
-(oracle/Makefile target `ref`) and records that library's outputs for seeded
-and constructed inputs.  The fixtures are data (inputs and expected outputs);
-the GPU box and CPU tests read them without the reference.
+oracle/_ref/libnsos_ref.so from the reference's sources (oracle/Makefile
+target `ref`: the AVX2 quantizer, Tensor, BitLinear and the files their link
+needs) and records that library's outputs for seeded and constructed inputs:
+
+  quant_ref.npz      the AVX2 activation quantizer and weight row sums
+  tensor_ref.npz     Tensor::rmsnorm / softmax / silu / silu_gate /
+                     squared_relu / rmsnorm_backward, tensor_abs_mean, and the
+                     RMS_PERI int8 codes of BitLinear::forward's quantizer
+  bitlinear_ref.npz  BitLinear::forward (packed ternary and float paths) and
+                     the packed STE backward
+
+Inputs are stored as float16-representable values (cast to float32 before
+use) so the fixtures stay small.  The fixtures are data (inputs and expected
+outputs); the GPU box and CPU tests read them without the reference.
 
     python tests/golden/gen_golden.py
 """
@@ -21,6 +31,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 
 from oracle import oracle  # noqa: E402
+from oracle import ref  # noqa: E402
 
 
 def tie_rows() -> np.ndarray:
@@ -60,12 +71,99 @@ def main() -> None:
     w = rng.integers(-1, 2, size=(6, 1000)).astype(np.int8)
     out["rowsum__w"] = w
     out["rowsum__sums"] = np.array([oracle.ref_row_sum_i8(r) for r in w], np.int32)
-    path = os.path.join(HERE, "quant_ref.npz")
-    np.savez_compressed(path, **out)
-    digest = hashlib.sha256(open(path, "rb").read()).hexdigest()
+    files = {"quant_ref.npz": out, "tensor_ref.npz": tensor_cases(),
+             "bitlinear_ref.npz": bitlinear_cases()}
+    lines = []
+    for name, data in files.items():
+        path = os.path.join(HERE, name)
+        np.savez_compressed(path, **data)
+        digest = hashlib.sha256(open(path, "rb").read()).hexdigest()
+        lines.append(f"{digest}  {name}\n")
+        print(f"wrote {path} sha256={digest}")
     with open(os.path.join(HERE, "MANIFEST.sha256"), "w") as fh:
-        fh.write(f"{digest}  quant_ref.npz\n")
-    print(f"wrote {path} sha256={digest}")
+        fh.writelines(lines)
+
+
+def _h(rng, shape, scale=1.0, loc=0.0) -> np.ndarray:
+    """Seeded normal values rounded to float16 (stored compactly, exact in float32)."""
+    return (rng.standard_normal(shape) * scale + loc).astype(np.float16)
+
+
+def tensor_cases() -> dict:
+    rng = np.random.default_rng(20261202)
+    out = {}
+    # Tensor::rmsnorm rows at the configs' widths and at odd widths (AVX body + tail)
+    for k in (768, 1024, 2048, 4096, 1003, 17, 7, 3):
+        x = _h(rng, (2, k), scale=float(rng.uniform(0.2, 8.0)))
+        out[f"rms_k{k}__x"] = x
+        xf = x.astype(np.float32)
+        out[f"rms_k{k}__y"] = ref.rmsnorm(xf, 1e-6)
+        # RMS_PERI then the AVX2 quantizer: the int8 codes BitLinear::forward multiplies
+        codes, scales = oracle.ref_quantize_rows(out[f"rms_k{k}__y"], 8)
+        out[f"rms_k{k}__codes"] = np.clip(codes, -127, 127).astype(np.int8)
+        out[f"rms_k{k}__scales"] = scales
+    # Tensor::softmax rows of config-5-shaped router logits (N(0,1), 8 experts)
+    lg = _h(rng, (1024, 8))
+    out["softmax__x"] = lg
+    out["softmax__y"] = ref.softmax(lg.astype(np.float32))
+    lg64 = _h(rng, (64, 64), scale=3.0)
+    out["softmax64__x"] = lg64
+    out["softmax64__y"] = ref.softmax(lg64.astype(np.float32))
+    # elementwise activations over a wide range, both signs
+    v = _h(rng, (4096,), scale=6.0)
+    g = _h(rng, (4096,), scale=6.0)
+    out["act__x"] = v
+    out["act__g"] = g
+    out["act__silu"] = ref.silu(v.astype(np.float32))
+    out["act__silu_gate"] = ref.silu_gate(v.astype(np.float32), g.astype(np.float32))
+    out["act__squared_relu"] = ref.squared_relu(v.astype(np.float32))
+    # tensor_abs_mean (double sum): sizes on either side of the AVX widths
+    for n in (1, 7, 1000, 4099):
+        w = _h(rng, (n,), scale=0.05)
+        out[f"absmean_n{n}__w"] = w
+        out[f"absmean_n{n}__m"] = np.array([ref.abs_mean(w.astype(np.float32))], np.float32)
+    # Tensor::rmsnorm_backward with BitLinear's saved x_norm
+    for k in (1024, 61):
+        x = _h(rng, (4, k), scale=2.0)
+        gr = _h(rng, (4, k))
+        xf = x.astype(np.float32)
+        xn = ref.rmsnorm(xf, 1e-6)
+        out[f"rmsbwd_k{k}__x"] = x
+        out[f"rmsbwd_k{k}__g"] = gr
+        out[f"rmsbwd_k{k}__dx"] = ref.rmsnorm_backward(xf, gr.astype(np.float32), xn, 1e-6)
+    return out
+
+
+def bitlinear_cases() -> dict:
+    rng = np.random.default_rng(20261203)
+    out = {}
+    # (name, M, K, N, exact_linear, magnitude, bias)
+    cases = [("rms_mag_bias", 8, 256, 48, False, True, True),
+             ("rms_mag", 5, 128, 32, False, True, False),
+             ("exact", 6, 192, 40, True, False, False),
+             ("exact_bias", 3, 64, 24, True, False, True)]
+    for name, m, k, n, exact, has_mag, has_bias in cases:
+        w = _h(rng, (n, k), scale=0.05)
+        x = _h(rng, (m, k))
+        gr = _h(rng, (m, n))
+        mag = rng.uniform(0.5, 1.5, n).astype(np.float16) if has_mag else None
+        bias = _h(rng, (n,)) if has_bias else None
+        f = lambda a: None if a is None else a.astype(np.float32)
+        out[f"{name}__w"] = w
+        out[f"{name}__x"] = x
+        out[f"{name}__grad"] = gr
+        if mag is not None:
+            out[f"{name}__mag"] = mag
+        if bias is not None:
+            out[f"{name}__bias"] = bias
+        out[f"{name}__y_packed"] = ref.bitlinear_forward(f(w), f(x), True, exact, f(mag), f(bias))
+        out[f"{name}__y_float"] = ref.bitlinear_forward(f(w), f(x), False, exact, f(mag), f(bias))
+        bwd = ref.bitlinear_packed_backward(f(w), f(x), f(gr), exact, f(mag), f(bias))
+        assert np.array_equal(bwd["y"], out[f"{name}__y_packed"])
+        for key in ("dx", "dW", "dmag", "dbias"):
+            if key in bwd:
+                out[f"{name}__{key}"] = bwd[key]
+    return out
 
 
 if __name__ == "__main__":

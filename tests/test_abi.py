@@ -48,3 +48,25 @@ def test_route_workspace_size():
     lib = reimagined_amd.lib()
     assert lib.nsosx_moe_route_workspace(8192, 8) == 32 * 8
     assert lib.nsosx_moe_route_workspace(0, 8) == 0
+
+
+def _header_param_counts():
+    import re
+    from reimagined_amd._lib import HEADER
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(nsosx_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_ctypes_signatures_match_header_arity():
+    """The host mirror's hand-kept ctypes table has one entry per header function,
+    with the header's parameter count."""
+    from reimagined_amd._lib import SIGNATURES
+    counts = _header_param_counts()
+    assert set(SIGNATURES) == set(counts), set(SIGNATURES) ^ set(counts)
+    bad = {n: (len(SIGNATURES[n][1]), c) for n, c in counts.items() if len(SIGNATURES[n][1]) != c}
+    assert not bad, bad

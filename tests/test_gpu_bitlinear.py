@@ -297,3 +297,30 @@ def test_gemm_epilogue_alignment(dev, orc, shift_y, shift_affine):
     call("nsosx_ternary_gemm_path", _p(qd), _p(sd), _p(pk), ws, m, k, n,
          _p(mg_buf[shift_affine:]), _p(bs_buf[shift_affine:]), _p(y), 1, None, 1, _stream())
     np.testing.assert_array_equal(y.float().cpu().numpy(), y_want)
+
+
+@pytest.mark.parametrize("n,k", [(6, 1000 // 16 * 16), (4096, 1024), (1, 16), (1023, 2048)])
+def test_weight_row_sums_match_oracle(dev, orc, n, k):
+    """compute_weight_row_sums on the device, from the packed words, against the oracle's
+    int8 row sums (pinned by the reference build's golden rowsum__sums)."""
+    rng = np.random.default_rng(n + k)
+    codes = rng.integers(-1, 2, size=(n, k)).astype(np.int8)
+    packed = orc.pack_codes(codes).view(np.uint32)
+    got = ops.weight_row_sums(torch.from_numpy(packed.view(np.int32)).to(dev), n, k)
+    np.testing.assert_array_equal(got.cpu().numpy(), orc.row_sums(codes))
+
+
+def test_weight_row_sums_golden_and_reserved_code(dev, orc):
+    g = np.load(GOLDEN, allow_pickle=False)
+    w = g["rowsum__w"][:, :992]          # K % 16 == 0 prefix of the golden rows
+    want = g["rowsum__w"][:, :992].astype(np.int32).sum(1)
+    packed = orc.pack_codes(w).view(np.uint32)
+    got = ops.weight_row_sums(torch.from_numpy(packed.view(np.int32)).to(dev), 6, 992)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+    np.testing.assert_array_equal(orc.row_sums(w), want)
+    # full golden rows through the oracle, which the reference build pinned
+    np.testing.assert_array_equal(orc.row_sums(g["rowsum__w"]), g["rowsum__sums"])
+    # the reserved code 3 decodes to 0 and adds nothing
+    words = np.array([0xFFFFFFFF, 0x66666666, 0x00000000, 0xAAAAAAAA], np.uint32)
+    got = ops.weight_row_sums(torch.from_numpy(words.view(np.int32)).to(dev), 4, 16)
+    np.testing.assert_array_equal(got.cpu().numpy(), [0, 8, -16, 16])

@@ -1,0 +1,91 @@
+"""Host-side argument checks of the scan wrappers (CPU only).
+
+The C ABI receives raw device pointers, so every tensor's shape has to be
+checked on the host before a call: an undersized state, dt, B, C, D, a_log or
+conv weight would otherwise be read or written out of bounds on the device.
+These run on CPU tensors; a wrapper must reject the bad shape with ValueError
+before it looks at the device, and a well-shaped CPU tensor gets as far as
+the device check."""
+import pytest
+import torch
+
+from reimagined_amd import ops
+
+T, H, P, N, G = 10, 4, 2, 16, 2
+
+
+def _good():
+    f = torch.float32
+    return dict(x=torch.zeros(T, H * P, dtype=f), dt=torch.zeros(T, H, dtype=f),
+                a_log=torch.zeros(H, N, dtype=f), B=torch.zeros(T, G * N, dtype=f),
+                C=torch.zeros(T, G * N, dtype=f), D=torch.zeros(H, dtype=f),
+                z=torch.zeros(T, H * P, dtype=f), cu=torch.tensor([0, 4, T], dtype=torch.int32),
+                conv_w=torch.zeros(H * P, 4, dtype=f), conv_b=torch.zeros(H * P, dtype=f),
+                state=torch.zeros(3, H * P, N, dtype=f), init=torch.zeros(2, H * P, N, dtype=f))
+
+
+def _fwd(a):
+    return ops.selective_scan_fwd(a["x"], a["dt"], a["a_log"], a["B"], a["C"], a["D"], a["z"],
+                                  a["cu"], H, P, N, G, initial_state=a["init"])
+
+
+def _conv_scan(a):
+    return ops.conv_scan_fwd(a["x"], a["conv_w"], a["conv_b"], a["dt"], a["a_log"], a["B"],
+                             a["C"], a["D"], a["z"], a["cu"], H, P, N, G,
+                             initial_state=a["init"])
+
+
+def _step(a):
+    r = a["state"].shape[0]
+    return ops.selective_scan_step(a["x"][:r], a["dt"][:r], a["a_log"], a["B"][:r], a["C"][:r],
+                                   a["D"], a["z"][:r], a["state"], H, P, N, G)
+
+
+BAD = [
+    ("x", torch.zeros(T, H * P + 1)),
+    ("dt", torch.zeros(T - 1, H)),
+    ("dt", torch.zeros(T, H - 1)),
+    ("B", torch.zeros(T, G * N - 1)),
+    ("C", torch.zeros(T - 1, G * N)),
+    ("z", torch.zeros(T, H * P - 2)),
+    ("D", torch.zeros(H - 1)),
+    ("a_log", torch.zeros(H, N - 1)),
+    ("init", torch.zeros(1, H * P, N)),
+    ("init", torch.zeros(2, H * P, N - 1)),
+]
+
+
+@pytest.mark.parametrize("name,bad", BAD)
+@pytest.mark.parametrize("fn", [_fwd, _conv_scan])
+def test_prefill_rejects_bad_shapes(fn, name, bad):
+    a = _good()
+    a[name] = bad
+    with pytest.raises(ValueError, match=name if name != "init" else "initial_state"):
+        fn(a)
+
+
+@pytest.mark.parametrize("name,bad", [("conv_w", torch.zeros(H * P - 1, 4)),
+                                      ("conv_w", torch.zeros(H * P, 9)),
+                                      ("conv_b", torch.zeros(H * P + 1)),
+                                      ("cu", torch.zeros(1, dtype=torch.int32))])
+def test_conv_scan_rejects_bad_conv_and_offsets(name, bad):
+    a = _good()
+    a[name] = bad
+    with pytest.raises(ValueError):
+        _conv_scan(a)
+
+
+@pytest.mark.parametrize("name,bad", [("state", torch.zeros(3, H * P, N - 1)),
+                                      ("state", torch.zeros(3, H * P - 1, N)),
+                                      ("D", torch.zeros(H + 1))])
+def test_step_rejects_bad_shapes(name, bad):
+    a = _good()
+    a[name] = bad
+    with pytest.raises(ValueError, match=name):
+        _step(a)
+
+
+@pytest.mark.parametrize("fn", [_fwd, _conv_scan, _step])
+def test_well_shaped_cpu_tensors_reach_the_device_check(fn):
+    with pytest.raises(ValueError, match="device tensor"):
+        fn(_good())
