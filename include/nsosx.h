@@ -160,6 +160,21 @@ int nsosx_bitlinear_forward(const void* x, int x_dtype, const uint32_t* packed,
                             int y_dtype, int8_t* q_workspace, float* scale_workspace,
                             float* rms_workspace, void* stream);
 
+/* No counterpart in the reference.  nsosx_bitlinear_forward for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc): the int8 codes, act_scale and RMS workspace live in
+ * a library-owned static device array of nsosx_bitlinear_forward_noalloc_max_bytes()
+ * bytes (8 MiB) per GPU, held until the process ends; no allocation happens.
+ * The workspace takes round256(M*K) + 2*round256(4*M) bytes; larger shapes
+ * return NSOSX_ERR_OVERFLOW.  Every call on one GPU shares that array, so
+ * calls that overlap on one GPU (different streams, or different host threads)
+ * race; calls enqueued on one stream are ordered and safe. */
+int64_t nsosx_bitlinear_forward_noalloc_max_bytes(void);
+int nsosx_bitlinear_forward_noalloc(const void* x, int x_dtype, const uint32_t* packed,
+                                    float weight_scale, int M, int K, int N, int precision_bits,
+                                    int rms_input, const float* magnitude, const float* bias,
+                                    void* y, int y_dtype, void* stream);
+
 /* One borrowed descriptor per weight set, the C shape of nsos::GpuLinearView
  * (include/gpu_linear_view.h:8-26) restricted to the packed path. */
 typedef struct nsosx_linear_view {
