@@ -175,6 +175,46 @@ int nsosx_bitlinear_forward_noalloc(const void* x, int x_dtype, const uint32_t* 
                                     int rms_input, const float* magnitude, const float* bias,
                                     void* y, int y_dtype, void* stream);
 
+/* The float reference path BitLinear keeps for quantization-sensitive layers
+ * (src/bitlinear.cpp:465-518): the faithful Mamba-2 block's B / C / dt
+ * projections (src/mamba2.cpp:588-599, 655-662, exact-linear mode: no input
+ * norm, no magnitude; dt with its bias) and the MoE router's gate
+ * (src/jamba.cpp:8086-8098: RMS_PERI and magnitude).
+ *   y = (rms_input ? rmsnorm(x, 1e-6) : x) @ w^T, then * magnitude[n], then + bias[n]
+ * x: [M, K] (x_dtype); w: f32 [N, K]; y: [M, N] (y_dtype); magnitude, bias:
+ * f32 [N] or NULL; rms_workspace: f32 [M] when rms_input.  K % 4 == 0.
+ * The normalised input x * inv equals Tensor::rmsnorm bit for bit; the dot
+ * products accumulate in fp32 (v_mfma_f32_32x32x2_f32, or a wave reduction
+ * for N <= 16 or M <= 16) in an order of their own. */
+int nsosx_linear_f32(const void* x, int x_dtype, int M, int K, const float* w, int N,
+                     int rms_input, const float* magnitude, const float* bias, void* y,
+                     int y_dtype, float* rms_workspace, void* stream);
+
+/* BitLinear::backward on the packed path: the straight-through estimator of
+ * src/bitlinear.cpp:1191-1357, given what the forward saved:
+ *   x          the layer input [M, K] (x_dtype; read only when rms_input)
+ *   q, act_scale  the int8 codes [M, K] and scales [M] the forward multiplied
+ *   w_latent   f32 [N, K] latent weights (for the clip); packed their ternary
+ *   grad       f32 [M, N], dL/dy
+ *   pre        = acc * (act_scale * weight_scale)           (GEMM without affine)
+ *   dmag[n]    = sum_m grad * pre          (magnitude given; dmag may be NULL)
+ *   dbias[n]   = sum_m grad                (NULL: no bias)
+ *   gp         = grad * magnitude (grad in exact-linear mode, magnitude NULL)
+ *   dW[n, k]   = sum_m gp[m, n] * (q[m, k] * act_scale[m]), 0 where
+ *                |w_latent / (weight_scale + 1e-8f)| > 1
+ *   d_act      = gp @ (ternary * weight_scale)
+ *   dx         = rms_input ? rmsnorm_backward(x, d_act, rmsnorm(x)) : d_act
+ * All outputs f32.  K % 16 == 0, N % 4 == 0.  workspace: device,
+ * nsosx_bitlinear_ste_backward_workspace(M, K, N, rms_input) bytes, 256-byte
+ * aligned.  Sums run in fp32 in an order of their own (tolerance parity). */
+int64_t nsosx_bitlinear_ste_backward_workspace(int M, int K, int N, int rms_input);
+int nsosx_bitlinear_ste_backward(const void* x, int x_dtype, const int8_t* q,
+                                 const float* act_scale, const float* w_latent,
+                                 const uint32_t* packed, float weight_scale, int M, int K, int N,
+                                 int rms_input, const float* magnitude, const float* grad,
+                                 float* dx, float* dW, float* dmag, float* dbias,
+                                 void* workspace, void* stream);
+
 /* One borrowed descriptor per weight set, the C shape of nsos::GpuLinearView
  * (include/gpu_linear_view.h:8-26) restricted to the packed path. */
 typedef struct nsosx_linear_view {

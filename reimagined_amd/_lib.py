@@ -34,6 +34,10 @@ SIGNATURES = {
     "nsosx_bitlinear_forward_noalloc_max_bytes": (_i64, []),
     "nsosx_bitlinear_forward_noalloc": (_i, [_vp, _i, _vp, _f, _i, _i, _i, _i, _i, _vp, _vp,
                                              _vp, _i, _vp]),
+    "nsosx_linear_f32": (_i, [_vp, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp, _i, _vp, _vp]),
+    "nsosx_bitlinear_ste_backward_workspace": (_i64, [_i, _i, _i, _i]),
+    "nsosx_bitlinear_ste_backward": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i, _vp,
+                                          _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "nsosx_grouped_gemv": (_i, [_vp, _i, _vp, _i64, _vp, _i64, _i, _vp, _i64, _i, _vp]),
     "nsosx_conv1d_causal": (_i, [_vp, _i, _i64, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i,
                                  _vp]),

@@ -563,6 +563,41 @@ static float q_max_for_bits(int bits) {
     return static_cast<float>((1 << (bits - 1)) - 1);
 }
 
+// inv[m] = 1 / sqrt(sum_k x[m,k]^2 / K + eps) with the reference's in-order sum
+// (Tensor::rmsnorm, src/tensor.cpp:3455-3492): the kernel is picked by shape.
+template <int DT>
+static void launch_rms_inv_t(const void* x, int M, int K, float eps, float* inv, hipStream_t st) {
+    const int elem = DT == NSOSX_F32 ? 4 : 2;
+    if (M <= 1024 && K <= kRmsSmallMaxK) {
+        hipLaunchKernelGGL((rms_inv_small_kernel<DT>), dim3(M), dim3(256), 0, st, x, K, eps, inv);
+    } else if (((int64_t)K * elem) % (kRmsTileBytes * kRmsDepth) == 0 &&
+               reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+        // fewer than 512 groups of 64 rows: the three-wave form (config 5's 16384 hidden rows of
+        // 4096 in 33 us, its 8192 input rows of 1024 in 5 us less); with more groups the one-wave
+        // form streams faster (config 4: 40796 rows of 1024 / 2048, 3 / 6 us less)
+        if ((M + 63) / 64 < 512 && ((int64_t)K * elem) % (kRmsTileBytes * kRmsPcDepth) == 0)
+            hipLaunchKernelGGL((rms_inv_pc_kernel<DT>), dim3((M + 63) / 64), dim3(192), 0, st, x, M,
+                               K, eps, inv);
+        else
+            hipLaunchKernelGGL((rms_inv_tiled_kernel<DT>), dim3((M + 63) / 64), dim3(64), 0, st, x,
+                               M, K, eps, inv);
+    } else {
+        const bool rvec = ((int64_t)K * elem) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
+        if (rvec)
+            hipLaunchKernelGGL((rms_inv_kernel<DT, true>), dim3((M + 63) / 64), dim3(64), 0, st, x,
+                               M, K, eps, inv);
+        else
+            hipLaunchKernelGGL((rms_inv_kernel<DT, false>), dim3((M + 63) / 64), dim3(64), 0, st,
+                               x, M, K, eps, inv);
+    }
+}
+
+void launch_rms_inv(const void* x, int dtype, int M, int K, float eps, float* inv,
+                    hipStream_t st) {
+    if (dtype == NSOSX_F32) launch_rms_inv_t<NSOSX_F32>(x, M, K, eps, inv, st);
+    else launch_rms_inv_t<NSOSX_BF16>(x, M, K, eps, inv, st);
+}
+
 template <int DT>
 static int launch_quantize(const void* x, int M, int K, int bits, int rms_input, int8_t* q,
                            float* act_scale, float* rms_ws, hipStream_t st) {
@@ -574,29 +609,7 @@ static int launch_quantize(const void* x, int M, int K, int bits, int rms_input,
                            1e-6f, rms_ws, q, act_scale);
         return check_launch("quantize_act");
     }
-    if (rms_input && M <= 1024 && K <= kRmsSmallMaxK) {
-        hipLaunchKernelGGL((rms_inv_small_kernel<DT>), dim3(M), dim3(256), 0, st, x, K, 1e-6f,
-                           rms_ws);
-    } else if (rms_input && ((int64_t)K * elem) % (kRmsTileBytes * kRmsDepth) == 0 &&
-               reinterpret_cast<uintptr_t>(x) % 16 == 0) {
-        // fewer than 512 groups of 64 rows: the three-wave form (config 5's 16384 hidden rows of
-        // 4096 in 33 us, its 8192 input rows of 1024 in 5 us less); with more groups the one-wave
-        // form streams faster (config 4: 40796 rows of 1024 / 2048, 3 / 6 us less)
-        if ((M + 63) / 64 < 512 && ((int64_t)K * elem) % (kRmsTileBytes * kRmsPcDepth) == 0)
-            hipLaunchKernelGGL((rms_inv_pc_kernel<DT>), dim3((M + 63) / 64), dim3(192), 0, st, x, M,
-                               K, 1e-6f, rms_ws);
-        else
-            hipLaunchKernelGGL((rms_inv_tiled_kernel<DT>), dim3((M + 63) / 64), dim3(64), 0, st, x,
-                               M, K, 1e-6f, rms_ws);
-    } else if (rms_input) {
-        const bool rvec = ((int64_t)K * elem) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0;
-        if (rvec)
-            hipLaunchKernelGGL((rms_inv_kernel<DT, true>), dim3((M + 63) / 64), dim3(64), 0, st, x,
-                               M, K, 1e-6f, rms_ws);
-        else
-            hipLaunchKernelGGL((rms_inv_kernel<DT, false>), dim3((M + 63) / 64), dim3(64), 0, st,
-                               x, M, K, 1e-6f, rms_ws);
-    }
+    if (rms_input) launch_rms_inv_t<DT>(x, M, K, 1e-6f, rms_ws, st);
     if ((K == 512 || K == 1024 || K == 2048 || K == 4096) && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
         reinterpret_cast<uintptr_t>(q) % 8 == 0) {
 #define NSOSX_QMULTI(CH)                                                                   \

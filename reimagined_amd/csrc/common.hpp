@@ -32,6 +32,11 @@ inline int check_launch(const char* what) {
 
 inline bool valid_dtype(int d) { return d == NSOSX_F32 || d == NSOSX_BF16; }
 
+// inv[m] = 1 / sqrt(mean_k x[m,k]^2 + eps), the row scale of Tensor::rmsnorm with its
+// in-order sum (bitlinear.hip); x [M, K] in `dtype`.
+void launch_rms_inv(const void* x, int dtype, int M, int K, float eps, float* inv,
+                    hipStream_t st);
+
 // ---- bf16 <-> f32 -----------------------------------------------------------
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {

@@ -124,15 +124,15 @@ class HybridMambaLayer:
             b = {
                 "xz": torch.empty((t, 2 * self.d_inner), dtype=dtype, device=device),
                 "ys": torch.empty((t, self.d_inner), dtype=dtype, device=device),
-                "out": torch.empty((t, self.d_model), dtype=dtype, device=device),
             }
             self._buf[t] = b
         return b
 
-    def forward(self, x, dt, B, C, cu_seqlens, final_state=None, marker=None):
+    def forward(self, x, dt, B, C, cu_seqlens, final_state=None, marker=None, out=None):
         """x [T, d_model]; dt [T, d_inner]; B, C [T, d_state]; cu_seqlens int32 [S+1].
 
-        marker(name), when given, is called after each kernel of the layer.
+        Returns `out` [T, d_model] (allocated when None; the in_proj and scan buffers stay
+        internal).  marker(name), when given, is called after each kernel of the layer.
         """
         t = x.shape[0]
         s = cu_seqlens.numel() - 1
@@ -149,8 +149,10 @@ class HybridMambaLayer:
              _p(b["ys"]), _stream())
         if marker:
             marker("conv_scan")
-        self.out_proj.forward_into(b["ys"], b["out"], mk("out_proj"))
-        return b["out"]
+        if out is None:
+            out = torch.empty((t, self.d_model), dtype=x.dtype, device=x.device)
+        self.out_proj.forward_into(b["ys"], out, mk("out_proj"))
+        return out
 
 
 class MoEFFN:
@@ -197,6 +199,9 @@ class MoEFFN:
         return b
 
     def forward(self, x: torch.Tensor, logits: torch.Tensor, out_dtype=None) -> dict:
+        """Returns {"out": a fresh [rows, d_model] tensor, plus the routing tensors and the
+        expert hidden / output rows}.  Those extras are views of this layer's per-row-count
+        workspaces: the next forward with the same row count overwrites them."""
         rows = x.shape[0]
         b = self._buffers(rows, x.device)
         e, k = self.experts, self.k
@@ -252,65 +257,100 @@ class HybridBlock:
         out = r + moe(f)                            (3305-3316)
 
     gammas None are the non-learnable norms.  The router logits are supplied by the
-    caller, or, with `gate_w`, come from a ternary gate BitLinear [experts, d_model]
-    over f (MoERouter's gate projection, src/jamba.cpp:8140-8319).
+    caller, or, with `gate_w` [experts, d_model], come from MoERouter's gate projection
+    over f (src/jamba.cpp:8140-8319).  The reference marks that gate quantization-
+    sensitive unless NSOS_MOE_FP_ROUTER=0 (src/jamba.cpp:8086-8098), so by default it is
+    BitLinear's float path: rmsnorm(f, 1e-6) @ gate_w^T * gate_magnitude (+ gate_bias);
+    ternary_gate=True builds the ternary BitLinear instead (the NSOS_MOE_FP_ROUTER=0
+    behaviour).
     """
 
     def __init__(self, mamba_params: dict, w_up: list, w_down: list, device="cuda", k: int = 2,
                  core_gamma=None, ff_gamma=None, gate_w=None, core_eps: float = 1e-6,
-                 ff_eps: float = 1e-6):
+                 ff_eps: float = 1e-6, gate_magnitude=None, gate_bias=None,
+                 ternary_gate: bool = False):
         self.mamba = HybridMambaLayer(mamba_params, device)
         self.moe = MoEFFN(w_up, w_down, device, k=k)
         f32 = dict(dtype=torch.float32, device=device)
         self.core_gamma = None if core_gamma is None else torch.as_tensor(core_gamma, **f32)
         self.ff_gamma = None if ff_gamma is None else torch.as_tensor(ff_gamma, **f32)
-        self.gate = None if gate_w is None else BitLinear(gate_w, device)
+        self.gate = None
+        self.gate_w = None
+        if gate_w is not None and ternary_gate:
+            self.gate = BitLinear(gate_w, device, magnitude=gate_magnitude, bias=gate_bias)
+        elif gate_w is not None:
+            self.gate_w = torch.as_tensor(np.ascontiguousarray(gate_w, np.float32), **f32)
+            self.gate_mag = (None if gate_magnitude is None
+                             else torch.as_tensor(gate_magnitude, **f32))
+            self.gate_bias = None if gate_bias is None else torch.as_tensor(gate_bias, **f32)
         self.core_eps, self.ff_eps = core_eps, ff_eps
+
+    def router_logits(self, f: torch.Tensor) -> torch.Tensor:
+        """MoERouter's gate over the normed block input f -> f32 logits [rows, experts]."""
+        if self.gate is not None:
+            return self.gate.forward(f, out_dtype=torch.float32)
+        return ops.linear_f32(f, self.gate_w, rms_input=True, magnitude=self.gate_mag,
+                              bias=self.gate_bias)
 
     def forward(self, x, dt, B, C, cu_seqlens, logits=None, final_state=None) -> dict:
         """x [T, d_model] (f32 or bf16); the remaining scan inputs as HybridMambaLayer."""
         ops._dev(cu_seqlens, "cu_seqlens", torch.int32)
-        if logits is None and self.gate is None:
+        if logits is None and self.gate is None and self.gate_w is None:
             raise ValueError("HybridBlock: pass router logits or build the block with gate_w")
         t, d = x.shape
         h = ops.rmsnorm_gated(x, None, self.core_gamma, eps=self.core_eps)
         core = self.mamba.forward(h, dt, B, C, cu_seqlens, final_state=final_state)
         r, f = ops.add_rmsnorm(x, core, self.ff_gamma, eps=self.ff_eps)
         if logits is None:
-            logits = self.gate.forward(f, out_dtype=torch.float32)
+            logits = self.router_logits(f)
         ff = self.moe.forward(f, logits, out_dtype=x.dtype)["out"]
         out, _ = ops.add_rmsnorm(r, ff, want_norm=False)
-        return {"out": out, "residual": r, "core": core, "ff": ff, "logits": logits}
+        return {"out": out, "residual": r, "core": core, "ff": ff, "logits": logits,
+                "h": h, "f": f}
 
 
 class Mamba2Block:
     """Faithful Mamba-2 block on the packed path (Mamba2SSD::forward_faithful,
-    src/mamba2.cpp:2360-2681; streaming step forward_faithful_step, 3947-4126):
+    src/mamba2.cpp:2360-2681; streaming step forward_faithful_step, 3947-4126), with
+    the reference's mixed precision (src/mamba2.cpp:584-662):
 
-        x, z, B, C, dt = five BitLinear projections of u (one RMS_PERI + int8
-                         quantization shared by five ternary GEMMs)
-        x, B, C        = SiLU(causal conv + bias) per sequence (x's conv is fused into
-                         the scan's staging; B and C go through the conv kernel)
-        y              = faithful scan: per-head A_log [H], P = d_head, G groups, D skip
-        out            = out_proj(RMSNorm(y * SiLU(z), eps) * gamma)
+        x, z   = ternary BitLinear projections of u in exact-linear mode (no input
+                 RMSNorm, no magnitude, no bias): one int8 quantization of u shared
+                 by the two ternary GEMMs
+        B, C   = float linears of u (quantization-sensitive, exact-linear), and
+        dt     = a float linear of u plus its bias: one fp32 GEMM over the stacked
+                 [w_B; w_C; w_dt] with the bias [0, 0, dt_bias]
+        x, B, C = SiLU(causal conv + bias) per sequence (x's conv is fused into
+                 the scan's staging; B and C go through the conv kernel)
+        y      = faithful scan: per-head A_log [H], P = d_head, G groups, D skip
+        out    = out_proj(RMSNorm(y * SiLU(z), eps) * gamma), out_proj a default
+                 BitLinear (RMS_PERI, magnitude)
 
     params: w_x [inner, d], w_z [inner, d], w_B [G*N, d], w_C [G*N, d], w_dt [H, d],
     w_out [d, inner], conv_w [inner + 2*G*N, K], conv_b [inner + 2*G*N], a_log [H],
-    d_skip [H], norm_w [inner]; shape keys H, P, N, G and optional eps (1e-5).
-    Activations run in `dtype` (f32 by default, the reference's).
+    d_skip [H], norm_w [inner]; optional dt_bias [H] (zeros), out_magnitude [d] (ones);
+    shape keys H, P, N, G and optional eps (1e-5).  Activations run in `dtype` (f32 by
+    default, the reference's).
     """
 
-    def __init__(self, params: dict, device="cuda", rms_input: bool = True, dtype=torch.float32):
+    def __init__(self, params: dict, device="cuda", dtype=torch.float32):
         self.H, self.P, self.N, self.G = (int(params[k]) for k in ("H", "P", "N", "G"))
         self.inner = self.H * self.P
         self.gs = self.G * self.N
         self.eps = float(params.get("eps", 1e-5))
         self.dtype = dtype
-        self.proj = [BitLinear(params[k], device, rms_input=rms_input)
-                     for k in ("w_x", "w_z", "w_B", "w_C", "w_dt")]
-        self.out_proj = BitLinear(params["w_out"], device, rms_input=rms_input)
-        self.d_model = self.proj[0].in_features
+        self.xz = [BitLinear(params[k], device, rms_input=False) for k in ("w_x", "w_z")]
+        self.d_model = self.xz[0].in_features
         f32 = dict(dtype=torch.float32, device=device)
+        w_sens = np.concatenate([params["w_B"], params["w_C"], params["w_dt"]]).astype(np.float32)
+        self.w_sens = torch.as_tensor(w_sens, **f32)
+        dt_bias = params.get("dt_bias")
+        bias = np.zeros(2 * self.gs + self.H, np.float32)
+        if dt_bias is not None:
+            bias[2 * self.gs:] = np.asarray(dt_bias, np.float32)
+        self.b_sens = torch.as_tensor(bias, **f32)
+        self.out_proj = BitLinear(params["w_out"], device, rms_input=True,
+                                  magnitude=params.get("out_magnitude"))
         cw = torch.as_tensor(params["conv_w"], **f32)
         cb = torch.as_tensor(params["conv_b"], **f32)
         self.K = cw.shape[1]
@@ -320,33 +360,33 @@ class Mamba2Block:
         self.a_log = torch.as_tensor(params["a_log"], **f32)
         self.d_skip = torch.as_tensor(params["d_skip"], **f32)
         self.norm_w = torch.as_tensor(params["norm_w"], **f32)
-        self.views = ops.LinearViewArray([p.view_entry() for p in self.proj], device)
-        self._ws = {}
+        self.views = ops.LinearViewArray([p.view_entry() for p in self.xz], device)
 
     def _project(self, u: torch.Tensor) -> list:
-        """One quantization, then the five ternary projections: one grouped GEMV launch
-        for <= 8 rows (launch_grouped_decode_projections' role), else five GEMMs."""
+        """x, z from one int8 quantization of u (one grouped GEMV launch for <= 8 rows,
+        else two ternary GEMMs); B, C, dt from one fp32 GEMM (dt contiguous for the scan,
+        B and C strided column slices for the conv)."""
         m = u.shape[0]
-        q, s, r = self.proj[0].workspace(m, u.device)
+        q, s, _ = self.xz[0].workspace(m, u.device)
         st = _stream()
-        call("nsosx_quantize_act_i8", _p(u), ops._dt(u), m, self.d_model, 8, 1, _p(q), _p(s),
-             _p(r), st)
+        call("nsosx_quantize_act_i8", _p(u), ops._dt(u), m, self.d_model, 8, 0, _p(q), _p(s),
+             None, st)
         if m <= 8:
-            widest = max(p.out_features for p in self.proj)
-            y = torch.empty((len(self.proj), m * widest), dtype=self.dtype, device=u.device)
-            # every group reads the same codes and scales: zero strides
-            call("nsosx_grouped_gemv", self.views.ptr, len(self.proj), _p(q), 0, _p(s), 0, m,
-                 _p(y), m * widest, _DT[self.dtype], st)
-            return [y[g, :m * p.out_features].view(m, p.out_features)
-                    for g, p in enumerate(self.proj)]
-        outs = []
-        for p in self.proj:
-            y = torch.empty((m, p.out_features), dtype=self.dtype, device=u.device)
-            call("nsosx_ternary_gemm", _p(q), _p(s), _p(p.packed), p.weight_scale, m,
-                 p.in_features, p.out_features, _p(p.magnitude), _p(p.bias), _p(y),
-                 _DT[self.dtype], None, st)
-            outs.append(y)
-        return outs
+            y = torch.empty((2, m * self.inner), dtype=self.dtype, device=u.device)
+            # both groups read the same codes and scales: zero strides
+            call("nsosx_grouped_gemv", self.views.ptr, 2, _p(q), 0, _p(s), 0, m, _p(y),
+                 m * self.inner, _DT[self.dtype], st)
+            xv, z = y[0].view(m, self.inner), y[1].view(m, self.inner)
+        else:
+            xv, z = (torch.empty((m, self.inner), dtype=self.dtype, device=u.device)
+                     for _ in range(2))
+            for p, out in zip(self.xz, (xv, z)):
+                call("nsosx_ternary_gemm", _p(q), _p(s), _p(p.packed), p.weight_scale, m,
+                     p.in_features, p.out_features, None, None, _p(out), _DT[self.dtype],
+                     None, st)
+        sens = ops.linear_f32(u, self.w_sens, bias=self.b_sens, out_dtype=self.dtype)
+        g = self.gs
+        return [xv, z, sens[:, :g], sens[:, g:2 * g], sens[:, 2 * g:].contiguous()]
 
     def forward(self, u: torch.Tensor, cu_seqlens: torch.Tensor, initial_state=None,
                 final_state=None) -> dict:
@@ -362,8 +402,8 @@ class Mamba2Block:
             final_state.copy_(fin)
         normed = ops.rmsnorm_gated(y, z, self.norm_w, eps=self.eps)
         out = self.out_proj.forward(normed, out_dtype=self.dtype)
-        return {"out": out, "x": xv, "z": z, "B": Bc, "C": Cc, "dt": dt, "y": y,
-                "normed": normed, "final_state": fin}
+        return {"out": out, "x": xv, "z": z, "Bv": Bv, "Cv": Cv, "B": Bc, "C": Cc, "dt": dt,
+                "y": y, "normed": normed, "final_state": fin}
 
     def new_decode_state(self, rows: int, device) -> dict:
         """Zero recurrent state [R, inner, N] and conv rings [R, K-1, channels]."""

@@ -152,6 +152,67 @@ def bitnet_gemm_158bit_gpu(x: torch.Tensor, packed: torch.Tensor, weight_scale: 
     return y
 
 
+def linear_f32(x: torch.Tensor, w: torch.Tensor, rms_input: bool = False, magnitude=None,
+               bias=None, out_dtype=torch.float32, out=None) -> torch.Tensor:
+    """BitLinear's float reference path for quantization-sensitive layers
+    (src/bitlinear.cpp:465-518): [rmsnorm] x @ w^T, then * magnitude, then + bias."""
+    _dev(x, "x")
+    _dev(w, "w", torch.float32)
+    _opt(magnitude, "magnitude")
+    _opt(bias, "bias")
+    if x.dim() != 2 or w.dim() != 2 or w.shape[1] != x.shape[1]:
+        raise ValueError("linear_f32: x [M, K] and w [N, K] must agree in K")
+    m, k = x.shape
+    n = w.shape[0]
+    for name, v in (("magnitude", magnitude), ("bias", bias)):
+        if v is not None and v.numel() != n:
+            raise ValueError(f"linear_f32: {name} must hold N = {n} values")
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype, device=x.device)
+    elif tuple(out.shape) != (m, n) or not out.is_contiguous():
+        raise ValueError("linear_f32: out must be a contiguous [M, N] tensor")
+    rw = torch.empty(m, dtype=torch.float32, device=x.device) if rms_input else None
+    call("nsosx_linear_f32", _p(x), _dt(x), m, k, _p(w), n, int(rms_input), _p(magnitude),
+         _p(bias), _p(out), _dt(out), _p(rw), _stream())
+    return out
+
+
+def bitlinear_ste_backward(x, q, act_scale, w_latent, packed, weight_scale: float, grad,
+                           rms_input: bool = True, magnitude=None, want_dbias: bool = False,
+                           want_dmag: bool = True) -> dict:
+    """BitLinear::backward on the packed path (src/bitlinear.cpp:1191-1357) from what the
+    forward saved: x [M, K], its int8 codes q and act_scale, the latent weights [N, K] and
+    their packed ternary; grad [M, N].  Returns dx, dW (+ dmag, dbias)."""
+    for name, v, dt in (("q", q, torch.int8), ("act_scale", act_scale, torch.float32),
+                        ("w_latent", w_latent, torch.float32), ("grad", grad, torch.float32)):
+        _dev(v, name, dt)
+    _dev(packed, "packed")
+    _opt(magnitude, "magnitude")
+    m, k = q.shape
+    n = w_latent.shape[0]
+    if tuple(grad.shape) != (m, n) or tuple(w_latent.shape) != (n, k) or \
+            act_scale.numel() != m or packed.numel() != n * k // 16:
+        raise ValueError("bitlinear_ste_backward: inconsistent shapes")
+    if rms_input:
+        _dev(x, "x")
+        if tuple(x.shape) != (m, k):
+            raise ValueError("bitlinear_ste_backward: x must be [M, K]")
+    dev = q.device
+    out = {"dx": torch.empty((m, k), dtype=torch.float32, device=dev),
+           "dW": torch.empty((n, k), dtype=torch.float32, device=dev)}
+    if magnitude is not None and want_dmag:
+        out["dmag"] = torch.empty(n, dtype=torch.float32, device=dev)
+    if want_dbias:
+        out["dbias"] = torch.empty(n, dtype=torch.float32, device=dev)
+    nbytes = int(lib().nsosx_bitlinear_ste_backward_workspace(m, k, n, int(rms_input)))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    call("nsosx_bitlinear_ste_backward", _p(x) if rms_input else None,
+         _dt(x) if rms_input else F32, _p(q), _p(act_scale), _p(w_latent), _p(packed),
+         float(weight_scale), m, k, n, int(rms_input), _p(magnitude), _p(grad), _p(out["dx"]),
+         _p(out["dW"]), _p(out.get("dmag")), _p(out.get("dbias")), _p(ws), _stream())
+    return out
+
+
 class LinearViewArray:
     """Device array of nsosx_linear_view descriptors (GpuLinearView's C shape).
 

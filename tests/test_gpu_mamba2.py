@@ -1,10 +1,17 @@
-"""Faithful Mamba-2 block (Mamba2SSD::forward_faithful and its decode step) on the GPU against the oracle's composition,
-stage by stage on the GPU's own upstream tensors (src/mamba2.cpp:2360-2681):
-the five projections and out_proj bit-exact, conv / scan / gated norm within the fp32
-bounds of their own tests (1e-4 rel, 1e-5 abs; norm 1e-5 / 1e-6).  The decode step equals
-the prefill token by token (to the conv's bias-first rounding and int8 code flips: 1e-3 of
-the output scale), and a HIP-graph replay of the step equals the eager step bit for bit on
-every replay."""
+"""Faithful Mamba-2 block (Mamba2SSD::forward_faithful and its decode step) on the GPU
+against the oracle's composition, stage by stage on the GPU's own upstream tensors
+(src/mamba2.cpp:2360-2681), with the reference's mixed precision (584-662):
+
+  * x and z: ternary BitLinear in exact-linear mode (no input norm, no magnitude),
+    bit-exact;
+  * B, C, dt: the float path (quantization-sensitive), dt with its bias, within the
+    fp32 bound 1e-4 / 1e-5 of the output scale;
+  * conv / scan / gated norm within the fp32 bounds of their own tests (1e-4 rel,
+    1e-5 abs; norm 1e-5 / 1e-6); out_proj (RMS_PERI + magnitude) bit-exact.
+
+The decode step equals the prefill token by token (to the conv's bias-first rounding
+and int8 code flips: 1e-3 of the output scale), and a HIP-graph replay of the step
+equals the eager step bit for bit on every replay."""
 import numpy as np
 import pytest
 import torch
@@ -18,8 +25,10 @@ def _params(rng, d=64, H=4, P=16, N=16, G=2, K=4):
     inner, gs = H * P, G * N
     w = lambda n, k: rng.standard_normal((n, k)).astype(np.float32)
     return {
-        "w_x": w(inner, d), "w_z": w(inner, d), "w_B": w(gs, d), "w_C": w(gs, d),
-        "w_dt": w(H, d), "w_out": w(d, inner),
+        "w_x": w(inner, d), "w_z": w(inner, d), "w_B": w(gs, d) / 8, "w_C": w(gs, d) / 8,
+        "w_dt": w(H, d) / 8, "w_out": w(d, inner),
+        "dt_bias": (rng.standard_normal(H) - 2.0).astype(np.float32),
+        "out_magnitude": rng.uniform(0.5, 1.5, d).astype(np.float32),
         "conv_w": (rng.standard_normal((inner + 2 * gs, K)) * 0.5).astype(np.float32),
         "conv_b": (rng.standard_normal(inner + 2 * gs) * 0.1).astype(np.float32),
         "a_log": rng.standard_normal(H).astype(np.float32),
@@ -44,15 +53,18 @@ def test_mamba2_block_prefill_matches_oracle(dev, orc):
     T = int(cu[-1])
     u = rng.standard_normal((T, 64)).astype(np.float32)
     res = blk.forward(torch.from_numpy(u).to(dev), torch.from_numpy(cu).to(dev))
-    # projections: bit-exact
-    for key, wk in (("x", "w_x"), ("z", "w_z"), ("dt", "w_dt")):
+    # x, z: ternary exact-linear (no RMS_PERI, no magnitude), bit-exact
+    for key, wk in (("x", "w_x"), ("z", "w_z")):
         pk, ws, _ = orc.pack_weights(p[wk])
-        want = orc.bitlinear_forward(u, pk, ws, p[wk].shape[0], rms_input=True)
+        want = orc.bitlinear_forward(u, pk, ws, p[wk].shape[0], rms_input=False)
         np.testing.assert_array_equal(_np(res[key]), want)
-    pk, ws, _ = orc.pack_weights(p["w_B"])
-    Bv = orc.bitlinear_forward(u, pk, ws, gs, rms_input=True)
-    pk, ws, _ = orc.pack_weights(p["w_C"])
-    Cv = orc.bitlinear_forward(u, pk, ws, gs, rms_input=True)
+    # B, C, dt: float linears of u, dt plus its bias (within the fp32 bound)
+    Bv = orc.linear_f32(u, p["w_B"])
+    Cv = orc.linear_f32(u, p["w_C"])
+    dtv = orc.linear_f32(u, p["w_dt"], bias=p["dt_bias"])
+    for got, want in ((res["Bv"], Bv), (res["Cv"], Cv), (res["dt"], dtv)):
+        np.testing.assert_allclose(_np(got), want, rtol=1e-4, atol=1e-5 * np.abs(want).max())
+    Bv, Cv = _np(res["Bv"]), _np(res["Cv"])
     # conv + SiLU on B and C
     cw, cb = p["conv_w"], p["conv_b"]
     Bc = orc.conv1d_causal(Bv, cw[inner:inner + gs], cu, bias=cb[inner:inner + gs], silu_act=True)
@@ -69,7 +81,8 @@ def test_mamba2_block_prefill_matches_oracle(dev, orc):
     normed = orc.rmsnorm_gated(_np(res["y"]), _np(res["z"]), p["norm_w"], eps=1e-5)
     np.testing.assert_allclose(_np(res["normed"]), normed, rtol=1e-5, atol=1e-6)
     pk, ws, _ = orc.pack_weights(p["w_out"])
-    out = orc.bitlinear_forward(_np(res["normed"]), pk, ws, 64, rms_input=True)
+    out = orc.bitlinear_forward(_np(res["normed"]), pk, ws, 64, rms_input=True,
+                                magnitude=p["out_magnitude"])
     np.testing.assert_array_equal(_np(res["out"]), out)
 
 
