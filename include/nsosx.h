@@ -288,6 +288,37 @@ int nsosx_conv_scan_fwd(const void* x_raw, int64_t x_stride, const float* conv_w
                         int total_tokens, int H, int P, int N, int G, int act_dtype,
                         const float* initial_state, float* final_state, void* y, void* stream);
 
+/* The scan (x_raw through the causal conv when conv_w != NULL, as
+ * nsosx_conv_scan_fwd; else as nsosx_selective_scan_fwd) with a launch plan
+ * built on the device:
+ *   - more than 64 sequences: one pre-pass ranks them longest-first for
+ *     dispatch (instead of a ranking in every workgroup);
+ *   - chunk_tokens > 0 (>= 4): the time-chunked scan.  Every sequence splits
+ *     into chunks of chunk_tokens tokens; a first pass runs each chunk's
+ *     recurrence from zero and records its end state and summed delta, a
+ *     combine carries the states across chunk boundaries (the decay product of
+ *     a chunk is exp of its summed exponents), and a second pass runs each
+ *     chunk from its carried state, its causal conv window taken from the
+ *     sequence's previous tokens.  For batches whose sequences x 16-channel
+ *     blocks cannot fill the GPU (one long prefill).  Needs N <= 16, channels
+ *     per group a multiple of 16, conv width <= 4.  Outputs equal the
+ *     sequential scan to rounding (the carried states differ by a few ulp);
+ *   - chunk_tokens == 0: never chunk; -1: chunk when sequences x (H*P/16) <
+ *     2048 and the sequences are at least two chunks long (chunk size aiming
+ *     at 8192 waves, at least 64 tokens).
+ * workspace: device, nsosx_scan_fwd_workspace(num_seqs, total_tokens, H, P,
+ * N, chunk_tokens) bytes, 256-byte aligned.  Other arguments as above. */
+int64_t nsosx_scan_fwd_workspace(int num_seqs, int total_tokens, int H, int P, int N,
+                                 int chunk_tokens);
+int nsosx_scan_fwd_planned(const void* x, int64_t x_stride, const float* conv_w,
+                           const float* conv_b, int conv_width, const void* dt,
+                           const float* A_log, int a_per_state, const void* B, const void* C,
+                           const float* D, const void* z, int64_t z_stride,
+                           const int32_t* cu_seqlens, int num_seqs, int total_tokens, int H,
+                           int P, int N, int G, int act_dtype, const float* initial_state,
+                           float* final_state, void* y, int chunk_tokens, void* workspace,
+                           void* stream);
+
 /* Decode step over `rows` independent sequences, one token each, state
  * updated in place (src/mamba2.cpp:4038-4125; GPU twin
  * launch_mamba2_faithful_step, src/cuda/mamba_kernels.cu:3332-3419).

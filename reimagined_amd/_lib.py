@@ -45,6 +45,10 @@ SIGNATURES = {
                                       _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "nsosx_conv_scan_fwd": (_i, [_vp, _i64, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i64,
                                  _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp]),
+    "nsosx_scan_fwd_workspace": (_i64, [_i, _i, _i, _i, _i, _i]),
+    "nsosx_scan_fwd_planned": (_i, [_vp, _i64, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp,
+                                    _i64, _vp, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i,
+                                    _vp, _vp]),
     "nsosx_selective_scan_step": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                                        _i, _i, _vp, _vp, _vp]),
     "nsosx_moe_route_workspace": (_i64, [_i, _i]),

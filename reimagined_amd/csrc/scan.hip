@@ -80,7 +80,8 @@ __device__ __forceinline__ float silu_fast(float v) {
 constexpr int kScanTC = 32;       // tokens per LDS chunk
 constexpr int kScanCh = 64;       // channels per workgroup
 constexpr int kMaxConvW = 8;
-constexpr int kOrderMax = 1024;   // sequences ordered longest-first up to this count
+constexpr int kOrderMax = 64;     // in-kernel longest-first ordering up to this count (more
+                                   // sequences: an order pre-pass, nsosx_scan_fwd_planned)
 
 // Workgroup y-index -> sequence, longest sequence first (ties by index), so
 // the longest recurrences start first and short ones fill in behind them.
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
     int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int num_seqs, int total_tokens,
     int H, int P, int N, int G, const float* __restrict__ conv_w, const float* __restrict__ conv_b,
     int W, const float* __restrict__ init_state, float* __restrict__ final_state,
-    void* __restrict__ y) {
+    void* __restrict__ y, const int32_t* __restrict__ order) {
     constexpr int NPAD = 4 * SPL;
     constexpr int NRAW = CONV ? 8 + kMaxConvW - 1 : 8;
     constexpr int BCPT = (kScanTC * NPAD + 255) / 256;  // B/C elements per thread per chunk
@@ -124,7 +125,8 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
     const int D = H * P;
     const int GN = G * N;
     const int c0 = blockIdx.x * kScanCh;
-    const int seq = scan_pick_sequence(cu_seqlens, num_seqs, total_tokens, s_order);
+    const int seq = order ? order[blockIdx.y]
+                          : scan_pick_sequence(cu_seqlens, num_seqs, total_tokens, s_order);
     // a malformed cu_seqlens can only shorten a sequence, never address past T
     const int t0 = min(max(cu_seqlens[seq], 0), total_tokens);
     const int t1 = min(max(cu_seqlens[seq + 1], t0), total_tokens);
@@ -341,6 +343,23 @@ __device__ __forceinline__ int quad_pick_sequence(const int32_t* cu, int num_seq
     return *s_pick;
 }
 
+// How a launch of the quad kernel maps its work items onto the tokens.  Plain
+// launches leave every pointer NULL: item = sequence.  The time-chunked scan
+// runs the kernel over chunks of sequences (item = chunk):
+//   order      rank -> item (the longest-first order computed once per launch)
+//   seq_start  per item: first token of the item's sequence (the causal conv
+//              window at a chunk start holds the sequence's previous tokens)
+//   init_row   per item: row of init_state to start from (-1: zeros)
+//   state_row  per item: row of final_state to write (-1: none)
+//   sum_dl     LOCAL pass: per (item, channel) sum of delta over the item
+struct QuadPlan {
+    const int32_t* order;
+    const int32_t* seq_start;
+    const int32_t* init_row;
+    const int32_t* state_row;
+    float* sum_dl;
+};
+
 // softplus_fast() without branches: the three regimes are formed and selected.
 __device__ __forceinline__ float softplus_sel(float v) {
     const float e = exp_native(v);
@@ -349,7 +368,9 @@ __device__ __forceinline__ float softplus_sel(float v) {
     return v > 20.0f ? v : (u == 1.0f ? e : mid);
 }
 
-template <int ADT, int SPL, bool GATE, bool CONV, bool PH = false>
+// LOCAL: the first pass of the time-chunked scan: the recurrence only (no
+// readout, no output), writing each item's end state and sum of delta.
+template <int ADT, int SPL, bool GATE, bool CONV, bool PH = false, bool LOCAL = false>
 __global__ __launch_bounds__(64) void scan_quad_kernel(
     const void* __restrict__ x, int64_t x_stride, const void* __restrict__ dt,
     const float* __restrict__ a_log, int a_per_state, const void* __restrict__ Bm,
@@ -357,7 +378,7 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
     int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int num_seqs, int total_tokens,
     int H, int P, int N, int G, const float* __restrict__ conv_w, const float* __restrict__ conv_b,
     int W, const float* __restrict__ init_state, float* __restrict__ final_state,
-    void* __restrict__ y) {
+    void* __restrict__ y, QuadPlan plan) {
     using raw_t = typename raw_word<ADT>::type;
     constexpr int NP = 4 * SPL;                 // padded states per channel
     constexpr int BCN = NP / 2;                 // states per staging lane (two lanes per row)
@@ -382,7 +403,10 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
     const int grp = (h * G) / H;
     // uniform across the wave: keeps the token bases in scalar registers
     const int seq = __builtin_amdgcn_readfirstlane(
-        quad_pick_sequence(cu_seqlens, num_seqs, total_tokens, rank, &s_pick));
+        plan.order ? plan.order[rank]
+                   : (plan.seq_start ? rank
+                                     : quad_pick_sequence(cu_seqlens, num_seqs, total_tokens,
+                                                          rank, &s_pick)));
     const int t0 = min(max(cu_seqlens[seq], 0), total_tokens);
     const int t1 = min(max(cu_seqlens[seq + 1], t0), total_tokens);
     const int tlast = total_tokens - 1;
@@ -406,8 +430,17 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
         const bool ok = n < N;
         const float al = a_per_state ? a_log[(int64_t)h * N + min(n, N - 1)] : a_log[h];
         a2[i] = ok ? a2_from_log(al) : 0.0f;
-        st[i] = (ok && init_state) ? init_state[((int64_t)seq * D + c) * N + n] : 0.0f;
     }
+    {
+        const int irow = plan.init_row ? plan.init_row[seq] : seq;
+#pragma unroll
+        for (int i = 0; i < SPL; ++i) {
+            const int n = q * SPL + i;
+            st[i] = (n < N && init_state && irow >= 0) ? init_state[((int64_t)irow * D + c) * N + n]
+                                                       : 0.0f;
+        }
+    }
+    float sdl = 0.0f;  // LOCAL: running sum of delta
 
     // Loads are branch-free: indices past the data are clamped to the last row and
     // the values masked where they are used, so the compiler keeps the loads in
@@ -508,7 +541,17 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
         tnext += 4;
     };
 
-    if (CONV) s_xw[lane >> 2][q] = 0.0f;  // the window before t0 is zero
+    if (CONV) {
+        // the window before t0: zeros at a sequence start; a chunk that starts inside its
+        // sequence takes the sequence's previous raw x
+        float w0 = 0.0f;
+        if (plan.seq_start) {
+            const int tt = t0 - 4 + q;
+            if (tt >= plan.seq_start[seq] && tt >= 0)
+                w0 = load_act<ADT>(x, (int64_t)tt * x_stride + c);
+        }
+        s_xw[lane >> 2][q] = w0;
+    }
     // the group whose readout is pending: its validity, conv output, raw gate and base token
     bool pv_valid = false;
     float pv_xv = 0.0f;
@@ -540,11 +583,14 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
 #pragma unroll
                 for (int i = 0; i < SPL; ++i) {
                     bq[k][i] = s_bc[0][r0 + k][q * SPL + i];
-                    cq[k][i] = s_bc[1][r0 + k][q * SPL + i];
+                    cq[k][i] = LOCAL ? 0.0f : s_bc[1][r0 + k][q * SPL + i];
                 }
             // the previous group's readout partials (written at the end of that group)
-            const float rd0 = s_red[red_r], rd1 = s_red[red_r + 4];
-            const float rd2 = s_red[red_r + 8], rd3 = s_red[red_r + 12];
+            float rd0 = 0.0f, rd1 = 0.0f, rd2 = 0.0f, rd3 = 0.0f;
+            if constexpr (!LOCAL) {
+                rd0 = s_red[red_r]; rd1 = s_red[red_r + 4];
+                rd2 = s_red[red_r + 8]; rd3 = s_red[red_r + 12];
+            }
             // tokens past the sequence feed only later tokens past it: no mask needed on x
             const float xcur = raw_to_f32<ADT>(xr);
             const float dtcur = raw_to_f32<ADT>(dtr);
@@ -606,9 +652,13 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
 #pragma unroll
                 for (int i = 0; i < SPL; ++i) {
                     st[i] = __fmaf_rn(a[k][i], st[i], dxk[k] * bq[k][i]);
-                    p = __fmaf_rn(st[i], cq[k][i], p);
+                    if constexpr (!LOCAL) p = __fmaf_rn(st[i], cq[k][i], p);
                 }
                 part[k] = p;
+            }
+            if constexpr (LOCAL) {
+                sdl += (dlk[0] + dlk[1]) + (dlk[2] + dlk[3]);
+                continue;
             }
             // ---- 4x4 transpose through the wave's LDS slice, one group behind:
             // lane q sums token q of the previous group over the channel's four state
@@ -623,13 +673,19 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
             pv_t = tgrp;
         }
     }
-    if (pv_valid)
-        finish_readout(((s_red[red_r] + s_red[red_r + 4]) + s_red[red_r + 8]) + s_red[red_r + 12]);
-    if (final_state) {
+    if constexpr (!LOCAL) {
+        if (pv_valid)
+            finish_readout(((s_red[red_r] + s_red[red_r + 4]) + s_red[red_r + 8]) +
+                           s_red[red_r + 12]);
+    } else {
+        if (q == 0) plan.sum_dl[(int64_t)seq * D + c] = sdl;
+    }
+    const int frow = plan.state_row ? plan.state_row[seq] : seq;
+    if (final_state && frow >= 0) {
 #pragma unroll
         for (int i = 0; i < SPL; ++i) {
             const int n = q * SPL + i;
-            if (n < N) final_state[((int64_t)seq * D + c) * N + n] = st[i];
+            if (n < N) final_state[((int64_t)frow * D + c) * N + n] = st[i];
         }
     }
 }
@@ -897,8 +953,9 @@ static int scan_fwd_launch(const void* x, int64_t x_stride, const void* dt, cons
                            int num_seqs, int total_tokens, int H, int P, int N, int G,
                            int act_dtype, const float* conv_w, const float* conv_b, int conv_width,
                            const float* initial_state, float* final_state, void* y,
-                           void* stream) {
-    if (!x || !dt || !A_log || !B || !C || !D || !cu_seqlens || !y)
+                           void* stream, const QuadPlan& plan = QuadPlan{},
+                           bool local = false) {
+    if (!x || !dt || !A_log || !B || !C || !D || !cu_seqlens || (!y && !local))
         return fail(NSOSX_ERR_INVALID, "selective_scan_fwd: null pointer");
     if (num_seqs <= 0 || num_seqs > 65535 || total_tokens < 0 || H <= 0 || P <= 0 || N <= 0 ||
         N > 64 || G <= 0 || H % G != 0)
@@ -927,21 +984,24 @@ static int scan_fwd_launch(const void* x, int64_t x_stride, const void* dt, cons
         const int spl = N <= 4 ? 1 : N <= 8 ? 2 : 4;
         // one A per head with N = 16 (the faithful Mamba-2 block): one decay exp per token
         const bool ph = !a_per_state && spl == 4;
+#define NSOSX_QK(ADT, SPL, GATE, CONV, PH, LOC)                                                  \
+    hipLaunchKernelGGL((scan_quad_kernel<ADT, SPL, GATE, CONV, PH, LOC>), grid, block, 0, st, x,   \
+                       x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens,         \
+                       num_seqs, total_tokens, H, P, N, G, conv_w, conv_b, conv_width,             \
+                       initial_state, final_state, y, plan);
 #define NSOSX_QSCAN(ADT, SPL, GATE, CONV)                                                          \
-    if (SPL == 4 && ph)                                                                            \
-        hipLaunchKernelGGL((scan_quad_kernel<ADT, SPL, GATE, CONV, SPL == 4>), grid, block, 0, st, \
-                           x, x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens,  \
-                           num_seqs, total_tokens, H, P, N, G, conv_w, conv_b, conv_width,         \
-                           initial_state, final_state, y);                                         \
-    else                                                                                           \
-        hipLaunchKernelGGL((scan_quad_kernel<ADT, SPL, GATE, CONV, false>), grid, block, 0, st, x, \
-                           x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens,     \
-                           num_seqs, total_tokens, H, P, N, G, conv_w, conv_b, conv_width,         \
-                           initial_state, final_state, y);
+    if (local) {                                                                                   \
+        if (SPL == 4 && ph) { NSOSX_QK(ADT, SPL, false, CONV, SPL == 4, true) }                    \
+        else { NSOSX_QK(ADT, SPL, false, CONV, false, true) }                                      \
+    } else if (SPL == 4 && ph) {                                                                   \
+        NSOSX_QK(ADT, SPL, GATE, CONV, SPL == 4, false)                                            \
+    } else {                                                                                       \
+        NSOSX_QK(ADT, SPL, GATE, CONV, false, false)                                               \
+    }
 #define NSOSX_QSCAN_C(ADT, SPL, GATE) \
     if (conv) { NSOSX_QSCAN(ADT, SPL, GATE, true) } else { NSOSX_QSCAN(ADT, SPL, GATE, false) }
 #define NSOSX_QSCAN_G(ADT, SPL) \
-    if (z) { NSOSX_QSCAN_C(ADT, SPL, true) } else { NSOSX_QSCAN_C(ADT, SPL, false) }
+    if (z && !local) { NSOSX_QSCAN_C(ADT, SPL, true) } else { NSOSX_QSCAN_C(ADT, SPL, false) }
 #define NSOSX_QSCAN_S(ADT)                          \
     switch (spl) {                                  \
         case 1: NSOSX_QSCAN_G(ADT, 1) break;        \
@@ -953,6 +1013,10 @@ static int scan_fwd_launch(const void* x, int64_t x_stride, const void* dt, cons
 #undef NSOSX_QSCAN_G
 #undef NSOSX_QSCAN_C
 #undef NSOSX_QSCAN
+#undef NSOSX_QK
+    } else if (local || plan.seq_start) {
+        return fail(NSOSX_ERR_INVALID, "selective_scan_fwd: the time-chunked scan needs N <= 16, "
+                                       "channels per group a multiple of 16, conv width <= 4");
     } else if (per_group % kScanCh == 0) {
         const dim3 grid(Dm / kScanCh, num_seqs), block(256);
         const int spl = N <= 4 ? 1 : N <= 8 ? 2 : N <= 16 ? 4 : N <= 32 ? 8 : 16;
@@ -960,7 +1024,7 @@ static int scan_fwd_launch(const void* x, int64_t x_stride, const void* dt, cons
     hipLaunchKernelGGL((scan_fwd_kernel<ADT, SPL, GATE, CONV>), grid, block, 0, st, x, x_stride, \
                        dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens, num_seqs,      \
                        total_tokens, H, P, N, G, conv_w, conv_b, conv_width, initial_state,     \
-                       final_state, y);
+                       final_state, y, plan.order);
 #define NSOSX_SCAN_C(ADT, SPL, GATE) \
     if (conv) { NSOSX_SCAN(ADT, SPL, GATE, true) } else { NSOSX_SCAN(ADT, SPL, GATE, false) }
 #define NSOSX_SCAN_G(ADT, SPL) \
@@ -1017,6 +1081,268 @@ extern "C" int nsosx_conv_scan_fwd(const void* x_raw, int64_t x_stride, const fl
     return scan_fwd_launch(x_raw, x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride,
                            cu_seqlens, num_seqs, total_tokens, H, P, N, G, act_dtype, conv_w,
                            conv_b, conv_width, initial_state, final_state, y, stream);
+}
+
+// ===========================================================================
+// Planned scan: a longest-first order computed once per launch (instead of in
+// every workgroup), and the time-chunked scan for batches too small to fill
+// the GPU (one long prefill).  The chunked scan runs in three launches:
+//   1. LOCAL pass over chunks: each chunk's recurrence from zero (the first
+//      chunk of a sequence from its initial state), writing the chunk's end
+//      state and the sum of delta over it;
+//   2. combine, one thread per (sequence, channel, state), sequential over the
+//      sequence's chunks: carry[j] = the state entering chunk j, and
+//      carry[j+1] = exp2(a2 * sum_delta[j]) * carry[j] + local[j]  (the product
+//      of a chunk's decays is exp of the summed exponents);
+//   3. the full scan over chunks from carry[j], with the causal conv window of a
+//      chunk start taken from the sequence's previous tokens, writing y and,
+//      from each sequence's last chunk, its final state.
+// ===========================================================================
+namespace nsosx {
+
+constexpr int kOrderPrepassMax = 8192;  // above this many sequences: dispatch order
+
+__global__ __launch_bounds__(256) void scan_order_kernel(const int32_t* __restrict__ cu, int S,
+                                                         int T, int32_t* __restrict__ order) {
+    __shared__ int s_len[256];
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    int li = -1;
+    if (i < S) {
+        const int a = min(max(cu[i], 0), T);
+        li = min(max(cu[i + 1], a), T) - a;
+    }
+    if (S > kOrderPrepassMax) {
+        if (i < S) order[i] = i;
+        return;
+    }
+    int rank = 0;
+    for (int base = 0; base < S; base += 256) {
+        const int k = base + threadIdx.x;
+        int lk = -1;
+        if (k < S) {
+            const int b = min(max(cu[k], 0), T);
+            lk = min(max(cu[k + 1], b), T) - b;
+        }
+        __syncthreads();
+        s_len[threadIdx.x] = lk;
+        __syncthreads();
+        const int cnt = min(256, S - base);
+        for (int j = 0; j < cnt; ++j) {
+            const int l = s_len[j];
+            rank += (l > li) || (l == li && base + j < i);
+        }
+    }
+    if (i < S) order[rank] = i;
+}
+
+// One workgroup: sequence s splits into max(1, ceil(len / C)) chunks, numbered
+// in sequence order (an exclusive scan of the counts).
+__global__ __launch_bounds__(1024) void chunk_plan_kernel(const int32_t* __restrict__ cu, int S,
+                                                          int T, int C, int maxc,
+                                                          int32_t* __restrict__ chunk_cu,
+                                                          int32_t* __restrict__ seq_start,
+                                                          int32_t* __restrict__ init_row,
+                                                          int32_t* __restrict__ state_row,
+                                                          int32_t* __restrict__ first_chunk) {
+    __shared__ int s_scan[1024];
+    __shared__ int s_end;
+    const int t = threadIdx.x;
+    int carry = 0;
+    if (t == 0) s_end = 0;
+    for (int base = 0; base < S; base += 1024) {
+        const int s = base + t;
+        int a = 0, l = 0, cnt = 0;
+        if (s < S) {
+            a = min(max(cu[s], 0), T);
+            l = min(max(cu[s + 1], a), T) - a;
+            cnt = max(1, (l + C - 1) / C);
+        }
+        __syncthreads();
+        s_scan[t] = cnt;
+        __syncthreads();
+        for (int off = 1; off < 1024; off <<= 1) {
+            const int v = t >= off ? s_scan[t - off] : 0;
+            __syncthreads();
+            s_scan[t] += v;
+            __syncthreads();
+        }
+        if (s < S) {
+            const int first = carry + s_scan[t] - cnt;
+            first_chunk[s] = min(first, maxc);  // a malformed cu_seqlens cannot overrun
+            for (int j = 0; j < cnt; ++j) {
+                const int idx = first + j;
+                if (idx >= maxc) break;   // cannot happen: maxc >= S + T / C
+                chunk_cu[idx] = a + min(j * C, l);
+                seq_start[idx] = a;
+                init_row[idx] = j == 0 ? s : -1;
+                state_row[idx] = j == cnt - 1 ? s : -1;
+            }
+            if (s == S - 1) s_end = a + l;
+        }
+        carry += s_scan[1023];
+        __syncthreads();
+    }
+    __syncthreads();
+    for (int idx = min(carry, maxc) + t; idx <= maxc; idx += 1024) {
+        chunk_cu[idx] = s_end;
+        if (idx < maxc) {
+            seq_start[idx] = s_end;
+            init_row[idx] = -1;
+            state_row[idx] = -1;
+        }
+    }
+    if (t == 0) first_chunk[S] = min(carry, maxc);
+}
+
+__global__ __launch_bounds__(256) void chunk_combine_kernel(
+    const int32_t* __restrict__ first_chunk, int S, int D, int P, int N,
+    const float* __restrict__ a_log, int a_per_state, const float* __restrict__ local,
+    const float* __restrict__ sum_dl, const float* __restrict__ init_state,
+    float* __restrict__ carry) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)S * D * N) return;
+    const int n = static_cast<int>(idx % N);
+    const int c = static_cast<int>((idx / N) % D);
+    const int s = static_cast<int>(idx / ((int64_t)N * D));
+    const int h = c / P;
+    const float a2 = a2_from_log(a_per_state ? a_log[(int64_t)h * N + n] : a_log[h]);
+    const int j0 = first_chunk[s], j1 = max(first_chunk[s + 1], j0);
+    float hs = init_state ? init_state[((int64_t)s * D + c) * N + n] : 0.0f;
+    for (int j = j0; j < j1; ++j) {
+        const int64_t o = ((int64_t)j * D + c) * N + n;
+        carry[o] = hs;
+        const float lj = local[o];
+        hs = j == j0 ? lj
+                     : __fmaf_rn(__builtin_amdgcn_exp2f(a2 * sum_dl[(int64_t)j * D + c]), hs, lj);
+    }
+}
+
+static int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+
+// chunk_tokens < 0: chunk when sequences x 16-channel blocks give fewer than two
+// waves per SIMD and the sequences are long enough to split; target ~8 waves.
+static int resolve_chunk(int S, int T, int H, int P, int N, int chunk_tokens) {
+    if (chunk_tokens >= 0) return chunk_tokens;
+    const int D = H * P;
+    if (N > 16 || D % kQuadCh != 0 || S <= 0 || T <= 0) return 0;
+    const int64_t blocks = D / kQuadCh;
+    if ((int64_t)S * blocks >= 2048) return 0;
+    int64_t c = ((int64_t)T * blocks + 8191) / 8192;
+    c = std::max<int64_t>(c, 64);
+    c = std::max<int64_t>(c, ((int64_t)T + 65535 - S - 1) / (65535 - S));  // chunks fit a grid
+    c = (c + 31) / 32 * 32;
+    if (2 * c > (int64_t)T / S) return 0;
+    return static_cast<int>(std::min<int64_t>(c, 1 << 20));
+}
+
+struct ScanWs {
+    int32_t* order;
+    int32_t *chunk_cu, *seq_start, *init_row, *state_row, *first_chunk;
+    float *local, *sum_dl, *carry;
+    int maxc;
+    int64_t bytes;
+};
+
+static ScanWs scan_ws_layout(void* base, int S, int T, int D, int N, int C) {
+    ScanWs w{};
+    int64_t off = 0;
+    auto take = [&](int64_t bytes) {
+        char* p = base ? static_cast<char*>(base) + off : nullptr;
+        off += align256(bytes);
+        return p;
+    };
+    w.order = reinterpret_cast<int32_t*>(take((int64_t)S * 4));
+    if (C > 0) {
+        const int64_t maxc = (int64_t)S + (T + C - 1) / C;
+        w.maxc = static_cast<int>(maxc);
+        w.chunk_cu = reinterpret_cast<int32_t*>(take((maxc + 1) * 4));
+        w.seq_start = reinterpret_cast<int32_t*>(take(maxc * 4));
+        w.init_row = reinterpret_cast<int32_t*>(take(maxc * 4));
+        w.state_row = reinterpret_cast<int32_t*>(take(maxc * 4));
+        w.first_chunk = reinterpret_cast<int32_t*>(take(((int64_t)S + 1) * 4));
+        w.local = reinterpret_cast<float*>(take(maxc * D * N * 4));
+        w.sum_dl = reinterpret_cast<float*>(take(maxc * D * 4));
+        w.carry = reinterpret_cast<float*>(take(maxc * D * N * 4));
+    }
+    w.bytes = off;
+    return w;
+}
+
+}  // namespace nsosx
+
+using namespace nsosx;
+
+extern "C" int64_t nsosx_scan_fwd_workspace(int num_seqs, int total_tokens, int H, int P, int N,
+                                            int chunk_tokens) {
+    if (num_seqs <= 0 || total_tokens < 0 || H <= 0 || P <= 0 || N <= 0) return 0;
+    const int C = resolve_chunk(num_seqs, total_tokens, H, P, N, chunk_tokens);
+    return scan_ws_layout(nullptr, num_seqs, total_tokens, H * P, N, C).bytes;
+}
+
+extern "C" int nsosx_scan_fwd_planned(const void* x, int64_t x_stride, const float* conv_w,
+                                      const float* conv_b, int conv_width, const void* dt,
+                                      const float* A_log, int a_per_state, const void* B,
+                                      const void* C, const float* D, const void* z,
+                                      int64_t z_stride, const int32_t* cu_seqlens, int num_seqs,
+                                      int total_tokens, int H, int P, int N, int G, int act_dtype,
+                                      const float* initial_state, float* final_state, void* y,
+                                      int chunk_tokens, void* workspace, void* stream) {
+    if (!workspace) return fail(NSOSX_ERR_INVALID, "scan_fwd_planned: null workspace");
+    if (reinterpret_cast<uintptr_t>(workspace) % 256)
+        return fail(NSOSX_ERR_INVALID, "scan_fwd_planned: workspace must be 256-byte aligned");
+    if (!cu_seqlens || num_seqs <= 0 || num_seqs > 65535 || total_tokens < 0 || H <= 0 || P <= 0 ||
+        N <= 0)
+        return fail(NSOSX_ERR_INVALID, "scan_fwd_planned: bad shape");
+    if (chunk_tokens > 0 && chunk_tokens < 4)
+        return fail(NSOSX_ERR_INVALID, "scan_fwd_planned: chunk_tokens must be >= 4, 0 or -1");
+    const int Cn = resolve_chunk(num_seqs, total_tokens, H, P, N, chunk_tokens);
+    const int Dm = H * P;
+    const ScanWs ws = scan_ws_layout(workspace, num_seqs, total_tokens, Dm, N, Cn);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (Cn == 0) {
+        // up to kOrderMax sequences the kernels rank in-workgroup (at most kOrderMax^2
+        // compares per wave); beyond, one pre-pass ranks every sequence once
+        const bool prepass = num_seqs > kOrderMax;
+        if (prepass)
+            hipLaunchKernelGGL(scan_order_kernel, dim3((num_seqs + 255) / 256), dim3(256), 0, st,
+                               cu_seqlens, num_seqs, total_tokens, ws.order);
+        QuadPlan plan{};
+        plan.order = prepass ? ws.order : nullptr;
+        return scan_fwd_launch(x, x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride,
+                               cu_seqlens, num_seqs, total_tokens, H, P, N, G, act_dtype, conv_w,
+                               conv_b, conv_width, initial_state, final_state, y, stream, plan);
+    }
+    if (N > 16 || (Dm / G) % kQuadCh != 0 || (conv_w && conv_width > kQuadMaxW))
+        return fail(NSOSX_ERR_INVALID, "scan_fwd_planned: the time-chunked scan needs N <= 16, "
+                                       "channels per group a multiple of 16, conv width <= 4");
+    if ((int64_t)ws.maxc * Dm * N >= ((int64_t)1 << 31) || ws.maxc > 65535)
+        return fail(NSOSX_ERR_OVERFLOW, "scan_fwd_planned: too many chunks (at most 65535 and "
+                                        "chunks * H*P * N < 2^31): use longer chunks");
+    hipLaunchKernelGGL(chunk_plan_kernel, dim3(1), dim3(1024), 0, st, cu_seqlens, num_seqs,
+                       total_tokens, Cn, ws.maxc, ws.chunk_cu, ws.seq_start, ws.init_row,
+                       ws.state_row, ws.first_chunk);
+    // 1. local pass: end states from zero (first chunks from the initial state)
+    QuadPlan p1{};
+    p1.seq_start = ws.seq_start;
+    p1.init_row = ws.init_row;
+    p1.sum_dl = ws.sum_dl;
+    int rc = scan_fwd_launch(x, x_stride, dt, A_log, a_per_state, B, C, D, nullptr, 0,
+                             ws.chunk_cu, ws.maxc, total_tokens, H, P, N, G, act_dtype, conv_w,
+                             conv_b, conv_width, initial_state, ws.local, nullptr, stream, p1,
+                             true);
+    if (rc) return rc;
+    // 2. carries across chunk boundaries
+    const int64_t threads = (int64_t)num_seqs * Dm * N;
+    hipLaunchKernelGGL(chunk_combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       st, ws.first_chunk, num_seqs, Dm, P, N, A_log, a_per_state, ws.local,
+                       ws.sum_dl, initial_state, ws.carry);
+    // 3. full pass from the carried states
+    QuadPlan p3{};
+    p3.seq_start = ws.seq_start;
+    p3.state_row = ws.state_row;
+    return scan_fwd_launch(x, x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride, ws.chunk_cu,
+                           ws.maxc, total_tokens, H, P, N, G, act_dtype, conv_w, conv_b,
+                           conv_width, ws.carry, final_state, y, stream, p3);
 }
 
 extern "C" int nsosx_selective_scan_step(const void* x, const void* dt, const float* A_log,

@@ -142,11 +142,17 @@ class HybridMambaLayer:
         self.in_proj.forward_into(x, b["xz"], mk("in_proj"))
         xin = b["xz"][:, :di]
         z = b["xz"][:, di:]
-        # causal conv + bias + SiLU fused into the scan's input staging
-        call("nsosx_conv_scan_fwd", _p(xin), xin.stride(0), _p(self.conv_w), _p(self.conv_b),
+        # causal conv + bias + SiLU fused into the scan's input staging; the planned entry
+        # orders many sequences once and chunks a batch too small to fill the GPU in time
+        ws = b.get(("scan_ws", s))
+        if ws is None:
+            nbytes = int(ops.lib().nsosx_scan_fwd_workspace(s, t, di, 1, n, -1))
+            ws = b[("scan_ws", s)] = torch.empty(max(nbytes, 1), dtype=torch.uint8,
+                                                 device=x.device)
+        call("nsosx_scan_fwd_planned", _p(xin), xin.stride(0), _p(self.conv_w), _p(self.conv_b),
              self.conv_w.shape[1], _p(dt), _p(self.a_log), 1, _p(B), _p(C), _p(self.d_skip), _p(z),
              z.stride(0), _p(cu_seqlens), s, t, di, 1, n, 1, ops._dt(x), None, _p(final_state),
-             _p(b["ys"]), _stream())
+             _p(b["ys"]), -1, _p(ws), _stream())
         if marker:
             marker("conv_scan")
         if out is None:

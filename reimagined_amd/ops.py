@@ -309,9 +309,18 @@ def conv1d_causal(x: torch.Tensor, weight: torch.Tensor, cu_seqlens: torch.Tenso
     return out
 
 
+def _scan_workspace(s, t, H, P, N, chunk_tokens, device):
+    nbytes = int(lib().nsosx_scan_fwd_workspace(s, t, H, P, N, chunk_tokens))
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+
+
 def selective_scan_fwd(x, dt, a_log, B, C, D, z, cu_seqlens, H, P, N, G, initial_state=None,
-                       want_final: bool = True):
-    """Packed ragged faithful scan (src/mamba2.cpp:2602-2675) -> (y [T, H*P], final [S, H*P, N])."""
+                       want_final: bool = True, chunk_tokens: int | None = -1):
+    """Packed ragged faithful scan (src/mamba2.cpp:2602-2675) -> (y [T, H*P], final [S, H*P, N]).
+
+    chunk_tokens: -1 lets the library chunk long sequences in time when the batch cannot
+    fill the GPU, 0 never chunks, > 0 forces that chunk length; None calls the unplanned
+    entry point (no order pre-pass, no chunking)."""
     _check_scan_shapes("selective_scan_fwd", x, dt, a_log, B, C, D, z, H, P, N, G)
     _check_cu_seqlens("selective_scan_fwd", cu_seqlens)
     t = x.shape[0]
@@ -332,15 +341,23 @@ def selective_scan_fwd(x, dt, a_log, B, C, D, z, cu_seqlens, H, P, N, G, initial
     a_per_state = int(a_log.numel() == H * N and N > 1)
     y = torch.empty((t, H * P), dtype=x.dtype, device=x.device)
     fin = torch.empty((s, H * P, N), dtype=torch.float32, device=x.device) if want_final else None
-    call("nsosx_selective_scan_fwd", _p(x), x.stride(0), _p(dt), _p(a_log), a_per_state, _p(B),
-         _p(C), _p(D), _p(z), 0 if z is None else z.stride(0), _p(cu_seqlens), s, t, H, P, N, G,
-         _dt(x), _p(initial_state), _p(fin), _p(y), _stream())
+    if chunk_tokens is None:
+        call("nsosx_selective_scan_fwd", _p(x), x.stride(0), _p(dt), _p(a_log), a_per_state,
+             _p(B), _p(C), _p(D), _p(z), 0 if z is None else z.stride(0), _p(cu_seqlens), s, t,
+             H, P, N, G, _dt(x), _p(initial_state), _p(fin), _p(y), _stream())
+    else:
+        ws = _scan_workspace(s, t, H, P, N, chunk_tokens, x.device)
+        call("nsosx_scan_fwd_planned", _p(x), x.stride(0), None, None, 0, _p(dt), _p(a_log),
+             a_per_state, _p(B), _p(C), _p(D), _p(z), 0 if z is None else z.stride(0),
+             _p(cu_seqlens), s, t, H, P, N, G, _dt(x), _p(initial_state), _p(fin), _p(y),
+             chunk_tokens, _p(ws), _stream())
     return y, fin
 
 
 def conv_scan_fwd(x_raw, conv_w, conv_b, dt, a_log, B, C, D, z, cu_seqlens, H, P, N, G,
-                  initial_state=None, want_final: bool = True):
-    """Causal conv + bias + SiLU fused into the scan's staging -> (y, final state)."""
+                  initial_state=None, want_final: bool = True, chunk_tokens: int | None = -1):
+    """Causal conv + bias + SiLU fused into the scan's staging -> (y, final state).
+    chunk_tokens as selective_scan_fwd."""
     _check_scan_shapes("conv_scan_fwd", x_raw, dt, a_log, B, C, D, z, H, P, N, G)
     _check_cu_seqlens("conv_scan_fwd", cu_seqlens)
     t = x_raw.shape[0]
@@ -367,10 +384,17 @@ def conv_scan_fwd(x_raw, conv_w, conv_b, dt, a_log, B, C, D, z, cu_seqlens, H, P
     y = torch.empty((t, H * P), dtype=x_raw.dtype, device=x_raw.device)
     fin = (torch.empty((s, H * P, N), dtype=torch.float32, device=x_raw.device)
            if want_final else None)
-    call("nsosx_conv_scan_fwd", _p(x_raw), x_raw.stride(0), _p(conv_w), _p(conv_b),
-         conv_w.shape[1], _p(dt), _p(a_log), a_per_state, _p(B), _p(C), _p(D), _p(z),
-         0 if z is None else z.stride(0), _p(cu_seqlens), s, t, H, P, N, G, _dt(x_raw),
-         _p(initial_state), _p(fin), _p(y), _stream())
+    if chunk_tokens is None:
+        call("nsosx_conv_scan_fwd", _p(x_raw), x_raw.stride(0), _p(conv_w), _p(conv_b),
+             conv_w.shape[1], _p(dt), _p(a_log), a_per_state, _p(B), _p(C), _p(D), _p(z),
+             0 if z is None else z.stride(0), _p(cu_seqlens), s, t, H, P, N, G, _dt(x_raw),
+             _p(initial_state), _p(fin), _p(y), _stream())
+    else:
+        ws = _scan_workspace(s, t, H, P, N, chunk_tokens, x_raw.device)
+        call("nsosx_scan_fwd_planned", _p(x_raw), x_raw.stride(0), _p(conv_w), _p(conv_b),
+             conv_w.shape[1], _p(dt), _p(a_log), a_per_state, _p(B), _p(C), _p(D), _p(z),
+             0 if z is None else z.stride(0), _p(cu_seqlens), s, t, H, P, N, G, _dt(x_raw),
+             _p(initial_state), _p(fin), _p(y), chunk_tokens, _p(ws), _stream())
     return y, fin
 
 

@@ -79,9 +79,9 @@ def test_scan_matches_oracle(dev, orc, H, P, N, G, per_state, lengths):
 
 @pytest.mark.parametrize("count,hi", [(40, 12), (1100, 3)])
 def test_scan_many_sequences_with_empty_ones(dev, orc, count, hi):
-    """Empty sequences (equal cu_seqlens entries) and more sequences than the longest-first
-    ordering covers (1100 > 1024): every non-empty sequence still matches the oracle and an
-    empty one's final state is its (zero) initial state."""
+    """Empty sequences (equal cu_seqlens entries) and more sequences than the in-kernel
+    longest-first ordering covers (1100 > 64: the order pre-pass): every non-empty sequence
+    still matches the oracle and an empty one's final state is its (zero) initial state."""
     rng = np.random.default_rng(count)
     H, P, N, G = 32, 1, 16, 1
     lengths = rng.integers(0, hi + 1, size=count)
@@ -272,3 +272,97 @@ def test_conv_scan_fused_matches_oracle(dev, orc, dtype, lengths, H, N, W):
         scale = np.abs(wy).max()
         np.testing.assert_allclose(y.float().cpu().numpy(), wy, rtol=2e-2, atol=2e-2 * scale / 64)
         np.testing.assert_allclose(fin.cpu().numpy(), wfin, rtol=1e-4, atol=1e-5)
+
+
+# ---- time-chunked scan and the order pre-pass (nsosx_scan_fwd_planned) ------------------
+
+def _scan_args(dev, inp, cu, dtype, gate):
+    return dict(dt=_t(dev, inp["dt"], dtype), a_log=_t(dev, inp["a_log"]),
+                B=_t(dev, inp["B"], dtype), C=_t(dev, inp["C"], dtype), D=_t(dev, inp["D"]),
+                z=_t(dev, inp["z"], dtype) if gate else None, cu_seqlens=_t(dev, cu))
+
+
+@pytest.mark.parametrize("conv", [False, True])
+@pytest.mark.parametrize("chunk", [4, 37, 64, 200])
+@pytest.mark.parametrize("per_state,P,gate,init", [(True, 1, True, False), (False, 16, False, True)])
+def test_chunked_scan_matches_oracle(dev, orc, conv, chunk, per_state, P, gate, init):
+    """Chunk boundaries inside sequences (carried state and conv window), sequences shorter
+    than a chunk, an empty sequence, a chunk length that divides nothing (37): against the
+    oracle within the fp32 bound, and against the unchunked scan to 1e-5."""
+    rng = np.random.default_rng(chunk * 7 + int(conv) + P)
+    H = 64 // P
+    N, G = 16, 1
+    lengths = [300, 0, 7, 64, 129, 1]
+    cu = _cu(lengths)
+    T = int(cu[-1])
+    inp = _inputs(rng, T, H, P, N, G, per_state)
+    a = _scan_args(dev, inp, cu, torch.float32, gate)
+    st0 = rng.normal(0, 0.1, (len(lengths), H * P, N)).astype(np.float32) if init else None
+    if conv:
+        w = (rng.standard_normal((H * P, 4)) * 0.5).astype(np.float32)
+        b = (rng.standard_normal(H * P) * 0.1).astype(np.float32)
+        run = lambda ck: ops.conv_scan_fwd(_t(dev, inp["x"]), _t(dev, w), _t(dev, b), a["dt"],
+                                           a["a_log"], a["B"], a["C"], a["D"], a["z"],
+                                           a["cu_seqlens"], H, P, N, G,
+                                           initial_state=_t(dev, st0), chunk_tokens=ck)
+        xc = orc.conv1d_causal(inp["x"], w, cu, bias=b, silu_act=True)
+    else:
+        run = lambda ck: ops.selective_scan_fwd(_t(dev, inp["x"]), a["dt"], a["a_log"], a["B"],
+                                                a["C"], a["D"], a["z"], a["cu_seqlens"], H, P, N,
+                                                G, initial_state=_t(dev, st0), chunk_tokens=ck)
+        xc = inp["x"]
+    y, fin = (v.cpu().numpy() for v in run(chunk))
+    y0, fin0 = (v.cpu().numpy() for v in run(0))
+    wy, wfin = orc.selective_scan(xc, inp["dt"], inp["a_log"], inp["B"], inp["C"], inp["D"],
+                                  inp["z"] if gate else None, cu, H, P, N, G,
+                                  initial_state=st0, gate_silu=gate)
+    np.testing.assert_allclose(y, wy, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(fin, wfin, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(y, y0, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(fin, fin0, rtol=1e-5, atol=1e-6)
+
+
+def test_chunked_scan_auto_long_prefill_bf16(dev, orc):
+    """One 4096-token sequence over 512 channels: too few waves unchunked, so the library
+    chunks it by itself; bf16 I/O within the bf16 bound, fp32 final state within 1e-4."""
+    rng = np.random.default_rng(101)
+    H, P, N, G = 512, 1, 16, 1
+    cu = _cu([4096])
+    inp = _inputs(rng, 4096, H, P, N, G)
+    rd = lambda v: torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+    w = (rng.standard_normal((H, 4)) * 0.5).astype(np.float32)
+    a = _scan_args(dev, inp, cu, torch.bfloat16, True)
+    assert int(ops.lib().nsosx_scan_fwd_workspace(1, 4096, H, P, N, -1)) > \
+        int(ops.lib().nsosx_scan_fwd_workspace(1, 4096, H, P, N, 0))   # auto picks chunking
+    y, fin = ops.conv_scan_fwd(_t(dev, inp["x"], torch.bfloat16), _t(dev, w), None, a["dt"],
+                               a["a_log"], a["B"], a["C"], a["D"], a["z"], a["cu_seqlens"],
+                               H, P, N, G)
+    xc = orc.conv1d_causal(rd(inp["x"]), w, cu, silu_act=True)
+    wy, wfin = orc.selective_scan(xc, rd(inp["dt"]), inp["a_log"], rd(inp["B"]), rd(inp["C"]),
+                                  inp["D"], rd(inp["z"]), cu, H, P, N, G)
+    scale = np.abs(wy).max()
+    np.testing.assert_allclose(y.float().cpu().numpy(), wy, rtol=2e-2, atol=2e-2 * scale / 64)
+    np.testing.assert_allclose(fin.cpu().numpy(), wfin, rtol=1e-4, atol=1e-5)
+
+
+def test_order_prepass_many_short_sequences(dev, orc):
+    """1024 sequences of 32-64 tokens (a continuous-batching step): the planned entry ranks
+    them once in a pre-pass; ordering changes only the schedule, so its outputs equal the
+    unplanned entry's bit for bit, and both match the oracle."""
+    rng = np.random.default_rng(55)
+    H, P, N, G = 128, 1, 16, 1
+    lengths = rng.integers(32, 65, size=1024)
+    cu = _cu(lengths)
+    inp = _inputs(rng, int(cu[-1]), H, P, N, G)
+    a = _scan_args(dev, inp, cu, torch.float32, True)
+    x = _t(dev, inp["x"])
+    outs = [ops.selective_scan_fwd(x, a["dt"], a["a_log"], a["B"], a["C"], a["D"], a["z"],
+                                   a["cu_seqlens"], H, P, N, G, chunk_tokens=ck)
+            for ck in (0, None)]
+    (y, fin), (yl, finl) = ((u.cpu().numpy(), v.cpu().numpy()) for u, v in outs)
+    np.testing.assert_array_equal(y, yl)
+    np.testing.assert_array_equal(fin, finl)
+    wy, wfin = orc.selective_scan(inp["x"], inp["dt"], inp["a_log"], inp["B"], inp["C"],
+                                  inp["D"], inp["z"], cu, H, P, N, G)
+    np.testing.assert_allclose(y, wy, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(fin, wfin, rtol=RTOL, atol=ATOL)
