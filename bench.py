@@ -12,8 +12,10 @@ the roofline object is for the kernel with the largest share.  The extra
 figures are the other two parts of the metric: the prefill ternary GEMM
 (config 3) in int8 TOPS and the HBM-bound kernels (decode GEMV over 128
 rotated weight sets, the decode step over 8 rotated state buffers) in GB/s.
-The CPU baseline is the oracle's restatement of the reference CPU path on a
-bounded sample of the same workload, timed on this host.
+The CPU baseline times the reference's own BitLinear::forward (oracle/_ref,
+built from the reference sources) for the projections and the oracle's
+sequential restatement for the conv + scan, on a bounded sample of the same
+workload on this host.
 """
 from __future__ import annotations
 
@@ -103,16 +105,17 @@ def bench_layer(torch, dev, steps, warmup):
 
 def bench_mamba2_decode(torch, dev, rows=1, reps=50):
     """Faithful Mamba-2 decode step (d_model 1024, 32 heads x 64, N 16, conv 4), eager vs one
-    HIP-graph replay per step: 9 kernels per token at one row (RMS + quantize fused, one grouped
-    GEMV for the five projections, three conv steps, the state step, the gated norm, RMS + quantize
-    and the out_proj GEMV), so the step is launch-bound."""
+    HIP-graph replay per step: one quantization of u, one grouped GEMV for the ternary x and z
+    projections, the fp32 B / C / dt projection, three conv steps, the state step, the gated
+    norm, RMS + quantize and the out_proj GEMV, so the step is launch-bound."""
     from reimagined_amd.layers import Mamba2Block
     rng = np.random.default_rng(41)
     d, H, P, N, G, K = 1024, 32, 64, 16, 1, 4
     inner, gs = H * P, G * N
     w = lambda n, k: rng.standard_normal((n, k)).astype(np.float32)
-    params = {"w_x": w(inner, d), "w_z": w(inner, d), "w_B": w(gs, d), "w_C": w(gs, d),
-              "w_dt": w(H, d), "w_out": w(d, inner),
+    params = {"w_x": w(inner, d), "w_z": w(inner, d), "w_B": w(gs, d) / 32,
+              "w_C": w(gs, d) / 32, "w_dt": w(H, d) / 32, "w_out": w(d, inner),
+              "dt_bias": np.full(H, -2.0, np.float32),
               "conv_w": (rng.standard_normal((inner + 2 * gs, K)) * 0.5).astype(np.float32),
               "conv_b": np.zeros(inner + 2 * gs, np.float32),
               "a_log": rng.standard_normal(H).astype(np.float32),
@@ -138,21 +141,23 @@ def bench_mamba2_decode(torch, dev, rows=1, reps=50):
     torch.cuda.synchronize()
     graph_us = (time.perf_counter() - t0) / reps * 1e6
     return {"rows": rows, "eager_us_per_step": round(eager_us, 1),
-            "graph_us_per_step": round(graph_us, 1), "kernels_per_step": 9}
+            "graph_us_per_step": round(graph_us, 1)}
 
 
 def bench_mamba2_prefill(torch, dev, reps=5):
     """Faithful Mamba-2 block forward (d_model 1024, 32 heads x 64, N 16, one A per head, conv 4,
     f32 activations as in the reference) over config 4's 32 ragged sequences (T = 40796): the
-    five projections, B/C conv, fused conv + scan, gated norm and out_proj."""
+    ternary x / z projections, the fp32 B / C / dt projection, B/C conv, fused conv + scan,
+    gated norm and out_proj."""
     from reimagined_amd import workloads
     from reimagined_amd.layers import Mamba2Block
     rng = np.random.default_rng(42)
     d, H, P, N, G, K = 1024, 32, 64, 16, 1, 4
     inner, gs = H * P, G * N
     w = lambda n, k: rng.standard_normal((n, k)).astype(np.float32)
-    params = {"w_x": w(inner, d), "w_z": w(inner, d), "w_B": w(gs, d), "w_C": w(gs, d),
-              "w_dt": w(H, d), "w_out": w(d, inner),
+    params = {"w_x": w(inner, d), "w_z": w(inner, d), "w_B": w(gs, d) / 32,
+              "w_C": w(gs, d) / 32, "w_dt": w(H, d) / 32, "w_out": w(d, inner),
+              "dt_bias": np.full(H, -2.0, np.float32),
               "conv_w": (rng.standard_normal((inner + 2 * gs, K)) * 0.5).astype(np.float32),
               "conv_b": np.zeros(inner + 2 * gs, np.float32),
               "a_log": rng.standard_normal(H).astype(np.float32),
@@ -210,9 +215,12 @@ def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=3
             # four FMA-class ops); at T*d_inner pairs this issue time exceeds the HBM time
             pairs = T * d_inner
             issue_s = pairs * d_state * (2 + 4) * 4 / 64 / 1024 / 2.4e9
+            roof["valu_issue_bound_ms"] = round(issue_s * 1e3, 4)
+            roof["valu_issue_frac"] = round(issue_s / sec, 4)
             roof["note"] = ("VALU/transcendental-issue bound, not HBM: the recurrence alone needs "
                             f"{issue_s * 1e3:.3f} ms of issue at 2.4 GHz (exp = 2 FMA slots) "
-                            f"against {amount / HBM_PEAK_GBS / 1e6:.3f} ms of HBM time")
+                            f"against {amount / HBM_PEAK_GBS / 1e6:.3f} ms of HBM time; "
+                            "valu_issue_frac = that bound / the kernel's time")
     return roof, work
 
 
@@ -394,34 +402,271 @@ def bench_decode_step(torch, dev, reps=8):
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def cpu_baseline(params, inp, seq_tokens=1024):
-    """The oracle's C4 layer on one sequence of `seq_tokens` tokens (fp32 on bf16 inputs)."""
+def _time_ms(torch, fn, reps):
+    fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def bench_scan_shapes(torch, dev):
+    """The scan where the 32-sequence layer batch does not reach: config 2 at batch 1 (one
+    512-token sequence over 768 channels, fp32), one 32768-token bf16 prefill over 2048
+    channels with the fused conv, 256 ragged sequences of 16-1024 tokens and a
+    continuous-batching step of 1024 sequences of 32-64 tokens.  The first two compare the
+    time-chunked scan (chunk chosen by the library) with the sequential one; the third the
+    once-per-launch longest-first pre-pass with dispatch order; the fourth the planned entry
+    with the unplanned one (no ranking in either)."""
+    from reimagined_amd import ops, workloads
+    out = {}
+
+    def make(T, D, N, lengths, dtype, seed):
+        rng = np.random.default_rng(seed)
+        p = workloads.scan_params(rng, T, D, N)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dtype).to(dev)
+        cu = torch.from_numpy(workloads.cu_seqlens(lengths)).to(dev)
+        return p, t, cu
+
+    # config 2: 1 x 512 tokens x 768 channels, fp32, no conv
+    p, t, cu = make(512, 768, 16, [512], torch.float32, 2)
+    f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    args = (t(p["x"]), t(p["dt"]), f32(p["a_log"]), t(p["B"]), t(p["C"]), f32(p["D"]),
+            t(p["z"]), cu, 768, 1, 16, 1)
+    c2 = {}
+    for name, ck in (("sequential", 0), ("chunked_auto", -1)):
+        c2[f"{name}_ms"] = round(_time_ms(torch, lambda: ops.selective_scan_fwd(
+            *args, chunk_tokens=ck), 20), 4)
+    bytes_ = 512 * 768 * 4 * 4 + 512 * 16 * 2 * 4 + 768 * 16 * 4 * 2
+    c2["bytes"] = bytes_
+    c2["chunk_tokens"] = 64
+    out["config2_batch1"] = c2
+
+    # one 32768-token prefill, d_inner 2048, N 16, conv 4, bf16
+    T, D = 32768, 2048
+    rng = np.random.default_rng(7)
+    x = torch.randn((T, D), device=dev).to(torch.bfloat16)
+    dt = (torch.randn((T, D), device=dev) * 0.5 - 2.0).to(torch.bfloat16)
+    z = torch.randn((T, D), device=dev).to(torch.bfloat16)
+    B = (torch.randn((T, 16), device=dev) * 0.25).to(torch.bfloat16)
+    C = (torch.randn((T, 16), device=dev) * 0.25).to(torch.bfloat16)
+    a_log = torch.randn((D, 16), device=dev)
+    Dk = torch.randn(D, device=dev)
+    cw = torch.randn((D, 4), device=dev) * 0.5
+    cb = torch.zeros(D, device=dev)
+    cu1 = torch.tensor([0, T], dtype=torch.int32, device=dev)
+    long = {}
+    for name, ck in (("sequential", 0), ("chunked_auto", -1)):
+        long[f"{name}_ms"] = round(_time_ms(torch, lambda: ops.conv_scan_fwd(
+            x, cw, cb, dt, a_log, B, C, Dk, z, cu1, D, 1, 16, 1, chunk_tokens=ck), 3), 4)
+    bytes_ = T * D * 2 * 4 + T * 16 * 2 * 2 + D * 16 * 4
+    long["bytes"] = bytes_
+    long["gbs_chunked"] = round(bytes_ / (long["chunked_auto_ms"] / 1e3) / 1e9, 1)
+    long["speedup"] = round(long["sequential_ms"] / long["chunked_auto_ms"], 2)
+    out["prefill_1x32768"] = long
+    del x, dt, z
+
+    # 256 sequences of 16-1024 tokens: the longest-first pre-pass against dispatch order
+    lengths = rng.integers(16, 1025, size=256)
+    T = int(lengths.sum())
+    cus = torch.from_numpy(workloads.cu_seqlens(lengths)).to(dev)
+    xs = torch.randn((T, D), device=dev).to(torch.bfloat16)
+    dts = (torch.randn((T, D), device=dev) * 0.5 - 2.0).to(torch.bfloat16)
+    zs = torch.randn((T, D), device=dev).to(torch.bfloat16)
+    Bs = (torch.randn((T, 16), device=dev) * 0.25).to(torch.bfloat16)
+    Cs = (torch.randn((T, 16), device=dev) * 0.25).to(torch.bfloat16)
+    mid = {"sequences": 256, "tokens": T}
+    mid["ordered_prepass_ms"] = round(_time_ms(torch, lambda: ops.conv_scan_fwd(
+        xs, cw, cb, dts, a_log, Bs, Cs, Dk, zs, cus, D, 1, 16, 1, chunk_tokens=0), 10), 4)
+    mid["unordered_ms"] = round(_time_ms(torch, lambda: ops.conv_scan_fwd(
+        xs, cw, cb, dts, a_log, Bs, Cs, Dk, zs, cus, D, 1, 16, 1, chunk_tokens=None), 10), 4)
+    out["ragged_256"] = mid
+    del xs, dts, zs
+
+    # 1024 sequences of 32-64 tokens (continuous batching), d_inner 2048, conv 4, bf16
+    lengths = rng.integers(32, 65, size=1024)
+    T = int(lengths.sum())
+    cus = torch.from_numpy(workloads.cu_seqlens(lengths)).to(dev)
+    xs = torch.randn((T, D), device=dev).to(torch.bfloat16)
+    dts = (torch.randn((T, D), device=dev) * 0.5 - 2.0).to(torch.bfloat16)
+    zs = torch.randn((T, D), device=dev).to(torch.bfloat16)
+    Bs = (torch.randn((T, 16), device=dev) * 0.25).to(torch.bfloat16)
+    Cs = (torch.randn((T, 16), device=dev) * 0.25).to(torch.bfloat16)
+    many = {"sequences": 1024, "tokens": T}
+    # the planned entry (dispatch order above 512 sequences) against the unplanned one
+    many["planned_ms"] = round(_time_ms(torch, lambda: ops.conv_scan_fwd(
+        xs, cw, cb, dts, a_log, Bs, Cs, Dk, zs, cus, D, 1, 16, 1, chunk_tokens=0), 10), 4)
+    many["unplanned_ms"] = round(_time_ms(torch, lambda: ops.conv_scan_fwd(
+        xs, cw, cb, dts, a_log, Bs, Cs, Dk, zs, cus, D, 1, 16, 1, chunk_tokens=None), 10), 4)
+    many["ordering_share"] = round((many["planned_ms"] - many["unplanned_ms"])
+                                   / many["planned_ms"], 4)
+    many["tokens_per_s"] = round(T / (many["planned_ms"] / 1e3), 1)
+    out["many_short_1024"] = many
+    return out
+
+
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def bench_linear_f32(torch, dev):
+    """BitLinear's float path (quantization-sensitive layers) on fp32 MFMA: the faithful
+    Mamba-2 block's stacked B / C / dt projections over config 4's 40796 tokens (K 1024,
+    N 2*16 + 32), and config 5's router gate (RMS_PERI, 8192 x 1024 -> 8)."""
+    from reimagined_amd import ops
+    out = {}
+    for name, (m, k, n, rms) in {"mamba2_bcdt_c4": (40796, 1024, 64, False),
+                                 "router_gate_c5": (8192, 1024, 8, True)}.items():
+        x = torch.randn((m, k), device=dev)
+        w = torch.randn((n, k), device=dev) / 32
+        y = torch.empty((m, n), device=dev)
+        ms = _time_ms(torch, lambda: ops.linear_f32(x, w, rms_input=rms, out=y), 20)
+        tf = 2.0 * m * n * k / (ms / 1e3) / 1e12
+        gbs = (m * k * 4 + n * k * 4 + m * n * 4) / (ms / 1e3) / 1e9
+        out[name] = {"shape": [m, k, n], "ms": round(ms, 4), "tflops": round(tf, 2),
+                     "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+                     "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def bench_ste_backward(torch, dev):
+    """The packed BitLinear STE backward at an in_proj-sized shape (M 4096 tokens, K 1024,
+    N 4096, RMS_PERI, magnitude): dW and d_act are 2*M*N*K fp32 MFMA flops each."""
+    from reimagined_amd import ops
+    m, k, n = 4096, 1024, 4096
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    packed, ws = ops.pack_ternary(w)
+    wt = torch.from_numpy(w).to(dev)
+    pk = torch.from_numpy(packed.view(np.int32)).to(dev)
+    x = torch.randn((m, k), device=dev)
+    q, s = ops.quantize_activations_bitnet(x, 8, rms_input=True)
+    g = torch.randn((m, n), device=dev)
+    mag = torch.ones(n, device=dev)
+    ms = _time_ms(torch, lambda: ops.bitlinear_ste_backward(x, q, s, wt, pk, ws, g, True, mag,
+                                                            True), 5)
+    flops = 2 * 2.0 * m * n * k
+    tf = flops / (ms / 1e3) / 1e12
+    return {"shape": [m, k, n], "ms": round(ms, 4), "tflops": round(tf, 2),
+            "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+
+
+def bench_gemv_published(torch, dev, reps=100):
+    """The reference's two published decode-GEMV shapes (M = 1; K x N = 1024 x 4096 and
+    4096 x 16384, docs/GPU_MODERNIZATION_RESULTS.md:95-105, bench_decode_gemv.cpp):
+      * rotated: grouped over enough distinct weight sets to exceed the 256 MB MALL, so the
+        kernel streams HBM (GB/s against peak);
+      * resident: back-to-back quantize + GEMV calls on one weight set, as the reference
+        measured (its figure is host wall time per call on an RX 7600): the stream time per
+        call from events here."""
+    from reimagined_amd import ops
+    from reimagined_amd._lib import call
+    from reimagined_amd.ops import _p, _stream
+    out = {}
+    rng = np.random.default_rng(17)
+    for k, n in ((1024, 4096), (4096, 16384)):
+        words = n * k // 16
+        sets = max(2, (512 << 20) // (words * 4))
+        packed = torch.randint(-2**31, 2**31 - 1, (sets, words), dtype=torch.int32, device=dev)
+        packed = (packed ^ ((packed & (packed >> 1) & 0x55555555) << 1)).contiguous()
+        views = ops.LinearViewArray([(packed[i], 1.0, k, n, None, None) for i in range(sets)], dev)
+        q = torch.from_numpy(rng.integers(-127, 128, size=(sets, 1, k)).astype(np.int8)).to(dev)
+        s = torch.full((sets, 1), 0.01, dtype=torch.float32, device=dev)
+        y = torch.empty((sets, 1, n), dtype=torch.float32, device=dev)
+        ms = _time_ms(torch, lambda: call("nsosx_grouped_gemv", views.ptr, sets, _p(q), k, _p(s),
+                                          1, 1, _p(y), n, 0, _stream()), 5)
+        bytes_ = sets * (n * k / 4 + k + n * 4)
+        gbs = bytes_ / (ms / 1e3) / 1e9
+        x = torch.randn((1, k), device=dev)
+        qw = torch.empty((1, k), dtype=torch.int8, device=dev)
+        sw = torch.empty(1, dtype=torch.float32, device=dev)
+        y1 = torch.empty((1, n), dtype=torch.float32, device=dev)
+        one = packed[0]
+
+        def fwd():
+            call("nsosx_bitlinear_forward", _p(x), 0, _p(one), 1.0, 1, k, n, 8, 0, None, None,
+                 _p(y1), 0, _p(qw), _p(sw), None, _stream())
+        res_ms = _time_ms(torch, fwd, reps)
+        out[f"k{k}_n{n}"] = {"rotated_sets": sets, "rotated_us_per_gemv": round(ms / sets * 1e3, 3),
+                             "rotated_gbs": round(gbs, 1),
+                             "rotated_frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                             "resident_quant_plus_gemv_us": round(res_ms * 1e3, 2)}
+        del packed, views
+    return out
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(params, inp, min_tokens=3000):
+    """The config-4 layer on the host CPU over the first sequences of the same batch (at least
+    `min_tokens` tokens).  in_proj and out_proj run the reference's own BitLinear::forward
+    (packed path: RMS_PERI with OpenMP, its AVX2 int8 GEMM single-threaded) from oracle/_ref
+    when that build is present; the causal conv and the scan, which the reference has no CPU
+    Mamba-1 [D, N] path for, run the oracle's sequential restatement (single-threaded)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import oracle as orc
+    from oracle import ref
     import torch
     r = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).float().numpy()
-    T = seq_tokens
+    cu_all = inp["cu_seqlens"]
+    S = int(np.searchsorted(cu_all, min_tokens)) if cu_all[-1] > min_tokens else len(cu_all) - 1
+    S = max(1, min(S, len(cu_all) - 1))
+    T = int(cu_all[S])
     x = r(inp["x"][:T])
     dt = r(inp["dt"][:T])
     B, C = r(inp["B"][:T]), r(inp["C"][:T])
-    cu = np.array([0, T], np.int32)
-    pin, wsi, _ = orc.pack_weights(params["w_in"])
-    pout, wso, _ = orc.pack_weights(params["w_out"])
+    cu = cu_all[:S + 1].astype(np.int32)
     di = params["w_out"].shape[1]
     n = params["a_log"].shape[1]
+    use_ref = ref.available()
+    stages = {}
+    if use_ref:
+        t_in, xz = ref.bitlinear_time_forward(params["w_in"], x, reps=1)
+    else:
+        pin, wsi, _ = orc.pack_weights(params["w_in"])
+        t0 = time.perf_counter()
+        xz = orc.bitlinear_forward(x, pin, wsi, 2 * di, rms_input=True)
+        t_in = time.perf_counter() - t0
+    stages["in_proj"] = {"s": round(t_in, 3), "kind": "reference" if use_ref else "port"}
     t0 = time.perf_counter()
-    xz = orc.bitlinear_forward(x, pin, wsi, 2 * di, rms_input=True)
     xc = orc.conv1d_causal(np.ascontiguousarray(xz[:, :di]), params["conv_w"], cu,
                            bias=params["conv_b"], silu_act=True)
     ys, _ = orc.selective_scan(xc, dt, params["a_log"], B, C, params["d_skip"],
                                np.ascontiguousarray(xz[:, di:]), cu, di, 1, n, 1)
-    orc.bitlinear_forward(ys, pout, wso, params["w_out"].shape[0], rms_input=True)
-    sec = time.perf_counter() - t0
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(T / sec, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"one sequence of {T} tokens through the config-4 layer (in_proj, conv, "
-                      f"scan, out_proj) in {sec:.2f} s; int8 GEMM and scan single-threaded as "
-                      f"in the reference, row quantization/RMSNorm OpenMP"}
+    t_scan = time.perf_counter() - t0
+    stages["conv_scan"] = {"s": round(t_scan, 3), "kind": "port", "threads": 1}
+    if use_ref:
+        t_out, _ = ref.bitlinear_time_forward(params["w_out"], ys, reps=1)
+    else:
+        pout, wso, _ = orc.pack_weights(params["w_out"])
+        t0 = time.perf_counter()
+        orc.bitlinear_forward(ys, pout, wso, params["w_out"].shape[0], rms_input=True)
+        t_out = time.perf_counter() - t0
+    stages["out_proj"] = {"s": round(t_out, 3), "kind": "reference" if use_ref else "port"}
+    sec = t_in + t_scan + t_out
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = int(omp) if omp and omp.isdigit() else (os.cpu_count() or 1)
+    # "reference" only when every stage ran the reference's own code; here the scan is the port
+    return {"value": round(T / sec, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "omp_num_threads": omp,
+            "stages": stages,
+            "sample": f"the first {S} sequences ({T} tokens) of the config-4 batch through the "
+                      f"layer in {sec:.2f} s: in_proj/out_proj by the reference's "
+                      f"BitLinear::forward ({'oracle/_ref build' if use_ref else 'oracle port'}; "
+                      f"RMSNorm and quantization on {threads} OpenMP threads, the AVX2 int8 "
+                      f"GEMM single-threaded), conv + scan by the oracle's sequential "
+                      f"restatement on 1 thread (the reference has no CPU Mamba-1 A[D,N] scan)"}
 
 
 def main():
@@ -467,6 +712,14 @@ def main():
         _log(f"mamba2 prefill {extra['mamba2_prefill']}")
         extra["mamba2_decode_step"] = bench_mamba2_decode(torch, dev)
         _log(f"mamba2 decode step {extra['mamba2_decode_step']}")
+        extra["scan_shapes"] = bench_scan_shapes(torch, dev)
+        _log(f"scan shapes {extra['scan_shapes']}")
+        extra["linear_f32"] = bench_linear_f32(torch, dev)
+        _log(f"linear f32 {extra['linear_f32']}")
+        extra["ste_backward"] = bench_ste_backward(torch, dev)
+        _log(f"ste backward {extra['ste_backward']}")
+        extra["gemv_published_shapes"] = bench_gemv_published(torch, dev)
+        _log(f"gemv published shapes {extra['gemv_published_shapes']}")
         sc = stages.get("conv_scan")
         if sc:
             _, work = layer_roofline(T, {"conv_scan": sc})

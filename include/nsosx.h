@@ -291,8 +291,9 @@ int nsosx_conv_scan_fwd(const void* x_raw, int64_t x_stride, const float* conv_w
 /* The scan (x_raw through the causal conv when conv_w != NULL, as
  * nsosx_conv_scan_fwd; else as nsosx_selective_scan_fwd) with a launch plan
  * built on the device:
- *   - more than 64 sequences: one pre-pass ranks them longest-first for
- *     dispatch (instead of a ranking in every workgroup);
+ *   - 65 to 512 sequences: one pre-pass ranks them longest-first for dispatch
+ *     (up to 64 each workgroup ranks them itself; above 512 they run in
+ *     dispatch order, no ranking at all);
  *   - chunk_tokens > 0 (>= 4): the time-chunked scan.  Every sequence splits
  *     into chunks of chunk_tokens tokens; a first pass runs each chunk's
  *     recurrence from zero and records its end state and summed delta, a
@@ -358,12 +359,15 @@ int nsosx_moe_route(const float* logits, int rows, int experts, int k, float* we
  * views[e]; the result goes to slot order y [slots, N] with the view's
  * epilogue and then, when squared_relu != 0, max(v,0)^2 (Tensor::squared_relu,
  * src/tensor.cpp:3209-3226).  act_scale is indexed like q.
- * offsets is a device array; max_rows_per_expert bounds the launch grid. */
+ * offsets is a device array.  max_rows_per_expert bounds any expert's rows;
+ * total_rows (offsets[experts], or an upper bound; 0 = unknown) lets the launch
+ * cover only the experts' real row tiles, found on the device from the offsets
+ * (without it every expert is given max_rows_per_expert rows of workgroups). */
 int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, int experts,
                                const int32_t* offsets, const int32_t* perm, int gather,
                                const int8_t* q, const float* act_scale, int K, int N,
-                               int max_rows_per_expert, int squared_relu, void* y, int y_dtype,
-                               void* stream);
+                               int max_rows_per_expert, int total_rows, int squared_relu,
+                               void* y, int y_dtype, void* stream);
 
 /* Weighted combine in ascending expert order (src/jamba.cpp:3947-3969):
  * out[r] = sum over the row's selected experts, lowest id first, of

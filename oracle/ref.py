@@ -1,10 +1,11 @@
 """numpy front end of oracle/_ref/libnsos_ref.so: the reference's own compiled operators.
 
-TEST INFRASTRUCTURE ONLY, and only where the reference tree is mounted (the
-library is built from its sources by `make -C oracle ref`).  tests/golden/
-gen_golden.py records these outputs as fixtures; the tests compare the oracle
-(and through it the GPU path) against those fixtures, so nothing at test time
-needs the reference itself.
+TEST INFRASTRUCTURE ONLY: the library is built from the reference's sources by
+`make -C oracle ref` where the reference tree is mounted.  tests/golden/
+gen_golden.py records its outputs as fixtures (the tests compare the oracle,
+and through it the GPU path, against those fixtures, so no test needs the
+reference itself), and bench.py's cpu_baseline leg times its BitLinear forward
+as the reference's CPU path when the built library is present.
 
 Every wrapper names the reference function it calls (paths under OXN/nsos/).
 """
@@ -47,6 +48,8 @@ def _load():
             "ref_bitlinear_forward": (_i, [_f32p, _i, _i, _f32p, _i, _i, _vp, _vp, _i, _f32p]),
             "ref_bitlinear_packed_backward": (_i, [_f32p, _i, _i, _f32p, _i, _i, _vp, _vp,
                                                    _f32p, _f32p, _f32p, _f32p, _vp, _vp]),
+            "ref_bitlinear_time_forward": (_i, [_f32p, _i, _i, _f32p, _i, _i, _i, _f32p,
+                                                ctypes.POINTER(ctypes.c_double)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -162,3 +165,16 @@ def bitlinear_packed_backward(w, x, grad, exact_linear: bool = False, magnitude=
     if dbias is not None:
         out["dbias"] = dbias
     return out
+
+
+def bitlinear_time_forward(w, x, exact_linear: bool = False, reps: int = 1):
+    """Seconds per BitLinear::forward call on the CPU packed path (one configured layer,
+    packing outside the timed loop) and the last output: the reference's own CPU hot path."""
+    w, x = _f32(w), _f32(x)
+    n, k = w.shape
+    m = x.shape[0]
+    y = np.empty((m, n), np.float32)
+    sec = ctypes.c_double()
+    _check(_load().ref_bitlinear_time_forward(w, n, k, x, m, int(exact_linear), int(reps), y,
+                                              ctypes.byref(sec)), "bitlinear_time_forward")
+    return sec.value, y

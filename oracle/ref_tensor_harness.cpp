@@ -8,6 +8,7 @@
 //
 // Every function returns 0 on success or -1 when the reference threw; the
 // message is then in ref_last_error().
+#include <chrono>
 #include <cstdint>
 #include <cstring>
 #include <exception>
@@ -149,6 +150,25 @@ int ref_bitlinear_packed_backward(const float* w, int N, int K, const float* x, 
     copy_out(bl.weight.grad, dW);
     if (dmag != nullptr) copy_out(bl.magnitude.grad, dmag);
     if (dbias != nullptr) copy_out(bl.bias.grad, dbias);
+  });
+}
+
+// Seconds per BitLinear::forward on the CPU packed path (RMS_PERI + magnitude,
+// or exact-linear), over `reps` calls on one configured layer (packing is done
+// once, outside the timed loop): the reference's own CPU hot path, for the
+// CPU baseline.  y receives the last call's output.
+int ref_bitlinear_time_forward(const float* w, int N, int K, const float* x, int M,
+                               int exact_linear, int reps, float* y, double* seconds) {
+  return guarded([&] {
+    BitLinear bl(K, N, false);
+    configure(bl, w, N, K, exact_linear, nullptr, nullptr, 1, 0);
+    Tensor in = host_tensor(x, {M, K});
+    Tensor out = bl.forward(in);  // warm (first-call allocations)
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int r = 0; r < reps; ++r) out = bl.forward(in);
+    const auto t1 = std::chrono::steady_clock::now();
+    *seconds = std::chrono::duration<double>(t1 - t0).count() / (reps > 0 ? reps : 1);
+    copy_out(out, y);
   });
 }
 

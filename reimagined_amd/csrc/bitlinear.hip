@@ -1700,16 +1700,39 @@ template <int YDT, bool GATHER, bool SQRELU>
 __global__ __launch_bounds__(kGemm3Threads, 2) void grouped_gemm3_kernel(
     const nsosx_linear_view* views, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ perm, const int8_t* __restrict__ q,
-    const float* __restrict__ act_scale, void* y, int ntn, int ntm, int experts) {
+    const float* __restrict__ act_scale, void* y, int ntn, int ntm, int experts, int compact) {
     extern __shared__ __align__(16) char smem3[];
-    // 1-D grid over (n tile, m tile, expert), n fastest; xcd_tile() hands each XCD a
-    // contiguous run, so the n tiles of one (expert, m tile) share its rows in one L2
+    // 1-D grid over (n tile, row tile), n fastest; xcd_tile() hands each XCD a
+    // contiguous run, so the n tiles of one (expert, m tile) share its rows in one L2.
+    // compact: the row tiles are the experts' real tiles in expert order (ntm is an
+    // upper bound on their count, sum ceil(rows_e / 128) <= ceil(total / 128) + E),
+    // found by walking the offsets; else ntm tiles per expert, most of them empty.
     int nt, rest;
-    xcd_tile(blockIdx.x, ntn, ntm * experts, nt, rest);
-    const int e = rest / ntm;
-    const int seg_begin = offsets[e];
-    const int seg_rows = offsets[e + 1] - seg_begin;
-    const int m0 = (rest % ntm) * kG3BM;
+    int e = -1, seg_begin = 0, seg_rows = 0, m0 = 0;
+    if (compact) {
+        xcd_tile(blockIdx.x, ntn, ntm, nt, rest);
+        int base = 0;
+        for (int j = 0; j < experts; ++j) {
+            const int b = offsets[j];
+            const int r = max(offsets[j + 1] - b, 0);
+            const int tj = (r + kG3BM - 1) / kG3BM;
+            if (rest < base + tj) {
+                e = j;
+                seg_begin = b;
+                seg_rows = r;
+                m0 = (rest - base) * kG3BM;
+                break;
+            }
+            base += tj;
+        }
+        if (e < 0) return;
+    } else {
+        xcd_tile(blockIdx.x, ntn, ntm * experts, nt, rest);
+        e = rest / ntm;
+        seg_begin = offsets[e];
+        seg_rows = offsets[e + 1] - seg_begin;
+        m0 = (rest % ntm) * kG3BM;
+    }
     if (m0 >= seg_rows) return;
     const nsosx_linear_view v = views[e];
     const int n0 = nt * kG3BN;
@@ -2258,25 +2281,31 @@ extern "C" int nsosx_grouped_gemv(const nsosx_linear_view* views_dev, int groups
 extern "C" int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, int experts,
                                           const int32_t* offsets, const int32_t* perm, int gather,
                                           const int8_t* q, const float* act_scale, int K, int N,
-                                          int max_rows_per_expert, int squared_relu, void* y,
-                                          int y_dtype, void* stream) {
+                                          int max_rows_per_expert, int total_rows,
+                                          int squared_relu, void* y, int y_dtype, void* stream) {
     if (!views_dev || !offsets || !q || !act_scale || !y || (gather && !perm))
         return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm: null pointer");
-    if (experts <= 0 || experts > 65535 || K <= 0 || K % 16 || N <= 0 || max_rows_per_expert < 0)
+    if (experts <= 0 || experts > 65535 || K <= 0 || K % 16 || N <= 0 || max_rows_per_expert < 0 ||
+        total_rows < 0)
         return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm: bad shape");
     if (!valid_dtype(y_dtype)) return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm: bad dtype");
     if (max_rows_per_expert == 0) return NSOSX_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const dim3 grid2((N + kBN2 - 1) / kBN2, (max_rows_per_expert + kBM2 - 1) / kBM2, experts);
-    const int ntn3 = (N + kG3BN - 1) / kG3BN, ntm3 = (max_rows_per_expert + kG3BM - 1) / kG3BM;
-    if ((int64_t)ntn3 * ntm3 * experts > 0x7fffffff)
+    const int ntn3 = (N + kG3BN - 1) / kG3BN;
+    // with the total row count the grid covers only the real row tiles (found on the
+    // device from the offsets); without it, every expert gets max_rows_per_expert rows
+    const int compact = total_rows > 0 && experts <= 1024 ? 1 : 0;
+    const int ntm3 = compact ? (total_rows + kG3BM - 1) / kG3BM + experts
+                             : (max_rows_per_expert + kG3BM - 1) / kG3BM;
+    if ((int64_t)ntn3 * ntm3 * (compact ? 1 : experts) > 0x7fffffff)
         return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm: too many tiles for one launch");
-    const dim3 grid3(ntn3 * ntm3 * experts);
+    const dim3 grid3(ntn3 * ntm3 * (compact ? 1 : experts));
 #define NSOSX_GGEMM(YDT, G, S)                                                                  \
     if (K % kG3BK == 0)                                                                         \
         hipLaunchKernelGGL((grouped_gemm3_kernel<YDT, G, S>), grid3, dim3(kGemm3Threads),        \
                            kGemm3Smem, st, views_dev, offsets, perm, q, act_scale, y, ntn3,     \
-                           ntm3, experts);                                                      \
+                           ntm3, experts, compact);                                             \
     else                                                                                        \
         hipLaunchKernelGGL((grouped_gemm2_kernel<YDT, G, S>), grid2, dim3(kGemm2Threads),        \
                            kGemm2Smem, st, views_dev, offsets, perm, q, act_scale, y);

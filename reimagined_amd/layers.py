@@ -217,14 +217,14 @@ class MoEFFN:
              _p(b["route_ws"]), st)
         call("nsosx_quantize_act_i8", _p(x), ops._dt(x), rows, self.d_model, 8,
              int(self.rms_input), _p(b["q1"]), _p(b["s1"]), _p(b["r1"]), st)
-        call("nsosx_grouped_ternary_gemm", self.up_views.ptr, e, _p(b["offsets"]), _p(b["perm"]),
-             1, _p(b["q1"]), _p(b["s1"]), self.d_model, self.d_ff, rows, 1, _p(b["h"]),
-             _DT[self.hidden_dtype], st)
         slots = rows * k
+        call("nsosx_grouped_ternary_gemm", self.up_views.ptr, e, _p(b["offsets"]), _p(b["perm"]),
+             1, _p(b["q1"]), _p(b["s1"]), self.d_model, self.d_ff, rows, slots, 1, _p(b["h"]),
+             _DT[self.hidden_dtype], st)
         call("nsosx_quantize_act_i8", _p(b["h"]), _DT[self.hidden_dtype], slots, self.d_ff, 8,
              int(self.rms_input), _p(b["q2"]), _p(b["s2"]), _p(b["r2"]), st)
         call("nsosx_grouped_ternary_gemm", self.down_views.ptr, e, _p(b["offsets"]), None, 0,
-             _p(b["q2"]), _p(b["s2"]), self.d_ff, self.d_model, rows, 0, _p(b["o"]),
+             _p(b["q2"]), _p(b["s2"]), self.d_ff, self.d_model, rows, slots, 0, _p(b["o"]),
              _DT[torch.float32], st)
         out = torch.empty((rows, self.d_model), dtype=out_dtype or x.dtype, device=x.device)
         call("nsosx_moe_combine", _p(b["o"]), _DT[torch.float32], _p(b["slot_of"]),

@@ -449,8 +449,12 @@ def moe_route(logits: torch.Tensor, k: int = 2, select_only: bool = False) -> di
 
 def grouped_ternary_gemm(views: LinearViewArray, offsets, perm, q, act_scale, n_out: int,
                          max_rows_per_expert: int, squared_relu: bool = False,
-                         gather: bool = True, out_dtype=torch.float32) -> torch.Tensor:
-    """Per-expert ternary GEMMs over slot segments -> y [slots, n_out] in slot order."""
+                         gather: bool = True, out_dtype=torch.float32,
+                         total_rows: int | None = None) -> torch.Tensor:
+    """Per-expert ternary GEMMs over slot segments -> y [slots, n_out] in slot order.
+
+    total_rows: an upper bound on offsets[E] (default: the slot count) so the launch covers
+    only the real row tiles; 0 launches max_rows_per_expert rows of tiles per expert."""
     _dev(offsets, "offsets", torch.int32)
     if gather:
         _dev(perm, "perm", torch.int32)
@@ -459,8 +463,9 @@ def grouped_ternary_gemm(views: LinearViewArray, offsets, perm, q, act_scale, n_
     slots = int(perm.numel()) if gather else q.shape[0]
     k = q.shape[1]
     y = torch.empty((slots, n_out), dtype=out_dtype, device=q.device)
+    total = slots if total_rows is None else int(total_rows)
     call("nsosx_grouped_ternary_gemm", views.ptr, views.count, _p(offsets), _p(perm), int(gather),
-         _p(q), _p(act_scale), k, n_out, max_rows_per_expert, int(squared_relu), _p(y),
+         _p(q), _p(act_scale), k, n_out, max_rows_per_expert, total, int(squared_relu), _p(y),
          _DT[out_dtype], _stream())
     return y
 

@@ -238,12 +238,14 @@ def test_grouped_gemm_segments(dev, orc, gather, sqrelu, out_dtype):
     views = ops.LinearViewArray(entries, dev)
     qd, sd = torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev)
     offd, permd = torch.from_numpy(offsets).to(dev), torch.from_numpy(perm).to(dev)
+    # compact (the real row tiles from the offsets) and the full per-expert grid
+    total = slots if (gather + sqrelu) % 2 == 0 else 0
     if gather:
         y = ops.grouped_ternary_gemm(views, offd, permd, qd, sd, N, max(counts), sqrelu, True,
-                                     out_dtype)
+                                     out_dtype, total_rows=total)
     else:
         y = ops.grouped_ternary_gemm(views, offd, None, qd[:slots], sd[:slots], N, max(counts),
-                                     sqrelu, False, out_dtype)
+                                     sqrelu, False, out_dtype, total_rows=total)
     got = y.float().cpu().numpy()
     for e in range(E):
         lo, hi = int(offsets[e]), int(offsets[e + 1])

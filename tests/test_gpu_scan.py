@@ -345,13 +345,15 @@ def test_chunked_scan_auto_long_prefill_bf16(dev, orc):
     np.testing.assert_allclose(fin.cpu().numpy(), wfin, rtol=1e-4, atol=1e-5)
 
 
-def test_order_prepass_many_short_sequences(dev, orc):
-    """1024 sequences of 32-64 tokens (a continuous-batching step): the planned entry ranks
-    them once in a pre-pass; ordering changes only the schedule, so its outputs equal the
-    unplanned entry's bit for bit, and both match the oracle."""
-    rng = np.random.default_rng(55)
+@pytest.mark.parametrize("count", [300, 1024])
+def test_order_prepass_many_short_sequences(dev, orc, count):
+    """Hundreds of sequences of 32-64 tokens (a continuous-batching step): with 300 the planned
+    entry ranks them once in a pre-pass, with 1024 it keeps dispatch order; ordering changes
+    only the schedule, so its outputs equal the unplanned entry's bit for bit, and both match
+    the oracle."""
+    rng = np.random.default_rng(55 + count)
     H, P, N, G = 128, 1, 16, 1
-    lengths = rng.integers(32, 65, size=1024)
+    lengths = rng.integers(32, 65, size=count)
     cu = _cu(lengths)
     inp = _inputs(rng, int(cu[-1]), H, P, N, G)
     a = _scan_args(dev, inp, cu, torch.float32, True)
