@@ -150,6 +150,23 @@ int nsosx_ternary_gemm_path(const int8_t* q, const float* act_scale, const uint3
                             const float* bias, void* y, int y_dtype, int32_t* acc_out,
                             int path, void* stream);
 
+/* The packed weights of one [N, K] matrix rewritten into the layout the
+ * prefill MFMA GEMM decodes fastest (an upload-time step, like the reference's
+ * repack of its packed cache, src/bitlinear.cpp:628-643): within each 16-code
+ * word, code k moves to bits 8 (k % 4) + 2 (k / 4), and the reserved code 3
+ * becomes 1 (both decode to 0).  Words stay row-major, K / 16 per row.
+ * packed, out: device uint32 [n_words] (distinct buffers). */
+int nsosx_pack_mfma_layout(const uint32_t* packed, int64_t n_words, uint32_t* out,
+                           void* stream);
+
+/* nsosx_ternary_gemm's contract on weights in the MFMA layout above, always
+ * on the int8 MFMA GEMM (the prefill shape; K % 128 == 0).  Same results bit
+ * for bit as nsosx_ternary_gemm on the reference-layout words. */
+int nsosx_ternary_gemm_mfma(const int8_t* q, const float* act_scale, const uint32_t* packed_mfma,
+                            float weight_scale, int M, int K, int N, const float* magnitude,
+                            const float* bias, void* y, int y_dtype, int32_t* acc_out,
+                            void* stream);
+
 /* bitnet_gemm_158bit_gpu (include/bitnet_gpu_dispatch.h:46-51,
  * src/bitnet_gpu_dispatch.cpp:65-174): quantize x then ternary GEMM.
  * q_workspace: int8 [M, K]; scale_workspace: f32 [M];
@@ -368,6 +385,16 @@ int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, int experts,
                                const int8_t* q, const float* act_scale, int K, int N,
                                int max_rows_per_expert, int total_rows, int squared_relu,
                                void* y, int y_dtype, void* stream);
+
+/* nsosx_grouped_ternary_gemm on views whose packed words are in the MFMA
+ * layout (nsosx_pack_mfma_layout), launching only the experts' real row tiles
+ * (total_rows: offsets[experts] or an upper bound).  K % 128 == 0, <= 1024
+ * experts.  Same results bit for bit. */
+int nsosx_grouped_ternary_gemm_mfma(const nsosx_linear_view* views_dev, int experts,
+                                    const int32_t* offsets, const int32_t* perm, int gather,
+                                    const int8_t* q, const float* act_scale, int K, int N,
+                                    int total_rows, int squared_relu, void* y, int y_dtype,
+                                    void* stream);
 
 /* Weighted combine in ascending expert order (src/jamba.cpp:3947-3969):
  * out[r] = sum over the row's selected experts, lowest id first, of

@@ -38,6 +38,10 @@ SIGNATURES = {
     "nsosx_bitlinear_ste_backward_workspace": (_i64, [_i, _i, _i, _i]),
     "nsosx_bitlinear_ste_backward": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _f, _i, _i, _i, _i, _vp,
                                           _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "nsosx_pack_mfma_layout": (_i, [_vp, _i64, _vp, _vp]),
+    "nsosx_ternary_gemm_mfma": (_i, [_vp, _vp, _vp, _f, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp]),
+    "nsosx_grouped_ternary_gemm_mfma": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i,
+                                             _vp, _i, _vp]),
     "nsosx_grouped_gemv": (_i, [_vp, _i, _vp, _i64, _vp, _i64, _i, _vp, _i64, _i, _vp]),
     "nsosx_conv1d_causal": (_i, [_vp, _i, _i64, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i,
                                  _vp]),

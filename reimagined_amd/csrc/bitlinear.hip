@@ -1382,6 +1382,7 @@ __device__ __forceinline__ lds_void_t* lds_ptr(const char* p) {
 // One 128-deep K stage of the 256 x 128 block from LDS stage `st`: each lane
 // reads its two 16-byte weight word groups once, then per MFMA step ks decodes
 // one word per n-tile and reads one 16-byte activation chunk per m-tile.
+template <bool SWZ>
 __device__ __forceinline__ void gemm3_stage(const char* st, int wave, int lane, v16i (&acc)[2][4]) {
     const int g = lane >> 5;
     const int li = lane & 31;
@@ -1409,8 +1410,12 @@ __device__ __forceinline__ void gemm3_stage(const char* st, int wave, int lane, 
             const uint32_t words[4] = {wq[nb].x, wq[nb].y, wq[nb].z, wq[nb].w};
             uint32_t wv[4], wt[4];
             unpack_word(words[ks], wv);
-            transpose16(wv, wt);                            // unpack order -> natural order
-            aw[nb] = v4i{(int)wt[0], (int)wt[1], (int)wt[2], (int)wt[3]};
+            if constexpr (SWZ) {
+                aw[nb] = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+            } else {
+                transpose16(wv, wt);                        // unpack order -> natural order
+                aw[nb] = v4i{(int)wt[0], (int)wt[1], (int)wt[2], (int)wt[3]};
+            }
         }
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
@@ -1579,7 +1584,7 @@ __device__ __forceinline__ void gemm3_epilogue_rows(const GemmProblem& pb,
     }
 }
 
-template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU>
+template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU, bool SWZ = false>
 __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* __restrict__ q,
                                            const float* __restrict__ act_scale,
                                            const int32_t* __restrict__ perm, int seg_begin,
@@ -1641,7 +1646,7 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (kt + 2 < KT) issue(kt + 2);
-        gemm3_stage(smem + (kt % kG3Stages) * kG3StageBytes, wave, lane, acc);
+        gemm3_stage<SWZ>(smem + (kt % kG3Stages) * kG3StageBytes, wave, lane, acc);
     }
 
     if constexpr (YDT == NSOSX_BF16 && !ACC_OUT) {
@@ -1740,6 +1745,74 @@ __global__ __launch_bounds__(kGemm3Threads, 2) void grouped_gemm3_kernel(
     GemmProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
     gemm3_tile<YDT, false, GATHER, SQRELU>(pb, q, act_scale, perm, seg_begin, seg_rows, n0, m0, y,
                                            nullptr, smem3);
+}
+
+// ===========================================================================
+// The prefill GEMM on weights repacked into the MFMA layout
+// (nsosx_pack_mfma_layout): inside each 16-code word, code k sits at bits
+// 8 (k % 4) + 2 (k / 4), and the reserved code 3 is stored as 1.  A word then
+// unpacks with one shift, mask and table lookup per output dword straight into
+// natural k order; the reference layout needs a further 4x4 byte transpose
+// per word (eight more VALU per decoded word, 2-5 % of the GEMM's time).
+// gemm3's block, ring and DMA otherwise.
+// ===========================================================================
+template <int YDT, bool ACC_OUT>
+__global__ __launch_bounds__(kGemm3Threads, 2) void gemm3_mfma_kernel(GemmProblem pb,
+                                                                 const int8_t* __restrict__ q,
+                                                                 const float* __restrict__ act_scale,
+                                                                 int M, void* y, int32_t* acc_out) {
+    extern __shared__ __align__(16) char smem4[];
+    const int ntn = (pb.N + kG3BN - 1) / kG3BN;
+    const int ntm = (M + kG3BM - 1) / kG3BM;
+    int nt, mt;
+    xcd_tile(blockIdx.x, ntn, ntm, nt, mt);
+    gemm3_tile<YDT, ACC_OUT, false, false, true>(pb, q, act_scale, nullptr, 0, M, nt * kG3BN,
+                                                 mt * kG3BM, y, acc_out, smem4);
+}
+
+template <int YDT, bool GATHER, bool SQRELU>
+__global__ __launch_bounds__(kGemm3Threads, 2) void grouped_gemm3_mfma_kernel(
+    const nsosx_linear_view* views, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ perm, const int8_t* __restrict__ q,
+    const float* __restrict__ act_scale, void* y, int ntn, int ntm, int experts) {
+    extern __shared__ __align__(16) char smem4[];
+    // compact row tiles, as grouped_gemm3_kernel's with total_rows
+    int nt, rest;
+    xcd_tile(blockIdx.x, ntn, ntm, nt, rest);
+    int e = -1, seg_begin = 0, seg_rows = 0, m0 = 0, base = 0;
+    for (int j = 0; j < experts; ++j) {
+        const int b = offsets[j];
+        const int r = max(offsets[j + 1] - b, 0);
+        const int tj = (r + kG3BM - 1) / kG3BM;
+        if (rest < base + tj) {
+            e = j;
+            seg_begin = b;
+            seg_rows = r;
+            m0 = (rest - base) * kG3BM;
+            break;
+        }
+        base += tj;
+    }
+    if (e < 0 || m0 >= seg_rows) return;
+    const nsosx_linear_view v = views[e];
+    const int n0 = nt * kG3BN;
+    if (n0 >= v.outputs) return;
+    GemmProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
+    gemm3_tile<YDT, false, GATHER, SQRELU, true>(pb, q, act_scale, perm, seg_begin, seg_rows, n0,
+                                                 m0, y, nullptr, smem4);
+}
+
+// Reference layout -> MFMA layout, word by word (code 3 -> 1, both decode to 0).
+__global__ __launch_bounds__(256) void pack_mfma_kernel(const uint32_t* __restrict__ src,
+                                                        int64_t n, uint32_t* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    uint32_t w = src[i];
+    w ^= (w & (w >> 1) & 0x55555555u) << 1;  // code 3 (11) -> 1 (01)
+    uint32_t o = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) o |= ((w >> (2 * k)) & 3u) << (8 * (k & 3) + 2 * (k >> 2));
+    dst[i] = o;
 }
 
 template <int YDT, bool GATHER, bool SQRELU>
@@ -2318,6 +2391,73 @@ extern "C" int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, in
     }
 #undef NSOSX_GGEMM
     return check_launch("grouped_ternary_gemm");
+}
+
+extern "C" int nsosx_pack_mfma_layout(const uint32_t* packed, int64_t n_words, uint32_t* out,
+                                      void* stream) {
+    if (!packed || !out || n_words < 0)
+        return fail(NSOSX_ERR_INVALID, "pack_mfma_layout: bad argument");
+    if (n_words == 0) return NSOSX_OK;
+    hipLaunchKernelGGL(pack_mfma_kernel, dim3((unsigned)((n_words + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), packed, n_words, out);
+    return check_launch("pack_mfma_layout");
+}
+
+extern "C" int nsosx_ternary_gemm_mfma(const int8_t* q, const float* act_scale,
+                                       const uint32_t* packed_mfma, float weight_scale, int M,
+                                       int K, int N, const float* magnitude, const float* bias,
+                                       void* y, int y_dtype, int32_t* acc_out, void* stream) {
+    int rc = check_gemm_args(q, act_scale, packed_mfma, weight_scale, M, K, N, y, y_dtype, acc_out);
+    if (rc) return rc;
+    if (K % kG3BK != 0)
+        return fail(NSOSX_ERR_INVALID, "ternary_gemm_mfma: K must be a multiple of 128");
+    const int tiles = ((N + kG3BN - 1) / kG3BN) * ((M + kG3BM - 1) / kG3BM);
+    GemmProblem pb{packed_mfma, magnitude, bias, weight_scale, N, K};
+    hipStream_t st = static_cast<hipStream_t>(stream);
+#define NSOSX_GM(YDT, ACC)                                                                    \
+    hipLaunchKernelGGL((gemm3_mfma_kernel<YDT, ACC>), dim3(tiles), dim3(kGemm3Threads), kGemm3Smem, \
+                       st, pb, q, act_scale, M, y, acc_out);
+    if (y_dtype == NSOSX_F32) {
+        if (acc_out) { NSOSX_GM(NSOSX_F32, true) } else { NSOSX_GM(NSOSX_F32, false) }
+    } else {
+        if (acc_out) { NSOSX_GM(NSOSX_BF16, true) } else { NSOSX_GM(NSOSX_BF16, false) }
+    }
+#undef NSOSX_GM
+    return check_launch("ternary_gemm_mfma");
+}
+
+extern "C" int nsosx_grouped_ternary_gemm_mfma(const nsosx_linear_view* views_dev, int experts,
+                                               const int32_t* offsets, const int32_t* perm,
+                                               int gather, const int8_t* q,
+                                               const float* act_scale, int K, int N,
+                                               int total_rows, int squared_relu, void* y,
+                                               int y_dtype, void* stream) {
+    if (!views_dev || !offsets || !q || !act_scale || !y || (gather && !perm))
+        return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm_mfma: null pointer");
+    if (experts <= 0 || experts > 1024 || K <= 0 || K % kG3BK || N <= 0 || total_rows < 0)
+        return fail(NSOSX_ERR_INVALID,
+                    "grouped_ternary_gemm_mfma: bad shape (K % 128 == 0, <= 1024 experts)");
+    if (!valid_dtype(y_dtype))
+        return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm_mfma: bad dtype");
+    if (total_rows == 0) return NSOSX_OK;
+    const int ntn = (N + kG3BN - 1) / kG3BN;
+    const int ntm = (total_rows + kG3BM - 1) / kG3BM + experts;
+    if ((int64_t)ntn * ntm > 0x7fffffff)
+        return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm_mfma: too many tiles");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+#define NSOSX_GGM(YDT, G, S)                                                                     \
+    hipLaunchKernelGGL((grouped_gemm3_mfma_kernel<YDT, G, S>), dim3(ntn * ntm), dim3(kGemm3Threads),   \
+                       kGemm3Smem, st, views_dev, offsets, perm, q, act_scale, y, ntn, ntm,       \
+                       experts);
+    if (y_dtype == NSOSX_F32) {
+        if (gather) { if (squared_relu) { NSOSX_GGM(NSOSX_F32, true, true) } else { NSOSX_GGM(NSOSX_F32, true, false) } }
+        else { if (squared_relu) { NSOSX_GGM(NSOSX_F32, false, true) } else { NSOSX_GGM(NSOSX_F32, false, false) } }
+    } else {
+        if (gather) { if (squared_relu) { NSOSX_GGM(NSOSX_BF16, true, true) } else { NSOSX_GGM(NSOSX_BF16, true, false) } }
+        else { if (squared_relu) { NSOSX_GGM(NSOSX_BF16, false, true) } else { NSOSX_GGM(NSOSX_BF16, false, false) } }
+    }
+#undef NSOSX_GGM
+    return check_launch("grouped_ternary_gemm_mfma");
 }
 
 extern "C" int nsosx_find_reserved_code(const uint32_t* packed, int64_t n_codes, int64_t* first_bad,

@@ -36,6 +36,7 @@ class BitLinear:
         self.out_features, self.in_features = w_float.shape
         packed, ws = ops.pack_ternary(w_float)
         self.packed = torch.from_numpy(packed.view(np.int32)).to(device)
+        self.packed_mfma = self._mfma_layout()
         self.weight_scale = ws
         self.bits = bits
         self.rms_input = rms_input
@@ -43,6 +44,22 @@ class BitLinear:
             magnitude, dtype=torch.float32).to(device)
         self.bias = None if bias is None else torch.as_tensor(bias, dtype=torch.float32).to(device)
         self._ws = {}
+
+    def _mfma_layout(self):
+        """The prefill GEMM's copy of the weights (MFMA layout), when K % 128 == 0."""
+        return ops.pack_mfma_layout(self.packed) if self.in_features % 128 == 0 else None
+
+    def gemm(self, q, s, m, y, st, magnitude=None, bias=None):
+        """The ternary GEMM of m rows of codes into y: the MFMA-layout prefill GEMM above
+        128 rows, else the dispatching entry (GEMV / skinny / small-M MFMA kernels)."""
+        if self.packed_mfma is not None and m > 128:
+            call("nsosx_ternary_gemm_mfma", _p(q), _p(s), _p(self.packed_mfma),
+                 self.weight_scale, m, self.in_features, self.out_features, _p(magnitude),
+                 _p(bias), _p(y), _DT[y.dtype], None, st)
+        else:
+            call("nsosx_ternary_gemm", _p(q), _p(s), _p(self.packed), self.weight_scale, m,
+                 self.in_features, self.out_features, _p(magnitude), _p(bias), _p(y),
+                 _DT[y.dtype], None, st)
 
     @classmethod
     def from_packed(cls, packed_u32: np.ndarray, weight_scale: float, out_features: int,
@@ -56,6 +73,7 @@ class BitLinear:
         bad = ops.find_reserved_code(self.packed, out_features * in_features)
         if bad >= 0:
             raise ValueError(f"packed weights hold the reserved code 3 at index {bad}")
+        self.packed_mfma = self._mfma_layout()
         self.weight_scale = float(weight_scale)
         self.bits = kw.get("bits", 8)
         self.rms_input = kw.get("rms_input", True)
@@ -85,9 +103,7 @@ class BitLinear:
              int(self.rms_input), _p(qw), _p(sw), _p(rw), st)
         if marker:
             marker("quant")
-        call("nsosx_ternary_gemm", _p(qw), _p(sw), _p(self.packed), self.weight_scale, m,
-             self.in_features, self.out_features, _p(self.magnitude), _p(self.bias), _p(y),
-             _DT[y.dtype], None, st)
+        self.gemm(qw, sw, m, y, st, self.magnitude, self.bias)
         if marker:
             marker("gemm")
         return y
@@ -97,9 +113,9 @@ class BitLinear:
                         device=x.device)
         return self.forward_into(x, y)
 
-    def view_entry(self):
-        return (self.packed, self.weight_scale, self.in_features, self.out_features,
-                self.magnitude, self.bias)
+    def view_entry(self, mfma: bool = False):
+        return (self.packed_mfma if mfma else self.packed, self.weight_scale, self.in_features,
+                self.out_features, self.magnitude, self.bias)
 
 
 class HybridMambaLayer:
@@ -176,6 +192,13 @@ class MoEFFN:
         self.hidden_dtype = hidden_dtype
         self.up_views = ops.LinearViewArray([e.view_entry() for e in self.up], device)
         self.down_views = ops.LinearViewArray([e.view_entry() for e in self.down], device)
+        # the prefill GEMMs read the MFMA-layout copies (K % 128 == 0); the sparse decode's
+        # GEMVs the reference layout
+        self.mfma = all(e.packed_mfma is not None for e in self.up + self.down)
+        if self.mfma:
+            self.up_views_mfma = ops.LinearViewArray([e.view_entry(True) for e in self.up], device)
+            self.down_views_mfma = ops.LinearViewArray([e.view_entry(True) for e in self.down],
+                                                       device)
         self._buf = {}
 
     def _buffers(self, rows: int, device):
@@ -218,14 +241,24 @@ class MoEFFN:
         call("nsosx_quantize_act_i8", _p(x), ops._dt(x), rows, self.d_model, 8,
              int(self.rms_input), _p(b["q1"]), _p(b["s1"]), _p(b["r1"]), st)
         slots = rows * k
-        call("nsosx_grouped_ternary_gemm", self.up_views.ptr, e, _p(b["offsets"]), _p(b["perm"]),
-             1, _p(b["q1"]), _p(b["s1"]), self.d_model, self.d_ff, rows, slots, 1, _p(b["h"]),
-             _DT[self.hidden_dtype], st)
+        if self.mfma:
+            call("nsosx_grouped_ternary_gemm_mfma", self.up_views_mfma.ptr, e, _p(b["offsets"]),
+                 _p(b["perm"]), 1, _p(b["q1"]), _p(b["s1"]), self.d_model, self.d_ff, slots, 1,
+                 _p(b["h"]), _DT[self.hidden_dtype], st)
+        else:
+            call("nsosx_grouped_ternary_gemm", self.up_views.ptr, e, _p(b["offsets"]),
+                 _p(b["perm"]), 1, _p(b["q1"]), _p(b["s1"]), self.d_model, self.d_ff, rows, slots,
+                 1, _p(b["h"]), _DT[self.hidden_dtype], st)
         call("nsosx_quantize_act_i8", _p(b["h"]), _DT[self.hidden_dtype], slots, self.d_ff, 8,
              int(self.rms_input), _p(b["q2"]), _p(b["s2"]), _p(b["r2"]), st)
-        call("nsosx_grouped_ternary_gemm", self.down_views.ptr, e, _p(b["offsets"]), None, 0,
-             _p(b["q2"]), _p(b["s2"]), self.d_ff, self.d_model, rows, slots, 0, _p(b["o"]),
-             _DT[torch.float32], st)
+        if self.mfma:
+            call("nsosx_grouped_ternary_gemm_mfma", self.down_views_mfma.ptr, e, _p(b["offsets"]),
+                 None, 0, _p(b["q2"]), _p(b["s2"]), self.d_ff, self.d_model, slots, 0, _p(b["o"]),
+                 _DT[torch.float32], st)
+        else:
+            call("nsosx_grouped_ternary_gemm", self.down_views.ptr, e, _p(b["offsets"]), None, 0,
+                 _p(b["q2"]), _p(b["s2"]), self.d_ff, self.d_model, rows, slots, 0, _p(b["o"]),
+                 _DT[torch.float32], st)
         out = torch.empty((rows, self.d_model), dtype=out_dtype or x.dtype, device=x.device)
         call("nsosx_moe_combine", _p(b["o"]), _DT[torch.float32], _p(b["slot_of"]),
              _p(b["selected"]), _p(b["weights"]), rows, e, k, self.d_model, _p(out),
@@ -387,9 +420,7 @@ class Mamba2Block:
             xv, z = (torch.empty((m, self.inner), dtype=self.dtype, device=u.device)
                      for _ in range(2))
             for p, out in zip(self.xz, (xv, z)):
-                call("nsosx_ternary_gemm", _p(q), _p(s), _p(p.packed), p.weight_scale, m,
-                     p.in_features, p.out_features, None, None, _p(out), _DT[self.dtype],
-                     None, st)
+                p.gemm(q, s, m, out, st)
         sens = ops.linear_f32(u, self.w_sens, bias=self.b_sens, out_dtype=self.dtype)
         g = self.gs
         return [xv, z, sens[:, :g], sens[:, g:2 * g], sens[:, 2 * g:].contiguous()]

@@ -134,6 +134,31 @@ def ternary_gemm(q: torch.Tensor, act_scale: torch.Tensor, packed: torch.Tensor,
     return y
 
 
+def pack_mfma_layout(packed: torch.Tensor) -> torch.Tensor:
+    """The prefill GEMM's weight layout (a device repack of reference-layout words)."""
+    _dev(packed, "packed")
+    out = torch.empty_like(packed)
+    call("nsosx_pack_mfma_layout", _p(packed), packed.numel(), _p(out), _stream())
+    return out
+
+
+def ternary_gemm_mfma(q: torch.Tensor, act_scale: torch.Tensor, packed_mfma: torch.Tensor,
+                      ws: float, n_out: int, magnitude=None, bias=None,
+                      out_dtype=torch.float32, want_acc: bool = False):
+    """ternary_gemm on MFMA-layout weights (the prefill MFMA GEMM, K % 128 == 0)."""
+    _dev(q, "q", torch.int8)
+    _dev(act_scale, "act_scale", torch.float32)
+    _dev(packed_mfma, "packed_mfma")
+    _opt(magnitude, "magnitude")
+    _opt(bias, "bias")
+    m, k = q.shape
+    y = torch.empty((m, n_out), dtype=out_dtype, device=q.device)
+    acc = torch.empty((m, n_out), dtype=torch.int32, device=q.device) if want_acc else None
+    call("nsosx_ternary_gemm_mfma", _p(q), _p(act_scale), _p(packed_mfma), ws, m, k, n_out,
+         _p(magnitude), _p(bias), _p(y), _DT[out_dtype], _p(acc), _stream())
+    return (y, acc) if want_acc else y
+
+
 def bitnet_gemm_158bit_gpu(x: torch.Tensor, packed: torch.Tensor, weight_scale: float, M: int,
                            K: int, N: int, precision_bits: int = 8, magnitude=None, bias=None,
                            rms_input: bool = False, out_dtype=torch.float32) -> torch.Tensor:
@@ -466,6 +491,24 @@ def grouped_ternary_gemm(views: LinearViewArray, offsets, perm, q, act_scale, n_
     total = slots if total_rows is None else int(total_rows)
     call("nsosx_grouped_ternary_gemm", views.ptr, views.count, _p(offsets), _p(perm), int(gather),
          _p(q), _p(act_scale), k, n_out, max_rows_per_expert, total, int(squared_relu), _p(y),
+         _DT[out_dtype], _stream())
+    return y
+
+
+def grouped_ternary_gemm_mfma(views: LinearViewArray, offsets, perm, q, act_scale, n_out: int,
+                              total_rows: int, squared_relu: bool = False, gather: bool = True,
+                              out_dtype=torch.float32) -> torch.Tensor:
+    """grouped_ternary_gemm on views holding MFMA-layout weights (compact row tiles)."""
+    _dev(offsets, "offsets", torch.int32)
+    if gather:
+        _dev(perm, "perm", torch.int32)
+    _dev(q, "q", torch.int8)
+    _dev(act_scale, "act_scale", torch.float32)
+    slots = int(perm.numel()) if gather else q.shape[0]
+    k = q.shape[1]
+    y = torch.empty((slots, n_out), dtype=out_dtype, device=q.device)
+    call("nsosx_grouped_ternary_gemm_mfma", views.ptr, views.count, _p(offsets), _p(perm),
+         int(gather), _p(q), _p(act_scale), k, n_out, int(total_rows), int(squared_relu), _p(y),
          _DT[out_dtype], _stream())
     return y
 

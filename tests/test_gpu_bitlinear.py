@@ -324,3 +324,60 @@ def test_weight_row_sums_golden_and_reserved_code(dev, orc):
     words = np.array([0xFFFFFFFF, 0x66666666, 0x00000000, 0xAAAAAAAA], np.uint32)
     got = ops.weight_row_sums(torch.from_numpy(words.view(np.int32)).to(dev), 4, 16)
     np.testing.assert_array_equal(got.cpu().numpy(), [0, 8, -16, 16])
+
+
+@pytest.mark.parametrize("m,k,n", [(300, 1024, 700), (129, 384, 256), (1000, 512, 520),
+                                   (4096, 2048, 8192), (1, 128, 16), (257, 2048, 1024)])
+@pytest.mark.parametrize("ydt,acc", [(torch.bfloat16, False), (torch.float32, True)])
+def test_gemm_mfma_layout_matches_reference_layout(dev, orc, m, k, n, ydt, acc):
+    """The prefill GEMM on repacked (MFMA-layout) weights gives the reference-layout GEMM's
+    outputs bit for bit, including words holding the reserved code 3 (decoded to 0 by both),
+    edge tiles in M and N, magnitude and bias; the accumulators match the oracle."""
+    rng = np.random.default_rng(m + k + n)
+    words = torch.randint(-2**31, 2**31 - 1, (n * k // 16,), dtype=torch.int32, device=dev)
+    q = torch.from_numpy(rng.integers(-127, 128, size=(m, k)).astype(np.int8)).to(dev)
+    s = torch.from_numpy(rng.uniform(0.001, 0.02, m).astype(np.float32)).to(dev)
+    mag = torch.from_numpy(rng.uniform(0.5, 1.5, n).astype(np.float32)).to(dev)
+    bias = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(dev)
+    mf = ops.pack_mfma_layout(words)
+    for mg, b in ((None, None), (mag, bias)):
+        want = ops.ternary_gemm(q, s, words, 0.37, n, mg, b, out_dtype=ydt, want_acc=acc, path=1)
+        got = ops.ternary_gemm_mfma(q, s, mf, 0.37, n, mg, b, out_dtype=ydt, want_acc=acc)
+        torch.cuda.synchronize()
+        if acc:
+            assert torch.equal(got[1], want[1])
+            got, want = got[0], want[0]
+        assert torch.equal(got, want)
+    if acc and m * n <= 300 * 1024:
+        codes = orc.unpack_codes(words.cpu().numpy().view(np.uint32), n * k).reshape(n, k)
+        _, a = ops.ternary_gemm_mfma(q, s, mf, 0.37, n, want_acc=True)
+        np.testing.assert_array_equal(a.cpu().numpy(), orc.gemm_i8(q.cpu().numpy(), codes))
+
+
+@pytest.mark.parametrize("gather,sqrelu", [(True, True), (False, False)])
+def test_grouped_gemm_mfma_matches_reference_layout(dev, gather, sqrelu):
+    rng = np.random.default_rng(5 + gather)
+    counts = [0, 1, 129, 0, 300, 64, 257]
+    E, K, N = len(counts), 384, 520
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    slots = int(offsets[-1])
+    rows = slots + 17
+    q = torch.from_numpy(rng.integers(-127, 128, size=(rows, K)).astype(np.int8)).to(dev)
+    s = torch.from_numpy(rng.uniform(0.001, 0.02, rows).astype(np.float32)).to(dev)
+    perm = torch.from_numpy((rng.permutation(rows)[:slots] if gather else np.arange(slots))
+                            .astype(np.int32)).to(dev)
+    ref_e, mf_e = [], []
+    for e in range(E):
+        w = torch.randint(-2**31, 2**31 - 1, (N * K // 16,), dtype=torch.int32, device=dev)
+        mg = torch.from_numpy(rng.uniform(0.5, 1.5, N).astype(np.float32)).to(dev)
+        bs = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).to(dev)
+        ref_e.append((w, 0.1 + 0.01 * e, K, N, mg, bs))
+        mf_e.append((ops.pack_mfma_layout(w), 0.1 + 0.01 * e, K, N, mg, bs))
+    off = torch.from_numpy(offsets).to(dev)
+    qq, ss = (q, s) if gather else (q[:slots], s[:slots])
+    want = ops.grouped_ternary_gemm(ops.LinearViewArray(ref_e, dev), off, perm, qq, ss, N,
+                                    max(counts), sqrelu, gather, torch.bfloat16)
+    got = ops.grouped_ternary_gemm_mfma(ops.LinearViewArray(mf_e, dev), off, perm, qq, ss, N,
+                                        slots, sqrelu, gather, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
