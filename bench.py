@@ -558,6 +558,22 @@ def bench_ste_backward(torch, dev):
             "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
 
 
+def _consumer_wall_us(k: int, n: int):
+    """Median host wall time per quantize + GEMV call from the compiled C++ consumer
+    (reimagined_amd/host/abi_consumer bench K N: the reference's warmup / 7 x 100-call
+    method, benchmarks/bench_decode_gemv.cpp:76-90), or None when it is not built."""
+    import subprocess
+    from reimagined_amd import build
+    if not os.path.exists(build.CONSUMER_OUT):
+        return None
+    proc = subprocess.run([build.CONSUMER_OUT, "bench", str(k), str(n)], capture_output=True,
+                          text=True, timeout=120)
+    if proc.returncode != 0:
+        _log(f"consumer bench failed: {proc.stderr.strip()}")
+        return None
+    return json.loads(proc.stdout)["median_wall_us"]
+
+
 def bench_gemv_published(torch, dev, reps=100):
     """The reference's two published decode-GEMV shapes (M = 1; K x N = 1024 x 4096 and
     4096 x 16384, docs/GPU_MODERNIZATION_RESULTS.md:95-105, bench_decode_gemv.cpp):
@@ -565,7 +581,8 @@ def bench_gemv_published(torch, dev, reps=100):
         kernel streams HBM (GB/s against peak);
       * resident: back-to-back quantize + GEMV calls on one weight set, as the reference
         measured (its figure is host wall time per call on an RX 7600): the stream time per
-        call from events here."""
+        call from events here, and the host wall time per call from the compiled C++
+        consumer, the reference's own method."""
     from reimagined_amd import ops
     from reimagined_amd._lib import call
     from reimagined_amd.ops import _p, _stream
@@ -598,6 +615,7 @@ def bench_gemv_published(torch, dev, reps=100):
                              "rotated_gbs": round(gbs, 1),
                              "rotated_frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                              "resident_quant_plus_gemv_us": round(res_ms * 1e3, 2)}
+        out[f"k{k}_n{n}"]["host_wall_us_cpp"] = _consumer_wall_us(k, n)
         del packed, views
     return out
 

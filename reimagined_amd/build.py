@@ -71,5 +71,30 @@ def build(verbose: bool = False) -> str:
     return OUT
 
 
+CONSUMER_SRC = os.path.join(os.path.dirname(HERE), "tests", "abi_consumer.cpp")
+CONSUMER_OUT = os.path.join(HERE, "host", "abi_consumer")
+
+
+def consumer_cmd(out: str = CONSUMER_OUT) -> list:
+    """g++ line of the C++ consumer of the C ABI (tests/abi_consumer.cpp through
+    reimagined_amd/host/nsosx.hpp): warnings are errors, linked to libnsosx.so."""
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    inc = os.path.join(os.path.dirname(HERE), "include")
+    return ["g++", "-std=c++17", "-O2", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__",
+            f"-I{inc}", f"-I{os.path.join(HERE, 'host')}", f"-I{rocm}/include", CONSUMER_SRC,
+            "-o", out, f"-L{HERE}", "-lnsosx", f"-Wl,-rpath,{HERE}", f"-L{rocm}/lib",
+            "-lamdhip64", f"-Wl,-rpath,{rocm}/lib"]
+
+
+def build_consumer(verbose: bool = False) -> str:
+    proc = subprocess.run(consumer_cmd(), capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"C++ consumer build failed:\n{proc.stderr}")
+    if verbose:
+        print(f"built {CONSUMER_OUT}")
+    return CONSUMER_OUT
+
+
 if __name__ == "__main__":
     build(verbose=True)
+    build_consumer(verbose=True)
