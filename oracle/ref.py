@@ -178,3 +178,24 @@ def bitlinear_time_forward(w, x, exact_linear: bool = False, reps: int = 1):
     _check(_load().ref_bitlinear_time_forward(w, n, k, x, m, int(exact_linear), int(reps), y,
                                               ctypes.byref(sec)), "bitlinear_time_forward")
     return sec.value, y
+
+
+def mamba2_faithful_forward(p: dict, u, packed: bool = True):
+    """Mamba2SSD::forward on the faithful path (src/mamba2.cpp:2360-2681) with the caller's
+    parameters (Mamba2Block's dict: w_x, w_z, w_B, w_C, w_dt, dt_bias, w_out, conv_w, conv_b,
+    a_log, d_skip, norm_w; H, P, N, G).  packed: x / z / out_proj on the packed ternary path,
+    B / C / dt float.  u [batch, seq, d] -> out [batch, seq, d]."""
+    lib = _load()
+    fn = lib.ref_mamba2_faithful_forward
+    fn.restype = _i
+    fn.argtypes = [_i] * 6 + [_f32p] * 12 + [_i, _f32p, _i, _i, _f32p]
+    u = _f32(u)
+    b, s, d = u.shape
+    H, P, N, G = (int(p[k]) for k in ("H", "P", "N", "G"))
+    inner = H * P
+    out = np.empty_like(u)
+    args = [_f32(p[k]) for k in ("w_x", "w_z", "w_B", "w_C", "w_dt", "dt_bias", "w_out",
+                                 "conv_w", "conv_b", "a_log", "d_skip", "norm_w")]
+    _check(fn(d, N, inner // d, P, G, p["conv_w"].shape[1], *args, int(packed), u, b, s, out),
+           "mamba2_faithful_forward")
+    return out

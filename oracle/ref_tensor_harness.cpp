@@ -12,10 +12,13 @@
 #include <cstdint>
 #include <cstring>
 #include <exception>
+#include <stdexcept>
+#include <utility>
 #include <string>
 #include <vector>
 
 #include "bitlinear.h"
+#include "mamba2.h"
 #include "tensor.h"
 
 using nsos::BitLinear;
@@ -169,6 +172,77 @@ int ref_bitlinear_time_forward(const float* w, int N, int K, const float* x, int
     const auto t1 = std::chrono::steady_clock::now();
     *seconds = std::chrono::duration<double>(t1 - t0).count() / (reps > 0 ? reps : 1);
     copy_out(out, y);
+  });
+}
+
+// Mamba2SSD::forward on the faithful Mamba-2 path (src/mamba2.cpp:2360-2681), CPU.
+// The block is built with MambaConfig{faithful_mamba2, expand, head_dim,
+// n_groups, conv_kernel}; every parameter is overwritten with the caller's
+// (w_x, w_z [inner, d]; w_B, w_C [G*N, d]; w_dt [H, d]; dt_bias [H]; w_out
+// [d, inner]; conv_w [inner + 2 G N, K]; conv_b [inner + 2 G N]; a_log, d_skip
+// [H]; norm_w [inner]).  packed != 0 puts the non-sensitive projections (x, z,
+// out_proj) on the packed ternary path, as quantized deployment runs them; B,
+// C and dt stay on the float path (quantization-sensitive).  u [batch, seq, d]
+// -> out [batch, seq, d].
+int ref_mamba2_faithful_forward(int d_model, int d_state, int expand, int head_dim,
+                                int n_groups, int conv_kernel, const float* w_x,
+                                const float* w_z, const float* w_B, const float* w_C,
+                                const float* w_dt, const float* dt_bias, const float* w_out,
+                                const float* conv_w, const float* conv_b, const float* a_log,
+                                const float* d_skip, const float* norm_w, int packed,
+                                const float* u, int batch, int seq, float* out) {
+  return guarded([&] {
+    nsos::MambaConfig cfg;
+    cfg.faithful_mamba2 = true;
+    cfg.expand = expand;
+    cfg.head_dim = head_dim;
+    cfg.n_groups = n_groups;
+    cfg.conv_kernel = conv_kernel;
+    nsos::Mamba2SSD blk(d_model, d_state, 1, cfg);
+    blk.set_training_mode(false);
+    const int inner = d_model * expand;
+    const int heads = inner / head_dim;
+    const int gs = n_groups * d_state;
+    const int conv_dim = inner + 2 * gs;
+    auto fill = [](nsos::Parameter* p, const float* src, size_t n) {
+      if (static_cast<size_t>(p->data.size) != n)
+        throw std::runtime_error("parameter " + p->name + " has an unexpected size");
+      std::memcpy(p->data.data(), src, sizeof(float) * n);
+      p->mark_updated();
+    };
+    const std::vector<std::pair<std::string, std::pair<const float*, size_t>>> want = {
+        {"x_proj.weight", {w_x, (size_t)inner * d_model}},
+        {"z_proj.weight", {w_z, (size_t)inner * d_model}},
+        {"B_proj.weight", {w_B, (size_t)gs * d_model}},
+        {"C_proj.weight", {w_C, (size_t)gs * d_model}},
+        {"dt_proj.weight", {w_dt, (size_t)heads * d_model}},
+        {"dt_proj.bias", {dt_bias, (size_t)heads}},
+        {"out_proj.weight", {w_out, (size_t)d_model * inner}},
+        {"conv1d_weight", {conv_w, (size_t)conv_dim * conv_kernel}},
+        {"conv1d_bias", {conv_b, (size_t)conv_dim}},
+        {"norm.weight", {norm_w, (size_t)inner}},
+        {"A", {a_log, (size_t)heads}},
+        {"D", {d_skip, (size_t)heads}},
+    };
+    std::vector<nsos::Parameter*> params = blk.parameters();
+    for (const auto& [name, src] : want) {
+      nsos::Parameter* hit = nullptr;
+      for (nsos::Parameter* p : params)
+        if (p->name == name) hit = p;
+      if (!hit) throw std::runtime_error("no parameter named " + name);
+      fill(hit, src.first, src.second);
+    }
+    std::vector<BitLinear*> layers;
+    blk.collect_bitlinear_layers(layers);  // x, z, B, C, dt, out_proj
+    for (size_t i = 0; i < layers.size(); ++i) {
+      BitLinear* bl = layers[i];
+      bl->set_training_mode(false);
+      const bool sensitive = i >= 2 && i <= 4;
+      bl->set_reference_path(!(packed && !sensitive));
+      bl->repack_weights();
+    }
+    Tensor in = host_tensor(u, {batch, seq, d_model});
+    copy_out(blk.forward(in), out);
   });
 }
 

@@ -362,13 +362,16 @@ class Mamba2Block:
         x, B, C = SiLU(causal conv + bias) per sequence (x's conv is fused into
                  the scan's staging; B and C go through the conv kernel)
         y      = faithful scan: per-head A_log [H], P = d_head, G groups, D skip
-        out    = out_proj(RMSNorm(y * SiLU(z), eps) * gamma), out_proj a default
-                 BitLinear (RMS_PERI, magnitude)
+        out    = out_proj(RMSNorm(y * SiLU(z), eps) * gamma), out_proj a ternary
+                 BitLinear in exact-linear mode too (src/mamba2.cpp:514)
 
     params: w_x [inner, d], w_z [inner, d], w_B [G*N, d], w_C [G*N, d], w_dt [H, d],
     w_out [d, inner], conv_w [inner + 2*G*N, K], conv_b [inner + 2*G*N], a_log [H],
-    d_skip [H], norm_w [inner]; optional dt_bias [H] (zeros), out_magnitude [d] (ones);
-    shape keys H, P, N, G and optional eps (1e-5).  Activations run in `dtype` (f32 by
+    d_skip [H], norm_w [inner]; optional dt_bias [H] (zeros); shape keys H, P, N, G and
+    optional eps (1e-5).  The composition equals the reference's Mamba2SSD::forward on its
+    packed deployment path (x, z, out_proj ternary; B, C, dt float) to rounding: the
+    oracle's restatement of this chain is pinned against a reference build of Mamba2SSD
+    (tests/golden/mamba2_ref.npz).  Activations run in `dtype` (f32 by
     default, the reference's).
     """
 
@@ -388,8 +391,7 @@ class Mamba2Block:
         if dt_bias is not None:
             bias[2 * self.gs:] = np.asarray(dt_bias, np.float32)
         self.b_sens = torch.as_tensor(bias, **f32)
-        self.out_proj = BitLinear(params["w_out"], device, rms_input=True,
-                                  magnitude=params.get("out_magnitude"))
+        self.out_proj = BitLinear(params["w_out"], device, rms_input=False)
         cw = torch.as_tensor(params["conv_w"], **f32)
         cb = torch.as_tensor(params["conv_b"], **f32)
         self.K = cw.shape[1]

@@ -11,6 +11,8 @@ needs) and records that library's outputs for seeded and constructed inputs:
                      RMS_PERI int8 codes of BitLinear::forward's quantizer
   bitlinear_ref.npz  BitLinear::forward (packed ternary and float paths) and
                      the packed STE backward
+  mamba2_ref.npz     Mamba2SSD::forward on the faithful Mamba-2 path, the
+                     non-sensitive projections packed ternary
 
 Inputs are stored as float16-representable values (cast to float32 before
 use) so the fixtures stay small.  The fixtures are data (inputs and expected
@@ -72,7 +74,7 @@ def main() -> None:
     out["rowsum__w"] = w
     out["rowsum__sums"] = np.array([oracle.ref_row_sum_i8(r) for r in w], np.int32)
     files = {"quant_ref.npz": out, "tensor_ref.npz": tensor_cases(),
-             "bitlinear_ref.npz": bitlinear_cases()}
+             "bitlinear_ref.npz": bitlinear_cases(), "mamba2_ref.npz": mamba2_cases()}
     lines = []
     for name, data in files.items():
         path = os.path.join(HERE, name)
@@ -131,6 +133,27 @@ def tensor_cases() -> dict:
         out[f"rmsbwd_k{k}__x"] = x
         out[f"rmsbwd_k{k}__g"] = gr
         out[f"rmsbwd_k{k}__dx"] = ref.rmsnorm_backward(xf, gr.astype(np.float32), xn, 1e-6)
+    return out
+
+
+def mamba2_cases() -> dict:
+    rng = np.random.default_rng(20261204)
+    d, H, P, N, G, K = 64, 4, 32, 16, 2, 4
+    inner, gs = H * P, G * N
+    p = {"w_x": _h(rng, (inner, d), 0.1), "w_z": _h(rng, (inner, d), 0.1),
+         "w_B": _h(rng, (gs, d), 0.1), "w_C": _h(rng, (gs, d), 0.1),
+         "w_dt": _h(rng, (H, d), 0.1), "dt_bias": _h(rng, (H,), 1.0, -2.0),
+         "w_out": _h(rng, (d, inner), 0.1), "conv_w": _h(rng, (inner + 2 * gs, K), 0.5),
+         "conv_b": _h(rng, (inner + 2 * gs,), 0.1), "a_log": _h(rng, (H,)),
+         "d_skip": _h(rng, (H,)), "norm_w": rng.uniform(0.5, 1.5, inner).astype(np.float16)}
+    u = _h(rng, (2, 19, d))
+    f32 = {k: v.astype(np.float32) for k, v in p.items()}
+    f32.update(H=H, P=P, N=N, G=G)
+    out = dict(p)
+    out["shape"] = np.array([H, P, N, G], np.int32)
+    out["u"] = u
+    out["out_packed"] = ref.mamba2_faithful_forward(f32, u.astype(np.float32), packed=True)
+    out["out_float"] = ref.mamba2_faithful_forward(f32, u.astype(np.float32), packed=False)
     return out
 
 

@@ -163,3 +163,49 @@ def test_oracle_matches_reference_build_random(orc):
     packed, ws, _ = orc.pack_weights(w)
     _bits_equal(orc.bitlinear_forward(x, packed, ws, 96, 8, True, mag, bias),
                 ref.bitlinear_forward(w, x, True, False, mag, bias), "packed forward")
+
+
+def _mamba2_chain(orc, g, out_rms=False, dt_bias=True):
+    """The oracle's restatement of Mamba2SSD::forward on its packed faithful path
+    (src/mamba2.cpp:2360-2681): x / z / out_proj exact-linear ternary, B / C / dt float
+    linear (dt with its bias), causal conv + SiLU per channel group, the selective scan
+    without a gate, then RMSNorm(y * SiLU(z)) * norm weight."""
+    H, P, N, G = (int(v) for v in g["shape"])
+    p = {k: _f(g[k]) for k in ("w_x", "w_z", "w_B", "w_C", "w_dt", "dt_bias", "w_out",
+                               "conv_w", "conv_b", "a_log", "d_skip", "norm_w")}
+    inner, gs, d = H * P, G * N, p["w_out"].shape[0]
+    px, wsx, _ = orc.pack_weights(p["w_x"])
+    pz, wsz, _ = orc.pack_weights(p["w_z"])
+    po, wso, _ = orc.pack_weights(p["w_out"])
+    cw, cb = p["conv_w"], p["conv_b"]
+    outs = []
+    for ub in _f(g["u"]):
+        cu = np.array([0, ub.shape[0]], np.int32)
+        xv = orc.bitlinear_forward(ub, px, wsx, inner, 8, False)
+        z = orc.bitlinear_forward(ub, pz, wsz, inner, 8, False)
+        Bv = orc.linear_f32(ub, p["w_B"])
+        Cv = orc.linear_f32(ub, p["w_C"])
+        dt = orc.linear_f32(ub, p["w_dt"], bias=p["dt_bias"] if dt_bias else None)
+        xc = orc.conv1d_causal(xv, cw[:inner], cu, bias=cb[:inner])
+        Bc = orc.conv1d_causal(Bv, cw[inner:inner + gs], cu, bias=cb[inner:inner + gs])
+        Cc = orc.conv1d_causal(Cv, cw[inner + gs:], cu, bias=cb[inner + gs:])
+        y, _ = orc.selective_scan(xc, dt, p["a_log"], Bc, Cc, p["d_skip"], None, cu, H, P, N, G,
+                                  gate_silu=False)
+        normed = orc.rmsnorm_gated(y, z, p["norm_w"], eps=1e-5)
+        outs.append(orc.bitlinear_forward(normed, po, wso, d, 8, out_rms))
+    return np.stack(outs)
+
+
+def test_mamba2_chain_matches_reference_build(orc):
+    """tests/golden/mamba2_ref.npz holds Mamba2SSD::forward from a reference build
+    (two sequences of 19 tokens, d_model 64, 4 heads of 32, d_state 16, 2 groups, conv 4).
+    The chain's float stages sum in another order than the reference's matmul / conv
+    loops, so the bound is fp32-level (1e-5 of the output scale); an out_proj with
+    RMS_PERI or a dt projection without its bias is far outside it."""
+    g = _load("mamba2_ref.npz")
+    want = g["out_packed"]
+    tol = 1e-5 * np.abs(want).max()
+    got = _mamba2_chain(orc, g)
+    assert np.abs(got - want).max() <= tol, np.abs(got - want).max()
+    assert np.abs(_mamba2_chain(orc, g, out_rms=True) - want).max() > 100 * tol
+    assert np.abs(_mamba2_chain(orc, g, dt_bias=False) - want).max() > 100 * tol
