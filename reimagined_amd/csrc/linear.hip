@@ -325,6 +325,207 @@ __global__ __launch_bounds__(256) void dot_kernel(const void* __restrict__ x,
 }
 
 // ---------------------------------------------------------------------------
+// Skinny outputs over many rows (N <= 64, M > kDotMax: the faithful Mamba-2
+// block's B / C / dt projections, router gates at prefill).  A workgroup of
+// four waves owns 32 rows x all N columns as 2 x NT tiles of
+// v_mfma_f32_16x16x4f32 and splits K among its waves: 32-deep slice s goes to
+// wave s % 4, x streaming from HBM and W (at most 64 x K floats) from L2, the
+// next slice's loads in flight while the current one is contracted.  Lane l
+// loads, for each of its rows (l % 16) + 16 i and columns (l % 16) + 16 j, the
+// eight elements k0 + 8 (l / 16) .. + 7 (two 16-byte loads per row, so a row's
+// four lanes read 128 contiguous bytes); MFMA step e (0..7) contracts, in lane
+// group l / 16, element k0 + 8 (l / 16) + e of both operands.  The D tile of a
+// 16x16x4 MFMA leaves row 4 (l / 16) + r, column l % 16 in register r.  The four
+// waves' partial tiles are added in wave order through LDS by wave 0.
+// ---------------------------------------------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int kSkinnyRows = 32;   // rows per workgroup
+constexpr int kSkinnyMaxN = 64;
+constexpr int kSkinnyWaves = 4;   // K split
+
+template <int XDT>
+__device__ __forceinline__ void load8(const void* p, int64_t i, float v[8]) {
+    if constexpr (XDT == NSOSX_F32) {
+        const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+        const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const u32x4 u = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p) + i);
+        const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[2 * j] = __uint_as_float(wd[j] << 16);
+            v[2 * j + 1] = __uint_as_float(wd[j] & 0xFFFF0000u);
+        }
+    }
+}
+
+template <int XDT, int NT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT <= 2 ? 2 : 3))) void skinny_kernel(const void* __restrict__ x, int rms,
+                                                     float eps, const float* __restrict__ w, int M,
+                                                     int N, int K, const float* __restrict__ mag,
+                                                     const float* __restrict__ bias, void* y,
+                                                     int y_bf16) {
+    __shared__ __align__(16) v4f s_part[kSkinnyWaves - 1][2 * NT][64];
+    __shared__ float s_ss[kSkinnyWaves][kSkinnyRows];  // per-wave sums of squares by row
+    __shared__ float s_inv[kSkinnyRows];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const int r0 = blockIdx.x * kSkinnyRows;
+    int64_t abase[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = min(r0 + lr + 16 * i, M - 1);  // rows past M are computed, not stored
+        abase[i] = (int64_t)r * K;
+    }
+    float ss[2] = {0.0f, 0.0f};  // RMS_PERI: the lane's share of its rows' sums of squares
+    int64_t bbase[NT];
+    bool bok[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int n = lr + 16 * j;
+        bok[j] = n < N;
+        bbase[j] = (int64_t)min(n, N - 1) * K;
+    }
+    // one slice of both operands: K % 4 == 0, so each 4-element half of a lane's
+    // eight is wholly in or out; columns past N contract zeros
+    auto load_slice = [&](int k0, float (&a)[2][8], float (&b)[NT][8]) {
+        const int kk = k0 + 8 * lg;
+        const bool in0 = kk < K, in1 = kk + 4 < K;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (in1) {
+                load8<XDT>(x, abase[i] + kk, a[i]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    a[i][e] = (e < 4 && in0) ? load_act<XDT>(x, abase[i] + kk + e) : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            if (in1 && bok[j]) {
+                load8<NSOSX_F32>(w, bbase[j] + kk, b[j]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    b[j][e] = (e < 4 && in0 && bok[j]) ? w[bbase[j] + kk + e] : 0.0f;
+            }
+        }
+    };
+    v4f acc[2][NT];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    auto contract = [&](const float (&a)[2][8], const float (&b)[NT][8]) {
+        if (rms) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss[i] = __fmaf_rn(a[i][e], a[i][e], ss[i]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j],
+                                                                     0, 0, 0);
+    };
+    // slices wave, wave + 4, ... (slices past K load nothing and contract zeros).  Up to
+    // two column tiles: two register sets, the next slice loading while the current one
+    // is contracted.  Three or four: one set (the loads' latency is covered by the other
+    // workgroups' waves on the SIMD, which two sets of NT = 4 would not leave room for).
+    constexpr int kStride = 32 * kSkinnyWaves;
+    float a0[2][8], b0[NT][8];
+    int k0 = 32 * wave;
+    if constexpr (NT <= 2) {
+        float a1[2][8], b1[NT][8];
+        load_slice(k0, a0, b0);
+        for (; k0 < K; k0 += 2 * kStride) {
+            load_slice(k0 + kStride, a1, b1);
+            contract(a0, b0);
+            load_slice(k0 + 2 * kStride, a0, b0);
+            contract(a1, b1);
+        }
+    } else {
+        for (; k0 < K; k0 += kStride) {
+            load_slice(k0, a0, b0);
+            contract(a0, b0);
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < NT; ++j) s_part[wave - 1][i * NT + j][lane] = acc[i][j];
+    }
+    if (rms) {
+        // the row's four lane groups, then its four waves
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            ss[i] += __shfl_xor(ss[i], 16);
+            ss[i] += __shfl_xor(ss[i], 32);
+            if (lg == 0) s_ss[wave][lr + 16 * i] = ss[i];
+        }
+    }
+    __syncthreads();
+    if (wave > 0) return;
+    if (rms && lane < kSkinnyRows) {
+        const float t = ((s_ss[0][lane] + s_ss[1][lane]) + s_ss[2][lane]) + s_ss[3][lane];
+        s_inv[lane] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(__fdiv_rn(t, static_cast<float>(K)), eps)));
+    }
+    asm volatile("" ::: "memory");  // LDS operations of one wave complete in order
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+            for (int v = 0; v < kSkinnyWaves - 1; ++v) acc[i][j] += s_part[v][i * NT + j][lane];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int n = lr + 16 * j;
+        if (n >= N) continue;
+        const float mg = mag ? mag[n] : 1.0f;
+        const float bs = bias ? bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = r0 + 16 * i + 4 * lg + r;
+                if (m >= M) continue;
+                float v = acc[i][j][r];
+                if (rms) v = __fmul_rn(v, s_inv[16 * i + 4 * lg + r]);
+                if (mag) v = __fmul_rn(v, mg);
+                if (bias) v = __fadd_rn(v, bs);
+                if (y_bf16) static_cast<uint16_t*>(y)[(int64_t)m * N + n] = f32_to_bf16(v);
+                else static_cast<float*>(y)[(int64_t)m * N + n] = v;
+            }
+    }
+}
+
+template <int XDT>
+static void launch_skinny(const void* x, int rms, const float* w, int M, int N, int K,
+                          const float* mag, const float* bias, void* y, int ybf, hipStream_t st) {
+    const float eps = 1e-6f;
+    const dim3 grid((M + kSkinnyRows - 1) / kSkinnyRows);
+    switch ((N + 15) / 16) {
+        case 1: hipLaunchKernelGGL((skinny_kernel<XDT, 1>), grid, dim3(256), 0, st, x, rms, eps, w,
+                                   M, N, K, mag, bias, y, ybf); break;
+        case 2: hipLaunchKernelGGL((skinny_kernel<XDT, 2>), grid, dim3(256), 0, st, x, rms, eps, w,
+                                   M, N, K, mag, bias, y, ybf); break;
+        case 3: hipLaunchKernelGGL((skinny_kernel<XDT, 3>), grid, dim3(256), 0, st, x, rms, eps, w,
+                                   M, N, K, mag, bias, y, ybf); break;
+        default: hipLaunchKernelGGL((skinny_kernel<XDT, 4>), grid, dim3(256), 0, st, x, rms, eps, w,
+                                    M, N, K, mag, bias, y, ybf); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // STE backward pieces.
 // ---------------------------------------------------------------------------
 constexpr int kColRows = 256;   // rows per partial of the column reductions
@@ -436,9 +637,20 @@ extern "C" int nsosx_linear_f32(const void* x, int x_dtype, int M, int K, const 
     if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w) % 16)
         return fail(NSOSX_ERR_INVALID, "linear_f32: x and w must be 16-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    const int ybf = y_dtype == NSOSX_BF16;
+    // Skinny outputs over many rows: one pass over x, the RMS_PERI sums of squares taken
+    // on the way and the 1 / rms applied to the row's dot products (equal to the dot of
+    // the normalised row to rounding; bf16 rows are read 16 bytes at a time: K % 8 keeps
+    // them aligned)
+    if (N <= kSkinnyMaxN && M > kDotMax && (x_dtype == NSOSX_F32 || K % 8 == 0)) {
+        if (x_dtype == NSOSX_F32)
+            launch_skinny<NSOSX_F32>(x, rms_input, w, M, N, K, magnitude, bias, y, ybf, st);
+        else
+            launch_skinny<NSOSX_BF16>(x, rms_input, w, M, N, K, magnitude, bias, y, ybf, st);
+        return check_launch("linear_f32");
+    }
     if (rms_input) launch_rms_inv(x, x_dtype, M, K, 1e-6f, rms_workspace, st);
     const float* inv = rms_input ? rms_workspace : nullptr;
-    const int ybf = y_dtype == NSOSX_BF16;
     if (N <= kDotMax || M <= kDotMax) {
         const bool per_m = N <= kDotMax && !(M <= kDotMax && M < N);
         const int rows = per_m ? M : N;

@@ -308,6 +308,7 @@ constexpr int kQuadTC = 32;       // tokens per B/C chunk
 constexpr int kQuadCh = 16;       // channels per wave
 constexpr int kQuadMaxW = 4;
 constexpr int kQuadRedStride = 20;  // floats per channel row of the readout transpose
+constexpr int kQuadOutStride = 20;  // floats per token row of the staged outputs (16-byte rows)
 
 // Workgroup -> (sequence rank, channel block).  Consecutive workgroup ids go
 // round-robin to the 8 XCDs, each with its own L2; this map hands every run of
@@ -371,7 +372,7 @@ __device__ __forceinline__ float softplus_sel(float v) {
 // LOCAL: the first pass of the time-chunked scan: the recurrence only (no
 // readout, no output), writing each item's end state and sum of delta.
 template <int ADT, int SPL, bool GATE, bool CONV, bool PH = false, bool LOCAL = false>
-__global__ __launch_bounds__(64) void scan_quad_kernel(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void scan_quad_kernel(
     const void* __restrict__ x, int64_t x_stride, const void* __restrict__ dt,
     const float* __restrict__ a_log, int a_per_state, const void* __restrict__ Bm,
     const void* __restrict__ Cm, const float* __restrict__ Dskip, const void* __restrict__ z,
@@ -386,6 +387,7 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
     __shared__ __align__(16) float s_red[kQuadCh * kQuadRedStride];
     __shared__ __align__(16) float2 s_dx[kQuadCh][4];  // {delta, delta * x} of the group's 4 tokens
     __shared__ float s_xw[kQuadCh][8];  // conv window: raw x of the previous and this group
+    __shared__ __align__(16) float s_out[kQuadTC][kQuadOutStride];  // the chunk's outputs
     __shared__ int s_pick;
 
     const int lane = threadIdx.x;
@@ -552,15 +554,48 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
         }
         s_xw[lane >> 2][q] = w0;
     }
-    // the group whose readout is pending: its validity, conv output, raw gate and base token
-    bool pv_valid = false;
+    // the group whose readout is pending: its conv output, raw gate and base token
     float pv_xv = 0.0f;
     raw_t pv_z = 0;
-    int pv_t = 0;
+    int pv_t = t0;
+    // Outputs go to the chunk's rows of s_out and leave with one vector store per lane
+    // per chunk.  On this architecture a load wait issued while a store is in flight
+    // waits for the store as well (loads and stores share one counter and may complete
+    // out of order), so a store per group would expose a full store round trip at every
+    // group's input wait; per chunk it is one in eight.  Rows of tokens past the sequence
+    // hold garbage and are not stored.
     auto finish_readout = [&](float tot) {
         float out = __fmaf_rn(dsk, pv_xv, tot);
         if (GATE) out = out * silu_fast(raw_to_f32<ADT>(pv_z));
-        buf_store_act<ADT>(group_rsrc(y, ey, static_cast<uint32_t>(pv_t) * D * ES), ly, out);
+        s_out[((pv_t - t0) & (kQuadTC - 1)) + q][lane >> 2] = out;
+    };
+    // lane l stores token row l / 2 of the chunk at tbase, channels 8 (l % 2) .. + 7
+    auto flush_out = [&](int tbase) {
+        asm volatile("" ::: "memory");
+        const int row = lane >> 1, half = lane & 1;
+        const float4 v0 = *reinterpret_cast<const float4*>(&s_out[row][half * 8]);
+        const float4 v1 = *reinterpret_cast<const float4*>(&s_out[row][half * 8 + 4]);
+        asm volatile("" ::: "memory");
+        const int tok = tbase + row;
+        const uint32_t off = tok < t1
+            ? static_cast<uint32_t>(tok * D + cblk * kQuadCh + half * 8) * ES : 0x80000000u;
+        const __amdgpu_buffer_rsrc_t ry = make_rsrc(y, ey);
+        if constexpr (ADT == NSOSX_F32) {
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__float_as_uint(v0.x), __float_as_uint(v0.y), __float_as_uint(v0.z),
+                      __float_as_uint(v0.w)}, ry, off, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__float_as_uint(v1.x), __float_as_uint(v1.y), __float_as_uint(v1.z),
+                      __float_as_uint(v1.w)}, ry, off + 16, 0, 0);
+        } else {
+            auto pk = [](float lo, float hi) {
+                return static_cast<uint32_t>(f32_to_bf16(lo)) |
+                       (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+            };
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{pk(v0.x, v0.y), pk(v0.z, v0.w), pk(v1.x, v1.y), pk(v1.z, v1.w)}, ry, off,
+                0, 0);
+        }
     };
     if (t0 < t1) {
         prefetch_bc(t0);
@@ -665,18 +700,20 @@ __global__ __launch_bounds__(64) void scan_quad_kernel(
             // lanes (its partials were read at the top of this group), then this
             // group's partials are written (LDS operations of one wave complete in
             // order, so the next group's reads see them) -------------------------
-            if (pv_valid) finish_readout(((rd0 + rd1) + rd2) + rd3);
+            finish_readout(((rd0 + rd1) + rd2) + rd3);
+            if (r0 == 0 && tb != t0) flush_out(tb - kQuadTC);  // the previous chunk is complete
             *reinterpret_cast<float4*>(&s_red[red_w]) = make_float4(part[0], part[1], part[2], part[3]);
-            pv_valid = valid;
             pv_xv = xv;
             pv_z = zraw;
             pv_t = tgrp;
         }
     }
     if constexpr (!LOCAL) {
-        if (pv_valid)
+        if (t0 < t1) {
             finish_readout(((s_red[red_r] + s_red[red_r + 4]) + s_red[red_r + 8]) +
                            s_red[red_r + 12]);
+            flush_out(t0 + ((t1 - 1 - t0) & ~(kQuadTC - 1)));
+        }
     } else {
         if (q == 0) plan.sum_dl[(int64_t)seq * D + c] = sdl;
     }

@@ -24,7 +24,9 @@ def _close(got, want, rtol=1e-4, atol=1e-5, what=""):
 
 @pytest.mark.parametrize("m,k,n", [(40, 1024, 160), (40796 // 64, 1024, 160), (5, 1024, 160),
                                    (1, 1024, 160), (300, 1024, 8), (8192 // 8, 1024, 8),
-                                   (1, 64, 3), (129, 256, 130), (17, 4096, 17), (16, 64, 16)])
+                                   (1, 64, 3), (129, 256, 130), (17, 4096, 17), (16, 64, 16),
+                                   (40796 // 16, 1024, 64), (100, 1000, 33), (33, 72, 48),
+                                   (4097, 512, 64), (257, 1028, 17), (18, 4, 1)])
 @pytest.mark.parametrize("rms", [False, True])
 def test_linear_f32_matches_oracle(dev, orc, m, k, n, rms):
     rng = np.random.default_rng(m * 31 + n)
@@ -40,10 +42,10 @@ def test_linear_f32_matches_oracle(dev, orc, m, k, n, rms):
         _close(y.cpu().numpy(), want, what=f"mag={mg is not None} bias={b is not None}")
 
 
-@pytest.mark.parametrize("m,n", [(600, 160), (3, 160), (700, 8)])
-def test_linear_f32_bf16_io(dev, orc, m, n):
+@pytest.mark.parametrize("m,n,k", [(600, 160, 1024), (3, 160, 1024), (700, 8, 1024),
+                                   (700, 64, 1024), (70, 40, 1028), (65, 33, 72)])
+def test_linear_f32_bf16_io(dev, orc, m, n, k):
     rng = np.random.default_rng(m + n)
-    k = 1024
     x = rng.standard_normal((m, k)).astype(np.float32)
     w = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
     xb = torch.from_numpy(x).to(torch.bfloat16)
