@@ -875,7 +875,9 @@ template <int MT, int YDT, bool ACC_OUT>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvProblem pb, const int8_t* __restrict__ q,
                                                    const float* __restrict__ act_scale, int M,
                                                    void* y, int32_t* acc_out) {
-    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // wave-uniform (readfirstlane): the tile loops then branch on scalars, with exact
+    // memory wait counts
+    const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     const int num_waves = gridDim.x * 4;
     gemv_body_long<MT, YDT, ACC_OUT>(pb, q, act_scale, M, y, acc_out, wave_id, num_waves);
 }
@@ -905,7 +907,9 @@ __global__ __launch_bounds__(256) void grouped_gemv_kernel(const nsosx_linear_vi
     char* yb = static_cast<char*>(y) + g * y_stride * (YDT == NSOSX_F32 ? 4 : 2);
     if (skip_skinny && skinny_group(v, yb)) return;
     GemvProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
-    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // wave-uniform (readfirstlane): the tile loops then branch on scalars, with exact
+    // memory wait counts
+    const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     const int num_waves = gridDim.x * 4;
     const int gi = g / q_div;
     gemv_body_long<MT, YDT, false, SQRELU>(pb, q + gi * q_stride, act_scale + gi * scale_stride,
@@ -1993,11 +1997,29 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
     for (int mt = 0; mt < MT; ++mt)
         comb[mt] = __fmul_rn(act_scale[min(mt * 16 + li, M - 1)], pb.ws);
 
+    // The affine terms of a tile's four output columns load with its weights (a null
+    // magnitude or bias reads through an empty resource, which returns zeros), so the
+    // epilogue waits on nothing the ring's loads do not already bring.
+    const bool has_mag = pb.mag != nullptr, has_bias = pb.bias != nullptr;
+    const __amdgpu_buffer_rsrc_t rmag = make_rsrc(pb.mag, has_mag ? pb.N * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rbias = make_rsrc(pb.bias, has_bias ? pb.N * 4u : 0u);
+    auto tile_n0 = [&](int ti) { return (wave_id + ti * num_waves) * 16 + 4 * g; };
+    auto load_affine = [&](int ti, float (&mg)[4], float (&bs)[4]) {
+        const uint32_t off = static_cast<uint32_t>(tile_n0(min(ti, my_tiles - 1))) * 4u;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            mg[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rmag, off + 4 * r, 0, 0));
+            bs[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rbias, off + 4 * r, 0, 0));
+        }
+    };
+
     uint4 ring[LT];
+    float mg_cur[4], bs_cur[4];
     {
         const int64_t b0 = tile_src(0);
 #pragma unroll
         for (int j = 0; j < LT; ++j) ring[j] = load_piece(b0, j);
+        load_affine(0, mg_cur, bs_cur);
     }
     const char* frag = lds + lane * 16;
     // the first m tile's fragments up to K = 2048 (512 bytes per lane) stay in
@@ -2009,92 +2031,128 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
         for (int st = 0; st < 4 * LT; ++st)
             held[st] = *reinterpret_cast<const uint4*>(frag + st * MT * 1024);
     }
-    for (int ti = 0; ti < my_tiles; ++ti) {
-        // this tile to the wave's LDS slice (in order with the reads below), then
-        // the next tile's loads into the ring
+    // Tiles go in batches of kSkBatch whose outputs are stored together after the
+    // batch.  On this architecture a wait for loads issued while a store is in flight
+    // waits for the store as well (loads and stores share one counter and may complete
+    // out of order), so a store per tile would expose a store round trip at every
+    // tile's wait for its weights; per batch it is one in kSkBatch.  The batch is
+    // unrolled (straight-line, exact wait counts); tiles past the wave's last compute on
+    // clamped loads and store nothing.
+    constexpr int kSkBatch = 2;
+    for (int t0 = 0; t0 < my_tiles; t0 += kSkBatch) {
+        float vb[kSkBatch][MT][4];
+        int ab[kSkBatch][MT][4];
 #pragma unroll
-        for (int j = 0; j < LT; ++j) {
-            const int b = 1024 * j + 16 * lane;
-            const int r = b / RB, c = (b % RB) >> 4;
-            *reinterpret_cast<uint4*>(stage + r * RB + ((c ^ (r & 15)) << 4)) = ring[j];
-        }
-        {
-            const int64_t nb0 = tile_src(ti + 1);
+        for (int u = 0; u < kSkBatch; ++u) {
+            const int ti = t0 + u;
+            // this tile to the wave's LDS slice (in order with the reads below), then
+            // the next tile's loads into the ring
 #pragma unroll
-            for (int j = 0; j < LT; ++j) ring[j] = load_piece(nb0, j);
-        }
-        v4i acc[MT];
+            for (int j = 0; j < LT; ++j) {
+                const int b = 1024 * j + 16 * lane;
+                const int r = b / RB, c = (b % RB) >> 4;
+                *reinterpret_cast<uint4*>(stage + r * RB + ((c ^ (r & 15)) << 4)) = ring[j];
+            }
+            float mg_nxt[4], bs_nxt[4];
+            {
+                const int64_t nb0 = tile_src(ti + 1);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+                for (int j = 0; j < LT; ++j) ring[j] = load_piece(nb0, j);
+                load_affine(ti + 1, mg_nxt, bs_nxt);
+            }
+            v4i acc[MT];
 #pragma unroll
-        for (int j = 0; j < LT; ++j) {
-            const uint4 w = *reinterpret_cast<const uint4*>(
-                stage + li * RB + (((4 * j + g) ^ li) << 4));
-            // 4 x 4 transpose (16-lane row g, slot u) -> (row u, slot g)
-            const auto p02 = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
-            const auto p13 = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
-            const auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
-            const auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
-            const uint32_t words[4] = {p01[0], p01[1], p23[0], p23[1]};
+            for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                uint32_t wv[4];
-                unpack_word(words[u], wv);
-                const v4i aw = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+            for (int j = 0; j < LT; ++j) {
+                const uint4 w = *reinterpret_cast<const uint4*>(
+                    stage + li * RB + (((4 * j + g) ^ li) << 4));
+                // 4 x 4 transpose (16-lane row g, slot u) -> (row u, slot g)
+                const auto p02 = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
+                const auto p13 = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
+                const auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+                const auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+                const uint32_t words[4] = {p01[0], p01[1], p23[0], p23[1]};
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    const uint4 v =
-                        kHold && mt == 0
-                            ? held[(4 * j + u) % (kHold ? 4 * LT : 1)]
-                            : *reinterpret_cast<const uint4*>(frag + ((4 * j + u) * MT + mt) * 1024);
-                    acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                        aw, v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w}, acc[mt], 0, 0, 0);
+                for (int uu = 0; uu < 4; ++uu) {
+                    uint32_t wv[4];
+                    unpack_word(words[uu], wv);
+                    const v4i aw = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const uint4 v =
+                            kHold && mt == 0
+                                ? held[(4 * j + uu) % (kHold ? 4 * LT : 1)]
+                                : *reinterpret_cast<const uint4*>(frag + ((4 * j + uu) * MT + mt) * 1024);
+                        acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            aw, v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w}, acc[mt], 0, 0, 0);
+                    }
                 }
             }
-        }
-        // lane holds outputs n = tile * 16 + 4 g + r of token mt * 16 + li
-        const int nb = (wave_id + ti * num_waves) * 16 + 4 * g;
+            // lane holds outputs n = tile * 16 + 4 g + r of token mt * 16 + li
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const int m = mt * 16 + li;
-            const int av[4] = {acc[mt].x, acc[mt].y, acc[mt].z, acc[mt].w};
-            float v[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                v[r] = dequant(av[r], comb[mt], pb.mag, pb.bias, min(nb + r, pb.N - 1));
-                if (SQRELU) {
-                    v[r] = v[r] > 0.0f ? v[r] : 0.0f;
-                    v[r] = __fmul_rn(v[r], v[r]);
-                }
-            }
-            const uint32_t e = static_cast<uint32_t>(m * pb.N + nb);
-            if (VEC4) {
-                // N % 4 == 0: the lane's four outputs are one aligned vector, inside N
-                // exactly when its first one is
-                const bool ok = m < M && nb < pb.N;
-                if (ACC_OUT)
-                    __builtin_amdgcn_raw_buffer_store_b128(
-                        v4i{av[0], av[1], av[2], av[3]}, racc, ok ? e * 4u : 0x80000000u, 0, 0);
-                if (y) {
-                    const uint32_t off = ok ? e * ES : 0x80000000u;
-                    if constexpr (YDT == NSOSX_F32)
-                        __builtin_amdgcn_raw_buffer_store_b128(
-                            v4i{(int)__float_as_uint(v[0]), (int)__float_as_uint(v[1]),
-                                (int)__float_as_uint(v[2]), (int)__float_as_uint(v[3])},
-                            ry, off, 0, 0);
-                    else
-                        __builtin_amdgcn_raw_buffer_store_b64(
-                            v2u{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])}, ry, off, 0, 0);
-                }
-            } else {
+            for (int mt = 0; mt < MT; ++mt) {
+                const int av[4] = {acc[mt].x, acc[mt].y, acc[mt].z, acc[mt].w};
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const bool ok = m < M && nb + r < pb.N;
-                    const uint32_t er = e + r;
+                    // the reference's affine: multiply, then add, each rounded
+                    float v = __fmul_rn(static_cast<float>(av[r]), comb[mt]);
+                    if (has_mag) v = __fmul_rn(v, mg_cur[r]);
+                    if (has_bias) v = __fadd_rn(v, bs_cur[r]);
+                    if (SQRELU) {
+                        v = v > 0.0f ? v : 0.0f;
+                        v = __fmul_rn(v, v);
+                    }
+                    vb[u][mt][r] = v;
+                    ab[u][mt][r] = av[r];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                mg_cur[r] = mg_nxt[r];
+                bs_cur[r] = bs_nxt[r];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kSkBatch; ++u) {
+            const int ti = t0 + u;
+            const int nb = tile_n0(ti);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int m = mt * 16 + li;
+                const uint32_t e = static_cast<uint32_t>(m * pb.N + nb);
+                const bool live = ti < my_tiles && m < M;
+                if (VEC4) {
+                    // N % 4 == 0: the lane's four outputs are one aligned vector, inside N
+                    // exactly when its first one is
+                    const bool ok = live && nb < pb.N;
                     if (ACC_OUT)
-                        __builtin_amdgcn_raw_buffer_store_b32(av[r], racc,
-                                                              ok ? er * 4u : 0x80000000u, 0, 0);
-                    if (y) buf_store_act<YDT>(ry, ok ? er * ES : 0x80000000u, v[r]);
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            v4i{ab[u][mt][0], ab[u][mt][1], ab[u][mt][2], ab[u][mt][3]}, racc,
+                            ok ? e * 4u : 0x80000000u, 0, 0);
+                    if (y) {
+                        const uint32_t off = ok ? e * ES : 0x80000000u;
+                        if constexpr (YDT == NSOSX_F32)
+                            __builtin_amdgcn_raw_buffer_store_b128(
+                                v4i{(int)__float_as_uint(vb[u][mt][0]), (int)__float_as_uint(vb[u][mt][1]),
+                                    (int)__float_as_uint(vb[u][mt][2]), (int)__float_as_uint(vb[u][mt][3])},
+                                ry, off, 0, 0);
+                        else
+                            __builtin_amdgcn_raw_buffer_store_b64(
+                                v2u{pack_bf16x2(vb[u][mt][0], vb[u][mt][1]),
+                                    pack_bf16x2(vb[u][mt][2], vb[u][mt][3])},
+                                ry, off, 0, 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const bool ok = live && nb + r < pb.N;
+                        const uint32_t er = e + r;
+                        if (ACC_OUT)
+                            __builtin_amdgcn_raw_buffer_store_b32(ab[u][mt][r], racc,
+                                                                  ok ? er * 4u : 0x80000000u, 0, 0);
+                        if (y) buf_store_act<YDT>(ry, ok ? er * ES : 0x80000000u, vb[u][mt][r]);
+                    }
                 }
             }
         }
@@ -2105,7 +2163,7 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
 // (the launch reserves 64 KB of LDS); the others are left to a grouped_gemv_kernel
 // launch over the same groups.  The decision is uniform per workgroup.
 template <int YDT, bool SQRELU>
-__global__ __launch_bounds__(256) void grouped_skinny_kernel(const nsosx_linear_view* views,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void grouped_skinny_kernel(const nsosx_linear_view* views,
                                                              const int32_t* __restrict__ view_sel,
                                                              const int8_t* __restrict__ q,
                                                              int64_t q_stride, int q_div,
@@ -2118,7 +2176,9 @@ __global__ __launch_bounds__(256) void grouped_skinny_kernel(const nsosx_linear_
     char* yb = static_cast<char*>(y) + g * y_stride * (YDT == NSOSX_F32 ? 4 : 2);
     if (!skinny_group(v, yb)) return;
     GemvProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
-    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // wave-uniform (readfirstlane): the tile loops then branch on scalars, with exact
+    // memory wait counts
+    const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     const int num_waves = gridDim.x * 4;
     const int gi = g / q_div;
     const int8_t* qg = q + gi * q_stride;
@@ -2132,11 +2192,13 @@ __global__ __launch_bounds__(256) void grouped_skinny_kernel(const nsosx_linear_
 }
 
 template <int MT, int LT, int YDT, bool ACC_OUT>
-__global__ __launch_bounds__(256) void skinny_kernel(GemvProblem pb, const int8_t* __restrict__ q,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void skinny_kernel(GemvProblem pb, const int8_t* __restrict__ q,
                                                      const float* __restrict__ act_scale, int M,
                                                      void* y, int32_t* acc_out) {
     extern __shared__ __align__(16) char lds_sk[];
-    const int wave_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // wave-uniform (readfirstlane): the tile loops then branch on scalars, with exact
+    // memory wait counts
+    const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     if ((pb.N & 3) == 0)
         skinny_body<MT, LT, YDT, ACC_OUT, false, true>(pb, q, act_scale, M, y, acc_out, wave_id,
                                                        gridDim.x * 4, lds_sk);

@@ -362,7 +362,7 @@ __device__ __forceinline__ void load8(const void* p, int64_t i, float v[8]) {
 }
 
 template <int XDT, int NT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT <= 2 ? 2 : 3))) void skinny_kernel(const void* __restrict__ x, int rms,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT <= 2 ? 2 : 3))) void skinny_f32_kernel(const void* __restrict__ x, int rms,
                                                      float eps, const float* __restrict__ w, int M,
                                                      int N, int K, const float* __restrict__ mag,
                                                      const float* __restrict__ bias, void* y,
@@ -514,13 +514,13 @@ static void launch_skinny(const void* x, int rms, const float* w, int M, int N, 
     const float eps = 1e-6f;
     const dim3 grid((M + kSkinnyRows - 1) / kSkinnyRows);
     switch ((N + 15) / 16) {
-        case 1: hipLaunchKernelGGL((skinny_kernel<XDT, 1>), grid, dim3(256), 0, st, x, rms, eps, w,
+        case 1: hipLaunchKernelGGL((skinny_f32_kernel<XDT, 1>), grid, dim3(256), 0, st, x, rms, eps, w,
                                    M, N, K, mag, bias, y, ybf); break;
-        case 2: hipLaunchKernelGGL((skinny_kernel<XDT, 2>), grid, dim3(256), 0, st, x, rms, eps, w,
+        case 2: hipLaunchKernelGGL((skinny_f32_kernel<XDT, 2>), grid, dim3(256), 0, st, x, rms, eps, w,
                                    M, N, K, mag, bias, y, ybf); break;
-        case 3: hipLaunchKernelGGL((skinny_kernel<XDT, 3>), grid, dim3(256), 0, st, x, rms, eps, w,
+        case 3: hipLaunchKernelGGL((skinny_f32_kernel<XDT, 3>), grid, dim3(256), 0, st, x, rms, eps, w,
                                    M, N, K, mag, bias, y, ybf); break;
-        default: hipLaunchKernelGGL((skinny_kernel<XDT, 4>), grid, dim3(256), 0, st, x, rms, eps, w,
+        default: hipLaunchKernelGGL((skinny_f32_kernel<XDT, 4>), grid, dim3(256), 0, st, x, rms, eps, w,
                                     M, N, K, mag, bias, y, ybf); break;
     }
 }
