@@ -305,12 +305,24 @@ def bench_moe_c5(torch, dev, reps=10):
     b.record()
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / reps
+    # per kernel: the same forwards with a stream event after every launch
+    timer = StageTimer(torch)
+    for _ in range(reps):
+        timer.start()
+        layer.forward(x, logits, marker=timer)
+    torch.cuda.synchronize()
+    stages = {n: round(v / reps, 4) for n, v in timer.totals_ms().items()}
     rows, d, f = 8192, 1024, 4096
-    ops_ = 2.0 * (rows * 2) * (2 * f * d)
+    gemm_ops = 2.0 * (rows * 2) * f * d  # one grouped GEMM over the 16384 routed slots
+    ops_ = 2 * gemm_ops
     tops = ops_ / (ms / 1e3) / 1e12
+    per_gemm = {g: {"ms": stages[g], "tops": round(gemm_ops / (stages[g] / 1e3) / 1e12, 1),
+                    "frac_int8_peak": round(gemm_ops / (stages[g] / 1e3) / 1e12 / INT8_PEAK_TOPS,
+                                            4)}
+                for g in ("up", "down")}
     return {"tokens": rows, "experts": 8, "k": 2, "ms": round(ms, 4),
             "tops_whole_forward": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-            "tokens_per_s": round(rows / (ms / 1e3), 1)}
+            "tokens_per_s": round(rows / (ms / 1e3), 1), "stages_ms": stages, "gemms": per_gemm}
 
 
 def bench_decode_gemv(torch, dev, m=1, sets=128, reps=5):

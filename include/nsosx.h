@@ -199,10 +199,14 @@ int nsosx_bitlinear_forward_noalloc(const void* x, int x_dtype, const uint32_t* 
  * (src/jamba.cpp:8086-8098: RMS_PERI and magnitude).
  *   y = (rms_input ? rmsnorm(x, 1e-6) : x) @ w^T, then * magnitude[n], then + bias[n]
  * x: [M, K] (x_dtype); w: f32 [N, K]; y: [M, N] (y_dtype); magnitude, bias:
- * f32 [N] or NULL; rms_workspace: f32 [M] when rms_input.  K % 4 == 0.
- * The normalised input x * inv equals Tensor::rmsnorm bit for bit; the dot
- * products accumulate in fp32 (v_mfma_f32_32x32x2_f32, or a wave reduction
- * for N <= 16 or M <= 16) in an order of their own. */
+ * f32 [N] or NULL; rms_workspace: f32 [M] when rms_input (required; the
+ * skinny shapes below do not use it).  K % 4 == 0.
+ * The dot products accumulate in fp32 in an order of their own: N <= 64 with
+ * M > 16 on v_mfma_f32_16x16x4_f32 in one pass over x, the RMS sums of
+ * squares taken on the way and 1 / rms applied to the dot products (equal to
+ * the dot of the normalised row to rounding); other shapes with the
+ * normalised input x * inv formed bit for bit as Tensor::rmsnorm, on
+ * v_mfma_f32_32x32x2_f32 or, for N <= 16 or M <= 16, a wave reduction. */
 int nsosx_linear_f32(const void* x, int x_dtype, int M, int K, const float* w, int N,
                      int rms_input, const float* magnitude, const float* bias, void* y,
                      int y_dtype, float* rms_workspace, void* stream);

@@ -227,19 +227,25 @@ class MoEFFN:
             self._buf[rows] = b
         return b
 
-    def forward(self, x: torch.Tensor, logits: torch.Tensor, out_dtype=None) -> dict:
+    def forward(self, x: torch.Tensor, logits: torch.Tensor, out_dtype=None,
+                marker=None) -> dict:
         """Returns {"out": a fresh [rows, d_model] tensor, plus the routing tensors and the
         expert hidden / output rows}.  Those extras are views of this layer's per-row-count
-        workspaces: the next forward with the same row count overwrites them."""
+        workspaces: the next forward with the same row count overwrites them.  marker(name),
+        when given, is called after each kernel (route, quant_in, up, quant_hidden, down,
+        combine)."""
         rows = x.shape[0]
         b = self._buffers(rows, x.device)
         e, k = self.experts, self.k
         st = _stream()
+        mk = marker or (lambda name: None)
         call("nsosx_moe_route", _p(logits), rows, e, k, _p(b["weights"]), _p(b["selected"]),
              _p(b["counts"]), _p(b["offsets"]), _p(b["perm"]), _p(b["slot_of"]),
              _p(b["route_ws"]), st)
+        mk("route")
         call("nsosx_quantize_act_i8", _p(x), ops._dt(x), rows, self.d_model, 8,
              int(self.rms_input), _p(b["q1"]), _p(b["s1"]), _p(b["r1"]), st)
+        mk("quant_in")
         slots = rows * k
         if self.mfma:
             call("nsosx_grouped_ternary_gemm_mfma", self.up_views_mfma.ptr, e, _p(b["offsets"]),
@@ -249,8 +255,10 @@ class MoEFFN:
             call("nsosx_grouped_ternary_gemm", self.up_views.ptr, e, _p(b["offsets"]),
                  _p(b["perm"]), 1, _p(b["q1"]), _p(b["s1"]), self.d_model, self.d_ff, rows, slots,
                  1, _p(b["h"]), _DT[self.hidden_dtype], st)
+        mk("up")
         call("nsosx_quantize_act_i8", _p(b["h"]), _DT[self.hidden_dtype], slots, self.d_ff, 8,
              int(self.rms_input), _p(b["q2"]), _p(b["s2"]), _p(b["r2"]), st)
+        mk("quant_hidden")
         if self.mfma:
             call("nsosx_grouped_ternary_gemm_mfma", self.down_views_mfma.ptr, e, _p(b["offsets"]),
                  None, 0, _p(b["q2"]), _p(b["s2"]), self.d_ff, self.d_model, slots, 0, _p(b["o"]),
@@ -259,10 +267,12 @@ class MoEFFN:
             call("nsosx_grouped_ternary_gemm", self.down_views.ptr, e, _p(b["offsets"]), None, 0,
                  _p(b["q2"]), _p(b["s2"]), self.d_ff, self.d_model, rows, slots, 0, _p(b["o"]),
                  _DT[torch.float32], st)
+        mk("down")
         out = torch.empty((rows, self.d_model), dtype=out_dtype or x.dtype, device=x.device)
         call("nsosx_moe_combine", _p(b["o"]), _DT[torch.float32], _p(b["slot_of"]),
              _p(b["selected"]), _p(b["weights"]), rows, e, k, self.d_model, _p(out),
              _DT[out.dtype], st)
+        mk("combine")
         return {"out": out, **{n: b[n] for n in ("weights", "selected", "counts", "offsets",
                                                  "perm", "slot_of", "h", "o")}}
 
