@@ -24,11 +24,9 @@ constexpr int kRouteBlock = 256;  // rows per dispatch block
 // runtime-indexed array of 64 lives in scratch memory); experts past E are
 // masked out.
 template <int EMAX>
-__global__ __launch_bounds__(256) void route_rows_kernel(const float* __restrict__ logits, int rows,
-                                                         int E, int k, float* __restrict__ weights,
-                                                         int32_t* __restrict__ selected) {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= rows) return;
+__device__ __forceinline__ void route_one_row(const float* __restrict__ logits, int r, int E, int k,
+                                              float* __restrict__ weights,
+                                              int32_t* __restrict__ selected, int (&sel)[8]) {
     const float* src = logits + (int64_t)r * E;
     float p[EMAX];
 #pragma unroll
@@ -62,6 +60,7 @@ __global__ __launch_bounds__(256) void route_rows_kernel(const float* __restrict
         }
         taken |= 1ull << best;
         selected[(int64_t)r * k + i] = best;
+        if (i < 8) sel[i] = best;
         ssum = ssum + bv;
     }
     // k == E keeps the raw softmax: the reference masks and renormalises only when
@@ -72,6 +71,38 @@ __global__ __launch_bounds__(256) void route_rows_kernel(const float* __restrict
 #pragma unroll
     for (int j = 0; j < EMAX; ++j)
         if (j < E) w[j] = ((taken >> j) & 1ull) ? (renorm ? p[j] * inv2 : p[j]) : 0.0f;
+}
+
+template <int EMAX>
+__global__ __launch_bounds__(256) void route_rows_kernel(const float* __restrict__ logits, int rows,
+                                                         int E, int k, float* __restrict__ weights,
+                                                         int32_t* __restrict__ selected) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    int sel[8];
+    if (r < rows) route_one_row<EMAX>(logits, r, E, k, weights, selected, sel);
+}
+
+// Routing fused with the per-block expert counts: one thread per row of a
+// dispatch block of kRouteBlock rows, then how many of the block's rows
+// selected each expert (LDS counters; counts are order-free).
+template <int EMAX>
+__global__ __launch_bounds__(256) void route_rows_count_kernel(const float* __restrict__ logits,
+                                                               int rows, int E, int k,
+                                                               float* __restrict__ weights,
+                                                               int32_t* __restrict__ selected,
+                                                               int32_t* __restrict__ block_counts) {
+    __shared__ int32_t cnt[kMaxExperts];
+    const int tid = threadIdx.x;
+    if (tid < E) cnt[tid] = 0;
+    __syncthreads();
+    const int r = blockIdx.x * kRouteBlock + tid;
+    if (r < rows) {
+        int sel[8];
+        route_one_row<EMAX>(logits, r, E, k, weights, selected, sel);
+        for (int i = 0; i < k; ++i) atomicAdd(&cnt[sel[i]], 1);
+    }
+    __syncthreads();
+    if (tid < E) block_counts[(int64_t)blockIdx.x * E + tid] = cnt[tid];
 }
 
 // Per dispatch block of 256 rows: how many of its rows selected each expert.
@@ -153,6 +184,77 @@ __global__ __launch_bounds__(256) void route_assign_kernel(const int32_t* __rest
             for (int w = 0; w < wave; ++w) before += wave_cnt[w][e];
             const int rank = before + __popcll(bal & lt);
             const int slot = offsets[e] + block_base[(int64_t)blockIdx.x * E + e] + rank;
+            perm[slot] = r;
+            slot_of[(int64_t)r * k + which] = slot;
+        }
+    }
+}
+
+// The exclusive scans fused into the assignment, for up to kPlaceMaxBlocks
+// dispatch blocks: every block sums the per-block counts itself (its own base
+// per expert, the totals, the expert offsets), block 0 publishes counts and
+// offsets, then the stable ranks as route_assign_kernel.  Same slots.
+constexpr int kPlaceMaxBlocks = 1024;
+
+__global__ __launch_bounds__(256) void route_place_kernel(const int32_t* __restrict__ selected,
+                                                          int rows, int E, int k, int nblocks,
+                                                          const int32_t* __restrict__ block_counts,
+                                                          int32_t* __restrict__ counts,
+                                                          int32_t* __restrict__ offsets,
+                                                          int32_t* __restrict__ perm,
+                                                          int32_t* __restrict__ slot_of) {
+    __shared__ int32_t base[kMaxExperts], tot[kMaxExperts], off[kMaxExperts + 1];
+    __shared__ int32_t wave_cnt[4][kMaxExperts];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    if (tid < E) {
+        int before = 0, all = 0;
+        for (int b = 0; b < nblocks; ++b) {
+            const int v = block_counts[(int64_t)b * E + tid];
+            before += b < (int)blockIdx.x ? v : 0;
+            all += v;
+        }
+        base[tid] = before;
+        tot[tid] = all;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int j = 0; j < E; ++j) {
+            off[j] = run;
+            run += tot[j];
+        }
+        off[E] = run;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        if (tid < E) counts[tid] = tot[tid];
+        if (tid <= E) offsets[tid] = off[tid];
+    }
+    const int r = blockIdx.x * kRouteBlock + tid;
+    const bool valid = r < rows;
+    int mine[8];
+    const int kk = k < 8 ? k : 8;
+    for (int i = 0; i < kk; ++i) mine[i] = valid ? selected[(int64_t)r * k + i] : -1;
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int e = 0; e < E; ++e) {
+        bool has = false;
+        for (int i = 0; i < kk; ++i) has |= mine[i] == e;
+        const uint64_t bal = __ballot(has);
+        if (lane == 0) wave_cnt[wave][e] = __popcll(bal);
+    }
+    __syncthreads();
+    for (int e = 0; e < E; ++e) {
+        bool has = false;
+        int which = -1;
+        for (int i = 0; i < kk; ++i)
+            if (mine[i] == e) { has = true; which = i; }
+        const uint64_t bal = __ballot(has);
+        if (has) {
+            int before = 0;
+            for (int w = 0; w < wave; ++w) before += wave_cnt[w][e];
+            const int rank = before + __popcll(bal & lt);
+            const int slot = off[e] + base[e] + rank;
             perm[slot] = r;
             slot_of[(int64_t)r * k + which] = slot;
         }
@@ -273,6 +375,21 @@ extern "C" int nsosx_moe_route(const float* logits, int rows, int experts, int k
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int nblocks = (rows + kRouteBlock - 1) / kRouteBlock;
     const dim3 rgrid((rows + 255) / 256), rblock(256);
+    if (!select_only && nblocks <= kPlaceMaxBlocks) {
+        // two launches: routing + block counts, then scans + stable ranks
+        if (experts <= 8)
+            hipLaunchKernelGGL(route_rows_count_kernel<8>, dim3(nblocks), rblock, 0, st, logits,
+                               rows, experts, k, weights, selected, workspace);
+        else if (experts <= 16)
+            hipLaunchKernelGGL(route_rows_count_kernel<16>, dim3(nblocks), rblock, 0, st, logits,
+                               rows, experts, k, weights, selected, workspace);
+        else
+            hipLaunchKernelGGL(route_rows_count_kernel<kMaxExperts>, dim3(nblocks), rblock, 0, st,
+                               logits, rows, experts, k, weights, selected, workspace);
+        hipLaunchKernelGGL(route_place_kernel, dim3(nblocks), rblock, 0, st, selected, rows,
+                           experts, k, nblocks, workspace, counts, offsets, perm, slot_of);
+        return check_launch("moe_route");
+    }
     if (experts <= 8)
         hipLaunchKernelGGL(route_rows_kernel<8>, rgrid, rblock, 0, st, logits, rows, experts, k,
                            weights, selected);
