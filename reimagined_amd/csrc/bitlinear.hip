@@ -1950,7 +1950,7 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
     // activation fragments: fragment (s, mt) of lane l at ((s * MT + mt) * 64 + l) * 16;
     // step s covers k = 64 s .. 64 s + 63, k group g its 16 k from 64 s + 16 g
     constexpr int nfrag = Q * MT * 64;
-    for (int f = tid; f < nfrag; f += 256) {
+    for (int f = tid; f < nfrag; f += blockDim.x) {
         const int l = f & 63;
         const int smt = f >> 6;
         const int mt = smt % MT, st = smt / MT;
@@ -2191,35 +2191,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
                                                      lds_gsk);
 }
 
-template <int MT, int LT, int YDT, bool ACC_OUT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void skinny_kernel(GemvProblem pb, const int8_t* __restrict__ q,
-                                                     const float* __restrict__ act_scale, int M,
-                                                     void* y, int32_t* acc_out) {
+// NW waves per workgroup share one copy of the activation fragments: 4, or 8
+// for two m tiles at K = 2048 (64 KB of fragments), so the LDS that caps the
+// workgroups per CU at one still holds two waves per SIMD.
+template <int MT, int LT, int YDT, bool ACC_OUT, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void skinny_kernel(
+    GemvProblem pb, const int8_t* __restrict__ q, const float* __restrict__ act_scale, int M,
+    void* y, int32_t* acc_out) {
     extern __shared__ __align__(16) char lds_sk[];
     // wave-uniform (readfirstlane): the tile loops then branch on scalars, with exact
     // memory wait counts
-    const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * NW + (threadIdx.x >> 6));
     if ((pb.N & 3) == 0)
         skinny_body<MT, LT, YDT, ACC_OUT, false, true>(pb, q, act_scale, M, y, acc_out, wave_id,
-                                                       gridDim.x * 4, lds_sk);
+                                                       gridDim.x * NW, lds_sk);
     else
         skinny_body<MT, LT, YDT, ACC_OUT, false, false>(pb, q, act_scale, M, y, acc_out, wave_id,
-                                                        gridDim.x * 4, lds_sk);
+                                                        gridDim.x * NW, lds_sk);
 }
 
 template <int MT, int YDT>
 static void launch_skinny_lt(const GemvProblem& pb, const int8_t* q, const float* as, int M,
-                             void* y, int32_t* acc, dim3 grid, size_t lds, hipStream_t st) {
-#define NSOSX_SK(LT)                                                                            \
-    if (acc)                                                                                    \
-        hipLaunchKernelGGL((skinny_kernel<MT, LT, YDT, true>), grid, dim3(256), lds, st, pb, q, as, \
-                           M, y, acc);                                                          \
-    else                                                                                        \
-        hipLaunchKernelGGL((skinny_kernel<MT, LT, YDT, false>), grid, dim3(256), lds, st, pb, q,    \
-                           as, M, y, acc);
-    if (pb.K == 1024) { NSOSX_SK(4) }
-    else if (pb.K == 2048) { NSOSX_SK(8) }
-    else { NSOSX_SK(16) }
+                             void* y, int32_t* acc, int tiles, hipStream_t st) {
+    // about 8 waves per CU: two workgroups of 4 waves (32 KB of fragments), or one of 8
+    // (64 KB); LDS = the fragments (M_pad x K bytes) + one tile per wave (16 rows of K / 4)
+#define NSOSX_SK(LT, NW_)                                                                       \
+    {                                                                                           \
+        constexpr int NW = (NW_);                                                               \
+        const int wgs = std::max(1, std::min((tiles + NW - 1) / NW, NW == 4 ? 512 : 256));      \
+        const size_t lds = (size_t)MT * pb.K * 16 + (size_t)NW * 4 * pb.K;                     \
+        if (acc)                                                                                \
+            hipLaunchKernelGGL((skinny_kernel<MT, LT, YDT, true, NW>), dim3(wgs), dim3(NW * 64), \
+                               lds, st, pb, q, as, M, y, acc);                                  \
+        else                                                                                    \
+            hipLaunchKernelGGL((skinny_kernel<MT, LT, YDT, false, NW>), dim3(wgs), dim3(NW * 64), \
+                               lds, st, pb, q, as, M, y, acc);                                  \
+    }
+    // (K = 4096: 64 KB of fragments + 4 waves' 16 KB tiles already fill 128 KB of the
+    // 160 KB, so it stays at one workgroup of 4 waves)
+    if (pb.K == 1024) NSOSX_SK(4, 4)
+    else if (pb.K == 2048) NSOSX_SK(8, MT == 1 ? 4 : 8)
+    else NSOSX_SK(16, 4)
 #undef NSOSX_SK
 }
 
@@ -2227,13 +2239,9 @@ template <int YDT>
 static void launch_skinny_t(const GemvProblem& pb, const int8_t* q, const float* as, int M,
                             void* y, int32_t* acc, hipStream_t st) {
     const int tiles = (pb.N + 15) / 16;
-    // about 8 waves per CU in all; the LDS fragments (up to 64 KB) allow 2 workgroups
-    const int wgs = std::max(1, std::min((tiles + 3) / 4, 512));
     const int mt = (M + 15) / 16;
-    // activation fragments + one tile per wave (16 rows of K / 4 bytes)
-    const size_t lds = (size_t)(mt + 1) * pb.K * 16;
-    if (mt == 1) launch_skinny_lt<1, YDT>(pb, q, as, M, y, acc, dim3(wgs), lds, st);
-    else launch_skinny_lt<2, YDT>(pb, q, as, M, y, acc, dim3(wgs), lds, st);
+    if (mt == 1) launch_skinny_lt<1, YDT>(pb, q, as, M, y, acc, tiles, st);
+    else launch_skinny_lt<2, YDT>(pb, q, as, M, y, acc, tiles, st);
 }
 
 // ===========================================================================
