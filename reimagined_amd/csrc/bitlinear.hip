@@ -1521,8 +1521,10 @@ __device__ __forceinline__ void gemm3_epilogue(const GemmProblem& pb,
 // row one aligned 128-byte line.  In a slice, 16-byte chunk c of row r sits in
 // slot c ^ ((r / 2) % 8), so neither the 8-byte writes (32 rows, one chunk)
 // nor the 16-byte reads (8 rows, 8 chunks) conflict on the 64 banks.
-// Magnitude, bias and every output pointer must be 16-byte aligned.
-template <bool GATHER, bool SQRELU>
+// Magnitude, bias and every output pointer must be 16-byte aligned.  MAG / BIAS
+// are template arguments (the caller branches once on the pointers): as runtime
+// conditions the compiler formed both results per element and selected one.
+template <bool GATHER, bool SQRELU, bool MAG, bool BIAS>
 __device__ __forceinline__ void gemm3_epilogue_rows(const GemmProblem& pb,
                                                     const float* __restrict__ act_scale,
                                                     const int32_t* __restrict__ perm, int seg_begin,
@@ -1533,8 +1535,6 @@ __device__ __forceinline__ void gemm3_epilogue_rows(const GemmProblem& pb,
     const int g = lane >> 5;
     const int li = lane & 31;
     const int nw = n0 + wave * 64 + 4 * g;  // this lane's first output column
-    const bool has_mag = pb.mag != nullptr;
-    const bool has_bias = pb.bias != nullptr;
     float comb[4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
@@ -1549,8 +1549,8 @@ __device__ __forceinline__ void gemm3_epilogue_rows(const GemmProblem& pb,
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
             const int n = nw + nb * 32 + 8 * q4;
-            const float4 mg = has_mag ? *reinterpret_cast<const float4*>(pb.mag + n) : float4{};
-            const float4 bs = has_bias ? *reinterpret_cast<const float4*>(pb.bias + n) : float4{};
+            const float4 mg = MAG ? *reinterpret_cast<const float4*>(pb.mag + n) : float4{};
+            const float4 bs = BIAS ? *reinterpret_cast<const float4*>(pb.bias + n) : float4{};
             const float mv[4] = {mg.x, mg.y, mg.z, mg.w};
             const float bv[4] = {bs.x, bs.y, bs.z, bs.w};
             const int c = nb * 4 + q4;
@@ -1561,8 +1561,8 @@ __device__ __forceinline__ void gemm3_epilogue_rows(const GemmProblem& pb,
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     float v = __fmul_rn(static_cast<float>(a[4 * q4 + r]), comb[mb]);
-                    if (has_mag) v = __fmul_rn(v, mv[r]);
-                    if (has_bias) v = __fadd_rn(v, bv[r]);
+                    if (MAG) v = __fmul_rn(v, mv[r]);
+                    if (BIAS) v = __fadd_rn(v, bv[r]);
                     if (SQRELU) {
                         v = v > 0.0f ? v : 0.0f;
                         v = __fmul_rn(v, v);
@@ -1657,8 +1657,16 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
         if (y && n0 + kG3BN <= pb.N && (pb.N & 7) == 0 &&
             ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(pb.mag) |
               reinterpret_cast<uintptr_t>(pb.bias)) & 15) == 0) {
-            gemm3_epilogue_rows<GATHER, SQRELU>(pb, act_scale, perm, seg_begin, seg_rows, n0, m0,
-                                                static_cast<uint16_t*>(y), acc, smem);
+            uint16_t* yb = static_cast<uint16_t*>(y);
+#define NSOSX_EPI(MG, BS)                                                                       \
+    gemm3_epilogue_rows<GATHER, SQRELU, MG, BS>(pb, act_scale, perm, seg_begin, seg_rows, n0, m0, \
+                                                yb, acc, smem)
+            if (pb.mag) {
+                if (pb.bias) NSOSX_EPI(true, true); else NSOSX_EPI(true, false);
+            } else {
+                if (pb.bias) NSOSX_EPI(false, true); else NSOSX_EPI(false, false);
+            }
+#undef NSOSX_EPI
             return;
         }
     }
