@@ -298,11 +298,13 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
 // through the wave's LDS slice then hands every lane all four tokens' delta and
 // delta * x (two reads instead of eight VALU broadcasts).  The recurrence runs
 // the four tokens, the 4x4 transpose-reduce leaves lane q with the readout of token
-// r0 + q, and lane q applies the D skip and the SiLU(z) gate and stores it.
-// B and C (shared by all channels of a group) are staged per 32-token chunk
-// in the wave's own LDS slice, converted to float once.  There is no
-// workgroup barrier: the raw inputs of the next group and the B/C rows of the
-// next chunk are loaded into registers one step ahead.
+// r0 + q, and lane q applies the D skip and the SiLU(z) gate and writes it to the
+// chunk's output rows in LDS; a finished 32-token chunk leaves with one 16-byte
+// store per lane.  B and C (shared by all channels of a group) are staged per
+// 32-token chunk in the wave's own LDS slice, converted to float once.  The
+// workgroup is one wave, so its barriers cost no waiting: the raw inputs of the
+// next group and the B/C rows of the next chunk are loaded into registers one
+// step ahead.
 // ===========================================================================
 constexpr int kQuadTC = 32;       // tokens per B/C chunk
 constexpr int kQuadCh = 16;       // channels per wave
