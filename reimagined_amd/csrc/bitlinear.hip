@@ -150,19 +150,22 @@ __global__ __launch_bounds__(64) void rms_inv_tiled_kernel(const void* __restric
 constexpr int kRmsPcPitch = 64 + 4;  // floats per LDS row (one tile of 64 squares + pad)
 constexpr int kRmsPcDepth = 8;       // tiles in flight per producer wave
 
-template <int DT>
-__global__ __launch_bounds__(192) void rms_inv_pc_kernel(const void* __restrict__ x, int M, int K,
-                                                         float eps, float* __restrict__ inv) {
+// NP producer waves of 32 rows each (the group is 32 NP rows): 2, or 1 where
+// two-wave groups would leave the CUs with fewer than two groups each.
+template <int DT, int NP>
+__global__ __launch_bounds__((NP + 1) * 64) void rms_inv_pc_kernel(const void* __restrict__ x,
+                                                                   int M, int K, float eps,
+                                                                   float* __restrict__ inv) {
     constexpr int ES = DT == NSOSX_F32 ? 4 : 2;
     constexpr int PER = 16 / ES;            // elements per 16-byte piece
     constexpr int TE = kRmsTileBytes / ES;  // elements of a row per tile
-    __shared__ __align__(16) float s_sq[2][64 * kRmsPcPitch];
+    __shared__ __align__(16) float s_sq[2][32 * NP * kRmsPcPitch];
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const int row0 = blockIdx.x * 64;
+    const int row0 = blockIdx.x * 32 * NP;
     const int tiles = K / TE;
     const int64_t row_bytes = (int64_t)K * ES;
-    if (wave < 2) {
+    if (wave < NP) {
         // load j (0..3) of a tile: row 32 wave + 8 j + lane / 8, 16-byte piece lane % 8;
         // rows past M re-read the last row and tiles past the end the last tile
         const char* src[4];
@@ -214,7 +217,8 @@ __global__ __launch_bounds__(192) void rms_inv_pc_kernel(const void* __restrict_
     } else {
         // one tile behind the producers: tile t - 1 during their tile t, the last after the loop
         float sum = 0.0f;
-        const int off = lane * kRmsPcPitch;
+        // (with one producer wave, lanes 32-63 repeat row 31's sums and store nothing)
+        const int off = min(lane, 32 * NP - 1) * kRmsPcPitch;
         auto add_tile = [&](int t) {
             const float* my = s_sq[t & 1] + off;
 #pragma unroll
@@ -232,7 +236,7 @@ __global__ __launch_bounds__(192) void rms_inv_pc_kernel(const void* __restrict_
         }
         add_tile(tiles - 1);
         const int row = row0 + lane;
-        if (row < M) {
+        if (lane < 32 * NP && row < M) {
             const float mean = __fdiv_rn(sum, static_cast<float>(K));
             inv[row] = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
         }
@@ -572,12 +576,18 @@ static void launch_rms_inv_t(const void* x, int M, int K, float eps, float* inv,
         hipLaunchKernelGGL((rms_inv_small_kernel<DT>), dim3(M), dim3(256), 0, st, x, K, eps, inv);
     } else if (((int64_t)K * elem) % (kRmsTileBytes * kRmsDepth) == 0 &&
                reinterpret_cast<uintptr_t>(x) % 16 == 0) {
-        // fewer than 512 groups of 64 rows: the three-wave form (config 5's 16384 hidden rows of
-        // 4096 in 33 us, its 8192 input rows of 1024 in 5 us less); with more groups the one-wave
-        // form streams faster (config 4: 40796 rows of 1024 / 2048, 3 / 6 us less)
-        if ((M + 63) / 64 < 512 && ((int64_t)K * elem) % (kRmsTileBytes * kRmsPcDepth) == 0)
-            hipLaunchKernelGGL((rms_inv_pc_kernel<DT>), dim3((M + 63) / 64), dim3(192), 0, st, x, M,
-                               K, eps, inv);
+        // fewer than 512 groups of 64 rows: the producer / consumer form (config 5's 16384
+        // hidden rows of 4096 in 33 us; its 8192 input rows of 1024, 128 groups, as 256 groups
+        // of 32 rows); with more groups the one-wave form streams faster (config 4: 40796 rows
+        // of 1024 / 2048, 3 / 6 us less)
+        if ((M + 63) / 64 < 512 && ((int64_t)K * elem) % (kRmsTileBytes * kRmsPcDepth) == 0) {
+            if ((M + 63) / 64 <= 128)
+                hipLaunchKernelGGL((rms_inv_pc_kernel<DT, 1>), dim3((M + 31) / 32), dim3(128), 0, st,
+                                   x, M, K, eps, inv);
+            else
+                hipLaunchKernelGGL((rms_inv_pc_kernel<DT, 2>), dim3((M + 63) / 64), dim3(192), 0, st,
+                                   x, M, K, eps, inv);
+        }
         else
             hipLaunchKernelGGL((rms_inv_tiled_kernel<DT>), dim3((M + 63) / 64), dim3(64), 0, st, x,
                                M, K, eps, inv);

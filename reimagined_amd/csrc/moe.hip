@@ -190,11 +190,12 @@ __global__ __launch_bounds__(256) void route_assign_kernel(const int32_t* __rest
     }
 }
 
-// The exclusive scans fused into the assignment, for up to kPlaceMaxBlocks
-// dispatch blocks: every block sums the per-block counts itself (its own base
-// per expert, the totals, the expert offsets), block 0 publishes counts and
-// offsets, then the stable ranks as route_assign_kernel.  Same slots.
-constexpr int kPlaceMaxBlocks = 1024;
+// The exclusive scans fused into the assignment, for up to kPlaceMaxCounts
+// per-block counts (dispatch blocks x experts): every block reads all the counts
+// into LDS in one coalesced pass and sums them itself (its own base per expert,
+// the totals, the expert offsets), block 0 publishes counts and offsets, then
+// the stable ranks as route_assign_kernel.  Same slots.
+constexpr int kPlaceMaxCounts = 4096;
 
 __global__ __launch_bounds__(256) void route_place_kernel(const int32_t* __restrict__ selected,
                                                           int rows, int E, int k, int nblocks,
@@ -205,12 +206,15 @@ __global__ __launch_bounds__(256) void route_place_kernel(const int32_t* __restr
                                                           int32_t* __restrict__ slot_of) {
     __shared__ int32_t base[kMaxExperts], tot[kMaxExperts], off[kMaxExperts + 1];
     __shared__ int32_t wave_cnt[4][kMaxExperts];
+    __shared__ int32_t s_counts[kPlaceMaxCounts];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < nblocks * E; i += blockDim.x) s_counts[i] = block_counts[i];
+    __syncthreads();
     if (tid < E) {
         int before = 0, all = 0;
         for (int b = 0; b < nblocks; ++b) {
-            const int v = block_counts[(int64_t)b * E + tid];
+            const int v = s_counts[b * E + tid];
             before += b < (int)blockIdx.x ? v : 0;
             all += v;
         }
@@ -375,7 +379,7 @@ extern "C" int nsosx_moe_route(const float* logits, int rows, int experts, int k
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int nblocks = (rows + kRouteBlock - 1) / kRouteBlock;
     const dim3 rgrid((rows + 255) / 256), rblock(256);
-    if (!select_only && nblocks <= kPlaceMaxBlocks) {
+    if (!select_only && (int64_t)nblocks * experts <= kPlaceMaxCounts) {
         // two launches: routing + block counts, then scans + stable ranks
         if (experts <= 8)
             hipLaunchKernelGGL(route_rows_count_kernel<8>, dim3(nblocks), rblock, 0, st, logits,
