@@ -458,8 +458,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
     const bool bc_vec = (SPL == 4) && N == 16 && (GN % 8) == 0 &&
                         ((reinterpret_cast<uintptr_t>(Bm) | reinterpret_cast<uintptr_t>(Cm)) & 15) == 0;
     constexpr int BCW = ADT == NSOSX_F32 ? BCN : (BCN + 1) / 2;  // dwords per lane per row
-    uint32_t bcv[2][BCW > 0 ? BCW : 1];
-    raw_t bcs[2][BCN];
+    // one register set for both load forms, in the vector load's word format (bf16:
+    // state 2i in the low half of word i, 2i + 1 in the high half): two arrays chosen
+    // by the runtime bc_vec were kept in scratch memory
+    uint32_t bcraw[2][BCW];
     int bc_ok = 0;
     auto prefetch_bc = [&](int tb) {
         bc_ok = 0;
@@ -475,19 +477,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
 #pragma unroll
                     for (int w4 = 0; w4 < BCW / 4; ++w4) {
                         const u32x4 v = src[w4];
-                        bcv[pass][4 * w4 + 0] = v.x; bcv[pass][4 * w4 + 1] = v.y;
-                        bcv[pass][4 * w4 + 2] = v.z; bcv[pass][4 * w4 + 3] = v.w;
+                        bcraw[pass][4 * w4 + 0] = v.x; bcraw[pass][4 * w4 + 1] = v.y;
+                        bcraw[pass][4 * w4 + 2] = v.z; bcraw[pass][4 * w4 + 3] = v.w;
                     }
                 } else {
                     src = (const global_u32x4*)((const uint16_t*)smat + base);
                     const u32x4 v = src[0];
-                    bcv[pass][0] = v.x; bcv[pass][1] = v.y; bcv[pass][2] = v.z; bcv[pass][3] = v.w;
+                    bcraw[pass][0] = v.x; bcraw[pass][1] = v.y;
+                    bcraw[pass][2] = v.z; bcraw[pass][3] = v.w;
                 }
             } else {
 #pragma unroll
                 for (int j = 0; j < BCN; ++j) {
                     const int n = shalf * BCN + j;
-                    bcs[pass][j] = load_raw<ADT>(smat, n < N ? base + j : 0);
+                    const uint32_t r = n < N ? static_cast<uint32_t>(load_raw<ADT>(smat, base + j)) : 0u;
+                    if (ADT == NSOSX_F32) bcraw[pass][j] = r;
+                    else if (j & 1) bcraw[pass][j >> 1] |= r << 16;
+                    else bcraw[pass][j >> 1] = r;
                 }
             }
         }
@@ -497,21 +503,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
         for (int pass = 0; pass < 2; ++pass) {
             const bool ok = (bc_ok >> pass) & 1;
             float v[BCN];
-            if (bc_vec) {
 #pragma unroll
-                for (int j = 0; j < BCN; ++j) {
-                    if (ADT == NSOSX_F32) {
-                        v[j] = __uint_as_float(bcv[pass][j]);
-                    } else {
-                        const uint32_t wd = bcv[pass][j >> 1];
-                        v[j] = __uint_as_float((j & 1) ? (wd & 0xFFFF0000u) : (wd << 16));
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < BCN; ++j) {
-                    const int n = shalf * BCN + j;
-                    v[j] = n < N ? raw_to_f32<ADT>(bcs[pass][j]) : 0.0f;
+            for (int j = 0; j < BCN; ++j) {
+                if (ADT == NSOSX_F32) {
+                    v[j] = __uint_as_float(bcraw[pass][j]);
+                } else {
+                    const uint32_t wd = bcraw[pass][j >> 1];
+                    v[j] = __uint_as_float((j & 1) ? (wd & 0xFFFF0000u) : (wd << 16));
                 }
             }
 #pragma unroll
