@@ -960,9 +960,12 @@ __global__ __launch_bounds__(256) void conv1d_kernel(const void* __restrict__ in
                                                      const int32_t* __restrict__ cu_seqlens,
                                                      int num_seqs, int T, int C, int W, int silu,
                                                      void* __restrict__ out) {
-    const int c = blockIdx.y * blockDim.x + threadIdx.x;
-    const int t = blockIdx.x;
-    if (c >= C || t >= T) return;
+    // thread = (token, channel) over the flat [T, C] output, so few channels (B and C
+    // of a group: 16) still fill whole waves
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)T * C) return;
+    const int t = static_cast<int>(i / C);
+    const int c = static_cast<int>(i - (int64_t)t * C);
     int lo = 0, hi = num_seqs;  // find s with cu[s] <= t < cu[s+1]
     while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
@@ -1465,7 +1468,9 @@ extern "C" int nsosx_conv1d_causal(const void* in, int in_dtype, int64_t in_stri
         return fail(NSOSX_ERR_INVALID, "conv1d_causal: bad dtype");
     if (total_tokens == 0) return NSOSX_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const dim3 grid(total_tokens, (channels + 255) / 256), block(256);
+    const int64_t elems = (int64_t)total_tokens * channels;
+    if (elems > (int64_t)256 * 0x7FFFFFFF) return fail(NSOSX_ERR_OVERFLOW, "conv1d_causal: too large");
+    const dim3 grid(static_cast<unsigned>((elems + 255) / 256)), block(256);
 #define NSOSX_CONV(I, O)                                                                        \
     hipLaunchKernelGGL((conv1d_kernel<I, O>), grid, block, 0, st, in, in_stride, weight, bias,    \
                        cu_seqlens, num_seqs, total_tokens, channels, width, apply_silu, out);
