@@ -164,7 +164,10 @@ def bitlinear_cases() -> dict:
     cases = [("rms_mag_bias", 8, 256, 48, False, True, True),
              ("rms_mag", 5, 128, 32, False, True, False),
              ("exact", 6, 192, 40, True, False, False),
-             ("exact_bias", 3, 64, 24, True, False, True)]
+             ("exact_bias", 3, 64, 24, True, False, True),
+             # more than 16 rows and at most 64 outputs: the float path's skinny MFMA form
+             ("gate_rms_mag", 40, 256, 8, False, True, False),
+             ("exact_wide_bias", 33, 128, 64, True, False, True)]
     for name, m, k, n, exact, has_mag, has_bias in cases:
         w = _h(rng, (n, k), scale=0.05)
         x = _h(rng, (m, k))

@@ -29,7 +29,8 @@ def test_rms_peri_codes_match_reference(dev, k):
                                   g[f"rms_k{k}__scales"].view(np.uint32))
 
 
-@pytest.mark.parametrize("name", ["rms_mag_bias", "rms_mag", "exact", "exact_bias"])
+@pytest.mark.parametrize("name", ["rms_mag_bias", "rms_mag", "exact", "exact_bias", "gate_rms_mag",
+                                  "exact_wide_bias"])
 def test_bitlinear_packed_forward_matches_reference(dev, orc, name):
     g = _g("bitlinear_ref.npz")
     f = lambda key: (torch.from_numpy(g[f"{name}__{key}"].astype(np.float32)).to(dev)

@@ -54,7 +54,8 @@ def test_linear_f32_bf16_io(dev, orc, m, n, k):
     _close(y.float().cpu().numpy(), want, rtol=2e-2, atol=2e-2)
 
 
-@pytest.mark.parametrize("name", ["rms_mag_bias", "rms_mag", "exact", "exact_bias"])
+@pytest.mark.parametrize("name", ["rms_mag_bias", "rms_mag", "exact", "exact_bias", "gate_rms_mag",
+                                  "exact_wide_bias"])
 def test_linear_f32_matches_reference_golden(dev, name):
     g = np.load(GOLDEN, allow_pickle=False)
     f = lambda key: (torch.from_numpy(g[f"{name}__{key}"].astype(np.float32)).to(dev)
@@ -93,7 +94,8 @@ def test_ste_backward_matches_oracle(dev, orc, m, k, n, rms, with_mag, use_bias)
     assert np.all(got["dW"][clip] == 0.0)
 
 
-@pytest.mark.parametrize("name", ["rms_mag_bias", "rms_mag", "exact", "exact_bias"])
+@pytest.mark.parametrize("name", ["rms_mag_bias", "rms_mag", "exact", "exact_bias", "gate_rms_mag",
+                                  "exact_wide_bias"])
 def test_ste_backward_matches_reference_golden(dev, orc, name):
     g = np.load(GOLDEN, allow_pickle=False)
     f = lambda key: g[f"{name}__{key}"].astype(np.float32) if f"{name}__{key}" in g.files else None

@@ -92,7 +92,8 @@ def test_rmsnorm_backward_bit_exact(orc, tg, k):
     _bits_equal(dx, tg[f"rmsbwd_k{k}__dx"], f"rmsnorm_backward K={k}")
 
 
-CASES = ["rms_mag_bias", "rms_mag", "exact", "exact_bias"]
+CASES = ["rms_mag_bias", "rms_mag", "exact", "exact_bias", "gate_rms_mag",
+                                  "exact_wide_bias"]
 
 
 def _case(bg, name):
