@@ -683,6 +683,31 @@ constexpr int kGemvDepth = 8;   // weight loads in flight per lane
 template <int MT>
 constexpr int gemv_steps() { return MT <= 2 ? 16 : (MT <= 4 ? 8 : 4); }
 
+// A small matrix (fewer than kGemvShortBlocks blocks of the default depth, e.g. a
+// 1024 x 2048 projection: 32 waves) is latency-bound: its waves then take
+// kGemvShortSteps steps each, all loads of a wave in flight at once, so the matrix is
+// spread over several times more waves and a wave waits for one memory round trip
+// instead of two.
+constexpr int kGemvShortSteps = 4;
+constexpr int kGemvShortBlocks = 512;
+
+// lanes that share a row: one 16-byte chunk (64 weights) each, up to the whole wave
+__host__ __device__ inline int gemv_lpr(int K) {
+    const int cpr = ((K >> 4) + 3) >> 2;
+    int lpr = 1;
+    while (lpr < cpr && lpr < 64) lpr <<= 1;
+    return lpr;
+}
+
+// steps per block for `sets` matrices [N, K] in one launch at MT token rows
+__host__ __device__ inline int gemv_steps_for(int MT, int N, int K, int sets) {
+    const int sd = MT <= 2 ? 16 : (MT <= 4 ? 8 : 4);
+    if (sd <= kGemvShortSteps || (K & 63) != 0) return sd;
+    const int rows = sd * (64 / gemv_lpr(K));
+    const int64_t blocks = (int64_t)((N + rows - 1) / rows) * sets;
+    return blocks < kGemvShortBlocks ? kGemvShortSteps : sd;
+}
+
 // Weight and activation loads of the GEMV are branch-free, so that the
 // compiler counts the loads in flight exactly instead of draining them at every
 // branch.  Out-of-range indices are clamped into the buffers instead: a row
@@ -806,7 +831,7 @@ __device__ __forceinline__ void gemv_finish(int (&part)[STEPS][MT], const GemvPr
 // weight loads of the next D items in flight, across round and block
 // boundaries.  The activation fragment stays in registers while K <= 64 * lpr
 // (one round); longer rows reload it at each round.
-template <int MT, int YDT, bool ACC_OUT, bool AL, bool SQRELU = false>
+template <int MT, int YDT, bool ACC_OUT, bool AL, int STEPS, bool SQRELU = false>
 __device__ __forceinline__ void gemv_body_impl(const GemvProblem& pb,
                                                const int8_t* __restrict__ q,
                                                const float* __restrict__ act_scale, int M,
@@ -821,7 +846,6 @@ __device__ __forceinline__ void gemv_body_impl(const GemvProblem& pb,
     const int lr = lane & (lpr - 1);
     const int sub = lane / lpr;
     const int rounds = (cpr + lpr - 1) / lpr;
-    constexpr int STEPS = gemv_steps<MT>();
     // unaligned rows (rare: K % 64 != 0) keep only two items in flight, as their four
     // word addresses per item would otherwise raise the register count of the kernel
     constexpr int DW = AL ? kGemvDepth : 2;
@@ -872,13 +896,18 @@ __device__ __forceinline__ void gemv_body_long(const GemvProblem& pb,
                                                const int8_t* __restrict__ q,
                                                const float* __restrict__ act_scale, int M,
                                                void* y, int32_t* acc_out, int wave_id,
-                                               int num_waves) {
-    if ((pb.K & 63) == 0)
-        gemv_body_impl<MT, YDT, ACC_OUT, true, SQRELU>(pb, q, act_scale, M, y, acc_out, wave_id,
-                                                       num_waves);
+                                               int num_waves, int sets) {
+    constexpr int SD = gemv_steps<MT>();
+    if ((pb.K & 63) != 0)
+        gemv_body_impl<MT, YDT, ACC_OUT, false, SD, SQRELU>(pb, q, act_scale, M, y, acc_out,
+                                                            wave_id, num_waves);
+    else if (SD > kGemvShortSteps && gemv_steps_for(MT, pb.N, pb.K, sets) == kGemvShortSteps)
+        gemv_body_impl<MT, YDT, ACC_OUT, true, kGemvShortSteps, SQRELU>(pb, q, act_scale, M, y,
+                                                                        acc_out, wave_id,
+                                                                        num_waves);
     else
-        gemv_body_impl<MT, YDT, ACC_OUT, false, SQRELU>(pb, q, act_scale, M, y, acc_out, wave_id,
-                                                        num_waves);
+        gemv_body_impl<MT, YDT, ACC_OUT, true, SD, SQRELU>(pb, q, act_scale, M, y, acc_out,
+                                                           wave_id, num_waves);
 }
 
 template <int MT, int YDT, bool ACC_OUT>
@@ -889,7 +918,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvProblem pb, const int8_t*
     // memory wait counts
     const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
     const int num_waves = gridDim.x * 4;
-    gemv_body_long<MT, YDT, ACC_OUT>(pb, q, act_scale, M, y, acc_out, wave_id, num_waves);
+    gemv_body_long<MT, YDT, ACC_OUT>(pb, q, act_scale, M, y, acc_out, wave_id, num_waves, 1);
 }
 
 // A group of a grouped GEMV with M >= 2 rows that the skinny MFMA body takes:
@@ -923,17 +952,11 @@ __global__ __launch_bounds__(256) void grouped_gemv_kernel(const nsosx_linear_vi
     const int num_waves = gridDim.x * 4;
     const int gi = g / q_div;
     gemv_body_long<MT, YDT, false, SQRELU>(pb, q + gi * q_stride, act_scale + gi * scale_stride,
-                                           M, yb, nullptr, wave_id, num_waves);
+                                           M, yb, nullptr, wave_id, num_waves, gridDim.y);
 }
 
-static int gemv_steps_host(int M) { return M <= 2 ? 16 : (M <= 4 ? 8 : 4); }
-
 static int gemv_blocks(int N, int K, int M) {
-    const int W16 = K / 16;
-    const int cpr = (W16 + 3) / 4;
-    int lpr = 1;
-    while (lpr < cpr && lpr < 64) lpr <<= 1;
-    const int rows = gemv_steps_host(M) * (64 / lpr);
+    const int rows = gemv_steps_for(M, N, K, 1) * (64 / gemv_lpr(K));
     return (N + rows - 1) / rows;
 }
 

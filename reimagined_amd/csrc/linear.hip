@@ -293,17 +293,38 @@ __global__ __launch_bounds__(256) void dot_kernel(const void* __restrict__ x,
     float acc[kDotMax];
 #pragma unroll
     for (int j = 0; j < kDotMax; ++j) acc[j] = 0.0f;
-    auto xval = [&](int m, int k) {
-        float v = load_act<XDT>(x, (int64_t)m * K + k);
-        return inv ? __fmul_rn(v, inv[m]) : v;
+    // four consecutive k per lane per step (K % 4 == 0, 16-byte aligned rows), so a
+    // step's loads are 16 bytes wide and a row of 1024 takes four steps, not sixteen
+    auto load4 = [&](const void* base, int dt, int64_t off, float v[4]) {
+        if (dt == NSOSX_F32) {
+            const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        } else {
+            const uint2 a = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
+            v[0] = __uint_as_float(a.x << 16); v[1] = __uint_as_float(a.x & 0xFFFF0000u);
+            v[2] = __uint_as_float(a.y << 16); v[3] = __uint_as_float(a.y & 0xFFFF0000u);
+        }
     };
-    for (int k = lane; k < K; k += 64) {
-        const float mine = PER_M ? xval(row, k) : w[(int64_t)row * K + k];
+    auto xval4 = [&](int m, int k, float v[4]) {
+        load4(x, XDT, (int64_t)m * K + k, v);
+        if (inv) {
+            const float s = inv[m];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = __fmul_rn(v[e], s);
+        }
+    };
+    for (int k = 4 * lane; k < K; k += 256) {
+        float mine[4];
+        if (PER_M) xval4(row, k, mine);
+        else load4(w, NSOSX_F32, (int64_t)row * K + k, mine);
 #pragma unroll
         for (int j = 0; j < kDotMax; ++j) {
             if (j < nsmall) {
-                const float other = PER_M ? w[(int64_t)j * K + k] : xval(j, k);
-                acc[j] = __fmaf_rn(mine, other, acc[j]);
+                float other[4];
+                if (PER_M) load4(w, NSOSX_F32, (int64_t)j * K + k, other);
+                else xval4(j, k, other);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[j] = __fmaf_rn(mine[e], other[e], acc[j]);
             }
         }
     }
