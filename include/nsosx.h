@@ -351,6 +351,37 @@ int nsosx_selective_scan_step(const void* x, const void* dt, const float* A_log,
                               int rows, int H, int P, int N, int G, int act_dtype, float* state,
                               void* y, void* stream);
 
+/* The faithful Mamba-2 decode step after its projections, in one launch
+ * (Mamba2SSD streaming step, src/mamba2.cpp:4038-4125 from the conv ring to
+ * out_proj's input; GPU twins launch_mamba2_faithful_conv_step and
+ * launch_mamba2_faithful_step, src/cuda/mamba_kernels.cu:3332-3419, then the
+ * gated norm and BitLinear::quantize_activations_bitnet, src/bitlinear.cpp:240-291
+ * with src/bitlinear_quantize_avx2.cpp:65-103): per row,
+ *   conv ring step + SiLU over the inner + 2*G*N channels x | B | C;
+ *   state = decay * state + delta * B * x; y = D * x + state . C;
+ *   normed = RMSNorm(y * SiLU(z), eps) * norm_w;
+ *   act_scale = (absmax(normed) + 1e-8) / q_max, q = round(normed / act_scale)
+ *   (q_max = 2^(act_bits-1) - 1, 1 at 2 bits), the input of a ternary GEMV.
+ * Two launches: the conv / state step over 64-channel slices of each row, then
+ * the B / C ring shift, norm and quantization per row.
+ * x, z [rows, H*P] and y [rows, H*P] (written: the pre-gate output, the norm's
+ * input) in act_dtype; B, C [rows, G*N] and dt [rows, H] (dt bias included) in act_dtype,
+ * sharing the row stride bcdt_stride; conv_w f32 [H*P + 2*G*N, conv_width],
+ * conv_b f32 [H*P + 2*G*N] or NULL; ring f32 [rows, conv_width - 1, H*P + 2*G*N]
+ * (the reference's single ring); A_log, D f32 [H]; norm_w f32 [H*P] or NULL;
+ * state f32 [rows, H*P, N], 16-byte aligned; q int8 [rows, H*P];
+ * act_scale f32 [rows].  Limits: rows <= 65535, H*P <= 8192, G*N <= 1024,
+ * N in {4, 8, 16, 32, 64} (the reference's MAX_N is 64), 1 <= conv_width <= 4.  The values equal nsosx_conv_step (x, B, C) +
+ * nsosx_selective_scan_step + nsosx_rmsnorm_gated + nsosx_quantize_act_i8 bit
+ * for bit when H*P is a multiple of 512 up to 4096 (the gated norm's register
+ * path sums in the same order); otherwise to that sum's rounding. */
+int nsosx_mamba2_step(const void* x, const void* z, const void* B, const void* C, const void* dt,
+                      int64_t bcdt_stride, const float* conv_w, const float* conv_b,
+                      int conv_width, float* ring, const float* A_log, const float* D,
+                      const float* norm_w, float eps, int rows, int H, int P, int N, int G,
+                      int act_dtype, float* state, void* y, int8_t* q, float* act_scale,
+                      int act_bits, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Top-k MoE routing.
  * ------------------------------------------------------------------------- */

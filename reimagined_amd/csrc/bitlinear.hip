@@ -304,15 +304,6 @@ __device__ __forceinline__ void load8(const void* x, int64_t off, float v[8]) {
     }
 }
 
-__device__ __forceinline__ uint32_t pack4_i8(float a, float b, float c, float d) {
-    const uint32_t ia = static_cast<uint32_t>(static_cast<int>(a)) & 0xffu;
-    const uint32_t ib = static_cast<uint32_t>(static_cast<int>(b)) & 0xffu;
-    const uint32_t ic = static_cast<uint32_t>(static_cast<int>(c)) & 0xffu;
-    const uint32_t id = static_cast<uint32_t>(static_cast<int>(d)) & 0xffu;
-    return ia | (ib << 8) | (ic << 16) | (id << 24);
-}
-
-__device__ __forceinline__ float clamp127(float c) { return fminf(fmaxf(c, -127.0f), 127.0f); }
 
 // ===========================================================================
 // Few rows with RMS_PERI (decode): the RMS pass and the quantization in one

@@ -124,11 +124,44 @@ __device__ __forceinline__ void store_act(void* p, int64_t i, float v) {
     }
 }
 
+// Value as stored in the activation dtype and read back (bf16: round to nearest even).
+template <int DT>
+__device__ __forceinline__ float round_act(float v) {
+    if constexpr (DT == NSOSX_F32) return v;
+    else return bf16_to_f32(f32_to_bf16(v));
+}
+
+// ---- activation math ---------------------------------------------------------
+
+// SiLU split on the sign (Tensor::silu, src/tensor.cpp:3261-3282; Mamba2SSD::silu_stable,
+// src/mamba2.cpp:737-739): libm expf, IEEE division
+__device__ __forceinline__ float silu_exact(float v) {
+    const float sig = v >= 0.0f ? 1.0f / (1.0f + expf(-v)) : expf(v) / (1.0f + expf(v));
+    return v * sig;
+}
+
+// int8 codes: clamp to [-127, 127], four codes packed little-endian
+__device__ __forceinline__ float clamp127(float c) { return fminf(fmaxf(c, -127.0f), 127.0f); }
+
+__device__ __forceinline__ uint32_t pack4_i8(float a, float b, float c, float d) {
+    const uint32_t ia = static_cast<uint32_t>(static_cast<int>(a)) & 0xffu;
+    const uint32_t ib = static_cast<uint32_t>(static_cast<int>(b)) & 0xffu;
+    const uint32_t ic = static_cast<uint32_t>(static_cast<int>(c)) & 0xffu;
+    const uint32_t id = static_cast<uint32_t>(static_cast<int>(d)) & 0xffu;
+    return ia | (ib << 8) | (ic << 16) | (id << 24);
+}
+
 // ---- wave reductions (wave64) ---------------------------------------------
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
     return v;
 }
 

@@ -278,7 +278,7 @@ static void launch_f32gemm(const GemmArgs& g, hipStream_t st) {
 //          of W (router gates);
 //   else : wave n holds W[n] and dots it with the M <= 16 rows of x (decode).
 // ---------------------------------------------------------------------------
-template <int XDT, bool PER_M>
+template <int XDT, bool PER_M, int JM>
 __global__ __launch_bounds__(256) void dot_kernel(const void* __restrict__ x,
                                                   const float* __restrict__ inv,
                                                   const float* __restrict__ w, int M, int N,
@@ -290,11 +290,13 @@ __global__ __launch_bounds__(256) void dot_kernel(const void* __restrict__ x,
     const int nbig = PER_M ? M : N;
     const int nsmall = PER_M ? N : M;
     if (row >= nbig) return;
-    float acc[kDotMax];
+    float acc[JM];
 #pragma unroll
-    for (int j = 0; j < kDotMax; ++j) acc[j] = 0.0f;
+    for (int j = 0; j < JM; ++j) acc[j] = 0.0f;
     // four consecutive k per lane per step (K % 4 == 0, 16-byte aligned rows), so a
-    // step's loads are 16 bytes wide and a row of 1024 takes four steps, not sixteen
+    // step's loads are 16 bytes wide; with at most 4 small rows the loads of U = 4
+    // steps (a row of 1024) are issued together, small rows past nsmall and steps
+    // past K re-reading valid addresses (their products are not added)
     auto load4 = [&](const void* base, int dt, int64_t off, float v[4]) {
         if (dt == NSOSX_F32) {
             const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
@@ -313,23 +315,33 @@ __global__ __launch_bounds__(256) void dot_kernel(const void* __restrict__ x,
             for (int e = 0; e < 4; ++e) v[e] = __fmul_rn(v[e], s);
         }
     };
-    for (int k = 4 * lane; k < K; k += 256) {
-        float mine[4];
-        if (PER_M) xval4(row, k, mine);
-        else load4(w, NSOSX_F32, (int64_t)row * K + k, mine);
+    constexpr int U = JM <= 4 ? 4 : 1;
+    for (int k0 = 4 * lane; k0 < K; k0 += 256 * U) {
+        float mine[U][4], other[U][JM][4];
 #pragma unroll
-        for (int j = 0; j < kDotMax; ++j) {
-            if (j < nsmall) {
-                float other[4];
-                if (PER_M) load4(w, NSOSX_F32, (int64_t)j * K + k, other);
-                else xval4(j, k, other);
+        for (int u = 0; u < U; ++u) {
+            const int k = min(k0 + 256 * u, K - 4);
+            if (PER_M) xval4(row, k, mine[u]);
+            else load4(w, NSOSX_F32, (int64_t)row * K + k, mine[u]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[j] = __fmaf_rn(mine[e], other[e], acc[j]);
+            for (int j = 0; j < JM; ++j) {
+                const int jj = min(j, nsmall - 1);
+                if (PER_M) load4(w, NSOSX_F32, (int64_t)jj * K + k, other[u][j]);
+                else xval4(jj, k, other[u][j]);
             }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (k0 + 256 * u >= K) break;
+#pragma unroll
+            for (int j = 0; j < JM; ++j)
+                if (j < nsmall)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[j] = __fmaf_rn(mine[u][e], other[u][j][e], acc[j]);
         }
     }
 #pragma unroll
-    for (int j = 0; j < kDotMax; ++j) {
+    for (int j = 0; j < JM; ++j) {
         if (j >= nsmall) continue;
         float v = acc[j];
 #pragma unroll
@@ -676,14 +688,20 @@ extern "C" int nsosx_linear_f32(const void* x, int x_dtype, int M, int K, const 
         const bool per_m = N <= kDotMax && !(M <= kDotMax && M < N);
         const int rows = per_m ? M : N;
         const dim3 grid((rows + 3) / 4);
-#define NSOSX_DOT(XDT, PM)                                                                   \
-    hipLaunchKernelGGL((dot_kernel<XDT, PM>), grid, dim3(256), 0, st, x, inv, w, M, N, K,   \
+        const int nsmall = per_m ? N : M;
+#define NSOSX_DOT(XDT, PM, JM)                                                                \
+    hipLaunchKernelGGL((dot_kernel<XDT, PM, JM>), grid, dim3(256), 0, st, x, inv, w, M, N, K, \
                        magnitude, bias, y, ybf)
+#define NSOSX_DOT_J(XDT, PM)                                                 \
+    if (nsmall == 1) NSOSX_DOT(XDT, PM, 1);                                  \
+    else if (nsmall <= 4) NSOSX_DOT(XDT, PM, 4);                             \
+    else NSOSX_DOT(XDT, PM, kDotMax);
         if (x_dtype == NSOSX_F32) {
-            if (per_m) NSOSX_DOT(NSOSX_F32, true); else NSOSX_DOT(NSOSX_F32, false);
+            if (per_m) { NSOSX_DOT_J(NSOSX_F32, true) } else { NSOSX_DOT_J(NSOSX_F32, false) }
         } else {
-            if (per_m) NSOSX_DOT(NSOSX_BF16, true); else NSOSX_DOT(NSOSX_BF16, false);
+            if (per_m) { NSOSX_DOT_J(NSOSX_BF16, true) } else { NSOSX_DOT_J(NSOSX_BF16, false) }
         }
+#undef NSOSX_DOT_J
 #undef NSOSX_DOT
         return check_launch("linear_f32");
     }

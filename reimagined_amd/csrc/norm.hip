@@ -18,17 +18,6 @@
 
 namespace nsosx {
 
-__device__ __forceinline__ float silu_exact(float v) {
-    const float sig = v >= 0.0f ? 1.0f / (1.0f + expf(-v)) : expf(v) / (1.0f + expf(v));
-    return v * sig;
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-
 // ===========================================================================
 // out = (g * inv) * gamma with g = y * silu(z) (GATED) or g = y, one wave per
 // row, two passes over the row (the second recomputes g).

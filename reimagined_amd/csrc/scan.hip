@@ -15,6 +15,7 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <cmath>
 
 namespace nsosx {
 
@@ -22,11 +23,6 @@ __device__ __forceinline__ float softplus_ref(float v) {
     if (v > 20.0f) return v;
     if (v < -20.0f) return expf(v);
     return log1pf(expf(v));
-}
-
-__device__ __forceinline__ float silu_ref(float v) {
-    const float sig = v >= 0.0f ? 1.0f / (1.0f + expf(-v)) : expf(v) / (1.0f + expf(v));
-    return v * sig;
 }
 
 __device__ __forceinline__ float a2_from_log(float a_log) {
@@ -760,7 +756,7 @@ __global__ __launch_bounds__(64) void scan_fwd_generic_kernel(
             st[n] = __fmaf_rn(a, st[n], (dl * load_act<ADT>(Bm, off)) * xv);
             out = __fmaf_rn(st[n], load_act<ADT>(Cm, off), out);
         }
-        if (z) out = out * silu_ref(load_act<ADT>(z, (int64_t)t * z_stride + c));
+        if (z) out = out * silu_exact(load_act<ADT>(z, (int64_t)t * z_stride + c));
         store_act<ADT>(y, (int64_t)t * D + c, out);
     }
     if (final_state)
@@ -826,7 +822,7 @@ __global__ __launch_bounds__(256) void scan_step_kernel(
     p += dpp_xor1(p);
     if (q == 0) {
         float out = __fmaf_rn(Dskip[h], xv, p);
-        if (GATE) out = out * silu_ref(load_act<ADT>(z, (int64_t)r * D + c));
+        if (GATE) out = out * silu_exact(load_act<ADT>(z, (int64_t)r * D + c));
         store_act<ADT>(y, (int64_t)r * D + c, out);
     }
 }
@@ -949,6 +945,278 @@ __global__ __launch_bounds__(256) void scan_step_rows_kernel(
 }
 
 // ===========================================================================
+// Decode step of the faithful Mamba-2 block after its projections, in two
+// launches: the conv ring step over x | B | C (mamba2_faithful_conv_step_kernel,
+// src/cuda/mamba_kernels.cu:3332-3358), the state step
+// (mamba2_faithful_step_kernel, 3376-3404; CPU src/mamba2.cpp:4072-4115), the
+// gated norm RMSNorm(y * SiLU(z)) * gamma (4117-4119) and out_proj's int8 input
+// quantization (its absmax, act_scale and codes).
+//   mamba2_step_scan_kernel, 64 channels of one row per workgroup (the rows'
+//     state traffic spread over many CUs): B and C of the workgroup's groups,
+//     conv + SiLU into LDS from the ring (read only here), then a quad per x
+//     channel as in scan_step_rows_kernel (same operations, same bits): conv +
+//     SiLU of x and its ring slots, the states, the readout, y.
+//   mamba2_step_norm_kernel, a workgroup per row: the B / C ring slots shifted
+//     (after every reader of the previous launch), g = y * SiLU(z), the sum of
+//     g^2 by one wave in the element order of the one-wave-per-row gated norm
+//     (lane l: elements (c * 64 + l) * 8 + k), inv = 1 / sqrt(mean + eps),
+//     normed = g * inv * gamma, the absmax, act_scale and the codes (ties to
+//     even over the first inner & ~7 elements, half away from zero after).
+// Values are rounded to the activation dtype wherever the unfused chain stores
+// them, so the step equals conv_step x3 + selective_scan_step + rmsnorm_gated +
+// quantize_act_i8 bit for bit when the gated norm takes its register path
+// (inner % 512 == 0, inner <= 4096).
+// ===========================================================================
+constexpr int kM2MaxInner = 8192;   // g and gamma of one row in LDS
+constexpr int kM2MaxGS = 1024;      // B and C of one row in LDS
+constexpr int kM2MaxW = 4;
+constexpr int kM2NormThreads = 512;
+constexpr int kM2Rounds = kM2MaxInner / (kM2NormThreads * 4);  // 4-element chunks per thread
+
+struct M2StepArgs {
+    const void* x;            // [rows, inner]
+    const void* z;            // [rows, inner]
+    const void* B;            // [rows, GS], row stride bcdt_stride
+    const void* C;
+    const void* dt;           // [rows, H], row stride bcdt_stride
+    int64_t bcdt_stride;
+    const float* conv_w;      // [inner + 2 GS, W]
+    const float* conv_b;      // [inner + 2 GS] or null
+    float* ring;              // [rows, W - 1, inner + 2 GS]
+    const float* a_log;       // [H]
+    const float* dskip;       // [H]
+    const float* norm_w;      // [inner] or null
+    float eps;
+    float q_max;
+    int H, P, N, G, W;
+    float* state;             // [rows, inner, N]
+    void* y;                  // [rows, inner]
+    int8_t* q;                // [rows, inner]
+    float* act_scale;         // [rows]
+};
+
+// conv ring value of channel c (conv_step_kernel's order: bias first, taps oldest
+// to newest, the new input last) and its SiLU, rounded as stored
+template <int ADT>
+__device__ __forceinline__ float m2_conv(const M2StepArgs& a, int c, float bias,
+                                         const float (&tap)[kM2MaxW - 1], float cur) {
+    const int taps = a.W - 1;
+    float v = bias;
+#pragma unroll
+    for (int j = 0; j < kM2MaxW; ++j)
+        if (j < a.W) v = __fmaf_rn(a.conv_w[(int64_t)c * a.W + j], j < taps ? tap[j] : cur, v);
+    return round_act<ADT>(silu_exact(v));
+}
+
+template <int ADT, int SPL>
+__global__ __launch_bounds__(256) void mamba2_step_scan_kernel(M2StepArgs a) {
+    __shared__ float s_bc[2 * kM2MaxGS];
+    const int r = blockIdx.y;
+    const int inner = a.H * a.P;
+    const int N = a.N, GS = a.G * N;
+    const int CD = inner + 2 * GS;
+    const int taps = a.W - 1;
+    const int q = threadIdx.x & 3;
+    const int c0 = blockIdx.x * 64;
+    const int c = min(c0 + (threadIdx.x >> 2), inner - 1);  // quads past inner store nothing
+    const bool live = c0 + (threadIdx.x >> 2) < inner;
+    const int h = c / a.P;
+    const int grp = (h * a.G) / a.H;
+    // the channel's inputs first: their loads overlap the B / C conv below
+    float sv[SPL];
+    load_states<SPL>(a.state + ((int64_t)r * inner + c) * N + q * SPL, sv);
+    const float* rg = a.ring + (int64_t)r * taps * CD + c;
+    float tap[kM2MaxW - 1];
+#pragma unroll
+    for (int j = 0; j < kM2MaxW - 1; ++j) tap[j] = j < taps ? rg[(int64_t)j * CD] : 0.0f;
+    const float cur = load_act<ADT>(a.x, (int64_t)r * inner + c);
+    const float bias = a.conv_b ? a.conv_b[c] : 0.0f;
+    const float dtv = load_act<ADT>(a.dt, (int64_t)r * a.bcdt_stride + h);
+    const float a2 = a2_from_log(a.a_log[h]);
+    const float dsk = a.dskip[h];
+    // B and C of the groups this workgroup's heads read
+    const int g0 = ((c0 / a.P) * a.G) / a.H;
+    const int g1 = ((min(c0 + 63, inner - 1) / a.P) * a.G) / a.H;
+    const int nv = (g1 - g0 + 1) * N;
+    for (int j = threadIdx.x; j < 2 * nv; j += 256) {
+        const bool isb = j < nv;
+        const int n = g0 * N + (isb ? j : j - nv);           // index within B or C
+        const int ch = inner + (isb ? 0 : GS) + n;            // conv channel
+        const float bcur = load_act<ADT>(isb ? a.B : a.C, (int64_t)r * a.bcdt_stride + n);
+        const float* brg = a.ring + (int64_t)r * taps * CD + ch;
+        float btap[kM2MaxW - 1];
+#pragma unroll
+        for (int t = 0; t < kM2MaxW - 1; ++t) btap[t] = t < taps ? brg[(int64_t)t * CD] : 0.0f;
+        s_bc[(isb ? 0 : kM2MaxGS) + j - (isb ? 0 : nv)] =
+            m2_conv<ADT>(a, ch, a.conv_b ? a.conv_b[ch] : 0.0f, btap, bcur);
+    }
+    __syncthreads();
+    if (!live) return;  // whole quads leave together
+    const float xc = m2_conv<ADT>(a, c, bias, tap, cur);
+    if (q == 0) {
+        float* wr = a.ring + (int64_t)r * taps * CD + c;
+#pragma unroll
+        for (int j = 0; j + 1 < kM2MaxW - 1; ++j)
+            if (j + 1 < taps) wr[(int64_t)j * CD] = tap[j + 1];
+        if (taps > 0) wr[(int64_t)(taps - 1) * CD] = cur;
+    }
+    // scan_step_rows_kernel's step and readout
+    const float dl = softplus_sel(dtv);
+    const float dx = dl * xc;
+    const float* bq = s_bc + (grp - g0) * N + q * SPL;
+    const float* cq = s_bc + kM2MaxGS + (grp - g0) * N + q * SPL;
+    float p = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) {
+        const float dec = __builtin_amdgcn_exp2f(dl * a2);
+        sv[i] = __fmaf_rn(dec, sv[i], dx * bq[i]);
+        p = __fmaf_rn(sv[i], cq[i], p);
+    }
+    p += dpp_xor2(p);
+    p += dpp_xor1(p);
+    store_states<SPL>(a.state + ((int64_t)r * inner + c) * N + q * SPL, sv);
+    if (q == 0) store_act<ADT>(a.y, (int64_t)r * inner + c, __fmaf_rn(dsk, xc, p));
+}
+
+template <int ADT>
+__global__ __launch_bounds__(kM2NormThreads) void mamba2_step_norm_kernel(M2StepArgs a) {
+    __shared__ __attribute__((aligned(16))) float s_g[kM2MaxInner];
+    __shared__ float s_red[kM2NormThreads / kWave];
+    __shared__ float s_inv;
+    const int r = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int inner = a.H * a.P;
+    const int GS = a.G * a.N;
+    const int CD = inner + 2 * GS;
+    const int taps = a.W - 1;
+    // every load of the launch first, one memory round trip: y, z and gamma of this
+    // thread's chunks (indices past inner re-read the last element), then the B / C
+    // ring slots of this thread's channel
+    float yv[kM2Rounds][4], zv[kM2Rounds][4], gm[kM2Rounds][4];
+#pragma unroll
+    for (int k = 0; k < kM2Rounds; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = min((k * kM2NormThreads + tid) * 4 + e, inner - 1);
+            yv[k][e] = load_act<ADT>(a.y, (int64_t)r * inner + idx);
+            zv[k][e] = load_act<ADT>(a.z, (int64_t)r * inner + idx);
+            gm[k][e] = a.norm_w ? a.norm_w[idx] : 1.0f;
+        }
+    const int j = tid;  // B / C channel (2 GS <= kM2NormThreads is the common case)
+    const bool shift = taps > 0 && j < 2 * GS;
+    float* rg = a.ring + (int64_t)r * taps * CD + inner + min(j, 2 * GS - 1);
+    float t[kM2MaxW - 1];
+    float bcur = 0.0f;
+    if (shift) {
+        bcur = load_act<ADT>(j < GS ? a.B : a.C, (int64_t)r * a.bcdt_stride + (j < GS ? j : j - GS));
+#pragma unroll
+        for (int s2 = 0; s2 < kM2MaxW - 1; ++s2) t[s2] = s2 < taps ? rg[(int64_t)s2 * CD] : 0.0f;
+    }
+    // g = y * SiLU(z), the gated norm kernel's product
+#pragma unroll
+    for (int k = 0; k < kM2Rounds; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = (k * kM2NormThreads + tid) * 4 + e;
+            if (idx < inner) s_g[idx] = yv[k][e] * silu_exact(zv[k][e]);
+        }
+    // the B / C ring slots: every reader (the scan launch) has finished
+    if (shift) {
+#pragma unroll
+        for (int s2 = 0; s2 + 1 < kM2MaxW - 1; ++s2)
+            if (s2 + 1 < taps) rg[(int64_t)s2 * CD] = t[s2 + 1];
+        rg[(int64_t)(taps - 1) * CD] = bcur;
+    }
+    for (int jj = j + kM2NormThreads; taps > 0 && jj < 2 * GS; jj += kM2NormThreads) {
+        const float cur2 = load_act<ADT>(jj < GS ? a.B : a.C,
+                                         (int64_t)r * a.bcdt_stride + (jj < GS ? jj : jj - GS));
+        float* rg2 = a.ring + (int64_t)r * taps * CD + inner + jj;
+        float t2[kM2MaxW - 1];
+#pragma unroll
+        for (int s2 = 0; s2 < kM2MaxW - 1; ++s2) t2[s2] = s2 < taps ? rg2[(int64_t)s2 * CD] : 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 + 1 < kM2MaxW - 1; ++s2)
+            if (s2 + 1 < taps) rg2[(int64_t)s2 * CD] = t2[s2 + 1];
+        rg2[(int64_t)(taps - 1) * CD] = cur2;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // four 512-element chunks per step, their LDS reads issued together; elements
+        // past inner (stale LDS) are masked to zero, and fma(0, 0, sum) == sum
+        float sum = 0.0f;
+        for (int b = 0; b < inner; b += 4 * 8 * kWave) {
+            float4 t[4][2];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e0 = min(b + (u * kWave + lane) * 8, kM2MaxInner - 8);
+                t[u][0] = *reinterpret_cast<const float4*>(s_g + e0);
+                t[u][1] = *reinterpret_cast<const float4*>(s_g + e0 + 4);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float v[8] = {t[u][0].x, t[u][0].y, t[u][0].z, t[u][0].w,
+                                    t[u][1].x, t[u][1].y, t[u][1].z, t[u][1].w};
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float g = b + (u * kWave + lane) * 8 + k < inner ? v[k] : 0.0f;
+                    sum = __fmaf_rn(g, g, sum);
+                }
+            }
+        }
+        sum = wave_sum(sum);
+        if (lane == 0) s_inv = 1.0f / sqrtf(sum / static_cast<float>(inner) + a.eps);
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    float nv[kM2Rounds][4];
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kM2Rounds; ++k) {
+        const int i0 = (k * kM2NormThreads + tid) * 4;
+        const float4 t = *reinterpret_cast<const float4*>(s_g + i0);
+        const float v[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float o = v[e] * inv;
+            if (a.norm_w) o = o * gm[k][e];
+            o = i0 + e < inner ? round_act<ADT>(o) : 0.0f;
+            nv[k][e] = o;
+            m = fmaxf(m, fabsf(o));
+        }
+    }
+    m = wave_max(m);
+    if (lane == 0) s_red[wave] = m;
+    __syncthreads();
+    m = s_red[0];
+#pragma unroll
+    for (int w = 1; w < kM2NormThreads / kWave; ++w) m = fmaxf(m, s_red[w]);
+    const float denom = __fadd_rn(m, 1e-8f);
+    const float sc = __fdiv_rn(a.q_max, denom);
+    if (tid == 0) a.act_scale[r] = __fdiv_rn(denom, a.q_max);
+    const int body = inner & ~7;
+    int8_t* qr = a.q + (int64_t)r * inner;
+#pragma unroll
+    for (int k = 0; k < kM2Rounds; ++k) {
+        const int i0 = (k * kM2NormThreads + tid) * 4;
+        if (i0 >= inner) break;
+        float code[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float val = __fmul_rn(nv[k][e], sc);
+            code[e] = clamp127(i0 + e < body ? rintf(val) : roundf(val));
+        }
+        if (i0 + 4 <= inner && ((reinterpret_cast<uintptr_t>(qr) + i0) & 3) == 0) {
+            *reinterpret_cast<uint32_t*>(qr + i0) = pack4_i8(code[0], code[1], code[2], code[3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (i0 + e < inner) qr[i0 + e] = static_cast<int8_t>(static_cast<int>(code[e]));
+        }
+    }
+}
+
+// ===========================================================================
 // Depthwise causal convolution + bias + SiLU, restarted per sequence.
 // Thread = (token, channel); the sequence start comes from a binary search
 // of cu_seqlens.
@@ -979,7 +1247,7 @@ __global__ __launch_bounds__(256) void conv1d_kernel(const void* __restrict__ in
         acc = __fmaf_rn(w[(int64_t)c * W + j], load_act<IDT>(in, (int64_t)src * in_stride + c), acc);
     }
     if (bias) acc = acc + bias[c];
-    if (silu) acc = silu_ref(acc);
+    if (silu) acc = silu_exact(acc);
     store_act<ODT>(out, (int64_t)t * C + c, acc);
 }
 
@@ -1452,6 +1720,64 @@ extern "C" int nsosx_selective_scan_step(const void* x, const void* dt, const fl
 #undef NSOSX_STEP_G
 #undef NSOSX_STEP
     return check_launch("selective_scan_step");
+}
+
+extern "C" int nsosx_mamba2_step(const void* x, const void* z, const void* B, const void* C,
+                                 const void* dt, int64_t bcdt_stride, const float* conv_w,
+                                 const float* conv_b, int conv_width, float* ring,
+                                 const float* A_log, const float* D, const float* norm_w,
+                                 float eps, int rows, int H, int P, int N, int G, int act_dtype,
+                                 float* state, void* y, int8_t* q, float* act_scale,
+                                 int act_bits, void* stream) {
+    if (!x || !z || !B || !C || !dt || !conv_w || !A_log || !D || !state || !y || !q ||
+        !act_scale || (conv_width > 1 && !ring))
+        return fail(NSOSX_ERR_INVALID, "mamba2_step: null pointer");
+    if (rows <= 0 || rows > 65535 || H <= 0 || P <= 0 || G <= 0 || H % G != 0 ||
+        bcdt_stride <= 0)
+        return fail(NSOSX_ERR_INVALID, "mamba2_step: bad shape");
+    if (!valid_dtype(act_dtype)) return fail(NSOSX_ERR_INVALID, "mamba2_step: bad dtype");
+    if (!(eps > 0.0f) || !std::isfinite(eps))
+        return fail(NSOSX_ERR_INVALID, "mamba2_step: eps must be finite and > 0");
+    if (act_bits < 2 || act_bits > 8)
+        return fail(NSOSX_ERR_INVALID, "mamba2_step: act_bits must be in [2, 8]");
+    if ((int64_t)H * P > kM2MaxInner || (int64_t)G * N > kM2MaxGS || conv_width < 1 ||
+        conv_width > kM2MaxW || !(N == 4 || N == 8 || N == 16 || N == 32 || N == 64))
+        return fail(NSOSX_ERR_INVALID,
+                    "mamba2_step: needs H*P <= 8192, G*N <= 1024, N in {4, 8, 16, 32, 64}, "
+                    "1 <= conv_width <= 4");
+    if (reinterpret_cast<uintptr_t>(state) % 16)
+        return fail(NSOSX_ERR_INVALID, "mamba2_step: state must be 16-byte aligned");
+    M2StepArgs a{};
+    a.x = x; a.z = z; a.B = B; a.C = C; a.dt = dt; a.bcdt_stride = bcdt_stride;
+    a.conv_w = conv_w; a.conv_b = conv_b; a.ring = ring;
+    a.a_log = A_log; a.dskip = D; a.norm_w = norm_w; a.eps = eps;
+    a.q_max = act_bits <= 2 ? 1.0f : static_cast<float>((1 << (act_bits - 1)) - 1);
+    a.H = H; a.P = P; a.N = N; a.G = G; a.W = conv_width;
+    a.state = state; a.y = y; a.q = q; a.act_scale = act_scale;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid((H * P + 63) / 64, rows);
+#define NSOSX_M2(ADT, SPL) \
+    hipLaunchKernelGGL((mamba2_step_scan_kernel<ADT, SPL>), grid, dim3(256), 0, st, a);
+#define NSOSX_M2_N(ADT)                         \
+    switch (N) {                                \
+        case 4: NSOSX_M2(ADT, 1) break;         \
+        case 8: NSOSX_M2(ADT, 2) break;         \
+        case 16: NSOSX_M2(ADT, 4) break;        \
+        case 32: NSOSX_M2(ADT, 8) break;        \
+        default: NSOSX_M2(ADT, 16) break;       \
+    }
+    if (act_dtype == NSOSX_F32) {
+        NSOSX_M2_N(NSOSX_F32)
+        hipLaunchKernelGGL((mamba2_step_norm_kernel<NSOSX_F32>), dim3(rows), dim3(kM2NormThreads),
+                           0, st, a);
+    } else {
+        NSOSX_M2_N(NSOSX_BF16)
+        hipLaunchKernelGGL((mamba2_step_norm_kernel<NSOSX_BF16>), dim3(rows),
+                           dim3(kM2NormThreads), 0, st, a);
+    }
+#undef NSOSX_M2_N
+#undef NSOSX_M2
+    return check_launch("mamba2_step");
 }
 
 extern "C" int nsosx_conv1d_causal(const void* in, int in_dtype, int64_t in_stride,

@@ -404,6 +404,7 @@ class Mamba2Block:
         self.out_proj = BitLinear(params["w_out"], device, rms_input=False)
         cw = torch.as_tensor(params["conv_w"], **f32)
         cb = torch.as_tensor(params["conv_b"], **f32)
+        self.conv_w_all, self.conv_b_all = cw.contiguous(), cb.contiguous()
         self.K = cw.shape[1]
         i, g = self.inner, self.gs
         self.conv_w = [cw[:i].contiguous(), cw[i:i + g].contiguous(), cw[i + g:].contiguous()]
@@ -413,10 +414,10 @@ class Mamba2Block:
         self.norm_w = torch.as_tensor(params["norm_w"], **f32)
         self.views = ops.LinearViewArray([p.view_entry() for p in self.xz], device)
 
-    def _project(self, u: torch.Tensor) -> list:
+    def _project(self, u: torch.Tensor, contiguous_dt: bool = True) -> list:
         """x, z from one int8 quantization of u (one grouped GEMV launch for <= 8 rows,
-        else two ternary GEMMs); B, C, dt from one fp32 GEMM (dt contiguous for the scan,
-        B and C strided column slices for the conv)."""
+        else two ternary GEMMs); B, C, dt from one fp32 GEMM (B and C strided column
+        slices; dt contiguous for the prefill scan, a slice too for the decode step)."""
         m = u.shape[0]
         q, s, _ = self.xz[0].workspace(m, u.device)
         st = _stream()
@@ -435,7 +436,8 @@ class Mamba2Block:
                 p.gemm(q, s, m, out, st)
         sens = ops.linear_f32(u, self.w_sens, bias=self.b_sens, out_dtype=self.dtype)
         g = self.gs
-        return [xv, z, sens[:, :g], sens[:, g:2 * g], sens[:, 2 * g:].contiguous()]
+        dt = sens[:, 2 * g:]
+        return [xv, z, sens[:, :g], sens[:, g:2 * g], dt.contiguous() if contiguous_dt else dt]
 
     def forward(self, u: torch.Tensor, cu_seqlens: torch.Tensor, initial_state=None,
                 final_state=None) -> dict:
@@ -455,24 +457,29 @@ class Mamba2Block:
                 "y": y, "normed": normed, "final_state": fin}
 
     def new_decode_state(self, rows: int, device) -> dict:
-        """Zero recurrent state [R, inner, N] and conv rings [R, K-1, channels]."""
+        """Zero recurrent state [R, inner, N] and conv ring [R, K-1, inner + 2*G*N]
+        (channels x | B | C, the reference's single ring)."""
         f32 = dict(dtype=torch.float32, device=device)
         taps = max(self.K - 1, 1)
         return {"state": torch.zeros((rows, self.inner, self.N), **f32),
-                "ring": [torch.zeros((rows, taps, c), **f32)
-                         for c in (self.inner, self.gs, self.gs)]}
+                "ring": torch.zeros((rows, taps, self.inner + 2 * self.gs), **f32)}
 
     def step(self, u: torch.Tensor, dec: dict) -> torch.Tensor:
-        """One decode token per row: u [R, d_model]; updates dec's state and rings in place."""
-        xv, z, Bv, Cv, dt = self._project(u)
-        rings = dec["ring"] if self.K > 1 else [None] * 3
-        xc = ops.conv_step(xv, self.conv_w[0], self.conv_b[0], rings[0])
-        Bc = ops.conv_step(Bv, self.conv_w[1], self.conv_b[1], rings[1])
-        Cc = ops.conv_step(Cv, self.conv_w[2], self.conv_b[2], rings[2])
-        y = ops.selective_scan_step(xc, dt, self.a_log, Bc, Cc, self.d_skip, None, dec["state"],
-                                    self.H, self.P, self.N, self.G)
-        normed = ops.rmsnorm_gated(y, z, self.norm_w, eps=self.eps)
-        return self.out_proj.forward(normed, out_dtype=self.dtype)
+        """One decode token per row: u [R, d_model]; updates dec's state and ring in place.
+
+        Six launches: the int8 quantization of u and the grouped x / z GEMV, the fp32
+        B / C / dt projection, the conv ring + state step and the gated norm + out_proj
+        quantization (nsosx_mamba2_step, two launches), the out_proj GEMV."""
+        xv, z, Bv, Cv, dt = self._project(u, contiguous_dt=False)
+        m = u.shape[0]
+        q, s, _ = self.out_proj.workspace(m, u.device)
+        ops.mamba2_step(xv, z, Bv, Cv, dt, self.conv_w_all, self.conv_b_all,
+                        dec["ring"] if self.K > 1 else None, self.a_log, self.d_skip,
+                        self.norm_w, dec["state"], self.H, self.P, self.N, self.G, eps=self.eps,
+                        act_bits=self.out_proj.bits, q=q, act_scale=s)
+        out = torch.empty((m, self.out_proj.out_features), dtype=self.dtype, device=u.device)
+        self.out_proj.gemm(q, s, m, out, _stream(), self.out_proj.magnitude, self.out_proj.bias)
+        return out
 
     def capture_step(self, u_static: torch.Tensor, dec: dict):
         """Records one decode step into a HIP graph (torch.cuda.CUDAGraph on ROCm).
@@ -484,7 +491,7 @@ class Mamba2Block:
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             self.step(u_static, {"state": dec["state"].clone(),
-                                 "ring": [r.clone() for r in dec["ring"]]})  # warm the pools
+                                 "ring": dec["ring"].clone()})  # warm the pools
         torch.cuda.current_stream().wait_stream(s)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):

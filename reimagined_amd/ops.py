@@ -442,6 +442,57 @@ def selective_scan_step(x, dt, a_log, B, C, D, z, state, H, P, N, G):
     return y
 
 
+def mamba2_step(x, z, B, C, dt, conv_w, conv_b, ring, a_log, D, norm_w, state, H, P, N, G,
+                eps: float = 1e-5, act_bits: int = 8, q=None, act_scale=None, y=None):
+    """The faithful Mamba-2 decode step after its projections, one launch
+    (src/mamba2.cpp:4038-4125 through out_proj's input quantization, src/bitlinear.cpp:240-291):
+    the conv ring over x | B | C, the state step, RMSNorm(y * SiLU(z)) * norm_w and its int8
+    codes, in place on `ring` [R, W-1, H*P + 2*G*N] and `state` [R, H*P, N].
+
+    x, z [R, H*P]; B, C [R, G*N] and dt [R, H] (bias included): column slices of one
+    projection output sharing its row stride.  -> (q int8 [R, H*P], act_scale f32 [R],
+    y [R, H*P] the pre-gate output)."""
+    inner, gs = H * P, G * N
+    r = x.shape[0]
+    _dev(x, "x")
+    _dev(z, "z", x.dtype)
+    _shape(x, (r, inner), "x", "mamba2_step")
+    _shape(z, (r, inner), "z", "mamba2_step")
+    stride = B.stride(0) if r > 1 else max(B.stride(0), C.stride(0), dt.stride(0))
+    for name, v, n in (("B", B, gs), ("C", C, gs), ("dt", dt, H)):
+        if not v.is_cuda or v.dtype != x.dtype or tuple(v.shape) != (r, n) or v.stride(1) != 1:
+            raise ValueError(f"mamba2_step: {name} must be a device [{r}, {n}] {x.dtype} view "
+                             "with unit column stride")
+        if r > 1 and v.stride(0) != stride:
+            raise ValueError("mamba2_step: B, C and dt must share one row stride")
+    cd = inner + 2 * gs
+    _dev(conv_w, "conv_w", torch.float32)
+    width = conv_w.shape[1]
+    _shape(conv_w, (cd, width), "conv_w", "mamba2_step")
+    if conv_b is not None:
+        _shape(_dev(conv_b, "conv_b", torch.float32), (cd,), "conv_b", "mamba2_step")
+    if width > 1:
+        _shape(_dev(ring, "ring", torch.float32), (r, width - 1, cd), "ring", "mamba2_step")
+    _shape(_dev(a_log, "a_log", torch.float32), (H,), "a_log", "mamba2_step")
+    _shape(_dev(D, "D", torch.float32), (H,), "D", "mamba2_step")
+    if norm_w is not None:
+        _shape(_dev(norm_w, "norm_w", torch.float32), (inner,), "norm_w", "mamba2_step")
+    _shape(_dev(state, "state", torch.float32), (r, inner, N), "state", "mamba2_step")
+    if q is None:
+        q = torch.empty((r, inner), dtype=torch.int8, device=x.device)
+    if act_scale is None:
+        act_scale = torch.empty(r, dtype=torch.float32, device=x.device)
+    _shape(_dev(q, "q", torch.int8), (r, inner), "q", "mamba2_step")
+    _shape(_dev(act_scale, "act_scale", torch.float32), (r,), "act_scale", "mamba2_step")
+    if y is None:
+        y = torch.empty_like(x)
+    _shape(_dev(y, "y", x.dtype), (r, inner), "y", "mamba2_step")
+    call("nsosx_mamba2_step", _p(x), _p(z), _p(B), _p(C), _p(dt), stride, _p(conv_w), _p(conv_b),
+         width, _p(ring) if width > 1 else None, _p(a_log), _p(D), _p(norm_w), eps, r, H, P, N, G,
+         _dt(x), _p(state), _p(y), _p(q), _p(act_scale), act_bits, _stream())
+    return q, act_scale, y
+
+
 # ---- MoE ------------------------------------------------------------------------
 
 def moe_route(logits: torch.Tensor, k: int = 2, select_only: bool = False) -> dict:

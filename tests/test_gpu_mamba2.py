@@ -13,7 +13,11 @@ against the oracle's composition, stage by stage on the GPU's own upstream tenso
 
 The decode step equals the prefill token by token (to the conv's bias-first rounding
 and int8 code flips: 1e-3 of the output scale), and a HIP-graph replay of the step
-equals the eager step bit for bit on every replay."""
+equals the eager step bit for bit on every replay.  Its fused launch (conv ring, state
+step, gated norm, out_proj quantization) equals the chain of the separate GPU ops
+(conv_step x3, selective_scan_step, rmsnorm_gated, quantize_act_i8) bit for bit where
+the gated norm's register path sums in the same order, and the oracle's decode chain
+within the fp32 bounds."""
 import numpy as np
 import pytest
 import torch
@@ -110,7 +114,7 @@ def test_mamba2_step_graph_replay_equals_eager(dev, orc):
     dec = blk.new_decode_state(R, dev)
     u_static = torch.zeros((R, 64), device=dev)
     g, out = blk.capture_step(u_static, dec)
-    eager = {"state": dec["state"].clone(), "ring": [r.clone() for r in dec["ring"]]}
+    eager = {"state": dec["state"].clone(), "ring": dec["ring"].clone()}
     for rep in range(3):
         u = torch.from_numpy(rng.standard_normal((R, 64)).astype(np.float32)).to(dev)
         want = blk.step(u, eager)          # eager work between the replays
@@ -144,3 +148,116 @@ def test_mamba2_block_matches_reference_build(dev):
     err = np.abs(got - want)
     assert err.max() <= scale / 127, (err.max(), scale)
     assert err.mean() <= 1e-3 * scale, (err.mean(), scale)
+
+
+def _step_inputs(rng, dev, R, H, P, N, G, W, dtype):
+    """Random projections (B / C / dt as column slices of one [R, 2*G*N + H] output, as the
+    block produces them), a non-zero ring and state."""
+    inner, gs = H * P, G * N
+    cd = inner + 2 * gs
+    t = lambda a, dt=torch.float32: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev, dt)
+    sens = t(np.concatenate([rng.standard_normal((R, 2 * gs)),
+                             rng.standard_normal((R, H)) - 1.0], 1), dtype)
+    return {
+        "x": t(rng.standard_normal((R, inner)), dtype), "z": t(rng.standard_normal((R, inner)), dtype),
+        "B": sens[:, :gs], "C": sens[:, gs:2 * gs], "dt": sens[:, 2 * gs:],
+        "conv_w": t(rng.standard_normal((cd, W)) * 0.5), "conv_b": t(rng.standard_normal(cd) * 0.1),
+        "ring": t(rng.standard_normal((R, max(W - 1, 1), cd))),
+        "a_log": t(rng.standard_normal(H)), "D": t(rng.standard_normal(H)),
+        "norm_w": t(rng.uniform(0.5, 1.5, inner)),
+        "state": t(rng.standard_normal((R, inner, N))),
+    }
+
+
+def _run_fused(ops, a, H, P, N, G):
+    ring, state = a["ring"].clone(), a["state"].clone()
+    W = a["conv_w"].shape[1]
+    q, s, y = ops.mamba2_step(a["x"], a["z"], a["B"], a["C"], a["dt"], a["conv_w"], a["conv_b"],
+                              ring if W > 1 else None, a["a_log"], a["D"], a["norm_w"], state,
+                              H, P, N, G)
+    return ring, state, y, q, s
+
+
+@pytest.mark.parametrize("R,H,P,N,G,W,dtype", [
+    (3, 8, 64, 16, 1, 4, torch.float32),      # inner 512: the norm's register path
+    (2, 16, 64, 32, 2, 4, torch.bfloat16),
+    (5, 8, 128, 64, 4, 3, torch.float32),
+    (4, 4, 128, 4, 1, 2, torch.float32),
+    (1, 32, 64, 16, 1, 4, torch.float32),     # the bench's block, one row
+    (2, 3, 40, 8, 3, 4, torch.float32),       # inner 120: the norm sums in another order
+    (6, 2, 24, 16, 1, 1, torch.bfloat16),     # no ring (width 1)
+])
+def test_mamba2_step_fused_equals_unfused_chain(dev, R, H, P, N, G, W, dtype):
+    from reimagined_amd import ops
+    rng = np.random.default_rng(R * 1000 + H * 10 + N)
+    a = _step_inputs(rng, dev, R, H, P, N, G, W, dtype)
+    inner, gs = H * P, G * N
+    ring, state, y, q, s = _run_fused(ops, a, H, P, N, G)
+    # the separate ops on separate copies of the ring's x / B / C slices
+    rings = [a["ring"][:, :, lo:hi].contiguous() for lo, hi in
+             ((0, inner), (inner, inner + gs), (inner + gs, inner + 2 * gs))]
+    cw, cb = a["conv_w"], a["conv_b"]
+    sl = ((0, inner), (inner, inner + gs), (inner + gs, inner + 2 * gs))
+    xc, Bc, Cc = (ops.conv_step(v, cw[lo:hi].contiguous(), cb[lo:hi].contiguous(),
+                                rg if W > 1 else None)
+                  for v, rg, (lo, hi) in zip((a["x"], a["B"], a["C"]), rings, sl))
+    st2 = a["state"].clone()
+    y2 = ops.selective_scan_step(xc, a["dt"].contiguous(), a["a_log"], Bc, Cc, a["D"], None, st2,
+                                 H, P, N, G)
+    normed = ops.rmsnorm_gated(y2, a["z"], a["norm_w"], eps=1e-5)
+    q2, s2 = ops.quantize_activations_bitnet(normed, bits=8)
+    if W > 1:
+        np.testing.assert_array_equal(ring.cpu().numpy(), torch.cat(rings, 2).cpu().numpy())
+    np.testing.assert_array_equal(state.cpu().numpy(), st2.cpu().numpy())
+    np.testing.assert_array_equal(y.float().cpu().numpy(), y2.float().cpu().numpy())
+    q, q2 = q.cpu().numpy().astype(np.int32), q2.cpu().numpy().astype(np.int32)
+    if inner % 512 == 0 and inner <= 4096:
+        np.testing.assert_array_equal(q, q2)
+        np.testing.assert_array_equal(s.cpu().numpy(), s2.cpu().numpy())
+    else:
+        # the row sum of squares in another order: the normed values agree to its rounding
+        assert np.abs(q - q2).max() <= 1
+        assert (q != q2).mean() <= 0.02
+        np.testing.assert_allclose(s.cpu().numpy(), s2.cpu().numpy(), rtol=1e-5)
+
+
+@pytest.mark.parametrize("R,H,P,N,G,W", [(3, 8, 64, 16, 1, 4), (2, 3, 40, 8, 3, 3),
+                                         (2, 4, 32, 64, 2, 4)])
+def test_mamba2_step_fused_matches_oracle(dev, orc, R, H, P, N, G, W):
+    """Against the oracle's decode chain (conv_step, scan_step, rmsnorm_gated, quantize_act,
+    src/mamba2.cpp:4072-4119 and src/bitlinear.cpp:240-291): ring exact; state and y within
+    the fp32 bound; codes within one step where the normed value sits near a rounding
+    boundary, act_scale within 1e-4."""
+    from reimagined_amd import ops
+    rng = np.random.default_rng(77 + N)
+    a = _step_inputs(rng, dev, R, H, P, N, G, W, torch.float32)
+    inner, gs = H * P, G * N
+    ring, state, y, q, s = _run_fused(ops, a, H, P, N, G)
+    h = {k: v.float().cpu().numpy() for k, v in a.items()}
+    xBC = np.concatenate([h["x"], h["B"], h["C"]], 1)
+    conv, ring_o = orc.conv_step(xBC, h["conv_w"], h["conv_b"], h["ring"])
+    np.testing.assert_array_equal(ring.cpu().numpy(), ring_o)
+    y_o, st_o = orc.scan_step(conv[:, :inner], h["dt"], h["a_log"], conv[:, inner:inner + gs],
+                              conv[:, inner + gs:], h["D"], None, h["state"], H, P, N, G,
+                              gate_silu=False)
+    np.testing.assert_allclose(state.cpu().numpy(), st_o, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(y.cpu().numpy(), y_o, rtol=1e-4, atol=1e-5 * np.abs(y_o).max())
+    normed = orc.rmsnorm_gated(y.cpu().numpy(), h["z"], h["norm_w"], eps=1e-5)
+    q_o, s_o = orc.quantize_act(normed, 8)
+    diff = np.abs(q.cpu().numpy().astype(np.int32) - q_o.astype(np.int32))
+    assert diff.max() <= 1 and (diff > 0).mean() <= 0.02
+    np.testing.assert_allclose(s.cpu().numpy(), s_o, rtol=1e-4)
+
+
+def test_mamba2_step_rejects_unsupported_shapes(dev):
+    """Shapes the fused launch does not take are refused (ValueError, as every rejected
+    shape), as the reference's strict GPU step refuses a shape with no device path
+    (src/mamba2.cpp:4031-4036)."""
+    from reimagined_amd import ops
+    rng = np.random.default_rng(1)
+    a = _step_inputs(rng, dev, 1, 2, 16, 12, 1, 4, torch.float32)      # N = 12
+    with pytest.raises(ValueError, match="N in"):
+        _run_fused(ops, a, 2, 16, 12, 1)
+    a = _step_inputs(rng, dev, 1, 2, 16, 16, 1, 5, torch.float32)      # width 5
+    with pytest.raises(ValueError, match="conv_width"):
+        _run_fused(ops, a, 2, 16, 16, 1)
