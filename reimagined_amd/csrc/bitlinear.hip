@@ -1410,7 +1410,7 @@ __device__ __forceinline__ lds_void_t* lds_ptr(const char* p) {
 // One 128-deep K stage of the 256 x 128 block from LDS stage `st`: each lane
 // reads its two 16-byte weight word groups once, then per MFMA step ks decodes
 // one word per n-tile and reads one 16-byte activation chunk per m-tile.
-template <bool SWZ>
+template <bool SWZ, int MB>
 __device__ __forceinline__ void gemm3_stage(const char* st, int wave, int lane, v16i (&acc)[2][4]) {
     const int g = lane >> 5;
     const int li = lane & 31;
@@ -1426,7 +1426,7 @@ __device__ __forceinline__ void gemm3_stage(const char* st, int wave, int lane, 
     for (int ks = 0; ks < 4; ++ks) {
         v4i bx[4];
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
+        for (int mb = 0; mb < MB; ++mb) {
             const int ml = mb * 32 + li;
             const int slot = (4 * g + ks) ^ ((ml >> 1) & 7);
             const uint4 v = *reinterpret_cast<const uint4*>(xl + ml * 128 + slot * 16);
@@ -1448,7 +1448,7 @@ __device__ __forceinline__ void gemm3_stage(const char* st, int wave, int lane, 
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+            for (int mb = 0; mb < MB; ++mb)
                 acc[nb][mb] =
                     __builtin_amdgcn_mfma_i32_32x32x32_i8(aw[nb], bx[mb], acc[nb][mb], 0, 0, 0);
     }
@@ -1612,7 +1612,21 @@ __device__ __forceinline__ void gemm3_epilogue_rows(const GemmProblem& pb,
     }
 }
 
-template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU, bool SWZ = false>
+// Memory wait of the stage loop: at most one stage's loads (2 + MB per thread) pending.
+template <int N>
+__device__ __forceinline__ void gemm3_wait_vm() {
+    static_assert(N >= 0 && N <= 6, "stage loads per thread");
+    if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if constexpr (N == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+    else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else if constexpr (N == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+}
+
+// MB: 32-row blocks of the tile that hold rows (a partial last tile of an expert's
+// segment skips the DMA and MFMAs of its empty blocks; their accumulators stay zero
+// and their rows are never stored).
+template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU, bool SWZ = false, int MB = 4>
 __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* __restrict__ q,
                                            const float* __restrict__ act_scale,
                                            const int32_t* __restrict__ perm, int seg_begin,
@@ -1652,7 +1666,7 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
             __builtin_amdgcn_global_load_lds(wsrc[j] + kt * 32,
                                              lds_ptr(st + (64 * wave + 32 * j) * 32), 16, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MB; ++i)
             __builtin_amdgcn_global_load_lds(xsrc[i] + kt * 128,
                                              lds_ptr(st + kG3WBytes + (32 * i + 8 * wave) * 128),
                                              16, 0, 0);
@@ -1668,13 +1682,13 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
     if (KT > 1) issue(1);
 
     for (int kt = 0; kt < KT; ++kt) {
-        // this thread's stage-kt DMA is done once at most one stage (6 loads) is pending
-        if (kt + 1 < KT) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // this thread's stage-kt DMA is done once at most one stage (2 + MB loads) is pending
+        if (kt + 1 < KT) gemm3_wait_vm<2 + MB>();
+        else gemm3_wait_vm<0>();
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (kt + 2 < KT) issue(kt + 2);
-        gemm3_stage<SWZ>(smem + (kt % kG3Stages) * kG3StageBytes, wave, lane, acc);
+        gemm3_stage<SWZ, MB>(smem + (kt % kG3Stages) * kG3StageBytes, wave, lane, acc);
     }
 
     if constexpr (YDT == NSOSX_BF16 && !ACC_OUT) {
@@ -1737,6 +1751,67 @@ __global__ __launch_bounds__(kGemm3Threads, 2) void gemm3_kernel(GemmProblem pb,
                                            mt * kG3BM, y, acc_out, smem3);
 }
 
+// Tile L of a grouped launch over the experts' real row tiles: every expert's full
+// 128-row tiles first (XCD-swizzled, n fastest), then each expert's partial last
+// tile, so that the partial tiles, cheaper by their skipped empty 32-row blocks,
+// make up the last round of a launch that does not divide into whole rounds.
+__device__ __forceinline__ bool grouped_tile(const int32_t* __restrict__ offsets, int experts,
+                                             int ntn, int L, int& nt, int& e, int& seg_begin,
+                                             int& seg_rows, int& m0) {
+    int full = 0;
+    for (int j = 0; j < experts; ++j) full += max(offsets[j + 1] - offsets[j], 0) / kG3BM;
+    if (L < ntn * full) {
+        int rest;
+        xcd_tile(L, ntn, full, nt, rest);
+        int base = 0;
+        for (int j = 0; j < experts; ++j) {
+            const int b = offsets[j];
+            const int f = max(offsets[j + 1] - b, 0) / kG3BM;
+            if (rest < base + f) {
+                e = j; seg_begin = b; seg_rows = offsets[j + 1] - b; m0 = (rest - base) * kG3BM;
+                return true;
+            }
+            base += f;
+        }
+        return false;
+    }
+    const int idx = L - ntn * full;
+    nt = idx % ntn;
+    int p = idx / ntn;
+    for (int j = 0; j < experts; ++j) {
+        const int b = offsets[j];
+        const int r = max(offsets[j + 1] - b, 0);
+        if (r % kG3BM == 0) continue;
+        if (p == 0) {
+            e = j; seg_begin = b; seg_rows = r; m0 = (r / kG3BM) * kG3BM;
+            return true;
+        }
+        --p;
+    }
+    return false;
+}
+
+// gemm3_tile with the 32-row blocks that hold rows of the segment
+template <int YDT, bool GATHER, bool SQRELU, bool SWZ>
+__device__ __forceinline__ void gemm3_tile_rows(const GemmProblem& pb, const int8_t* __restrict__ q,
+                                                const float* __restrict__ act_scale,
+                                                const int32_t* __restrict__ perm, int seg_begin,
+                                                int seg_rows, int n0, int m0, void* y, char* smem) {
+    const int rows = seg_rows - m0;
+    if (rows > 96)
+        gemm3_tile<YDT, false, GATHER, SQRELU, SWZ, 4>(pb, q, act_scale, perm, seg_begin, seg_rows,
+                                                        n0, m0, y, nullptr, smem);
+    else if (rows > 64)
+        gemm3_tile<YDT, false, GATHER, SQRELU, SWZ, 3>(pb, q, act_scale, perm, seg_begin, seg_rows,
+                                                        n0, m0, y, nullptr, smem);
+    else if (rows > 32)
+        gemm3_tile<YDT, false, GATHER, SQRELU, SWZ, 2>(pb, q, act_scale, perm, seg_begin, seg_rows,
+                                                        n0, m0, y, nullptr, smem);
+    else
+        gemm3_tile<YDT, false, GATHER, SQRELU, SWZ, 1>(pb, q, act_scale, perm, seg_begin, seg_rows,
+                                                        n0, m0, y, nullptr, smem);
+}
+
 template <int YDT, bool GATHER, bool SQRELU>
 __global__ __launch_bounds__(kGemm3Threads, 2) void grouped_gemm3_kernel(
     const nsosx_linear_view* views, const int32_t* __restrict__ offsets,
@@ -1751,22 +1826,8 @@ __global__ __launch_bounds__(kGemm3Threads, 2) void grouped_gemm3_kernel(
     int nt, rest;
     int e = -1, seg_begin = 0, seg_rows = 0, m0 = 0;
     if (compact) {
-        xcd_tile(blockIdx.x, ntn, ntm, nt, rest);
-        int base = 0;
-        for (int j = 0; j < experts; ++j) {
-            const int b = offsets[j];
-            const int r = max(offsets[j + 1] - b, 0);
-            const int tj = (r + kG3BM - 1) / kG3BM;
-            if (rest < base + tj) {
-                e = j;
-                seg_begin = b;
-                seg_rows = r;
-                m0 = (rest - base) * kG3BM;
-                break;
-            }
-            base += tj;
-        }
-        if (e < 0) return;
+        if (!grouped_tile(offsets, experts, ntn, blockIdx.x, nt, e, seg_begin, seg_rows, m0))
+            return;
     } else {
         xcd_tile(blockIdx.x, ntn, ntm * experts, nt, rest);
         e = rest / ntm;
@@ -1779,8 +1840,8 @@ __global__ __launch_bounds__(kGemm3Threads, 2) void grouped_gemm3_kernel(
     const int n0 = nt * kG3BN;
     if (n0 >= v.outputs) return;
     GemmProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
-    gemm3_tile<YDT, false, GATHER, SQRELU>(pb, q, act_scale, perm, seg_begin, seg_rows, n0, m0, y,
-                                           nullptr, smem3);
+    gemm3_tile_rows<YDT, GATHER, SQRELU, false>(pb, q, act_scale, perm, seg_begin, seg_rows, n0, m0,
+                                                y, smem3);
 }
 
 // ===========================================================================
@@ -1812,30 +1873,16 @@ __global__ __launch_bounds__(kGemm3Threads, 2) void grouped_gemm3_mfma_kernel(
     const int32_t* __restrict__ perm, const int8_t* __restrict__ q,
     const float* __restrict__ act_scale, void* y, int ntn, int ntm, int experts) {
     extern __shared__ __align__(16) char smem4[];
-    // compact row tiles, as grouped_gemm3_kernel's with total_rows
-    int nt, rest;
-    xcd_tile(blockIdx.x, ntn, ntm, nt, rest);
-    int e = -1, seg_begin = 0, seg_rows = 0, m0 = 0, base = 0;
-    for (int j = 0; j < experts; ++j) {
-        const int b = offsets[j];
-        const int r = max(offsets[j + 1] - b, 0);
-        const int tj = (r + kG3BM - 1) / kG3BM;
-        if (rest < base + tj) {
-            e = j;
-            seg_begin = b;
-            seg_rows = r;
-            m0 = (rest - base) * kG3BM;
-            break;
-        }
-        base += tj;
-    }
-    if (e < 0 || m0 >= seg_rows) return;
+    // compact row tiles, as grouped_gemm3_kernel's
+    int nt, e = -1, seg_begin = 0, seg_rows = 0, m0 = 0;
+    if (!grouped_tile(offsets, experts, ntn, blockIdx.x, nt, e, seg_begin, seg_rows, m0)) return;
+    if (m0 >= seg_rows) return;
     const nsosx_linear_view v = views[e];
     const int n0 = nt * kG3BN;
     if (n0 >= v.outputs) return;
     GemmProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, v.outputs, v.inputs};
-    gemm3_tile<YDT, false, GATHER, SQRELU, true>(pb, q, act_scale, perm, seg_begin, seg_rows, n0,
-                                                 m0, y, nullptr, smem4);
+    gemm3_tile_rows<YDT, GATHER, SQRELU, true>(pb, q, act_scale, perm, seg_begin, seg_rows, n0, m0,
+                                               y, smem4);
 }
 
 // Reference layout -> MFMA layout, word by word (code 3 -> 1, both decode to 0).
