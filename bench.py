@@ -103,11 +103,12 @@ def bench_layer(torch, dev, steps, warmup):
     return T, wall, stages, params, inp
 
 
-def bench_mamba2_decode(torch, dev, rows=1, reps=50):
+def bench_mamba2_decode(torch, dev, rows=1, reps=200):
     """Faithful Mamba-2 decode step (d_model 1024, 32 heads x 64, N 16, conv 4), eager vs one
     HIP-graph replay per step: one quantization of u, one grouped GEMV for the ternary x and z
-    projections, the fp32 B / C / dt projection, three conv steps, the state step, the gated
-    norm, RMS + quantize and the out_proj GEMV, so the step is launch-bound."""
+    projections, the fp32 B / C / dt projection, the conv ring + state step and the gated norm
+    + out_proj quantization (nsosx_mamba2_step, two launches) and the out_proj GEMV, so the
+    step is launch-bound."""
     from reimagined_amd.layers import Mamba2Block
     rng = np.random.default_rng(41)
     d, H, P, N, G, K = 1024, 32, 64, 16, 1, 4
@@ -133,7 +134,8 @@ def bench_mamba2_decode(torch, dev, rows=1, reps=50):
     torch.cuda.synchronize()
     eager_us = (time.perf_counter() - t0) / reps * 1e6
     g, _ = blk.capture_step(u, dec)
-    g.replay()
+    for _ in range(20):  # replays before the timed ones: the clocks settle
+        g.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(reps):

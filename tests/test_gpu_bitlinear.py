@@ -36,7 +36,8 @@ def test_quantize_matches_reference_golden(dev, orc):
 
 
 @pytest.mark.parametrize("m,k", [(1, 16), (5, 1003), (33, 768), (7, 4096), (3, 8200), (64, 2048),
-                                 (1500, 1024), (1100, 1003), (1029, 512), (1030, 4096), (1027, 2048)])
+                                 (1500, 1024), (1100, 1003), (1029, 512), (1030, 4096), (1027, 2048),
+                                 (8195, 1024), (4100, 2048)])
 @pytest.mark.parametrize("rms", [False, True])
 def test_quantize_random_f32(dev, orc, m, k, rms):
     rng = np.random.default_rng(m * 1000 + k)
@@ -50,11 +51,12 @@ def test_quantize_random_f32(dev, orc, m, k, rms):
 
 @pytest.mark.parametrize("rms", [False, True])
 @pytest.mark.parametrize("m,k", [(37, 1024), (1200, 1024), (1201, 2048), (1029, 512), (1026, 4096),
-                                 (32769, 1024)])
+                                 (32769, 1024), (16411, 1024), (8200, 2048), (40796, 2048)])
 def test_quantize_bf16_input(dev, orc, rms, m, k):
     """bf16 rows; M > 1024 with K = 512 / 1024 / 2048 / 4096 takes the several-rows-per-wave
     kernel, including row counts that leave a wave with rows past M.  The RMS pass is the
-    three-wave form below 512 groups of 64 rows and the one-wave tiled form from 32705 rows."""
+    three-wave form below 512 groups of 64 rows and the one-wave tiled form from 32705 rows
+    (40796 x 2048: the out_proj input of the config-4 layer)."""
     rng = np.random.default_rng(3)
     x = (rng.standard_normal((m, k)) * rng.uniform(0.5, 8.0, (m, 1))).astype(np.float32)
     xb = torch.from_numpy(x).to(torch.bfloat16)
@@ -381,3 +383,26 @@ def test_grouped_gemm_mfma_matches_reference_layout(dev, gather, sqrelu):
                                         slots, sqrelu, gather, torch.bfloat16)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("m,k,dtype", [(16411, 1024, torch.bfloat16), (8200, 2048, torch.bfloat16),
+                                       (8195, 1024, torch.float32), (4100, 2048, torch.float32)])
+def test_rms_workspace_in_order_sum(dev, m, k, dtype):
+    """The RMS_PERI row scale left in rms_workspace (the STE backward reads it):
+    1 / sqrt(mean + 1e-6) of the in-order float sum of the rounded squares
+    (Tensor::rmsnorm, src/tensor.cpp:3455-3492); numpy's add.accumulate adds in order."""
+    from reimagined_amd._lib import call
+    from reimagined_amd.ops import _p, _dt, _stream
+    rng = np.random.default_rng(m + k)
+    x = (rng.standard_normal((m, k)) * rng.uniform(0.5, 8.0, (m, 1))).astype(np.float32)
+    xt = torch.from_numpy(x).to(dtype)
+    xf = xt.float().numpy()
+    xd = xt.to(dev)
+    q = torch.empty((m, k), dtype=torch.int8, device=dev)
+    s = torch.empty(m, dtype=torch.float32, device=dev)
+    rw = torch.empty(m, dtype=torch.float32, device=dev)
+    call("nsosx_quantize_act_i8", _p(xd), _dt(xd), m, k, 8, 1, _p(q), _p(s), _p(rw), _stream())
+    sq = (xf * xf).astype(np.float32)
+    total = np.add.accumulate(sq, axis=1, dtype=np.float32)[:, -1]
+    want = (np.float32(1.0) / np.sqrt(total / np.float32(k) + np.float32(1e-6))).astype(np.float32)
+    np.testing.assert_array_equal(rw.cpu().numpy(), want)
