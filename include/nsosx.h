@@ -469,6 +469,17 @@ int nsosx_moe_sparse_decode(const nsosx_linear_view* up_views,
 int nsosx_rmsnorm_gated(const void* y, const void* z, const float* gamma, int rows, int dim,
                         float eps, int act_dtype, void* out, int out_dtype, void* stream);
 
+/* nsosx_rmsnorm_gated followed by the out_proj BitLinear's int8 input quantization
+ * (quantize_activations_bitnet without RMS_PERI, src/bitlinear.cpp:240-291), as in
+ * Mamba2SSD::forward_faithful (src/mamba2.cpp:2677-2681): the codes quantize the
+ * normed values as stored in out_dtype.  q int8 [rows, dim], act_scale f32 [rows].
+ * For dim % 512 == 0, dim <= 4096 and 16-byte aligned buffers one pass, and out
+ * may be NULL (the normed rows are then not stored); otherwise the two passes of
+ * nsosx_rmsnorm_gated + nsosx_quantize_act_i8 and out is required. */
+int nsosx_rmsnorm_gated_quant(const void* y, const void* z, const float* gamma, int rows, int dim,
+                              float eps, int act_dtype, void* out, int out_dtype, int bits,
+                              int8_t* q, float* act_scale, void* stream);
+
 /* Residual add and the next block norm of JambaBlock::forward
  * (src/jamba.cpp:3253, 3286-3290, 3316): residual_out = x + delta (act_dtype);
  * when norm_out is not NULL, norm_out = rmsnorm(residual_out, eps) * gamma

@@ -63,6 +63,8 @@ SIGNATURES = {
                                         _vp, _i, _vp]),
     "nsosx_moe_combine": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),
     "nsosx_rmsnorm_gated": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp, _i, _vp]),
+    "nsosx_rmsnorm_gated_quant": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp, _i, _i, _vp, _vp,
+                                       _vp]),
     "nsosx_add_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _i, _vp, _vp, _vp]),
     "nsosx_conv_step": (_i, [_vp, _i, _i64, _i, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _vp]),
     "nsosx_edge_pack_parse": (_i, [_vp, ctypes.c_uint64, _vp, _i, _vp, _vp]),

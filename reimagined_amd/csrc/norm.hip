@@ -107,12 +107,18 @@ __device__ __forceinline__ void store8v(void* p, int64_t i, const float v[8]) {
     }
 }
 
-template <int DT, int ODT, bool GATED, int CH>
+// QUANT: the next BitLinear's int8 input quantization of the normed row (as stored in
+// ODT) in the same pass: absmax, act_scale and codes (ties to even; dim % 8 == 0 here),
+// and out only when non-null.
+template <int DT, int ODT, bool GATED, int CH, bool QUANT = false>
 __global__ __launch_bounds__(256) void rmsnorm_rows_reg_kernel(const void* __restrict__ y,
                                                                const void* __restrict__ z,
                                                                const float* __restrict__ gamma,
                                                                int rows, float eps,
-                                                               void* __restrict__ out) {
+                                                               void* __restrict__ out,
+                                                               int8_t* __restrict__ q = nullptr,
+                                                               float* __restrict__ act_scale = nullptr,
+                                                               float q_max = 0.0f) {
     constexpr int dim = 512 * CH;
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -143,6 +149,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_reg_kernel(const void* __res
         for (int k = 0; k < 8; ++k) sum = __fmaf_rn(g[c][k], g[c][k], sum);
     sum = wave_sum(sum);
     const float inv = 1.0f / sqrtf(sum / static_cast<float>(dim) + eps);
+    float mx = 0.0f;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
         const int e0 = (c * 64 + lane) * 8;
@@ -152,7 +159,29 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_reg_kernel(const void* __res
             o[k] = g[c][k] * inv;
             if (gamma) o[k] = o[k] * gm[c][k];
         }
-        store8v<ODT>(out, base + e0, o);
+        if (!QUANT || out) store8v<ODT>(out, base + e0, o);
+        if constexpr (QUANT) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                g[c][k] = round_act<ODT>(o[k]);  // the value as stored, kept for the codes
+                mx = fmaxf(mx, fabsf(g[c][k]));
+            }
+        }
+    }
+    if constexpr (QUANT) {
+        mx = wave_max(mx);
+        const float denom = __fadd_rn(mx, 1e-8f);
+        const float sc = __fdiv_rn(q_max, denom);
+        if (lane == 0) act_scale[row] = __fdiv_rn(denom, q_max);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            float code[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) code[k] = clamp127(rintf(__fmul_rn(g[c][k], sc)));
+            *reinterpret_cast<uint2*>(q + base + (c * 64 + lane) * 8) =
+                make_uint2(pack4_i8(code[0], code[1], code[2], code[3]),
+                           pack4_i8(code[4], code[5], code[6], code[7]));
+        }
     }
 }
 
@@ -277,6 +306,64 @@ extern "C" int nsosx_rmsnorm_gated(const void* y, const void* z, const float* ga
     }
 #undef NSOSX_RN
     return check_launch("rmsnorm_gated");
+}
+
+extern "C" int nsosx_rmsnorm_gated_quant(const void* y, const void* z, const float* gamma,
+                                         int rows, int dim, float eps, int act_dtype, void* out,
+                                         int out_dtype, int bits, int8_t* q, float* act_scale,
+                                         void* stream) {
+    if (!y || !q || !act_scale) return fail(NSOSX_ERR_INVALID, "rmsnorm_gated_quant: null pointer");
+    if (rows < 0 || dim <= 0 || !(eps > 0.0f) || !std::isfinite(eps))
+        return fail(NSOSX_ERR_INVALID,
+                    "rmsnorm_gated_quant: need rows >= 0, dim > 0, finite eps > 0");
+    if (!valid_dtype(act_dtype) || !valid_dtype(out_dtype))
+        return fail(NSOSX_ERR_INVALID, "rmsnorm_gated_quant: bad dtype");
+    if (bits < 2 || bits > 8)
+        return fail(NSOSX_ERR_INVALID, "rmsnorm_gated_quant: bits must be in [2, 8]");
+    if (rows == 0) return NSOSX_OK;
+    const bool reg = dim % 512 == 0 && dim <= 4096 &&
+                     ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(z) |
+                       reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(gamma) |
+                       reinterpret_cast<uintptr_t>(q)) & 15) == 0;
+    if (!reg) {
+        // the two-pass form: the normed rows are the quantization's input
+        if (!out)
+            return fail(NSOSX_ERR_INVALID,
+                        "rmsnorm_gated_quant: out is required unless dim % 512 == 0, dim <= 4096 "
+                        "and the buffers are 16-byte aligned");
+        int rc = nsosx_rmsnorm_gated(y, z, gamma, rows, dim, eps, act_dtype, out, out_dtype, stream);
+        if (rc) return rc;
+        return nsosx_quantize_act_i8(out, out_dtype, rows, dim, bits, 0, q, act_scale, nullptr,
+                                     stream);
+    }
+    const float qm = bits <= 2 ? 1.0f : static_cast<float>((1 << (bits - 1)) - 1);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const dim3 grid((rows + 3) / 4), block(256);
+#define NSOSX_RNQ(D, O, GT, CH)                                                                  \
+    hipLaunchKernelGGL((rmsnorm_rows_reg_kernel<D, O, GT, CH, true>), grid, block, 0, st, y, z,  \
+                       gamma, rows, eps, out, q, act_scale, qm);
+#define NSOSX_RNQ_CH(D, O, GT)                                \
+    switch (dim / 512) {                                      \
+        case 1: NSOSX_RNQ(D, O, GT, 1) break;                 \
+        case 2: NSOSX_RNQ(D, O, GT, 2) break;                 \
+        case 3: NSOSX_RNQ(D, O, GT, 3) break;                 \
+        case 4: NSOSX_RNQ(D, O, GT, 4) break;                 \
+        case 5: NSOSX_RNQ(D, O, GT, 5) break;                 \
+        case 6: NSOSX_RNQ(D, O, GT, 6) break;                 \
+        case 7: NSOSX_RNQ(D, O, GT, 7) break;                 \
+        default: NSOSX_RNQ(D, O, GT, 8) break;                \
+    }
+#define NSOSX_RNQ_G(D, O) \
+    if (z) { NSOSX_RNQ_CH(D, O, true) } else { NSOSX_RNQ_CH(D, O, false) }
+    if (act_dtype == NSOSX_F32) {
+        if (out_dtype == NSOSX_F32) { NSOSX_RNQ_G(NSOSX_F32, NSOSX_F32) } else { NSOSX_RNQ_G(NSOSX_F32, NSOSX_BF16) }
+    } else {
+        if (out_dtype == NSOSX_F32) { NSOSX_RNQ_G(NSOSX_BF16, NSOSX_F32) } else { NSOSX_RNQ_G(NSOSX_BF16, NSOSX_BF16) }
+    }
+#undef NSOSX_RNQ_G
+#undef NSOSX_RNQ_CH
+#undef NSOSX_RNQ
+    return check_launch("rmsnorm_gated_quant");
 }
 
 extern "C" int nsosx_add_rmsnorm(const void* x, const void* delta, const float* gamma, int rows,

@@ -440,8 +440,11 @@ class Mamba2Block:
         return [xv, z, sens[:, :g], sens[:, g:2 * g], dt.contiguous() if contiguous_dt else dt]
 
     def forward(self, u: torch.Tensor, cu_seqlens: torch.Tensor, initial_state=None,
-                final_state=None) -> dict:
-        """u [T, d_model] over the packed ragged batch cu_seqlens (int32 [S+1])."""
+                final_state=None, keep_normed: bool = False) -> dict:
+        """u [T, d_model] over the packed ragged batch cu_seqlens (int32 [S+1]).
+
+        The gated norm and out_proj's input quantization run as one pass
+        (nsosx_rmsnorm_gated_quant); the normed rows are stored only with keep_normed."""
         ops._dev(cu_seqlens, "cu_seqlens", torch.int32)
         xv, z, Bv, Cv, dt = self._project(u)
         Bc = ops.conv1d_causal(Bv, self.conv_w[1], cu_seqlens, self.conv_b[1], True)
@@ -451,8 +454,12 @@ class Mamba2Block:
                                    initial_state=initial_state, want_final=True)
         if final_state is not None:
             final_state.copy_(fin)
-        normed = ops.rmsnorm_gated(y, z, self.norm_w, eps=self.eps)
-        out = self.out_proj.forward(normed, out_dtype=self.dtype)
+        q, s, normed = ops.rmsnorm_gated_quant(y, z, self.norm_w, eps=self.eps,
+                                               bits=self.out_proj.bits, want_out=keep_normed)
+        out = torch.empty((u.shape[0], self.out_proj.out_features), dtype=self.dtype,
+                          device=u.device)
+        self.out_proj.gemm(q, s, u.shape[0], out, _stream(), self.out_proj.magnitude,
+                           self.out_proj.bias)
         return {"out": out, "x": xv, "z": z, "Bv": Bv, "Cv": Cv, "B": Bc, "C": Cc, "dt": dt,
                 "y": y, "normed": normed, "final_state": fin}
 

@@ -598,6 +598,33 @@ def rmsnorm_gated(y: torch.Tensor, z=None, gamma=None, eps: float = 1e-5,
     return out
 
 
+def rmsnorm_gated_quant(y: torch.Tensor, z=None, gamma=None, eps: float = 1e-5, bits: int = 8,
+                        want_out: bool = False, out_dtype=None):
+    """rmsnorm_gated + the next BitLinear's int8 input quantization (src/mamba2.cpp:2677-2681,
+    src/bitlinear.cpp:240-291) -> (q int8 [rows, dim], act_scale f32 [rows], normed or None).
+    The normed rows are stored only with want_out (or where the one-pass form does not
+    apply: dim % 512 != 0 or dim > 4096)."""
+    _dev(y, "y")
+    if y.dim() != 2:
+        raise ValueError("rmsnorm_gated_quant: y must be [rows, dim]")
+    if z is not None:
+        _dev(z, "z", y.dtype)
+        if z.shape != y.shape:
+            raise ValueError("rmsnorm_gated_quant: z must match y")
+    _opt(gamma, "gamma")
+    rows, dim = y.shape
+    if gamma is not None and gamma.numel() != dim:
+        raise ValueError("rmsnorm_gated_quant: gamma must have dim elements")
+    odt = out_dtype or y.dtype
+    one_pass = dim % 512 == 0 and dim <= 4096
+    out = torch.empty(y.shape, dtype=odt, device=y.device) if (want_out or not one_pass) else None
+    q = torch.empty((rows, dim), dtype=torch.int8, device=y.device)
+    s = torch.empty(rows, dtype=torch.float32, device=y.device)
+    call("nsosx_rmsnorm_gated_quant", _p(y), _p(z), _p(gamma), rows, dim, eps, _dt(y), _p(out),
+         _DT[odt], bits, _p(q), _p(s), _stream())
+    return q, s, out
+
+
 def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor, gamma=None, eps: float = 1e-6,
                 want_norm: bool = True):
     """residual = x + delta; norm = rmsnorm(residual) * gamma (src/jamba.cpp:3253, 3286-3290).

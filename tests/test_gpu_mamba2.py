@@ -57,7 +57,7 @@ def test_mamba2_block_prefill_matches_oracle(dev, orc):
     cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
     T = int(cu[-1])
     u = rng.standard_normal((T, 64)).astype(np.float32)
-    res = blk.forward(torch.from_numpy(u).to(dev), torch.from_numpy(cu).to(dev))
+    res = blk.forward(torch.from_numpy(u).to(dev), torch.from_numpy(cu).to(dev), keep_normed=True)
     # x, z: ternary exact-linear (no RMS_PERI, no magnitude), bit-exact
     for key, wk in (("x", "w_x"), ("z", "w_z")):
         pk, ws, _ = orc.pack_weights(p[wk])

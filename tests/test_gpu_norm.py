@@ -107,3 +107,29 @@ def test_conv_step_strided_input_and_rejections(dev, orc):
         ops.conv_step(xt, _t(dev, w), None, torch.zeros((R, W, C), device=dev))
     with pytest.raises(ValueError):
         ops.rmsnorm_gated(_t(dev, wide), gamma=torch.ones(5, device=dev))
+
+
+@pytest.mark.parametrize("rows,dim,dtype,keep", [(40, 2048, torch.float32, False),
+                                                 (37, 2048, torch.float32, True),
+                                                 (9, 1024, torch.bfloat16, False),
+                                                 (5, 4096, torch.bfloat16, True),
+                                                 (6, 120, torch.float32, False)])
+def test_rmsnorm_gated_quant_equals_two_passes(dev, orc, rows, dim, dtype, keep):
+    """The gated norm with out_proj's int8 input quantization in one pass equals the
+    gated norm followed by quantize_act_i8 on its stored rows, bit for bit (dim 120
+    takes the two passes themselves); the codes also match the oracle's quantization of
+    the GPU's normed rows."""
+    rng = np.random.default_rng(rows + dim)
+    y = _t(dev, rng.standard_normal((rows, dim)), dtype)
+    z = _t(dev, rng.standard_normal((rows, dim)), dtype)
+    g = _t(dev, rng.uniform(0.5, 1.5, dim))
+    q, s, out = ops.rmsnorm_gated_quant(y, z, g, eps=1e-5, want_out=keep)
+    normed = ops.rmsnorm_gated(y, z, g, eps=1e-5)
+    q2, s2 = ops.quantize_activations_bitnet(normed, 8)
+    np.testing.assert_array_equal(q.cpu().numpy(), q2.cpu().numpy())
+    np.testing.assert_array_equal(s.cpu().numpy(), s2.cpu().numpy())
+    if keep:
+        np.testing.assert_array_equal(out.float().cpu().numpy(), normed.float().cpu().numpy())
+    wq, ws = orc.quantize_act(normed.float().cpu().numpy(), 8)
+    np.testing.assert_array_equal(q.cpu().numpy(), wq)
+    np.testing.assert_array_equal(s.cpu().numpy(), ws)
