@@ -301,9 +301,51 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ e
 
 // The same sums with a wave per output row: the row's k (expert, slot, weight)
 // triples are wave-uniform (scalar loads, sorted once per wave) and each lane
-// takes 4 consecutive elements per step with one vector load per expert.  Needs
-// dim % 4 == 0 and 16-byte (f32) / 8-byte (bf16) aligned rows.
-template <int IDT, int ODT>
+// takes V consecutive elements per step with one vector load per expert (V = 8:
+// 16-byte bf16 loads, V = 4 otherwise).  With k <= 2 the loads of up to four steps
+// (a row of 2048 bf16) are issued before any is used.  Needs dim % V == 0 and
+// 16-byte (f32, or V = 8) / 8-byte (bf16) aligned rows.
+template <int IDT, int V>
+__device__ __forceinline__ void combine_load(const void* p, int64_t off, float v[V]) {
+    if constexpr (IDT == NSOSX_F32) {
+#pragma unroll
+        for (int j = 0; j < V; j += 4) {
+            const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + off + j);
+            v[j] = t.x; v[j + 1] = t.y; v[j + 2] = t.z; v[j + 3] = t.w;
+        }
+    } else if constexpr (V == 8) {
+        const uint4 t = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + off);
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[2 * j] = __uint_as_float(w[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        }
+    } else {
+        const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + off);
+        v[0] = __uint_as_float(t.x << 16); v[1] = __uint_as_float(t.x & 0xffff0000u);
+        v[2] = __uint_as_float(t.y << 16); v[3] = __uint_as_float(t.y & 0xffff0000u);
+    }
+}
+
+template <int ODT, int V>
+__device__ __forceinline__ void combine_store(void* p, int64_t o, const float acc[V]) {
+    if constexpr (ODT == NSOSX_F32) {
+#pragma unroll
+        for (int j = 0; j < V; j += 4)
+            *reinterpret_cast<float4*>(static_cast<float*>(p) + o + j) =
+                make_float4(acc[j], acc[j + 1], acc[j + 2], acc[j + 3]);
+    } else if constexpr (V == 8) {
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + o) =
+            make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
+                       pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7]));
+    } else {
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + o) =
+            make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
+    }
+}
+
+template <int IDT, int ODT, int V>
 __global__ __launch_bounds__(256) void combine_rows_kernel(const void* __restrict__ expert_out,
                                                            const int32_t* __restrict__ slot_of,
                                                            const int32_t* __restrict__ selected,
@@ -328,29 +370,45 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const void* __restric
         ss[j + 1] = sl;
     }
     for (int i = 0; i < kk; ++i) ws[i] = weights[(int64_t)r * E + es[i]];
-    for (int d = 4 * lane; d < dim; d += 4 * kWave) {
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int i = 0; i < kk; ++i) {
-            const int64_t off = (int64_t)ss[i] * dim + d;
-            float v[4];
-            if constexpr (IDT == NSOSX_F32) {
-                const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(expert_out) + off);
-                v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-            } else {
-                const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(expert_out) + off);
-                v[0] = __uint_as_float(t.x << 16); v[1] = __uint_as_float(t.x & 0xffff0000u);
-                v[2] = __uint_as_float(t.y << 16); v[3] = __uint_as_float(t.y & 0xffff0000u);
+    const int64_t orow = (int64_t)r * dim;
+    constexpr int S = 4;  // steps whose loads go out together (k <= 2)
+    if (kk <= 2) {
+        // a missing second expert re-reads the first with weight 0 (never added)
+        const int64_t b0 = (int64_t)ss[0] * dim, b1 = (int64_t)ss[kk - 1] * dim;
+        for (int d0 = V * lane; d0 < dim; d0 += S * V * kWave) {
+            float v0[S][V], v1[S][V];
+#pragma unroll
+            for (int u = 0; u < S; ++u) {
+                const int d = min(d0 + u * V * kWave, dim - V);
+                combine_load<IDT, V>(expert_out, b0 + d, v0[u]);
+                combine_load<IDT, V>(expert_out, b1 + d, v1[u]);
             }
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[j] = acc[j] + __fmul_rn(v[j], ws[i]);
+            for (int u = 0; u < S; ++u) {
+                const int d = d0 + u * V * kWave;
+                if (d >= dim) break;
+                float acc[V];
+#pragma unroll
+                for (int j = 0; j < V; ++j) {
+                    acc[j] = 0.0f + __fmul_rn(v0[u][j], ws[0]);
+                    if (kk == 2) acc[j] = acc[j] + __fmul_rn(v1[u][j], ws[1]);
+                }
+                combine_store<ODT, V>(out, orow + d, acc);
+            }
         }
-        const int64_t o = (int64_t)r * dim + d;
-        if constexpr (ODT == NSOSX_F32) {
-            *reinterpret_cast<float4*>(static_cast<float*>(out) + o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-        } else {
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + o) =
-                make_uint2(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]));
+        return;
+    }
+    for (int d = V * lane; d < dim; d += V * kWave) {
+        float acc[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) acc[j] = 0.0f;
+        for (int i = 0; i < kk; ++i) {
+            float v[V];
+            combine_load<IDT, V>(expert_out, (int64_t)ss[i] * dim + d, v);
+#pragma unroll
+            for (int j = 0; j < V; ++j) acc[j] = acc[j] + __fmul_rn(v[j], ws[i]);
         }
+        combine_store<ODT, V>(out, orow + d, acc);
     }
 }
 
@@ -425,13 +483,16 @@ extern "C" int nsosx_moe_combine(const void* expert_out, int in_dtype, const int
     if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype))
         return fail(NSOSX_ERR_INVALID, "moe_combine: bad dtype");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const uintptr_t align = (reinterpret_cast<uintptr_t>(expert_out) | reinterpret_cast<uintptr_t>(out)) &
-                            (in_dtype == NSOSX_F32 || out_dtype == NSOSX_F32 ? 15 : 7);
+    const uintptr_t ptrs = reinterpret_cast<uintptr_t>(expert_out) | reinterpret_cast<uintptr_t>(out);
+    const uintptr_t align = ptrs & (in_dtype == NSOSX_F32 || out_dtype == NSOSX_F32 ? 15 : 7);
     if (dim % 4 == 0 && align == 0) {
         const dim3 rgrid((rows + 3) / 4), rblock(256);
-#define NSOSX_COMBR(I, O)                                                                      \
-    hipLaunchKernelGGL((combine_rows_kernel<I, O>), rgrid, rblock, 0, st, expert_out, slot_of, \
-                       selected, weights, rows, experts, k, dim, out);
+        const bool v8 = dim % 8 == 0 && (ptrs & 15) == 0;
+#define NSOSX_COMBR(I, O)                                                                        \
+    if (v8) hipLaunchKernelGGL((combine_rows_kernel<I, O, 8>), rgrid, rblock, 0, st, expert_out, \
+                               slot_of, selected, weights, rows, experts, k, dim, out);          \
+    else hipLaunchKernelGGL((combine_rows_kernel<I, O, 4>), rgrid, rblock, 0, st, expert_out,    \
+                            slot_of, selected, weights, rows, experts, k, dim, out);
         if (in_dtype == NSOSX_F32) {
             if (out_dtype == NSOSX_F32) { NSOSX_COMBR(NSOSX_F32, NSOSX_F32) } else { NSOSX_COMBR(NSOSX_F32, NSOSX_BF16) }
         } else {
