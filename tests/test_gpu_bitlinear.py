@@ -386,9 +386,12 @@ def test_grouped_gemm_mfma_matches_reference_layout(dev, gather, sqrelu):
 
 
 @pytest.mark.parametrize("m,k,dtype", [(16411, 1024, torch.bfloat16), (8200, 2048, torch.bfloat16),
-                                       (8195, 1024, torch.float32), (4100, 2048, torch.float32)])
+                                       (8195, 1024, torch.float32), (4100, 2048, torch.float32),
+                                       (8000, 1024, torch.bfloat16), (3001, 2048, torch.bfloat16),
+                                       (1500, 1024, torch.float32), (1027, 2048, torch.float32)])
 def test_rms_workspace_in_order_sum(dev, m, k, dtype):
-    """The RMS_PERI row scale left in rms_workspace (the STE backward reads it):
+    """The RMS_PERI row scale left in rms_workspace (the STE backward reads it) by the
+    tiled and the producer / consumer RMS passes:
     1 / sqrt(mean + 1e-6) of the in-order float sum of the rounded squares
     (Tensor::rmsnorm, src/tensor.cpp:3455-3492); numpy's add.accumulate adds in order."""
     from reimagined_amd._lib import call
