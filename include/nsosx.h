@@ -382,6 +382,23 @@ int nsosx_mamba2_step(const void* x, const void* z, const void* B, const void* C
                       int act_dtype, float* state, void* y, int8_t* q, float* act_scale,
                       int act_bits, void* stream);
 
+/* nsosx_mamba2_step and then the block's out_proj (Mamba2SSD's ternary out_proj in
+ * exact-linear mode, src/mamba2.cpp:514 and 4121; bitnet_gemm_158bit_gpu semantics)
+ * on its codes: out [rows, out_features] (out_dtype) = the ternary GEMM of q with
+ * out_packed [out_features, H*P / 16] words and out_weight_scale, times
+ * out_magnitude and plus out_bias where given.  One row with H*P % 64 == 0 and
+ * H*P <= 4096 takes two launches (the out_proj GEMV forms the norm and codes itself
+ * as its prologue); otherwise nsosx_mamba2_step + nsosx_ternary_gemm.  Either way y,
+ * q and act_scale are written as by nsosx_mamba2_step, with the same values. */
+int nsosx_mamba2_step_out(const void* x, const void* z, const void* B, const void* C,
+                          const void* dt, int64_t bcdt_stride, const float* conv_w,
+                          const float* conv_b, int conv_width, float* ring, const float* A_log,
+                          const float* D, const float* norm_w, float eps, int rows, int H, int P,
+                          int N, int G, int act_dtype, float* state, void* y, int8_t* q,
+                          float* act_scale, int act_bits, const uint32_t* out_packed,
+                          float out_weight_scale, int out_features, const float* out_magnitude,
+                          const float* out_bias, void* out, int out_dtype, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Top-k MoE routing.
  * ------------------------------------------------------------------------- */

@@ -7,6 +7,7 @@
 //   GEMM + affine src/bitnet_adapter_avx2.cpp:52-158
 //   packed format src/bitnet_adapter.cpp:570-606
 #include "common.hpp"
+#include "mamba2_step.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -957,6 +958,33 @@ static int gemv_grid(int N, int K, int M) {
     return std::max(1, (waves + 3) / 4);
 }
 
+// The faithful Mamba-2 decode step's out_proj for one row with the gated norm and
+// its int8 quantization as a prologue: every workgroup forms the row's codes and
+// act_scale in LDS (m2_norm_row: the same operations as mamba2_step_norm_kernel,
+// so the same bits; workgroup 0 also shifts the B / C ring slots and writes the
+// codes and scale out), then its waves run the M = 1 GEMV on them.  One launch
+// where the norm kernel and the GEMV were two.
+constexpr int kM2GemvMaxK = 4096;
+
+template <int ADT, int YDT>
+__global__ __launch_bounds__(256) void mamba2_norm_gemv_kernel(M2StepArgs a, GemvProblem pb,
+                                                               void* out) {
+    __shared__ __attribute__((aligned(16))) float s_g[kM2GemvMaxK];
+    __shared__ __attribute__((aligned(16))) int8_t s_q[kM2GemvMaxK];
+    __shared__ float s_red[4];
+    __shared__ float s_inv, s_scale;
+    m2_norm_row<ADT, 256, kM2GemvMaxK / (256 * 4)>(a, 0, blockIdx.x == 0, s_q, &s_scale, s_g,
+                                                   s_red, &s_inv);
+    __syncthreads();
+    if (blockIdx.x == 0) {
+        for (int i = threadIdx.x * 4; i < pb.K; i += 256 * 4)
+            *reinterpret_cast<uint32_t*>(a.q + i) = *reinterpret_cast<const uint32_t*>(s_q + i);
+        if (threadIdx.x == 0) a.act_scale[0] = s_scale;
+    }
+    const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+    gemv_body_long<1, YDT, false>(pb, s_q, &s_scale, 1, out, nullptr, wave_id, gridDim.x * 4, 1);
+}
+
 template <int YDT>
 static void launch_gemv_t(const GemvProblem& pb, const int8_t* q, const float* as, int M,
                           void* y, int32_t* acc, hipStream_t st) {
@@ -973,6 +1001,27 @@ static void launch_gemv_t(const GemvProblem& pb, const int8_t* q, const float* a
     else if (M <= 4) { NSOSX_GEMV(4) }
     else { NSOSX_GEMV(8) }
 #undef NSOSX_GEMV
+}
+
+bool mamba2_norm_gemv_ok(int rows, int K) {
+    return rows == 1 && K % 64 == 0 && K <= kM2GemvMaxK;
+}
+
+int launch_mamba2_norm_gemv(const M2StepArgs& a, int act_dtype, const uint32_t* packed,
+                            float weight_scale, int N, const float* magnitude, const float* bias,
+                            void* out, int out_dtype, hipStream_t st) {
+    const int K = a.H * a.P;
+    GemvProblem pb{packed, magnitude, bias, weight_scale, N, K};
+    const dim3 grid(gemv_grid(N, K, 1)), block(256);
+#define NSOSX_M2G(ADT, YDT) \
+    hipLaunchKernelGGL((mamba2_norm_gemv_kernel<ADT, YDT>), grid, block, 0, st, a, pb, out);
+    if (act_dtype == NSOSX_F32) {
+        if (out_dtype == NSOSX_F32) { NSOSX_M2G(NSOSX_F32, NSOSX_F32) } else { NSOSX_M2G(NSOSX_F32, NSOSX_BF16) }
+    } else {
+        if (out_dtype == NSOSX_F32) { NSOSX_M2G(NSOSX_BF16, NSOSX_F32) } else { NSOSX_M2G(NSOSX_BF16, NSOSX_BF16) }
+    }
+#undef NSOSX_M2G
+    return check_launch("mamba2_step_out");
 }
 
 // ===========================================================================

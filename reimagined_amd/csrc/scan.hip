@@ -13,9 +13,11 @@
 // state) in double and rounded to float; v_exp_f32 then costs one
 // transcendental per (token, channel, state).
 #include "common.hpp"
+#include "mamba2_step.hpp"
 
 #include <algorithm>
 #include <cmath>
+#include <string>
 
 namespace nsosx {
 
@@ -967,34 +969,6 @@ __global__ __launch_bounds__(256) void scan_step_rows_kernel(
 // quantize_act_i8 bit for bit when the gated norm takes its register path
 // (inner % 512 == 0, inner <= 4096).
 // ===========================================================================
-constexpr int kM2MaxInner = 8192;   // g and gamma of one row in LDS
-constexpr int kM2MaxGS = 1024;      // B and C of one row in LDS
-constexpr int kM2MaxW = 4;
-constexpr int kM2NormThreads = 512;
-constexpr int kM2Rounds = kM2MaxInner / (kM2NormThreads * 4);  // 4-element chunks per thread
-
-struct M2StepArgs {
-    const void* x;            // [rows, inner]
-    const void* z;            // [rows, inner]
-    const void* B;            // [rows, GS], row stride bcdt_stride
-    const void* C;
-    const void* dt;           // [rows, H], row stride bcdt_stride
-    int64_t bcdt_stride;
-    const float* conv_w;      // [inner + 2 GS, W]
-    const float* conv_b;      // [inner + 2 GS] or null
-    float* ring;              // [rows, W - 1, inner + 2 GS]
-    const float* a_log;       // [H]
-    const float* dskip;       // [H]
-    const float* norm_w;      // [inner] or null
-    float eps;
-    float q_max;
-    int H, P, N, G, W;
-    float* state;             // [rows, inner, N]
-    void* y;                  // [rows, inner]
-    int8_t* q;                // [rows, inner]
-    float* act_scale;         // [rows]
-};
-
 // conv ring value of channel c (conv_step_kernel's order: bias first, taps oldest
 // to newest, the new input last) and its SiLU, rounded as stored
 template <int ADT>
@@ -1083,137 +1057,9 @@ __global__ __launch_bounds__(kM2NormThreads) void mamba2_step_norm_kernel(M2Step
     __shared__ __attribute__((aligned(16))) float s_g[kM2MaxInner];
     __shared__ float s_red[kM2NormThreads / kWave];
     __shared__ float s_inv;
-    const int r = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int inner = a.H * a.P;
-    const int GS = a.G * a.N;
-    const int CD = inner + 2 * GS;
-    const int taps = a.W - 1;
-    // every load of the launch first, one memory round trip: y, z and gamma of this
-    // thread's chunks (indices past inner re-read the last element), then the B / C
-    // ring slots of this thread's channel
-    float yv[kM2Rounds][4], zv[kM2Rounds][4], gm[kM2Rounds][4];
-#pragma unroll
-    for (int k = 0; k < kM2Rounds; ++k)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int idx = min((k * kM2NormThreads + tid) * 4 + e, inner - 1);
-            yv[k][e] = load_act<ADT>(a.y, (int64_t)r * inner + idx);
-            zv[k][e] = load_act<ADT>(a.z, (int64_t)r * inner + idx);
-            gm[k][e] = a.norm_w ? a.norm_w[idx] : 1.0f;
-        }
-    const int j = tid;  // B / C channel (2 GS <= kM2NormThreads is the common case)
-    const bool shift = taps > 0 && j < 2 * GS;
-    float* rg = a.ring + (int64_t)r * taps * CD + inner + min(j, 2 * GS - 1);
-    float t[kM2MaxW - 1];
-    float bcur = 0.0f;
-    if (shift) {
-        bcur = load_act<ADT>(j < GS ? a.B : a.C, (int64_t)r * a.bcdt_stride + (j < GS ? j : j - GS));
-#pragma unroll
-        for (int s2 = 0; s2 < kM2MaxW - 1; ++s2) t[s2] = s2 < taps ? rg[(int64_t)s2 * CD] : 0.0f;
-    }
-    // g = y * SiLU(z), the gated norm kernel's product
-#pragma unroll
-    for (int k = 0; k < kM2Rounds; ++k)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int idx = (k * kM2NormThreads + tid) * 4 + e;
-            if (idx < inner) s_g[idx] = yv[k][e] * silu_exact(zv[k][e]);
-        }
-    // the B / C ring slots: every reader (the scan launch) has finished
-    if (shift) {
-#pragma unroll
-        for (int s2 = 0; s2 + 1 < kM2MaxW - 1; ++s2)
-            if (s2 + 1 < taps) rg[(int64_t)s2 * CD] = t[s2 + 1];
-        rg[(int64_t)(taps - 1) * CD] = bcur;
-    }
-    for (int jj = j + kM2NormThreads; taps > 0 && jj < 2 * GS; jj += kM2NormThreads) {
-        const float cur2 = load_act<ADT>(jj < GS ? a.B : a.C,
-                                         (int64_t)r * a.bcdt_stride + (jj < GS ? jj : jj - GS));
-        float* rg2 = a.ring + (int64_t)r * taps * CD + inner + jj;
-        float t2[kM2MaxW - 1];
-#pragma unroll
-        for (int s2 = 0; s2 < kM2MaxW - 1; ++s2) t2[s2] = s2 < taps ? rg2[(int64_t)s2 * CD] : 0.0f;
-#pragma unroll
-        for (int s2 = 0; s2 + 1 < kM2MaxW - 1; ++s2)
-            if (s2 + 1 < taps) rg2[(int64_t)s2 * CD] = t2[s2 + 1];
-        rg2[(int64_t)(taps - 1) * CD] = cur2;
-    }
-    __syncthreads();
-    if (wave == 0) {
-        // four 512-element chunks per step, their LDS reads issued together; elements
-        // past inner (stale LDS) are masked to zero, and fma(0, 0, sum) == sum
-        float sum = 0.0f;
-        for (int b = 0; b < inner; b += 4 * 8 * kWave) {
-            float4 t[4][2];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int e0 = min(b + (u * kWave + lane) * 8, kM2MaxInner - 8);
-                t[u][0] = *reinterpret_cast<const float4*>(s_g + e0);
-                t[u][1] = *reinterpret_cast<const float4*>(s_g + e0 + 4);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float v[8] = {t[u][0].x, t[u][0].y, t[u][0].z, t[u][0].w,
-                                    t[u][1].x, t[u][1].y, t[u][1].z, t[u][1].w};
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const float g = b + (u * kWave + lane) * 8 + k < inner ? v[k] : 0.0f;
-                    sum = __fmaf_rn(g, g, sum);
-                }
-            }
-        }
-        sum = wave_sum(sum);
-        if (lane == 0) s_inv = 1.0f / sqrtf(sum / static_cast<float>(inner) + a.eps);
-    }
-    __syncthreads();
-    const float inv = s_inv;
-    float nv[kM2Rounds][4];
-    float m = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kM2Rounds; ++k) {
-        const int i0 = (k * kM2NormThreads + tid) * 4;
-        const float4 t = *reinterpret_cast<const float4*>(s_g + i0);
-        const float v[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float o = v[e] * inv;
-            if (a.norm_w) o = o * gm[k][e];
-            o = i0 + e < inner ? round_act<ADT>(o) : 0.0f;
-            nv[k][e] = o;
-            m = fmaxf(m, fabsf(o));
-        }
-    }
-    m = wave_max(m);
-    if (lane == 0) s_red[wave] = m;
-    __syncthreads();
-    m = s_red[0];
-#pragma unroll
-    for (int w = 1; w < kM2NormThreads / kWave; ++w) m = fmaxf(m, s_red[w]);
-    const float denom = __fadd_rn(m, 1e-8f);
-    const float sc = __fdiv_rn(a.q_max, denom);
-    if (tid == 0) a.act_scale[r] = __fdiv_rn(denom, a.q_max);
-    const int body = inner & ~7;
-    int8_t* qr = a.q + (int64_t)r * inner;
-#pragma unroll
-    for (int k = 0; k < kM2Rounds; ++k) {
-        const int i0 = (k * kM2NormThreads + tid) * 4;
-        if (i0 >= inner) break;
-        float code[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float val = __fmul_rn(nv[k][e], sc);
-            code[e] = clamp127(i0 + e < body ? rintf(val) : roundf(val));
-        }
-        if (i0 + 4 <= inner && ((reinterpret_cast<uintptr_t>(qr) + i0) & 3) == 0) {
-            *reinterpret_cast<uint32_t*>(qr + i0) = pack4_i8(code[0], code[1], code[2], code[3]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (i0 + e < inner) qr[i0 + e] = static_cast<int8_t>(static_cast<int>(code[e]));
-        }
-    }
+    m2_norm_row<ADT, kM2NormThreads, kM2MaxInner / (kM2NormThreads * 4)>(
+        a, blockIdx.x, true, a.q + (int64_t)blockIdx.x * a.H * a.P, a.act_scale + blockIdx.x, s_g,
+        s_red, &s_inv);
 }
 
 // ===========================================================================
@@ -1722,6 +1568,68 @@ extern "C" int nsosx_selective_scan_step(const void* x, const void* dt, const fl
     return check_launch("selective_scan_step");
 }
 
+// Argument checks and the argument block of the Mamba-2 decode step entries.
+static int m2_prepare(const char* what, const void* x, const void* z, const void* B,
+                      const void* C, const void* dt, int64_t bcdt_stride, const float* conv_w,
+                      const float* conv_b, int conv_width, float* ring, const float* A_log,
+                      const float* D, const float* norm_w, float eps, int rows, int H, int P,
+                      int N, int G, int act_dtype, float* state, void* y, int8_t* q,
+                      float* act_scale, int act_bits, M2StepArgs& a) {
+    const std::string w(what);
+    if (!x || !z || !B || !C || !dt || !conv_w || !A_log || !D || !state || !y || !q ||
+        !act_scale || (conv_width > 1 && !ring))
+        return fail(NSOSX_ERR_INVALID, w + ": null pointer");
+    if (rows <= 0 || rows > 65535 || H <= 0 || P <= 0 || G <= 0 || H % G != 0 ||
+        bcdt_stride <= 0)
+        return fail(NSOSX_ERR_INVALID, w + ": bad shape");
+    if (!valid_dtype(act_dtype)) return fail(NSOSX_ERR_INVALID, w + ": bad dtype");
+    if (!(eps > 0.0f) || !std::isfinite(eps))
+        return fail(NSOSX_ERR_INVALID, w + ": eps must be finite and > 0");
+    if (act_bits < 2 || act_bits > 8)
+        return fail(NSOSX_ERR_INVALID, w + ": act_bits must be in [2, 8]");
+    if ((int64_t)H * P > kM2MaxInner || (int64_t)G * N > kM2MaxGS || conv_width < 1 ||
+        conv_width > kM2MaxW || !(N == 4 || N == 8 || N == 16 || N == 32 || N == 64))
+        return fail(NSOSX_ERR_INVALID,
+                    w + ": needs H*P <= 8192, G*N <= 1024, N in {4, 8, 16, 32, 64}, "
+                        "1 <= conv_width <= 4");
+    if (reinterpret_cast<uintptr_t>(state) % 16)
+        return fail(NSOSX_ERR_INVALID, w + ": state must be 16-byte aligned");
+    a = M2StepArgs{};
+    a.x = x; a.z = z; a.B = B; a.C = C; a.dt = dt; a.bcdt_stride = bcdt_stride;
+    a.conv_w = conv_w; a.conv_b = conv_b; a.ring = ring;
+    a.a_log = A_log; a.dskip = D; a.norm_w = norm_w; a.eps = eps;
+    a.q_max = act_bits <= 2 ? 1.0f : static_cast<float>((1 << (act_bits - 1)) - 1);
+    a.H = H; a.P = P; a.N = N; a.G = G; a.W = conv_width;
+    a.state = state; a.y = y; a.q = q; a.act_scale = act_scale;
+    return NSOSX_OK;
+}
+
+static void m2_launch_scan(const M2StepArgs& a, int rows, int act_dtype, hipStream_t st) {
+    const dim3 grid((a.H * a.P + 63) / 64, rows);
+#define NSOSX_M2(ADT, SPL) \
+    hipLaunchKernelGGL((mamba2_step_scan_kernel<ADT, SPL>), grid, dim3(256), 0, st, a);
+#define NSOSX_M2_N(ADT)                         \
+    switch (a.N) {                              \
+        case 4: NSOSX_M2(ADT, 1) break;         \
+        case 8: NSOSX_M2(ADT, 2) break;         \
+        case 16: NSOSX_M2(ADT, 4) break;        \
+        case 32: NSOSX_M2(ADT, 8) break;        \
+        default: NSOSX_M2(ADT, 16) break;       \
+    }
+    if (act_dtype == NSOSX_F32) { NSOSX_M2_N(NSOSX_F32) } else { NSOSX_M2_N(NSOSX_BF16) }
+#undef NSOSX_M2_N
+#undef NSOSX_M2
+}
+
+static void m2_launch_norm(const M2StepArgs& a, int rows, int act_dtype, hipStream_t st) {
+    if (act_dtype == NSOSX_F32)
+        hipLaunchKernelGGL((mamba2_step_norm_kernel<NSOSX_F32>), dim3(rows), dim3(kM2NormThreads),
+                           0, st, a);
+    else
+        hipLaunchKernelGGL((mamba2_step_norm_kernel<NSOSX_BF16>), dim3(rows),
+                           dim3(kM2NormThreads), 0, st, a);
+}
+
 extern "C" int nsosx_mamba2_step(const void* x, const void* z, const void* B, const void* C,
                                  const void* dt, int64_t bcdt_stride, const float* conv_w,
                                  const float* conv_b, int conv_width, float* ring,
@@ -1729,55 +1637,52 @@ extern "C" int nsosx_mamba2_step(const void* x, const void* z, const void* B, co
                                  float eps, int rows, int H, int P, int N, int G, int act_dtype,
                                  float* state, void* y, int8_t* q, float* act_scale,
                                  int act_bits, void* stream) {
-    if (!x || !z || !B || !C || !dt || !conv_w || !A_log || !D || !state || !y || !q ||
-        !act_scale || (conv_width > 1 && !ring))
-        return fail(NSOSX_ERR_INVALID, "mamba2_step: null pointer");
-    if (rows <= 0 || rows > 65535 || H <= 0 || P <= 0 || G <= 0 || H % G != 0 ||
-        bcdt_stride <= 0)
-        return fail(NSOSX_ERR_INVALID, "mamba2_step: bad shape");
-    if (!valid_dtype(act_dtype)) return fail(NSOSX_ERR_INVALID, "mamba2_step: bad dtype");
-    if (!(eps > 0.0f) || !std::isfinite(eps))
-        return fail(NSOSX_ERR_INVALID, "mamba2_step: eps must be finite and > 0");
-    if (act_bits < 2 || act_bits > 8)
-        return fail(NSOSX_ERR_INVALID, "mamba2_step: act_bits must be in [2, 8]");
-    if ((int64_t)H * P > kM2MaxInner || (int64_t)G * N > kM2MaxGS || conv_width < 1 ||
-        conv_width > kM2MaxW || !(N == 4 || N == 8 || N == 16 || N == 32 || N == 64))
-        return fail(NSOSX_ERR_INVALID,
-                    "mamba2_step: needs H*P <= 8192, G*N <= 1024, N in {4, 8, 16, 32, 64}, "
-                    "1 <= conv_width <= 4");
-    if (reinterpret_cast<uintptr_t>(state) % 16)
-        return fail(NSOSX_ERR_INVALID, "mamba2_step: state must be 16-byte aligned");
-    M2StepArgs a{};
-    a.x = x; a.z = z; a.B = B; a.C = C; a.dt = dt; a.bcdt_stride = bcdt_stride;
-    a.conv_w = conv_w; a.conv_b = conv_b; a.ring = ring;
-    a.a_log = A_log; a.dskip = D; a.norm_w = norm_w; a.eps = eps;
-    a.q_max = act_bits <= 2 ? 1.0f : static_cast<float>((1 << (act_bits - 1)) - 1);
-    a.H = H; a.P = P; a.N = N; a.G = G; a.W = conv_width;
-    a.state = state; a.y = y; a.q = q; a.act_scale = act_scale;
+    M2StepArgs a;
+    const int rc = m2_prepare("mamba2_step", x, z, B, C, dt, bcdt_stride, conv_w, conv_b,
+                              conv_width, ring, A_log, D, norm_w, eps, rows, H, P, N, G,
+                              act_dtype, state, y, q, act_scale, act_bits, a);
+    if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const dim3 grid((H * P + 63) / 64, rows);
-#define NSOSX_M2(ADT, SPL) \
-    hipLaunchKernelGGL((mamba2_step_scan_kernel<ADT, SPL>), grid, dim3(256), 0, st, a);
-#define NSOSX_M2_N(ADT)                         \
-    switch (N) {                                \
-        case 4: NSOSX_M2(ADT, 1) break;         \
-        case 8: NSOSX_M2(ADT, 2) break;         \
-        case 16: NSOSX_M2(ADT, 4) break;        \
-        case 32: NSOSX_M2(ADT, 8) break;        \
-        default: NSOSX_M2(ADT, 16) break;       \
-    }
-    if (act_dtype == NSOSX_F32) {
-        NSOSX_M2_N(NSOSX_F32)
-        hipLaunchKernelGGL((mamba2_step_norm_kernel<NSOSX_F32>), dim3(rows), dim3(kM2NormThreads),
-                           0, st, a);
-    } else {
-        NSOSX_M2_N(NSOSX_BF16)
-        hipLaunchKernelGGL((mamba2_step_norm_kernel<NSOSX_BF16>), dim3(rows),
-                           dim3(kM2NormThreads), 0, st, a);
-    }
-#undef NSOSX_M2_N
-#undef NSOSX_M2
+    m2_launch_scan(a, rows, act_dtype, st);
+    m2_launch_norm(a, rows, act_dtype, st);
     return check_launch("mamba2_step");
+}
+
+extern "C" int nsosx_mamba2_step_out(const void* x, const void* z, const void* B, const void* C,
+                                     const void* dt, int64_t bcdt_stride, const float* conv_w,
+                                     const float* conv_b, int conv_width, float* ring,
+                                     const float* A_log, const float* D, const float* norm_w,
+                                     float eps, int rows, int H, int P, int N, int G,
+                                     int act_dtype, float* state, void* y, int8_t* q,
+                                     float* act_scale, int act_bits, const uint32_t* out_packed,
+                                     float out_weight_scale, int out_features,
+                                     const float* out_magnitude, const float* out_bias, void* out,
+                                     int out_dtype, void* stream) {
+    M2StepArgs a;
+    int rc = m2_prepare("mamba2_step_out", x, z, B, C, dt, bcdt_stride, conv_w, conv_b,
+                        conv_width, ring, A_log, D, norm_w, eps, rows, H, P, N, G, act_dtype,
+                        state, y, q, act_scale, act_bits, a);
+    if (rc) return rc;
+    const int K = H * P;
+    if (!out_packed || !out) return fail(NSOSX_ERR_INVALID, "mamba2_step_out: null pointer");
+    if (out_features <= 0 || K % 16 != 0 || !valid_dtype(out_dtype) ||
+        !(out_weight_scale > 0.0f) || !std::isfinite(out_weight_scale))
+        return fail(NSOSX_ERR_INVALID,
+                    "mamba2_step_out: need out_features > 0, H*P % 16 == 0, a finite weight "
+                    "scale > 0");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    m2_launch_scan(a, rows, act_dtype, st);
+    if (mamba2_norm_gemv_ok(rows, K) && (reinterpret_cast<uintptr_t>(out_packed) & 15) == 0) {
+        rc = check_launch("mamba2_step_out");
+        if (rc) return rc;
+        return launch_mamba2_norm_gemv(a, act_dtype, out_packed, out_weight_scale, out_features,
+                                       out_magnitude, out_bias, out, out_dtype, st);
+    }
+    m2_launch_norm(a, rows, act_dtype, st);
+    rc = check_launch("mamba2_step_out");
+    if (rc) return rc;
+    return nsosx_ternary_gemm(q, act_scale, out_packed, out_weight_scale, rows, K, out_features,
+                              out_magnitude, out_bias, out, out_dtype, nullptr, stream);
 }
 
 extern "C" int nsosx_conv1d_causal(const void* in, int in_dtype, int64_t in_stride,

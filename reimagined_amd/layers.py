@@ -474,18 +474,20 @@ class Mamba2Block:
     def step(self, u: torch.Tensor, dec: dict) -> torch.Tensor:
         """One decode token per row: u [R, d_model]; updates dec's state and ring in place.
 
-        Six launches: the int8 quantization of u and the grouped x / z GEMV, the fp32
-        B / C / dt projection, the conv ring + state step and the gated norm + out_proj
-        quantization (nsosx_mamba2_step, two launches), the out_proj GEMV."""
+        Five launches at one row: the int8 quantization of u and the grouped x / z GEMV,
+        the fp32 B / C / dt projection, the conv ring + state step, and the out_proj GEMV
+        with the gated norm and its quantization as its prologue (nsosx_mamba2_step_out;
+        more rows: a norm launch, then the out_proj GEMM)."""
         xv, z, Bv, Cv, dt = self._project(u, contiguous_dt=False)
         m = u.shape[0]
         q, s, _ = self.out_proj.workspace(m, u.device)
+        out = torch.empty((m, self.out_proj.out_features), dtype=self.dtype, device=u.device)
+        op = self.out_proj
         ops.mamba2_step(xv, z, Bv, Cv, dt, self.conv_w_all, self.conv_b_all,
                         dec["ring"] if self.K > 1 else None, self.a_log, self.d_skip,
                         self.norm_w, dec["state"], self.H, self.P, self.N, self.G, eps=self.eps,
-                        act_bits=self.out_proj.bits, q=q, act_scale=s)
-        out = torch.empty((m, self.out_proj.out_features), dtype=self.dtype, device=u.device)
-        self.out_proj.gemm(q, s, m, out, _stream(), self.out_proj.magnitude, self.out_proj.bias)
+                        act_bits=op.bits, q=q, act_scale=s,
+                        out_proj=(op.packed, op.weight_scale, op.magnitude, op.bias), out=out)
         return out
 
     def capture_step(self, u_static: torch.Tensor, dec: dict):

@@ -443,7 +443,8 @@ def selective_scan_step(x, dt, a_log, B, C, D, z, state, H, P, N, G):
 
 
 def mamba2_step(x, z, B, C, dt, conv_w, conv_b, ring, a_log, D, norm_w, state, H, P, N, G,
-                eps: float = 1e-5, act_bits: int = 8, q=None, act_scale=None, y=None):
+                eps: float = 1e-5, act_bits: int = 8, q=None, act_scale=None, y=None,
+                out_proj=None, out=None):
     """The faithful Mamba-2 decode step after its projections, one launch
     (src/mamba2.cpp:4038-4125 through out_proj's input quantization, src/bitlinear.cpp:240-291):
     the conv ring over x | B | C, the state step, RMSNorm(y * SiLU(z)) * norm_w and its int8
@@ -451,7 +452,11 @@ def mamba2_step(x, z, B, C, dt, conv_w, conv_b, ring, a_log, D, norm_w, state, H
 
     x, z [R, H*P]; B, C [R, G*N] and dt [R, H] (bias included): column slices of one
     projection output sharing its row stride.  -> (q int8 [R, H*P], act_scale f32 [R],
-    y [R, H*P] the pre-gate output)."""
+    y [R, H*P] the pre-gate output).
+
+    out_proj: (packed int32 words [d, H*P / 16], weight_scale, magnitude, bias) of the
+    block's ternary out_proj; with it and `out` [R, d] the step also runs the out_proj
+    on the codes (nsosx_mamba2_step_out: one launch fewer at one row)."""
     inner, gs = H * P, G * N
     r = x.shape[0]
     _dev(x, "x")
@@ -487,9 +492,21 @@ def mamba2_step(x, z, B, C, dt, conv_w, conv_b, ring, a_log, D, norm_w, state, H
     if y is None:
         y = torch.empty_like(x)
     _shape(_dev(y, "y", x.dtype), (r, inner), "y", "mamba2_step")
-    call("nsosx_mamba2_step", _p(x), _p(z), _p(B), _p(C), _p(dt), stride, _p(conv_w), _p(conv_b),
-         width, _p(ring) if width > 1 else None, _p(a_log), _p(D), _p(norm_w), eps, r, H, P, N, G,
-         _dt(x), _p(state), _p(y), _p(q), _p(act_scale), act_bits, _stream())
+    args = (_p(x), _p(z), _p(B), _p(C), _p(dt), stride, _p(conv_w), _p(conv_b), width,
+            _p(ring) if width > 1 else None, _p(a_log), _p(D), _p(norm_w), eps, r, H, P, N, G,
+            _dt(x), _p(state), _p(y), _p(q), _p(act_scale), act_bits)
+    if out_proj is None:
+        call("nsosx_mamba2_step", *args, _stream())
+        return q, act_scale, y
+    packed, ws, mag, bias = out_proj
+    _dev(packed, "out_proj packed")
+    d = out.shape[1]
+    if packed.numel() != d * inner // 16 or tuple(out.shape) != (r, d) or not out.is_contiguous():
+        raise ValueError("mamba2_step: out_proj weights must be [d, H*P/16] words and out [R, d]")
+    _opt(mag, "out_proj magnitude")
+    _opt(bias, "out_proj bias")
+    call("nsosx_mamba2_step_out", *args, _p(packed), ws, d, _p(mag), _p(bias), _p(out), _dt(out),
+         _stream())
     return q, act_scale, y
 
 

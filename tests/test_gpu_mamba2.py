@@ -261,3 +261,40 @@ def test_mamba2_step_rejects_unsupported_shapes(dev):
     a = _step_inputs(rng, dev, 1, 2, 16, 16, 1, 5, torch.float32)      # width 5
     with pytest.raises(ValueError, match="conv_width"):
         _run_fused(ops, a, 2, 16, 16, 1)
+
+
+@pytest.mark.parametrize("R,H,P,N,G,W,dtype,d", [
+    (1, 32, 64, 16, 1, 4, torch.float32, 1024),   # the bench block: GEMV with the norm prologue
+    (1, 8, 64, 16, 1, 4, torch.bfloat16, 256),
+    (1, 3, 48, 8, 3, 4, torch.float32, 64),       # inner 144 (not % 64): norm launch + GEMM
+    (3, 8, 64, 32, 2, 3, torch.float32, 128),     # three rows: norm launch + GEMM
+])
+def test_mamba2_step_out_equals_step_then_gemm(dev, R, H, P, N, G, W, dtype, d):
+    """nsosx_mamba2_step_out equals nsosx_mamba2_step followed by the out_proj ternary GEMM
+    on its codes, bit for bit: out, codes, act_scale, state, ring and y."""
+    from reimagined_amd import ops
+    rng = np.random.default_rng(R * 100 + H + d)
+    a = _step_inputs(rng, dev, R, H, P, N, G, W, dtype)
+    inner = H * P
+    w = rng.standard_normal((d, inner)).astype(np.float32)
+    packed, ws = ops.pack_ternary(w)
+    pk = torch.from_numpy(packed.view(np.int32)).to(dev)
+    mag = torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(dev)
+    res = []
+    for fused in (False, True):
+        ring, state = a["ring"].clone(), a["state"].clone()
+        q = torch.empty((R, inner), dtype=torch.int8, device=dev)
+        s = torch.empty(R, dtype=torch.float32, device=dev)
+        out = torch.empty((R, d), dtype=dtype, device=dev)
+        kw = dict(q=q, act_scale=s)
+        if fused:
+            kw.update(out_proj=(pk, ws, mag, None), out=out)
+        _, _, y = ops.mamba2_step(a["x"], a["z"], a["B"], a["C"], a["dt"], a["conv_w"],
+                                  a["conv_b"], ring if W > 1 else None, a["a_log"], a["D"],
+                                  a["norm_w"], state, H, P, N, G, **kw)
+        if not fused:
+            out = ops.ternary_gemm(q, s, pk, ws, d, magnitude=mag, out_dtype=dtype)
+        torch.cuda.synchronize()
+        res.append([t.float().cpu().numpy() for t in (out, q, s, state, ring, y)])
+    for want, got in zip(*res):
+        np.testing.assert_array_equal(got, want)
