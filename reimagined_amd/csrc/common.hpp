@@ -153,15 +153,50 @@ __device__ __forceinline__ uint32_t pack4_i8(float a, float b, float c, float d)
 
 // ---- wave reductions (wave64) ---------------------------------------------
 
+// The value of lane (lane ^ O) without a trip through LDS memory: DPP quad
+// permutes for 1 and 2, a row rotation by 8 (within a 16-lane row that is lane ^ 8),
+// the swizzle unit's xor mode for 4 and 16 (within 32 lanes), and the 32-lane swap
+// for 32.  The same exchange as __shfl_xor(v, O), so the butterflies below add and
+// compare the same pairs in the same order.
+template <int O>
+__device__ __forceinline__ float lane_xor(float v) {
+    const int u = __float_as_int(v);
+    if constexpr (O == 1) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0xB1, 0xF, 0xF, true));
+    } else if constexpr (O == 2) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0x4E, 0xF, 0xF, true));
+    } else if constexpr (O == 8) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0x128, 0xF, 0xF, true));
+    } else if constexpr (O == 4 || O == 16) {
+        return __int_as_float(__builtin_amdgcn_ds_swizzle(u, 0x1F | (O << 10)));
+    } else {
+        static_assert(O == 32, "lane_xor: 1, 2, 4, 8, 16 or 32");
+        // lanes 0-31 of the swapped source hold lanes 32-63, lanes 32-63 of the
+        // swapped destination lanes 0-31
+        const auto p = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(u),
+                                                        static_cast<unsigned>(u), false, false);
+        const bool hi = (threadIdx.x & 32) != 0;
+        return __uint_as_float(hi ? p[0] : p[1]);
+    }
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    v = fmaxf(v, lane_xor<32>(v));
+    v = fmaxf(v, lane_xor<16>(v));
+    v = fmaxf(v, lane_xor<8>(v));
+    v = fmaxf(v, lane_xor<4>(v));
+    v = fmaxf(v, lane_xor<2>(v));
+    v = fmaxf(v, lane_xor<1>(v));
     return v;
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    v += lane_xor<32>(v);
+    v += lane_xor<16>(v);
+    v += lane_xor<8>(v);
+    v += lane_xor<4>(v);
+    v += lane_xor<2>(v);
+    v += lane_xor<1>(v);
     return v;
 }
 
