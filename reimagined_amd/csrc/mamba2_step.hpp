@@ -59,15 +59,45 @@ __device__ __forceinline__ void m2_norm_row(const M2StepArgs& a, int r, bool shi
     // thread's chunks (indices past inner re-read the last element), then the B / C
     // ring slots of this thread's channel
     float yv[ROUNDS][4], zv[ROUNDS][4], gm[ROUNDS][4];
+    constexpr uintptr_t VA = ADT == NSOSX_F32 ? 15 : 7;  // alignment of a 4-element load
+    const bool vec = (inner & 3) == 0 &&
+                     ((reinterpret_cast<uintptr_t>(a.y) | reinterpret_cast<uintptr_t>(a.z)) & VA) == 0 &&
+                     (reinterpret_cast<uintptr_t>(a.norm_w) & 15) == 0;
+    if (vec) {
+        // one load per chunk and tensor (chunks past inner re-read the last chunk)
+        auto load4 = [&](const void* p, int64_t off, float v[4]) {
+            if constexpr (ADT == NSOSX_F32) {
+                const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + off);
+                v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+            } else {
+                const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + off);
+                v[0] = __uint_as_float(t.x << 16); v[1] = __uint_as_float(t.x & 0xffff0000u);
+                v[2] = __uint_as_float(t.y << 16); v[3] = __uint_as_float(t.y & 0xffff0000u);
+            }
+        };
 #pragma unroll
-    for (int k = 0; k < ROUNDS; ++k)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int idx = min((k * NT + tid) * 4 + e, inner - 1);
-            yv[k][e] = load_act<ADT>(a.y, (int64_t)r * inner + idx);
-            zv[k][e] = load_act<ADT>(a.z, (int64_t)r * inner + idx);
-            gm[k][e] = a.norm_w ? a.norm_w[idx] : 1.0f;
+        for (int k = 0; k < ROUNDS; ++k) {
+            const int i0 = min((k * NT + tid) * 4, inner - 4);
+            load4(a.y, (int64_t)r * inner + i0, yv[k]);
+            load4(a.z, (int64_t)r * inner + i0, zv[k]);
+            if (a.norm_w) {
+                const float4 t = *reinterpret_cast<const float4*>(a.norm_w + i0);
+                gm[k][0] = t.x; gm[k][1] = t.y; gm[k][2] = t.z; gm[k][3] = t.w;
+            } else {
+                gm[k][0] = gm[k][1] = gm[k][2] = gm[k][3] = 1.0f;
+            }
         }
+    } else {
+#pragma unroll
+        for (int k = 0; k < ROUNDS; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int idx = min((k * NT + tid) * 4 + e, inner - 1);
+                yv[k][e] = load_act<ADT>(a.y, (int64_t)r * inner + idx);
+                zv[k][e] = load_act<ADT>(a.z, (int64_t)r * inner + idx);
+                gm[k][e] = a.norm_w ? a.norm_w[idx] : 1.0f;
+            }
+    }
     const int j = tid;  // B / C channel (2 GS <= NT is the common case)
     const bool shift = shift_ring && taps > 0 && j < 2 * GS;
     float* rg = a.ring + (int64_t)r * taps * CD + inner + min(j, 2 * GS - 1);
