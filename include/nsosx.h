@@ -259,6 +259,39 @@ int nsosx_grouped_gemv(const nsosx_linear_view* views_dev, int groups, const int
                        int64_t q_stride, const float* act_scale, int64_t scale_stride, int M,
                        void* y, int64_t y_stride, int y_dtype, void* stream);
 
+/* A decode projection (GpuLinearView, include/gpu_linear_view.h:8-25): a packed
+ * ternary BitLinear (packed != NULL, activation_bits 2..8) or a float linear
+ * (weight f32 [outputs, inputs], activation_bits 0), optional magnitude and bias,
+ * optional RMS_PERI input norm. */
+typedef struct nsosx_decode_view {
+    const float* weight;      /* device f32 [outputs, inputs] or NULL */
+    const uint32_t* packed;   /* device [outputs * inputs / 16] or NULL */
+    const float* magnitude;   /* device [outputs] or NULL */
+    const float* bias;        /* device [outputs] or NULL */
+    int inputs;
+    int outputs;
+    int activation_bits;      /* 0: unquantized activations (float views) */
+    int rms_input;
+    float weight_scale;
+} nsosx_decode_view;
+
+/* GpuProjectionGroup::forward / launch_grouped_decode_projections
+ * (src/gpu_projection_group.cpp:12-49, src/cuda/moe_kernels.cu:779-784): one
+ * input row (in_dtype, each view reads its first `inputs` elements) through
+ * `groups` projections in one launch; view g writes output + g * output_stride
+ * ([outputs_g], out_dtype).  With the CPU path's numerics, as every other
+ * entry: a packed view quantizes the row like nsosx_quantize_act_i8 (RMS_PERI
+ * when rms_input) and runs the ternary GEMV, so its output equals
+ * nsosx_bitlinear_forward at M = 1 bit for bit; a float view equals
+ * nsosx_linear_f32 at M = 1 bit for bit.  Each workgroup of a packed view
+ * quantizes the row itself (no prepared buffer).  A packed view needs
+ * inputs % 64 == 0 and inputs <= 4096; a float view inputs % 4 == 0 and
+ * 16-byte aligned rows; a view that does not meet them is skipped.
+ * views_dev: device array of `groups` descriptors. */
+int nsosx_grouped_decode_projections(const nsosx_decode_view* views_dev, int groups,
+                                     const void* input, int in_dtype, void* output,
+                                     int64_t output_stride, int out_dtype, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Mamba selective scan.
  * ------------------------------------------------------------------------- */

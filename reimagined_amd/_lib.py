@@ -43,6 +43,7 @@ SIGNATURES = {
     "nsosx_grouped_ternary_gemm_mfma": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i,
                                              _vp, _i, _vp]),
     "nsosx_grouped_gemv": (_i, [_vp, _i, _vp, _i64, _vp, _i64, _i, _vp, _i64, _i, _vp]),
+    "nsosx_grouped_decode_projections": (_i, [_vp, _i, _vp, _i, _vp, _i64, _i, _vp]),
     "nsosx_conv1d_causal": (_i, [_vp, _i, _i64, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i,
                                  _vp]),
     "nsosx_selective_scan_fwd": (_i, [_vp, _i64, _vp, _vp, _i, _vp, _vp, _vp, _vp, _i64, _vp,

@@ -316,17 +316,17 @@ __device__ __forceinline__ void load8(const void* x, int64_t off, float v[8]) {
 // ===========================================================================
 constexpr int kQSmallMaxK = 4096;
 
-template <int DT>
-__global__ __launch_bounds__(256) void quantize_small_rms_kernel(const void* __restrict__ x,
-                                                                 int K, float q_max, float eps,
-                                                                 float* __restrict__ rms_inv,
-                                                                 int8_t* __restrict__ q,
-                                                                 float* __restrict__ act_scale) {
-    __shared__ __align__(16) float s_row[kQSmallMaxK];
-    __shared__ float s_red[5];
-    const int row = blockIdx.x;
+// One row by a 256-thread workgroup (K % 8 == 0, K <= 4096): with RMS, the squares
+// to s_row and the in-order sum by lane 0 (rms_inv_small_kernel's operations), then
+// the absmax of x * inv (x without RMS) and the codes, as quantize_rows_vec_kernel;
+// the codes to qrow and act_scale / inv (RMS) to *scale_out / *inv_out (global
+// memory or LDS).
+template <int DT, bool RMS>
+__device__ __forceinline__ void quantize_row_wg(const void* __restrict__ x, int64_t base, int K,
+                                                float q_max, float eps, float* s_row,
+                                                float* s_red, int8_t* qrow, float* scale_out,
+                                                float* inv_out) {
     const int tid = threadIdx.x;
-    const int64_t base = (int64_t)row * K;
     float v[2][8];
     // the squares (each rounded on its own, as in the in-order sum) go to LDS, so the
     // one lane that walks the row only adds: a chain of K dependent adds
@@ -335,49 +335,54 @@ __global__ __launch_bounds__(256) void quantize_small_rms_kernel(const void* __r
         const int e0 = (c * 256 + tid) * 8;
         if (e0 < K) {
             load8<DT>(x, base + e0, v[c]);
-            float q[8];
+            if (RMS) {
+                float q[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) q[j] = __fmul_rn(v[c][j], v[c][j]);
-            *reinterpret_cast<float4*>(s_row + e0) = make_float4(q[0], q[1], q[2], q[3]);
-            *reinterpret_cast<float4*>(s_row + e0 + 4) = make_float4(q[4], q[5], q[6], q[7]);
+                for (int j = 0; j < 8; ++j) q[j] = __fmul_rn(v[c][j], v[c][j]);
+                *reinterpret_cast<float4*>(s_row + e0) = make_float4(q[0], q[1], q[2], q[3]);
+                *reinterpret_cast<float4*>(s_row + e0 + 4) = make_float4(q[4], q[5], q[6], q[7]);
+            }
         } else {
 #pragma unroll
             for (int j = 0; j < 8; ++j) v[c][j] = 0.0f;
         }
     }
-    __syncthreads();
-    if (tid == 0) {
-        float sum = 0.0f;
+    if (RMS) {
+        __syncthreads();
+        if (tid == 0) {
+            float sum = 0.0f;
 #pragma unroll 8
-        for (int k = 0; k < K; k += 4) {
-            const float4 a = *reinterpret_cast<const float4*>(s_row + k);
-            sum = __fadd_rn(sum, a.x);
-            sum = __fadd_rn(sum, a.y);
-            sum = __fadd_rn(sum, a.z);
-            sum = __fadd_rn(sum, a.w);
+            for (int k = 0; k < K; k += 4) {
+                const float4 a = *reinterpret_cast<const float4*>(s_row + k);
+                sum = __fadd_rn(sum, a.x);
+                sum = __fadd_rn(sum, a.y);
+                sum = __fadd_rn(sum, a.z);
+                sum = __fadd_rn(sum, a.w);
+            }
+            const float mean = __fdiv_rn(sum, static_cast<float>(K));
+            const float inv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
+            s_red[4] = inv;
+            if (inv_out) *inv_out = inv;
         }
-        const float mean = __fdiv_rn(sum, static_cast<float>(K));
-        const float inv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, eps)));
-        s_red[4] = inv;
-        rms_inv[row] = inv;
+        __syncthreads();
+        const float inv = s_red[4];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[c][j] = __fmul_rn(v[c][j], inv);
     }
-    __syncthreads();
-    const float inv = s_red[4];
     float m = 0.0f;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            v[c][j] = __fmul_rn(v[c][j], inv);
-            m = fmaxf(m, fabsf(v[c][j]));
-        }
+        for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[c][j]));
     m = wave_max(m);
     if ((tid & 63) == 0) s_red[tid >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
     const float denom = __fadd_rn(m, 1e-8f);
     const float sc = __fdiv_rn(q_max, denom);
-    if (tid == 0) act_scale[row] = __fdiv_rn(denom, q_max);
+    if (tid == 0) *scale_out = __fdiv_rn(denom, q_max);
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
         const int e0 = (c * 256 + tid) * 8;
@@ -388,9 +393,22 @@ __global__ __launch_bounds__(256) void quantize_small_rms_kernel(const void* __r
             uint2 out;
             out.x = pack4_i8(code[0], code[1], code[2], code[3]);
             out.y = pack4_i8(code[4], code[5], code[6], code[7]);
-            *reinterpret_cast<uint2*>(q + base + e0) = out;
+            *reinterpret_cast<uint2*>(qrow + e0) = out;
         }
     }
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void quantize_small_rms_kernel(const void* __restrict__ x,
+                                                                 int K, float q_max, float eps,
+                                                                 float* __restrict__ rms_inv,
+                                                                 int8_t* __restrict__ q,
+                                                                 float* __restrict__ act_scale) {
+    __shared__ __align__(16) float s_row[kQSmallMaxK];
+    __shared__ float s_red[5];
+    const int row = blockIdx.x;
+    quantize_row_wg<DT, true>(x, (int64_t)row * K, K, q_max, eps, s_row, s_red,
+                              q + (int64_t)row * K, act_scale + row, rms_inv + row);
 }
 
 template <int DT, bool RMS>
@@ -1001,6 +1019,114 @@ static void launch_gemv_t(const GemvProblem& pb, const int8_t* q, const float* a
     else if (M <= 4) { NSOSX_GEMV(4) }
     else { NSOSX_GEMV(8) }
 #undef NSOSX_GEMV
+}
+
+// Grouped decode projections of one input row (GpuProjectionGroup::forward,
+// src/gpu_projection_group.cpp:12-49): blockIdx.y = view.  A packed view's
+// workgroups with row blocks to run quantize the row themselves into LDS
+// (quantize_row_wg: nsosx_quantize_act_i8's operations) and run the M = 1 GEMV on
+// it; a float view's waves each take output rows with dot_kernel<.., false, 1>'s
+// operations (the row's RMS scale, when asked, from the same in-order sum as
+// rms_inv_small_kernel).  Views outside the supported shapes write nothing.
+template <int IDT, int ODT>
+__global__ __launch_bounds__(256) void decode_proj_kernel(const nsosx_decode_view* __restrict__ views,
+                                                          const void* __restrict__ input,
+                                                          void* __restrict__ output,
+                                                          int64_t output_stride) {
+    __shared__ __align__(16) float s_row[kQSmallMaxK];
+    __shared__ __align__(16) int8_t s_q[kQSmallMaxK];
+    __shared__ float s_red[5];
+    __shared__ float s_scale, s_inv;
+    const nsosx_decode_view v = views[blockIdx.y];
+    constexpr int OES = ODT == NSOSX_F32 ? 4 : 2;
+    char* out = static_cast<char*>(output) + (int64_t)blockIdx.y * output_stride * OES;
+    const int K = v.inputs, N = v.outputs;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + wave);
+    const int num_waves = gridDim.x * 4;
+    if (v.packed) {
+        if (K <= 0 || (K & 63) != 0 || K > kQSmallMaxK || N <= 0 || v.activation_bits < 2 ||
+            v.activation_bits > 8)
+            return;
+        // workgroups without a row block leave before the prologue
+        const int rows = gemv_steps_for(1, N, K, 1) * (64 / gemv_lpr(K));
+        if ((int)blockIdx.x * 4 >= (N + rows - 1) / rows) return;
+        const float qm = v.activation_bits <= 2 ? 1.0f
+                                                : static_cast<float>((1 << (v.activation_bits - 1)) - 1);
+        if (v.rms_input)
+            quantize_row_wg<IDT, true>(input, 0, K, qm, 1e-6f, s_row, s_red, s_q, &s_scale, nullptr);
+        else
+            quantize_row_wg<IDT, false>(input, 0, K, qm, 1e-6f, s_row, s_red, s_q, &s_scale, nullptr);
+        __syncthreads();
+        GemvProblem pb{v.packed, v.magnitude, v.bias, v.weight_scale, N, K};
+        gemv_body_long<1, ODT, false>(pb, s_q, &s_scale, 1, out, nullptr, wave_id, num_waves, 1);
+        return;
+    }
+    if (!v.weight || K <= 0 || (K & 3) != 0 || N <= 0 || v.activation_bits != 0 ||
+        (reinterpret_cast<uintptr_t>(v.weight) & 15) != 0)
+        return;
+    if ((int)blockIdx.x * 4 >= N) return;
+    float inv = 1.0f;
+    if (v.rms_input) {
+        if (K > kQSmallMaxK) return;
+        for (int k = threadIdx.x; k < K; k += 256) {
+            const float t = load_act<IDT>(input, k);
+            s_row[k] = (k < (K & ~3)) ? __fmul_rn(t, t) : t;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float sum = 0.0f;
+            for (int k = 0; k < (K & ~3); k += 4) {
+                const float4 a = *reinterpret_cast<const float4*>(s_row + k);
+                sum = __fadd_rn(sum, a.x);
+                sum = __fadd_rn(sum, a.y);
+                sum = __fadd_rn(sum, a.z);
+                sum = __fadd_rn(sum, a.w);
+            }
+            const float mean = __fdiv_rn(sum, static_cast<float>(K));
+            s_inv = __fdiv_rn(1.0f, sqrtf(__fadd_rn(mean, 1e-6f)));
+        }
+        __syncthreads();
+        inv = s_inv;
+    }
+    auto load4 = [&](const void* base, bool is_x, int64_t off, float r[4]) {
+        if (!is_x || IDT == NSOSX_F32) {
+            const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
+            r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
+        } else {
+            const uint2 a = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
+            r[0] = __uint_as_float(a.x << 16); r[1] = __uint_as_float(a.x & 0xFFFF0000u);
+            r[2] = __uint_as_float(a.y << 16); r[3] = __uint_as_float(a.y & 0xFFFF0000u);
+        }
+    };
+    for (int row = wave_id; row < N; row += num_waves) {
+        float acc = 0.0f;
+        for (int k0 = 4 * lane; k0 < K; k0 += 1024) {
+            float mine[4][4], other[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int k = min(k0 + 256 * u, K - 4);
+                load4(v.weight, false, (int64_t)row * K + k, mine[u]);
+                load4(input, true, k, other[u]);
+                if (v.rms_input) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) other[u][e] = __fmul_rn(other[u][e], inv);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (k0 + 256 * u >= K) break;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc = __fmaf_rn(mine[u][e], other[u][e], acc);
+            }
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) {
+            if (v.magnitude) acc = __fmul_rn(acc, v.magnitude[row]);
+            if (v.bias) acc = __fadd_rn(acc, v.bias[row]);
+            store_act<ODT>(out, row, acc);
+        }
+    }
 }
 
 bool mamba2_norm_gemv_ok(int rows, int K) {
@@ -2499,6 +2625,34 @@ extern "C" int nsosx_bitlinear_forward(const void* x, int x_dtype, const uint32_
     if (rc) return rc;
     return nsosx_ternary_gemm(q_workspace, scale_workspace, packed, weight_scale, M, K, N,
                               magnitude, bias, y, y_dtype, nullptr, stream);
+}
+
+extern "C" int nsosx_grouped_decode_projections(const nsosx_decode_view* views_dev, int groups,
+                                                const void* input, int in_dtype, void* output,
+                                                int64_t output_stride, int out_dtype,
+                                                void* stream) {
+    if (!views_dev || !input || !output)
+        return fail(NSOSX_ERR_INVALID, "grouped_decode_projections: null pointer");
+    if (groups <= 0 || groups > 65535 || output_stride < 0)
+        return fail(NSOSX_ERR_INVALID, "grouped_decode_projections: groups in [1, 65535]");
+    if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype))
+        return fail(NSOSX_ERR_INVALID, "grouped_decode_projections: bad dtype");
+    if (reinterpret_cast<uintptr_t>(input) % 16)
+        return fail(NSOSX_ERR_INVALID, "grouped_decode_projections: input must be 16-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // as the grouped GEMV at M = 1: about 8192 workgroups in all, each view's waves
+    // striding over its row blocks (or rows)
+    const dim3 grid(std::max(4, std::min(512, 8192 / groups)), groups), block(256);
+#define NSOSX_DP(I, O) \
+    hipLaunchKernelGGL((decode_proj_kernel<I, O>), grid, block, 0, st, views_dev, input, output, \
+                       output_stride);
+    if (in_dtype == NSOSX_F32) {
+        if (out_dtype == NSOSX_F32) { NSOSX_DP(NSOSX_F32, NSOSX_F32) } else { NSOSX_DP(NSOSX_F32, NSOSX_BF16) }
+    } else {
+        if (out_dtype == NSOSX_F32) { NSOSX_DP(NSOSX_BF16, NSOSX_F32) } else { NSOSX_DP(NSOSX_BF16, NSOSX_BF16) }
+    }
+#undef NSOSX_DP
+    return check_launch("grouped_decode_projections");
 }
 
 extern "C" int nsosx_grouped_gemv(const nsosx_linear_view* views_dev, int groups, const int8_t* q,

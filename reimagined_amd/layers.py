@@ -413,12 +413,27 @@ class Mamba2Block:
         self.d_skip = torch.as_tensor(params["d_skip"], **f32)
         self.norm_w = torch.as_tensor(params["norm_w"], **f32)
         self.views = ops.LinearViewArray([p.view_entry() for p in self.xz], device)
+        # one decode row: x, z (packed, 8-bit activations) and B / C / dt (float, with
+        # the dt bias) in one grouped launch
+        self.decode_views = ops.DecodeViewArray(
+            [{"packed": p.packed, "weight_scale": p.weight_scale, "bits": 8,
+              "inputs": self.d_model, "outputs": self.inner} for p in self.xz] +
+            [{"weight": self.w_sens, "bias": self.b_sens, "inputs": self.d_model,
+              "outputs": self.w_sens.shape[0]}], device)
 
     def _project(self, u: torch.Tensor, contiguous_dt: bool = True) -> list:
         """x, z from one int8 quantization of u (one grouped GEMV launch for <= 8 rows,
         else two ternary GEMMs); B, C, dt from one fp32 GEMM (B and C strided column
         slices; dt contiguous for the prefill scan, a slice too for the decode step)."""
         m = u.shape[0]
+        g = self.gs
+        if m == 1 and self.d_model % 64 == 0 and self.d_model <= 4096:
+            # x / z quantize their row per workgroup; B / C / dt on the float path
+            out = ops.grouped_decode_projections(self.decode_views, u[0], out_dtype=self.dtype)
+            sens = out[2:3, :self.w_sens.shape[0]]
+            dt = sens[:, 2 * g:]
+            return [out[0:1, :self.inner], out[1:2, :self.inner], sens[:, :g], sens[:, g:2 * g],
+                    dt.contiguous() if contiguous_dt else dt]
         q, s, _ = self.xz[0].workspace(m, u.device)
         st = _stream()
         call("nsosx_quantize_act_i8", _p(u), ops._dt(u), m, self.d_model, 8, 0, _p(q), _p(s),
@@ -435,7 +450,6 @@ class Mamba2Block:
             for p, out in zip(self.xz, (xv, z)):
                 p.gemm(q, s, m, out, st)
         sens = ops.linear_f32(u, self.w_sens, bias=self.b_sens, out_dtype=self.dtype)
-        g = self.gs
         dt = sens[:, 2 * g:]
         return [xv, z, sens[:, :g], sens[:, g:2 * g], dt.contiguous() if contiguous_dt else dt]
 
@@ -474,10 +488,11 @@ class Mamba2Block:
     def step(self, u: torch.Tensor, dec: dict) -> torch.Tensor:
         """One decode token per row: u [R, d_model]; updates dec's state and ring in place.
 
-        Five launches at one row: the int8 quantization of u and the grouped x / z GEMV,
-        the fp32 B / C / dt projection, the conv ring + state step, and the out_proj GEMV
-        with the gated norm and its quantization as its prologue (nsosx_mamba2_step_out;
-        more rows: a norm launch, then the out_proj GEMM)."""
+        Three launches at one row: the x / z / B / C / dt projections
+        (nsosx_grouped_decode_projections), the conv ring + state step, and the out_proj
+        GEMV with the gated norm and its quantization as its prologue
+        (nsosx_mamba2_step_out).  More rows: the quantization of u and the grouped x / z
+        GEMV, the fp32 B / C / dt projection, the step, a norm launch and the out_proj."""
         xv, z, Bv, Cv, dt = self._project(u, contiguous_dt=False)
         m = u.shape[0]
         q, s, _ = self.out_proj.workspace(m, u.device)

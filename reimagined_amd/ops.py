@@ -270,6 +270,61 @@ class LinearViewArray:
         return ctypes.c_void_p(self.tensor.data_ptr())
 
 
+class DecodeViewArray:
+    """Device array of nsosx_decode_view descriptors (GpuLinearView, include/gpu_linear_view.h:8-25):
+    entries are dicts with either `packed` (int32 words) + `weight_scale` + `bits`, or `weight`
+    (f32 [outputs, inputs]); `inputs`, `outputs`, optional `magnitude`, `bias`, `rms_input`."""
+
+    class _View(ctypes.Structure):
+        _fields_ = [("weight", ctypes.c_void_p), ("packed", ctypes.c_void_p),
+                    ("magnitude", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+                    ("inputs", ctypes.c_int), ("outputs", ctypes.c_int),
+                    ("activation_bits", ctypes.c_int), ("rms_input", ctypes.c_int),
+                    ("weight_scale", ctypes.c_float)]
+
+    def __init__(self, entries, device):
+        self._keep = []
+        arr = (self._View * len(entries))()
+        for i, e in enumerate(entries):
+            ptr = lambda t: None if t is None else t.data_ptr()
+            for k in ("weight", "packed", "magnitude", "bias"):
+                if e.get(k) is not None:
+                    self._keep.append(e[k])
+            arr[i].weight = ptr(e.get("weight"))
+            arr[i].packed = ptr(e.get("packed"))
+            arr[i].magnitude = ptr(e.get("magnitude"))
+            arr[i].bias = ptr(e.get("bias"))
+            arr[i].inputs = int(e["inputs"])
+            arr[i].outputs = int(e["outputs"])
+            arr[i].activation_bits = int(e.get("bits", 0 if e.get("packed") is None else 8))
+            arr[i].rms_input = int(bool(e.get("rms_input", False)))
+            arr[i].weight_scale = float(e.get("weight_scale", 1.0))
+        self.tensor = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8).to(device)
+        self.count = len(entries)
+        self.max_outputs = max(int(e["outputs"]) for e in entries)
+
+    @property
+    def ptr(self):
+        return ctypes.c_void_p(self.tensor.data_ptr())
+
+
+def grouped_decode_projections(views: DecodeViewArray, x: torch.Tensor, out_dtype=None,
+                               out=None) -> torch.Tensor:
+    """GpuProjectionGroup::forward (src/gpu_projection_group.cpp:12-49): one input row
+    through every view -> [views, max outputs] (row g holds view g's outputs first)."""
+    _dev(x, "x")
+    if x.dim() != 1 and not (x.dim() == 2 and x.shape[0] == 1):
+        raise ValueError("grouped_decode_projections: x must be one row")
+    odt = out_dtype or x.dtype
+    if out is None:
+        out = torch.empty((views.count, views.max_outputs), dtype=odt, device=x.device)
+    elif tuple(out.shape) != (views.count, views.max_outputs) or not out.is_contiguous():
+        raise ValueError("grouped_decode_projections: out must be [views, max outputs]")
+    call("nsosx_grouped_decode_projections", views.ptr, views.count, _p(x), _dt(x), _p(out),
+         views.max_outputs, _dt(out), _stream())
+    return out
+
+
 def grouped_gemv(views: LinearViewArray, q: torch.Tensor, act_scale: torch.Tensor, n_out: int,
                  out_dtype=torch.bfloat16) -> torch.Tensor:
     """Grouped decode projections (include/cuda/kernels.cuh:27-29).

@@ -409,3 +409,47 @@ def test_rms_workspace_in_order_sum(dev, m, k, dtype):
     total = np.add.accumulate(sq, axis=1, dtype=np.float32)[:, -1]
     want = (np.float32(1.0) / np.sqrt(total / np.float32(k) + np.float32(1e-6))).astype(np.float32)
     np.testing.assert_array_equal(rw.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_grouped_decode_projections_match_single_calls(dev, dtype):
+    """One input row through packed and float views in one launch
+    (GpuProjectionGroup::forward, src/gpu_projection_group.cpp:12-49): each packed view
+    equals nsosx_bitlinear_forward at M = 1 and each float view nsosx_linear_f32 at M = 1,
+    bit for bit (RMS_PERI, magnitude, bias, 4-bit activations, a view over the first 512
+    inputs); a view outside the supported shapes writes nothing."""
+    rng = np.random.default_rng(44)
+    K = 1024
+    x = torch.from_numpy(rng.standard_normal((1, K)).astype(np.float32) * 3).to(dtype).to(dev)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dev)
+    specs = [("packed", 2048, K, 8, False, False, False), ("packed", 1024, K, 8, True, True, True),
+             ("float", 64, K, 0, False, False, True), ("float", 8, K, 0, True, True, False),
+             ("packed", 768, K, 4, False, True, False), ("packed", 256, 512, 8, True, False, True),
+             ("packed", 16, 1000, 8, False, False, False)]
+    entries, refs = [], []
+    for kind, n, k, bits, rms, mag, bias in specs:
+        w = rng.standard_normal((n, k)).astype(np.float32)
+        m_ = t(rng.uniform(0.5, 1.5, n)) if mag else None
+        b_ = t(rng.standard_normal(n)) if bias else None
+        e = {"inputs": k, "outputs": n, "rms_input": rms, "magnitude": m_, "bias": b_}
+        if kind == "packed":
+            packed, ws = ops.pack_ternary(w) if k % 16 == 0 else (np.zeros(n * k // 16 + 1, np.uint32), 1.0)
+            pk = torch.from_numpy(packed.view(np.int32)).to(dev)
+            e.update(packed=pk, weight_scale=ws, bits=bits)
+            want = (ops.bitnet_gemm_158bit_gpu(x[:, :k].contiguous(), pk, ws, 1, k, n, bits, m_, b_,
+                                               rms_input=rms) if k % 64 == 0 else None)
+        else:
+            wt = t(w)
+            e.update(weight=wt)
+            want = ops.linear_f32(x[:, :k].contiguous(), wt, rms_input=rms, magnitude=m_, bias=b_)
+        entries.append(e)
+        refs.append(want)
+    views = ops.DecodeViewArray(entries, dev)
+    out = torch.full((len(specs), views.max_outputs), 7.0, device=dev)
+    ops.grouped_decode_projections(views, x[0], out=out)
+    got = out.cpu().numpy()
+    for i, ((kind, n, *_), want) in enumerate(zip(specs, refs)):
+        if want is None:
+            assert (got[i] == 7.0).all()
+        else:
+            np.testing.assert_array_equal(got[i, :n], want.float().cpu().numpy()[0])

@@ -90,13 +90,16 @@ def test_mamba2_block_prefill_matches_oracle(dev, orc):
     np.testing.assert_array_equal(_np(res["out"]), out)
 
 
-def test_mamba2_decode_step_equals_prefill(dev, orc):
+@pytest.mark.parametrize("R", [3, 1])
+def test_mamba2_decode_step_equals_prefill(dev, orc, R):
+    """(one row: the projections in one grouped launch and the out_proj GEMV with the
+    norm prologue; three rows: the separate launches)"""
     rng = np.random.default_rng(5)
     p = _params(rng, H=2, P=32, G=1)
     blk = Mamba2Block(p, dev)
-    R, T = 3, 7
+    T = 7
     u = rng.standard_normal((R, T, 64)).astype(np.float32)
-    cu = torch.tensor([0, T, 2 * T, 3 * T], dtype=torch.int32, device=dev)
+    cu = torch.arange(R + 1, dtype=torch.int32, device=dev) * T
     pre = blk.forward(torch.from_numpy(u.reshape(R * T, 64)).to(dev), cu)["out"]
     pre = _np(pre).reshape(R, T, 64)
     dec = blk.new_decode_state(R, dev)
@@ -106,11 +109,11 @@ def test_mamba2_decode_step_equals_prefill(dev, orc):
         np.testing.assert_allclose(out, pre[:, t], rtol=1e-3, atol=1e-3 * scale)
 
 
-def test_mamba2_step_graph_replay_equals_eager(dev, orc):
+@pytest.mark.parametrize("R", [4, 1])
+def test_mamba2_step_graph_replay_equals_eager(dev, orc, R):
     rng = np.random.default_rng(8)
     p = _params(rng)
     blk = Mamba2Block(p, dev)
-    R = 4
     dec = blk.new_decode_state(R, dev)
     u_static = torch.zeros((R, 64), device=dev)
     g, out = blk.capture_step(u_static, dec)
