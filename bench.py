@@ -105,10 +105,9 @@ def bench_layer(torch, dev, steps, warmup):
 
 def bench_mamba2_decode(torch, dev, rows=1, reps=200):
     """Faithful Mamba-2 decode step (d_model 1024, 32 heads x 64, N 16, conv 4), eager vs one
-    HIP-graph replay per step: one quantization of u, one grouped GEMV for the ternary x and z
-    projections, the fp32 B / C / dt projection, the conv ring + state step and the gated norm
-    + out_proj quantization (nsosx_mamba2_step, two launches) and the out_proj GEMV, so the
-    step is launch-bound."""
+    HIP-graph replay per step.  One row: the x / z / B / C / dt projections in one grouped
+    launch, the conv ring + state step, the out_proj GEMV with the gated norm and its
+    quantization as its prologue; more rows: five launches.  The step is launch-bound."""
     from reimagined_amd.layers import Mamba2Block
     rng = np.random.default_rng(41)
     d, H, P, N, G, K = 1024, 32, 64, 16, 1, 4
@@ -348,7 +347,8 @@ def bench_decode_gemv(torch, dev, m=1, sets=128, reps=5):
     def run():
         call("nsosx_grouped_gemv", views.ptr, sets, _p(q), m * K, _p(s), m, m, _p(y), m * N, 1,
              _stream())
-    run()
+    for _ in range(5):
+        run()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):
@@ -362,7 +362,7 @@ def bench_decode_gemv(torch, dev, m=1, sets=128, reps=5):
             "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def bench_decode_gemv_sweep(torch, dev, ms=(1, 2, 4, 8, 16, 32), reps=10):
+def bench_decode_gemv_sweep(torch, dev, ms=(1, 2, 4, 8, 16, 32), reps=20):
     """Config 3's decode GEMV at M = 1..32 through the dispatching entry point, on one tall
     weight matrix of 128 config-3 weight sets stacked in N (N = 128 * 8192, K = 2048; 537 MB,
     so every launch streams the weights from HBM)."""
@@ -381,7 +381,8 @@ def bench_decode_gemv_sweep(torch, dev, ms=(1, 2, 4, 8, 16, 32), reps=10):
         def run():
             call("nsosx_ternary_gemm", _p(q), _p(s), _p(packed), 1.0, m, K, N, None, None, _p(y),
                  1, None, _stream())
-        run()
+        for _ in range(10):  # ~1 ms of launches before the timed ones: the clocks settle
+            run()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for _ in range(reps):
