@@ -347,8 +347,7 @@ def bench_decode_gemv(torch, dev, m=1, sets=128, reps=5):
     def run():
         call("nsosx_grouped_gemv", views.ptr, sets, _p(q), m * K, _p(s), m, m, _p(y), m * N, 1,
              _stream())
-    for _ in range(5):
-        run()
+    _settle(torch, run)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):
@@ -381,7 +380,9 @@ def bench_decode_gemv_sweep(torch, dev, ms=(1, 2, 4, 8, 16, 32), reps=20):
         def run():
             call("nsosx_ternary_gemm", _p(q), _p(s), _p(packed), 1.0, m, K, N, None, None, _p(y),
                  1, None, _stream())
-        for _ in range(10):  # ~1 ms of launches before the timed ones: the clocks settle
+        if m == ms[0]:
+            _settle(torch, run)
+        for _ in range(10):
             run()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
@@ -408,6 +409,7 @@ def bench_decode_step(torch, dev, reps=8):
     states = [_f32(torch, dec["state"], dev) for _ in range(8)]
     for st in states:
         ops.selective_scan_step(x, dt, a_log, B, C, Dk, z, st, Dm, 1, N, 1)
+    _settle(torch, lambda: ops.selective_scan_step(x, dt, a_log, B, C, Dk, z, states[0], Dm, 1, N, 1))
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for i in range(reps * len(states)):
@@ -419,6 +421,17 @@ def bench_decode_step(torch, dev, reps=8):
     gbs = bytes_ / (ms / 1e3) / 1e9
     return {"rows": R, "ms": round(ms, 4), "gbs": round(gbs, 1),
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def _settle(torch, fn, ms=150.0):
+    """Runs fn back to back for about `ms` of wall time: the GPU raises its clocks over
+    the first ~100 ms of sustained load, so short HBM-bound timings taken from a cold
+    start read low by up to a fifth."""
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
 
 
 def _time_ms(torch, fn, reps):
@@ -638,8 +651,10 @@ def bench_gemv_published(torch, dev, reps=100):
         q = torch.from_numpy(rng.integers(-127, 128, size=(sets, 1, k)).astype(np.int8)).to(dev)
         s = torch.full((sets, 1), 0.01, dtype=torch.float32, device=dev)
         y = torch.empty((sets, 1, n), dtype=torch.float32, device=dev)
-        ms = _time_ms(torch, lambda: call("nsosx_grouped_gemv", views.ptr, sets, _p(q), k, _p(s),
-                                          1, 1, _p(y), n, 0, _stream()), 5)
+        rot = lambda: call("nsosx_grouped_gemv", views.ptr, sets, _p(q), k, _p(s), 1, 1, _p(y), n, 0,
+                           _stream())
+        _settle(torch, rot)
+        ms = _time_ms(torch, rot, 5)
         bytes_ = sets * (n * k / 4 + k + n * 4)
         gbs = bytes_ / (ms / 1e3) / 1e9
         x = torch.randn((1, k), device=dev)
