@@ -169,9 +169,7 @@ def bench_mamba2_prefill(torch, dev, reps=5):
     cu = torch.from_numpy(inp["cu_seqlens"]).to(dev)
     T = int(inp["cu_seqlens"][-1])
     u = torch.randn((T, d), device=dev)
-    for _ in range(2):
-        blk.forward(u, cu)
-    torch.cuda.synchronize()
+    _settle(torch, lambda: blk.forward(u, cu))
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):
@@ -251,8 +249,8 @@ def pmc_traffic(stage: str):
 
 def bench_prefill_gemm(torch, dev, reps=50):
     """Config 3's prefill GEMM (4096 x 2048 x 8192, bf16 out) on the MFMA-layout weights the
-    layers use, and on the reference-layout words for comparison; 10 untimed launches first
-    (the first launches after an idle GPU run at lower clocks)."""
+    layers use, and on the reference-layout words for comparison; ~150 ms of untimed launches
+    first (the first launches after an idle GPU run at lower clocks)."""
     from reimagined_amd import ops, workloads
     from reimagined_amd._lib import call
     from reimagined_amd.ops import _p, _stream
@@ -272,8 +270,6 @@ def bench_prefill_gemm(torch, dev, reps=50):
     def run_ref():
         call("nsosx_ternary_gemm_path", _p(q), _p(s), _p(pk), ws, M, K, N, None, None, _p(y), 1,
              None, 1, _stream())
-    for _ in range(10):
-        run_mfma()
     ms = _time_ms(torch, run_mfma, reps)
     ms_ref = _time_ms(torch, run_ref, reps)
     tops = 2.0 * M * N * K / (ms / 1e3) / 1e12
@@ -296,9 +292,7 @@ def bench_moe_c5(torch, dev, reps=10):
                    hidden_dtype=torch.bfloat16)
     x = _bf16(torch, moe["x"], dev)
     logits = _f32(torch, moe["logits"], dev)
-    for _ in range(3):
-        layer.forward(x, logits)
-    torch.cuda.synchronize()
+    _settle(torch, lambda: layer.forward(x, logits))
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):
@@ -435,8 +429,7 @@ def _settle(torch, fn, ms=150.0):
 
 
 def _time_ms(torch, fn, reps):
-    fn()
-    torch.cuda.synchronize()
+    _settle(torch, fn)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):
@@ -581,7 +574,9 @@ def bench_linear_f32(torch, dev):
         x = torch.randn((m, k), device=dev)
         w = torch.randn((n, k), device=dev) / 32
         y = torch.empty((m, n), device=dev)
-        ms = _time_graph_ms(torch, lambda: ops.linear_f32(x, w, rms_input=rms, out=y), 20)
+        fwd = lambda: ops.linear_f32(x, w, rms_input=rms, out=y)
+        _settle(torch, fwd)
+        ms = _time_graph_ms(torch, fwd, 20)
         tf = 2.0 * m * n * k / (ms / 1e3) / 1e12
         gbs = (m * k * 4 + n * k * 4 + m * n * 4) / (ms / 1e3) / 1e9
         out[name] = {"shape": [m, k, n], "ms": round(ms, 4), "tflops": round(tf, 2),
@@ -653,7 +648,6 @@ def bench_gemv_published(torch, dev, reps=100):
         y = torch.empty((sets, 1, n), dtype=torch.float32, device=dev)
         rot = lambda: call("nsosx_grouped_gemv", views.ptr, sets, _p(q), k, _p(s), 1, 1, _p(y), n, 0,
                            _stream())
-        _settle(torch, rot)
         ms = _time_ms(torch, rot, 5)
         bytes_ = sets * (n * k / 4 + k + n * 4)
         gbs = bytes_ / (ms / 1e3) / 1e9
