@@ -153,8 +153,9 @@ int nsosx_ternary_gemm_path(const int8_t* q, const float* act_scale, const uint3
 /* The packed weights of one [N, K] matrix rewritten into the layout the
  * prefill MFMA GEMM decodes fastest (an upload-time step, like the reference's
  * repack of its packed cache, src/bitlinear.cpp:628-643): within each 16-code
- * word, code k moves to bits 8 (k % 4) + 2 (k / 4), and the reserved code 3
- * becomes 1 (both decode to 0).  Words stay row-major, K / 16 per row.
+ * word, code k becomes its ternary value as a two's-complement 2-bit field
+ * (-1 -> 3, 0 -> 0, +1 -> 1; the reserved code 3 -> 0) at bits
+ * 8 (k % 4) + 6 - 2 (k / 4).  Words stay row-major, K / 16 per row.
  * packed, out: device uint32 [n_words] (distinct buffers). */
 int nsosx_pack_mfma_layout(const uint32_t* packed, int64_t n_words, uint32_t* out,
                            void* stream);

@@ -1549,12 +1549,12 @@ __device__ __forceinline__ void gemm2_tile(const GemmProblem& pb, const int8_t* 
 }
 
 // ===========================================================================
-// Direct-to-LDS int8 MFMA GEMM (M > 128, K % 128 == 0).  Block tile 256 (n)
+// LDS-staged int8 MFMA GEMM (M > 128, K % 128 == 0).  Block tile 256 (n)
 // x 128 (m), four waves each owning 64 n x 128 m = 2 x 4 tiles of
-// v_mfma_i32_32x32x32_i8 (128 accumulators, 8 independent chains).  Global
-// memory goes straight into LDS with global_load_lds_dwordx4 (no VGPR
-// staging) through a 3-stage ring of 128-deep K stages (24 KB each, 72 KB in
-// all), so two workgroups share a CU and their barrier phases interleave.
+// v_mfma_i32_32x32x32_i8 (128 accumulators, 8 independent chains).  Each stage
+// is fetched into registers with 16-byte loads two stages ahead and written
+// into a 3-stage ring of 128-deep K stages (24 KB each, 72 KB in all), so two
+// workgroups share a CU and their barrier phases interleave.
 // K mapping inside a stage: MFMA step ks, lane group g (lane / 32) takes the
 // 16 k values of chunk 4 g + ks, so each lane's weights for the whole stage
 // are one 16-byte packed word group (read once, decoded one word per step)
@@ -1563,9 +1563,10 @@ __device__ __forceinline__ void gemm2_tile(const GemmProblem& pb, const int8_t* 
 // which global chunk each lane fetches:
 //   weights     the two 16-byte halves of row r swap when (r / 8) is odd
 //   activations 16-byte chunk c of row r sits in slot c ^ ((r / 2) % 8)
-// Activation rows land in natural byte order; each decoded weight word is
-// byte-transposed to match.  Rows past N or M are fetched from a clamped,
-// in-bounds row; their outputs are never stored.
+// Activation rows land in natural byte order; a reference-layout weight word is
+// byte-transposed to match after decoding (the MFMA layout decodes into natural
+// order directly).  Rows past N or M are fetched from a clamped, in-bounds row;
+// their outputs are never stored.
 // ===========================================================================
 constexpr int kG3BN = 256, kG3BM = 128, kG3BK = 128;
 constexpr int kG3Stages = 3;
@@ -1575,11 +1576,21 @@ constexpr int kG3StageBytes = kG3WBytes + kG3XBytes;
 constexpr int kGemm3Smem = kG3Stages * kG3StageBytes;
 constexpr int kGemm3Threads = 256;
 
-typedef __attribute__((address_space(3))) void lds_void_t;
+// 16-byte load of a stage through a global-memory pointer (a flat load would also
+// count against the LDS wait counter the stage loop drains before its barrier).
+__device__ __forceinline__ uint4 load_stage16(const char* p) {
+    const u32x4 v = *(global_u32x4*)(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 
-__device__ __forceinline__ lds_void_t* lds_ptr(const char* p) {
-    return (lds_void_t*)((__attribute__((address_space(3))) char*)nullptr +
-                         static_cast<unsigned>(reinterpret_cast<size_t>(p)));
+// MFMA layout word -> the 16 int8 operand bytes of codes k = 0..15 in natural
+// order, each 64 x its ternary value: code k is a two's-complement 2-bit field at
+// bits 8 (k % 4) + 6 - 2 (k / 4), so dword s (codes 4s .. 4s+3) is the word
+// shifted left by 2s with all but the top two bits of every byte cleared.  The
+// accumulators come out 64 x the true sums (exact in int32 for K < 2^18 / 127).
+__device__ __forceinline__ v4i unpack_word_mfma(uint32_t w) {
+    return v4i{(int)(w & 0xC0C0C0C0u), (int)((w << 2) & 0xC0C0C0C0u), (int)((w << 4) & 0xC0C0C0C0u),
+               (int)((w << 6) & 0xC0C0C0C0u)};
 }
 
 // One 128-deep K stage of the 256 x 128 block from LDS stage `st`: each lane
@@ -1611,11 +1622,11 @@ __device__ __forceinline__ void gemm3_stage(const char* st, int wave, int lane, 
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
             const uint32_t words[4] = {wq[nb].x, wq[nb].y, wq[nb].z, wq[nb].w};
-            uint32_t wv[4], wt[4];
-            unpack_word(words[ks], wv);
             if constexpr (SWZ) {
-                aw[nb] = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+                aw[nb] = unpack_word_mfma(words[ks]);       // 64 x the values, natural order
             } else {
+                uint32_t wv[4], wt[4];
+                unpack_word(words[ks], wv);
                 transpose16(wv, wt);                        // unpack order -> natural order
                 aw[nb] = v4i{(int)wt[0], (int)wt[1], (int)wt[2], (int)wt[3]};
             }
@@ -1787,17 +1798,6 @@ __device__ __forceinline__ void gemm3_epilogue_rows(const GemmProblem& pb,
     }
 }
 
-// Memory wait of the stage loop: at most one stage's loads (2 + MB per thread) pending.
-template <int N>
-__device__ __forceinline__ void gemm3_wait_vm() {
-    static_assert(N >= 0 && N <= 6, "stage loads per thread");
-    if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    else if constexpr (N == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
-    else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else if constexpr (N == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-}
-
 // MB: 32-row blocks of the tile that hold rows (a partial last tile of an expert's
 // segment skips the DMA and MFMAs of its empty blocks; their accumulators stay zero
 // and their rows are never stored).
@@ -1834,17 +1834,29 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
         const int src = GATHER ? perm[seg_begin + m] : seg_begin + m;
         xsrc[i] = reinterpret_cast<const char*>(q + (int64_t)src * pb.K) + c * 16;
     }
-    auto issue = [&](int kt) {
-        char* st = smem + (kt % kG3Stages) * kG3StageBytes;
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            __builtin_amdgcn_global_load_lds(wsrc[j] + kt * 32,
-                                             lds_ptr(st + (64 * wave + 32 * j) * 32), 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-            __builtin_amdgcn_global_load_lds(xsrc[i] + kt * 128,
-                                             lds_ptr(st + kG3WBytes + (32 * i + 8 * wave) * 128),
-                                             16, 0, 0);
+    // Stage kt is fetched into registers at iteration kt - 2 (16-byte loads: 2 of
+    // weights, MB of activations per lane) and written to its LDS slot at kt - 1;
+    // the slot it overwrites was last read at kt - 3, before the barrier of kt - 2.
+    // (global_load_lds straight into LDS was measured slower: its LDS writes stall
+    // the MFMA stream even when the data is already in L2.)
+    uint4 rw0, rw1, rx0, rx1, rx2, rx3;
+    auto fetch = [&](int kt) {
+        rw0 = load_stage16(wsrc[0] + kt * 32);
+        rw1 = load_stage16(wsrc[1] + kt * 32);
+        rx0 = load_stage16(xsrc[0] + kt * 128);
+        if (MB > 1) rx1 = load_stage16(xsrc[1] + kt * 128);
+        if (MB > 2) rx2 = load_stage16(xsrc[2] + kt * 128);
+        if (MB > 3) rx3 = load_stage16(xsrc[3] + kt * 128);
+    };
+    auto put = [&](int kt) {
+        char* st = smem + (kt % kG3Stages) * kG3StageBytes + lane * 16;
+        *reinterpret_cast<uint4*>(st + (64 * wave) * 32) = rw0;
+        *reinterpret_cast<uint4*>(st + (64 * wave + 32) * 32) = rw1;
+        char* sx = st + kG3WBytes + (8 * wave) * 128;
+        *reinterpret_cast<uint4*>(sx) = rx0;
+        if (MB > 1) *reinterpret_cast<uint4*>(sx + 32 * 128) = rx1;
+        if (MB > 2) *reinterpret_cast<uint4*>(sx + 64 * 128) = rx2;
+        if (MB > 3) *reinterpret_cast<uint4*>(sx + 96 * 128) = rx3;
     };
 
     v16i acc[2][4];
@@ -1853,17 +1865,29 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
 
-    issue(0);
-    if (KT > 1) issue(1);
-
+    fetch(0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    put(0);
+    if (KT > 1) fetch(1);
     for (int kt = 0; kt < KT; ++kt) {
-        // this thread's stage-kt DMA is done once at most one stage (2 + MB loads) is pending
-        if (kt + 1 < KT) gemm3_wait_vm<2 + MB>();
-        else gemm3_wait_vm<0>();
+        if (kt + 1 < KT) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt + 1 is in registers
+            put(kt + 1);
+            if (kt + 2 < KT) fetch(kt + 2);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (kt + 2 < KT) issue(kt + 2);
         gemm3_stage<SWZ, MB>(smem + (kt % kG3Stages) * kG3StageBytes, wave, lane, acc);
+    }
+    if constexpr (SWZ) {
+        // MFMA-layout operands carry 64 x the ternary values (unpack_word_mfma)
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[a][b][e] >>= 6;
     }
 
     if constexpr (YDT == NSOSX_BF16 && !ACC_OUT) {
@@ -2021,12 +2045,12 @@ __global__ __launch_bounds__(kGemm3Threads, 2) void grouped_gemm3_kernel(
 
 // ===========================================================================
 // The prefill GEMM on weights repacked into the MFMA layout
-// (nsosx_pack_mfma_layout): inside each 16-code word, code k sits at bits
-// 8 (k % 4) + 2 (k / 4), and the reserved code 3 is stored as 1.  A word then
-// unpacks with one shift, mask and table lookup per output dword straight into
-// natural k order; the reference layout needs a further 4x4 byte transpose
-// per word (eight more VALU per decoded word, 2-5 % of the GEMM's time).
-// gemm3's block, ring and DMA otherwise.
+// (nsosx_pack_mfma_layout): inside each 16-code word, code k is the two's-
+// complement ternary value at bits 8 (k % 4) + 6 - 2 (k / 4) (the reserved code
+// 3 is stored as 0).  A word then unpacks with one shift and one mask per output
+// dword straight into natural k order, each byte 64 x its value; the reference
+// layout needs a table lookup per dword and a further 4x4 byte transpose per
+// word.  gemm3's block, ring and loads otherwise.
 // ===========================================================================
 template <int YDT, bool ACC_OUT>
 __global__ __launch_bounds__(kGemm3Threads, 2) void gemm3_mfma_kernel(GemmProblem pb,
@@ -2060,16 +2084,20 @@ __global__ __launch_bounds__(kGemm3Threads, 2) void grouped_gemm3_mfma_kernel(
                                                y, smem4);
 }
 
-// Reference layout -> MFMA layout, word by word (code 3 -> 1, both decode to 0).
+// Reference layout -> MFMA layout, word by word: code k (-1 / 0 / +1 / reserved 0
+// for 0 / 1 / 2 / 3) becomes the two's-complement field (3 / 0 / 1 / 0) at bits
+// 8 (k % 4) + 6 - 2 (k / 4), the layout unpack_word_mfma() reads.
 __global__ __launch_bounds__(256) void pack_mfma_kernel(const uint32_t* __restrict__ src,
                                                         int64_t n, uint32_t* __restrict__ dst) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    uint32_t w = src[i];
-    w ^= (w & (w >> 1) & 0x55555555u) << 1;  // code 3 (11) -> 1 (01)
+    const uint32_t w = src[i];
     uint32_t o = 0;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) o |= ((w >> (2 * k)) & 3u) << (8 * (k & 3) + 2 * (k >> 2));
+    for (int k = 0; k < 16; ++k) {
+        const uint32_t f = (0x0103u >> (4 * ((w >> (2 * k)) & 3u))) & 3u;
+        o |= f << (8 * (k & 3) + 6 - 2 * (k >> 2));
+    }
     dst[i] = o;
 }
 
