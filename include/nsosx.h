@@ -161,8 +161,10 @@ int nsosx_pack_mfma_layout(const uint32_t* packed, int64_t n_words, uint32_t* ou
                            void* stream);
 
 /* nsosx_ternary_gemm's contract on weights in the MFMA layout above, always
- * on the int8 MFMA GEMM (the prefill shape; K % 128 == 0).  Same results bit
- * for bit as nsosx_ternary_gemm on the reference-layout words. */
+ * on the int8 MFMA GEMM (the prefill shape; K % 128 == 0, K <= 264208: the
+ * layout's operands are 64 x the ternary values, so 64 * 127 * K must fit
+ * int32; larger K returns NSOSX_ERR_OVERFLOW).  Same results bit for bit as
+ * nsosx_ternary_gemm on the reference-layout words. */
 int nsosx_ternary_gemm_mfma(const int8_t* q, const float* act_scale, const uint32_t* packed_mfma,
                             float weight_scale, int M, int K, int N, const float* magnitude,
                             const float* bias, void* y, int y_dtype, int32_t* acc_out,
@@ -474,8 +476,9 @@ int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, int experts,
 
 /* nsosx_grouped_ternary_gemm on views whose packed words are in the MFMA
  * layout (nsosx_pack_mfma_layout), launching only the experts' real row tiles
- * (total_rows: offsets[experts] or an upper bound).  K % 128 == 0, <= 1024
- * experts.  Same results bit for bit. */
+ * (total_rows: offsets[experts] or an upper bound).  K % 128 == 0,
+ * K <= 264208 (as nsosx_ternary_gemm_mfma), <= 1024 experts.  Same results bit
+ * for bit. */
 int nsosx_grouped_ternary_gemm_mfma(const nsosx_linear_view* views_dev, int experts,
                                     const int32_t* offsets, const int32_t* perm, int gather,
                                     const int8_t* q, const float* act_scale, int K, int N,

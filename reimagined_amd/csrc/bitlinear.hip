@@ -1588,6 +1588,7 @@ __device__ __forceinline__ uint4 load_stage16(const char* p) {
 // bits 8 (k % 4) + 6 - 2 (k / 4), so dword s (codes 4s .. 4s+3) is the word
 // shifted left by 2s with all but the top two bits of every byte cleared.  The
 // accumulators come out 64 x the true sums (exact in int32 for K < 2^18 / 127).
+constexpr int kMfmaLayoutMaxK = 2147483647 / (64 * 127);  // 64 * 127 * K fits int32
 __device__ __forceinline__ v4i unpack_word_mfma(uint32_t w) {
     return v4i{(int)(w & 0xC0C0C0C0u), (int)((w << 2) & 0xC0C0C0C0u), (int)((w << 4) & 0xC0C0C0C0u),
                (int)((w << 6) & 0xC0C0C0C0u)};
@@ -2791,6 +2792,9 @@ extern "C" int nsosx_ternary_gemm_mfma(const int8_t* q, const float* act_scale,
     if (rc) return rc;
     if (K % kG3BK != 0)
         return fail(NSOSX_ERR_INVALID, "ternary_gemm_mfma: K must be a multiple of 128");
+    if (K > kMfmaLayoutMaxK)
+        return fail(NSOSX_ERR_OVERFLOW, "ternary_gemm_mfma: K too large for the MFMA layout's "
+                                        "64x-scaled int32 sums");
     const int tiles = ((N + kG3BN - 1) / kG3BN) * ((M + kG3BM - 1) / kG3BM);
     GemmProblem pb{packed_mfma, magnitude, bias, weight_scale, N, K};
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -2817,6 +2821,9 @@ extern "C" int nsosx_grouped_ternary_gemm_mfma(const nsosx_linear_view* views_de
     if (experts <= 0 || experts > 1024 || K <= 0 || K % kG3BK || N <= 0 || total_rows < 0)
         return fail(NSOSX_ERR_INVALID,
                     "grouped_ternary_gemm_mfma: bad shape (K % 128 == 0, <= 1024 experts)");
+    if (K > kMfmaLayoutMaxK)
+        return fail(NSOSX_ERR_OVERFLOW, "grouped_ternary_gemm_mfma: K too large for the MFMA "
+                                        "layout's 64x-scaled int32 sums");
     if (!valid_dtype(y_dtype))
         return fail(NSOSX_ERR_INVALID, "grouped_ternary_gemm_mfma: bad dtype");
     if (total_rows == 0) return NSOSX_OK;

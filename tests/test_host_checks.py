@@ -89,3 +89,22 @@ def test_step_rejects_bad_shapes(name, bad):
 def test_well_shaped_cpu_tensors_reach_the_device_check(fn):
     with pytest.raises(ValueError, match="device tensor"):
         fn(_good())
+
+
+def test_mfma_layout_gemm_rejects_k_past_int32_range():
+    """MFMA-layout operands carry 64 x the ternary values, so the int32 sums hold
+    64 * 127 * K at most: K past 2^31 / (64 * 127) is refused before any device work
+    (the pointers here are host placeholders and are never dereferenced)."""
+    import ctypes
+    import numpy as np
+    from reimagined_amd import _lib
+    lib = _lib.lib()
+    buf = np.zeros(64, np.uint8)
+    base = buf.ctypes.data
+    p = ctypes.c_void_p((base + 15) & ~15)  # 16-byte aligned placeholder
+    k_big = ((2147483647 // (64 * 127)) // 128 + 1) * 128
+    f = lib.nsosx_ternary_gemm_mfma
+    f.restype = ctypes.c_int
+    rc = f(p, p, p, ctypes.c_float(1.0), 1, k_big, 16, None, None, p, 1, None, None)
+    assert rc == 2, lib.nsosx_last_error().decode()   # NSOSX_ERR_OVERFLOW
+    assert "64x-scaled" in lib.nsosx_last_error().decode()
