@@ -356,14 +356,18 @@ def bench_decode_gemv(torch, dev, m=1, sets=128, reps=5):
 
 
 def bench_decode_gemv_sweep(torch, dev, ms=(1, 2, 4, 8, 16, 32), reps=20):
-    """Config 3's decode GEMV at M = 1..32 through the dispatching entry point, on one tall
-    weight matrix of 128 config-3 weight sets stacked in N (N = 128 * 8192, K = 2048; 537 MB,
-    so every launch streams the weights from HBM)."""
+    """Config 3's decode GEMV at M = 1..32 on one tall weight matrix of 128 config-3 weight
+    sets stacked in N (N = 128 * 8192, K = 2048; 537 MB, so every launch streams the weights
+    from HBM), by the entry BitLinear uses: M = 1 through the dispatching entry on the
+    reference words (the VALU GEMV), M >= 2 through nsosx_ternary_gemm_mfma on the MFMA-layout
+    copy (the skinny MFMA kernel, shift-and-mask decode)."""
+    from reimagined_amd import ops
     from reimagined_amd._lib import call
     from reimagined_amd.ops import _p, _stream
     K, N = 2048, 128 * 8192
     packed = torch.randint(-2**31, 2**31 - 1, (N * K // 16,), dtype=torch.int32, device=dev)
     packed = (packed ^ ((packed & (packed >> 1) & 0x55555555) << 1)).contiguous()
+    packed_mfma = ops.pack_mfma_layout(packed)
     rng = np.random.default_rng(32)
     out = {}
     for m in ms:
@@ -372,8 +376,12 @@ def bench_decode_gemv_sweep(torch, dev, ms=(1, 2, 4, 8, 16, 32), reps=20):
         y = torch.empty((m, N), dtype=torch.bfloat16, device=dev)
 
         def run():
-            call("nsosx_ternary_gemm", _p(q), _p(s), _p(packed), 1.0, m, K, N, None, None, _p(y),
-                 1, None, _stream())
+            if m == 1:
+                call("nsosx_ternary_gemm", _p(q), _p(s), _p(packed), 1.0, m, K, N, None, None,
+                     _p(y), 1, None, _stream())
+            else:
+                call("nsosx_ternary_gemm_mfma", _p(q), _p(s), _p(packed_mfma), 1.0, m, K, N,
+                     None, None, _p(y), 1, None, _stream())
         if m == ms[0]:
             _settle(torch, run)
         for _ in range(10):
@@ -389,7 +397,7 @@ def bench_decode_gemv_sweep(torch, dev, ms=(1, 2, 4, 8, 16, 32), reps=20):
         gbs = bytes_ / (t / 1e3) / 1e9
         out[f"m{m}"] = {"ms": round(t, 4), "gbs": round(gbs, 1),
                         "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
-    del packed
+    del packed, packed_mfma
     return out
 
 

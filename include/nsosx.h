@@ -160,11 +160,13 @@ int nsosx_ternary_gemm_path(const int8_t* q, const float* act_scale, const uint3
 int nsosx_pack_mfma_layout(const uint32_t* packed, int64_t n_words, uint32_t* out,
                            void* stream);
 
-/* nsosx_ternary_gemm's contract on weights in the MFMA layout above, always
- * on the int8 MFMA GEMM (the prefill shape; K % 128 == 0, K <= 264208: the
- * layout's operands are 64 x the ternary values, so 64 * 127 * K must fit
- * int32; larger K returns NSOSX_ERR_OVERFLOW).  Same results bit for bit as
- * nsosx_ternary_gemm on the reference-layout words. */
+/* nsosx_ternary_gemm's contract on weights in the MFMA layout above: the
+ * int8 MFMA GEMM, or for decode batches the skinny path takes (2 <= M <= 32,
+ * K in {1024, 2048, 4096}) the skinny MFMA kernel on the same words.
+ * K % 128 == 0, K <= 264208 (the layout's operands are 64 x the ternary
+ * values, so 64 * 127 * K must fit int32; larger K returns
+ * NSOSX_ERR_OVERFLOW).  Same results bit for bit as nsosx_ternary_gemm on the
+ * reference-layout words. */
 int nsosx_ternary_gemm_mfma(const int8_t* q, const float* act_scale, const uint32_t* packed_mfma,
                             float weight_scale, int M, int K, int N, const float* magnitude,
                             const float* bias, void* y, int y_dtype, int32_t* acc_out,

@@ -2220,7 +2220,10 @@ static bool skinny_ok(int M, int K, int N) {
 // hardware drops them.
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
-template <int MT, int LT, int YDT, bool ACC_OUT, bool SQRELU, bool VEC4>
+// ML: the weights are in the MFMA layout (nsosx_pack_mfma_layout): each word decodes by
+// shift and mask into natural k order (64 x the values, unpack_word_mfma), so the
+// activation fragments stay in natural order and the sums are shifted back by 6.
+template <int MT, int LT, int YDT, bool ACC_OUT, bool SQRELU, bool VEC4, bool ML = false>
 __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t* __restrict__ q,
                                             const float* __restrict__ act_scale, int M, void* y,
                                             int32_t* acc_out, int wave_id, int num_waves,
@@ -2244,8 +2247,8 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
             const uint4 v = *reinterpret_cast<const uint4*>(q + (int64_t)m * pb.K + k0);
             d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
         }
-        uint32_t e[4];
-        transpose16(d, e);
+        uint32_t e[4] = {d[0], d[1], d[2], d[3]};
+        if constexpr (!ML) transpose16(d, e);
         *reinterpret_cast<uint4*>(lds + f * 16) = make_uint4(e[0], e[1], e[2], e[3]);
     }
     __syncthreads();
@@ -2358,9 +2361,14 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
                 const uint32_t words[4] = {p01[0], p01[1], p23[0], p23[1]};
 #pragma unroll
                 for (int uu = 0; uu < 4; ++uu) {
-                    uint32_t wv[4];
-                    unpack_word(words[uu], wv);
-                    const v4i aw = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+                    v4i aw;
+                    if constexpr (ML) {
+                        aw = unpack_word_mfma(words[uu]);
+                    } else {
+                        uint32_t wv[4];
+                        unpack_word(words[uu], wv);
+                        aw = v4i{(int)wv[0], (int)wv[1], (int)wv[2], (int)wv[3]};
+                    }
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) {
                         const uint4 v =
@@ -2375,7 +2383,8 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
             // lane holds outputs n = tile * 16 + 4 g + r of token mt * 16 + li
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const int av[4] = {acc[mt].x, acc[mt].y, acc[mt].z, acc[mt].w};
+                constexpr int sh = ML ? 6 : 0;
+                const int av[4] = {acc[mt].x >> sh, acc[mt].y >> sh, acc[mt].z >> sh, acc[mt].w >> sh};
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     // the reference's affine: multiply, then add, each rounded
@@ -2477,7 +2486,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 // NW waves per workgroup share one copy of the activation fragments: 4, or 8
 // for two m tiles at K = 2048 (64 KB of fragments), so the LDS that caps the
 // workgroups per CU at one still holds two waves per SIMD.
-template <int MT, int LT, int YDT, bool ACC_OUT, int NW>
+template <int MT, int LT, int YDT, bool ACC_OUT, int NW, bool ML>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void skinny_kernel(
     GemvProblem pb, const int8_t* __restrict__ q, const float* __restrict__ act_scale, int M,
     void* y, int32_t* acc_out) {
@@ -2486,14 +2495,14 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     // memory wait counts
     const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * NW + (threadIdx.x >> 6));
     if ((pb.N & 3) == 0)
-        skinny_body<MT, LT, YDT, ACC_OUT, false, true>(pb, q, act_scale, M, y, acc_out, wave_id,
-                                                       gridDim.x * NW, lds_sk);
+        skinny_body<MT, LT, YDT, ACC_OUT, false, true, ML>(pb, q, act_scale, M, y, acc_out,
+                                                           wave_id, gridDim.x * NW, lds_sk);
     else
-        skinny_body<MT, LT, YDT, ACC_OUT, false, false>(pb, q, act_scale, M, y, acc_out, wave_id,
-                                                        gridDim.x * NW, lds_sk);
+        skinny_body<MT, LT, YDT, ACC_OUT, false, false, ML>(pb, q, act_scale, M, y, acc_out,
+                                                            wave_id, gridDim.x * NW, lds_sk);
 }
 
-template <int MT, int YDT>
+template <int MT, int YDT, bool ML>
 static void launch_skinny_lt(const GemvProblem& pb, const int8_t* q, const float* as, int M,
                              void* y, int32_t* acc, int tiles, hipStream_t st) {
     // about 8 waves per CU: two workgroups of 4 waves (32 KB of fragments), or one of 8
@@ -2504,10 +2513,10 @@ static void launch_skinny_lt(const GemvProblem& pb, const int8_t* q, const float
         const int wgs = std::max(1, std::min((tiles + NW - 1) / NW, NW == 4 ? 512 : 256));      \
         const size_t lds = (size_t)MT * pb.K * 16 + (size_t)NW * 4 * pb.K;                     \
         if (acc)                                                                                \
-            hipLaunchKernelGGL((skinny_kernel<MT, LT, YDT, true, NW>), dim3(wgs), dim3(NW * 64), \
+            hipLaunchKernelGGL((skinny_kernel<MT, LT, YDT, true, NW, ML>), dim3(wgs), dim3(NW * 64), \
                                lds, st, pb, q, as, M, y, acc);                                  \
         else                                                                                    \
-            hipLaunchKernelGGL((skinny_kernel<MT, LT, YDT, false, NW>), dim3(wgs), dim3(NW * 64), \
+            hipLaunchKernelGGL((skinny_kernel<MT, LT, YDT, false, NW, ML>), dim3(wgs), dim3(NW * 64), \
                                lds, st, pb, q, as, M, y, acc);                                  \
     }
     // (K = 4096: 64 KB of fragments + 4 waves' 16 KB tiles already fill 128 KB of the
@@ -2518,13 +2527,13 @@ static void launch_skinny_lt(const GemvProblem& pb, const int8_t* q, const float
 #undef NSOSX_SK
 }
 
-template <int YDT>
+template <int YDT, bool ML = false>
 static void launch_skinny_t(const GemvProblem& pb, const int8_t* q, const float* as, int M,
                             void* y, int32_t* acc, hipStream_t st) {
     const int tiles = (pb.N + 15) / 16;
     const int mt = (M + 15) / 16;
-    if (mt == 1) launch_skinny_lt<1, YDT>(pb, q, as, M, y, acc, tiles, st);
-    else launch_skinny_lt<2, YDT>(pb, q, as, M, y, acc, tiles, st);
+    if (mt == 1) launch_skinny_lt<1, YDT, ML>(pb, q, as, M, y, acc, tiles, st);
+    else launch_skinny_lt<2, YDT, ML>(pb, q, as, M, y, acc, tiles, st);
 }
 
 // ===========================================================================
@@ -2795,6 +2804,14 @@ extern "C" int nsosx_ternary_gemm_mfma(const int8_t* q, const float* act_scale,
     if (K > kMfmaLayoutMaxK)
         return fail(NSOSX_ERR_OVERFLOW, "ternary_gemm_mfma: K too large for the MFMA layout's "
                                         "64x-scaled int32 sums");
+    if (skinny_ok(M, K, N)) {
+        // decode batches: the skinny MFMA kernel on the same words
+        GemvProblem pb{packed_mfma, magnitude, bias, weight_scale, N, K};
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        if (y_dtype == NSOSX_F32) launch_skinny_t<NSOSX_F32, true>(pb, q, act_scale, M, y, acc_out, st);
+        else launch_skinny_t<NSOSX_BF16, true>(pb, q, act_scale, M, y, acc_out, st);
+        return check_launch("ternary_gemm_mfma");
+    }
     const int tiles = ((N + kG3BN - 1) / kG3BN) * ((M + kG3BM - 1) / kG3BM);
     GemmProblem pb{packed_mfma, magnitude, bias, weight_scale, N, K};
     hipStream_t st = static_cast<hipStream_t>(stream);

@@ -50,9 +50,11 @@ class BitLinear:
         return ops.pack_mfma_layout(self.packed) if self.in_features % 128 == 0 else None
 
     def gemm(self, q, s, m, y, st, magnitude=None, bias=None):
-        """The ternary GEMM of m rows of codes into y: the MFMA-layout prefill GEMM above
-        128 rows, else the dispatching entry (GEMV / skinny / small-M MFMA kernels)."""
-        if self.packed_mfma is not None and m > 128:
+        """The ternary GEMM of m rows of codes into y: on the MFMA-layout words the prefill
+        GEMM above 128 rows and the skinny decode kernel at its shapes, else the dispatching
+        entry on the reference words (GEMV / small-M MFMA kernels)."""
+        if self.packed_mfma is not None and (m > 128 or ops.skinny_shape(m, self.in_features,
+                                                                          self.out_features)):
             call("nsosx_ternary_gemm_mfma", _p(q), _p(s), _p(self.packed_mfma),
                  self.weight_scale, m, self.in_features, self.out_features, _p(magnitude),
                  _p(bias), _p(y), _DT[y.dtype], None, st)

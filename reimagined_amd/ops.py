@@ -134,6 +134,13 @@ def ternary_gemm(q: torch.Tensor, act_scale: torch.Tensor, packed: torch.Tensor,
     return y
 
 
+def skinny_shape(m: int, k: int, n: int) -> bool:
+    """The shapes the skinny MFMA decode kernel takes (the library's skinny_ok): 2 <= m <=
+    32, k in {1024, 2048, 4096}, ceil(m / 16) * k <= 4096, m * n * 4 < 2^31."""
+    return (2 <= m <= 32 and k in (1024, 2048, 4096) and ((m + 15) // 16) * k <= 4096
+            and m * n * 4 < 2**31)
+
+
 def pack_mfma_layout(packed: torch.Tensor) -> torch.Tensor:
     """The prefill GEMM's weight layout (a device repack of reference-layout words)."""
     _dev(packed, "packed")

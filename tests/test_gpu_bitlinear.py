@@ -329,12 +329,16 @@ def test_weight_row_sums_golden_and_reserved_code(dev, orc):
 
 
 @pytest.mark.parametrize("m,k,n", [(300, 1024, 700), (129, 384, 256), (1000, 512, 520),
-                                   (4096, 2048, 8192), (1, 128, 16), (257, 2048, 1024)])
+                                   (4096, 2048, 8192), (1, 128, 16), (257, 2048, 1024),
+                                   # decode batches: the skinny kernel on the MFMA layout
+                                   (2, 1024, 700), (16, 2048, 520), (17, 2048, 1024),
+                                   (32, 2048, 8192), (5, 4096, 66)])
 @pytest.mark.parametrize("ydt,acc", [(torch.bfloat16, False), (torch.float32, True)])
 def test_gemm_mfma_layout_matches_reference_layout(dev, orc, m, k, n, ydt, acc):
-    """The prefill GEMM on repacked (MFMA-layout) weights gives the reference-layout GEMM's
-    outputs bit for bit, including words holding the reserved code 3 (decoded to 0 by both),
-    edge tiles in M and N, magnitude and bias; the accumulators match the oracle."""
+    """The GEMM on repacked (MFMA-layout) weights -- the prefill MFMA GEMM, and the skinny
+    decode kernel at 2 <= M <= 32 -- gives the reference-layout GEMM's outputs bit for bit,
+    including words holding the reserved code 3 (decoded to 0 by both), edge tiles in M and N,
+    magnitude and bias; the accumulators match the oracle."""
     rng = np.random.default_rng(m + k + n)
     words = torch.randint(-2**31, 2**31 - 1, (n * k // 16,), dtype=torch.int32, device=dev)
     q = torch.from_numpy(rng.integers(-127, 128, size=(m, k)).astype(np.int8)).to(dev)
