@@ -1799,6 +1799,83 @@ __device__ __forceinline__ void gemm3_epilogue_rows(const GemmProblem& pb,
     }
 }
 
+// f32 epilogue of a tile that lies inside N (N % 4 == 0), staged like the bf16 one:
+// a wave's 64 n x 128 m block is 32 KB of floats, so it goes out in two halves of
+// 64 rows (mb 0-1, then 2-3) through the wave's 16 KB slice of the idle ring, each
+// row 256 bytes (16 chunks of 16 bytes, chunk c of row r at slot c ^ (r % 16): the
+// 16-byte writes of 16 rows and the reads of one row's 16 chunks are conflict-free).
+// One store instruction then writes 4 rows as whole 256-byte segments.
+template <bool GATHER, bool SQRELU, bool MAG, bool BIAS>
+__device__ __forceinline__ void gemm3_epilogue_rows_f32(const GemmProblem& pb,
+                                                        const float* __restrict__ act_scale,
+                                                        const int32_t* __restrict__ perm,
+                                                        int seg_begin, int seg_rows, int n0, int m0,
+                                                        float* y, const v16i (&acc)[2][4],
+                                                        char* smem) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 5;
+    const int li = lane & 31;
+    const int nw = n0 + wave * 64 + 4 * g;  // this lane's first output column
+    float comb[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+        const int ml = min(m0 + mb * 32 + li, seg_rows - 1);  // rows past the segment are never stored
+        const int arow = GATHER ? perm[seg_begin + ml] : seg_begin + ml;
+        comb[mb] = __fmul_rn(act_scale[arow], pb.ws);
+    }
+    __syncthreads();  // every wave is done reading the stage ring
+    char* slice = smem + wave * (kG3BM * 128);
+    float* ycol = y + n0 + wave * 64 + (lane & 15) * 4;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int c = nb * 8 + 2 * q4 + g;  // this lane's 16-byte chunk of the row
+                const int n = nw + nb * 32 + 8 * q4;
+                const float4 mg = MAG ? *reinterpret_cast<const float4*>(pb.mag + n) : float4{};
+                const float4 bs = BIAS ? *reinterpret_cast<const float4*>(pb.bias + n) : float4{};
+                const float mv[4] = {mg.x, mg.y, mg.z, mg.w};
+                const float bv[4] = {bs.x, bs.y, bs.z, bs.w};
+#pragma unroll
+                for (int mh = 0; mh < 2; ++mh) {
+                    const int mb = 2 * half + mh;
+                    const v16i& a = acc[nb][mb];
+                    float o[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        float v = __fmul_rn(static_cast<float>(a[4 * q4 + r]), comb[mb]);
+                        if (MAG) v = __fmul_rn(v, mv[r]);
+                        if (BIAS) v = __fadd_rn(v, bv[r]);
+                        if (SQRELU) {
+                            v = v > 0.0f ? v : 0.0f;
+                            v = __fmul_rn(v, v);
+                        }
+                        o[r] = v;
+                    }
+                    const int row = mh * 32 + li;
+                    *reinterpret_cast<float4*>(slice + row * 256 + ((c ^ (row & 15)) << 4)) =
+                        make_float4(o[0], o[1], o[2], o[3]);
+                }
+            }
+        // the wave reads back what its own lanes wrote (LDS operations of one wave
+        // complete in order; the wait keeps the compiler from hoisting the reads)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int c = lane & 15;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = i * 4 + (lane >> 4);
+            const float4 v = *reinterpret_cast<const float4*>(slice + row * 256 + ((c ^ (row & 15)) << 4));
+            const int m = m0 + half * 64 + row;
+            if (m < seg_rows) *reinterpret_cast<float4*>(ycol + (int64_t)(seg_begin + m) * pb.N) = v;
+        }
+        // the next half overwrites the slice: its writes follow these reads in order
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+}
+
 // MB: 32-row blocks of the tile that hold rows (a partial last tile of an expert's
 // segment skips the DMA and MFMAs of its empty blocks; their accumulators stay zero
 // and their rows are never stored).
@@ -1899,6 +1976,23 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
 #define NSOSX_EPI(MG, BS)                                                                       \
     gemm3_epilogue_rows<GATHER, SQRELU, MG, BS>(pb, act_scale, perm, seg_begin, seg_rows, n0, m0, \
                                                 yb, acc, smem)
+            if (pb.mag) {
+                if (pb.bias) NSOSX_EPI(true, true); else NSOSX_EPI(true, false);
+            } else {
+                if (pb.bias) NSOSX_EPI(false, true); else NSOSX_EPI(false, false);
+            }
+#undef NSOSX_EPI
+            return;
+        }
+    }
+    if constexpr (YDT == NSOSX_F32 && !ACC_OUT) {
+        if (y && n0 + kG3BN <= pb.N && (pb.N & 3) == 0 &&
+            ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(pb.mag) |
+              reinterpret_cast<uintptr_t>(pb.bias)) & 15) == 0) {
+            float* yf = static_cast<float*>(y);
+#define NSOSX_EPI(MG, BS)                                                                 \
+    gemm3_epilogue_rows_f32<GATHER, SQRELU, MG, BS>(pb, act_scale, perm, seg_begin, seg_rows, n0, \
+                                                    m0, yf, acc, smem)
             if (pb.mag) {
                 if (pb.bias) NSOSX_EPI(true, true); else NSOSX_EPI(true, false);
             } else {

@@ -83,6 +83,9 @@ def _gemm_case(dev, orc, m, n, k, path, mag=False, bias=False, seed=0):
                               path=path)
     np.testing.assert_array_equal(acc.cpu().numpy(), acc_want)
     np.testing.assert_array_equal(y.cpu().numpy(), y_want)
+    # f32 without the accumulators: the MFMA GEMM's staged row epilogue where the tile allows
+    yf = ops.ternary_gemm(t(q), t(s), pk, ws, n, t(mg), t(bs), torch.float32, path=path)
+    np.testing.assert_array_equal(yf.cpu().numpy(), y_want)
     yb = ops.ternary_gemm(t(q), t(s), pk, ws, n, t(mg), t(bs), torch.bfloat16, path=path)
     np.testing.assert_array_equal(yb.float().cpu().numpy(), _bf16_round(y_want))
 
@@ -104,7 +107,7 @@ def test_mfma_gemm_bit_exact(dev, orc, m, n, k):
 @pytest.mark.parametrize("m,n,k", [(1000, 700, 512), (129, 256, 256), (513, 1024, 384),
                                    (2000, 96, 1024)])
 def test_mfma_gemm_more_shapes_bit_exact(dev, orc, m, n, k):
-    """Direct-to-LDS GEMM: edge tiles in n and m, the shortest ring (K = 256), odd stage counts."""
+    """LDS-staged MFMA GEMM: edge tiles in n and m, the shortest ring (K = 256), odd stage counts."""
     _gemm_case(dev, orc, m, n, k, path=1, mag=(m % 2 == 0), bias=True)
 
 
@@ -333,7 +336,8 @@ def test_weight_row_sums_golden_and_reserved_code(dev, orc):
                                    # decode batches: the skinny kernel on the MFMA layout
                                    (2, 1024, 700), (16, 2048, 520), (17, 2048, 1024),
                                    (32, 2048, 8192), (5, 4096, 66)])
-@pytest.mark.parametrize("ydt,acc", [(torch.bfloat16, False), (torch.float32, True)])
+@pytest.mark.parametrize("ydt,acc", [(torch.bfloat16, False), (torch.float32, True),
+                                     (torch.float32, False)])
 def test_gemm_mfma_layout_matches_reference_layout(dev, orc, m, k, n, ydt, acc):
     """The GEMM on repacked (MFMA-layout) weights -- the prefill MFMA GEMM, and the skinny
     decode kernel at 2 <= M <= 32 -- gives the reference-layout GEMM's outputs bit for bit,
