@@ -758,6 +758,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", default=None,
+                    help="run only this extra (e.g. prefill_gemm_c3), for counter runs")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="end with a plain 256 MiB device copy, the known-size kernel that "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by")
@@ -777,29 +779,28 @@ def main():
     roof, _ = layer_roofline(T, stages)
     _log(f"layer: {ms_step:.3f} ms/step, stages {stages}")
     extra = {}
+    extras = [
+        ("prefill_gemm_c3", "prefill gemm", lambda: bench_prefill_gemm(torch, dev)),
+        ("decode_gemv_c3_m1", "decode gemv", lambda: bench_decode_gemv(torch, dev, m=1)),
+        ("decode_gemv_c3_sweep", "decode gemv sweep", lambda: bench_decode_gemv_sweep(torch, dev)),
+        ("moe_c5", "moe c5", lambda: bench_moe_c5(torch, dev)),
+        ("decode_step_c5", "decode step", lambda: bench_decode_step(torch, dev)),
+        ("mamba2_prefill", "mamba2 prefill", lambda: bench_mamba2_prefill(torch, dev)),
+        ("mamba2_decode_step", "mamba2 decode step", lambda: bench_mamba2_decode(torch, dev)),
+        ("scan_shapes", "scan shapes", lambda: bench_scan_shapes(torch, dev)),
+        ("linear_f32", "linear f32", lambda: bench_linear_f32(torch, dev)),
+        ("ste_backward", "ste backward", lambda: bench_ste_backward(torch, dev)),
+        ("gemv_published_shapes", "gemv published shapes", lambda: bench_gemv_published(torch, dev)),
+    ]
+    if args.only and args.only not in [k for k, _, _ in extras]:
+        print(f"--only: unknown extra {args.only!r}", file=sys.stderr)
+        sys.exit(2)
     if not args.no_extra:
-        extra["prefill_gemm_c3"] = bench_prefill_gemm(torch, dev)
-        _log(f"prefill gemm {extra['prefill_gemm_c3']}")
-        extra["decode_gemv_c3_m1"] = bench_decode_gemv(torch, dev, m=1)
-        _log(f"decode gemv {extra['decode_gemv_c3_m1']}")
-        extra["decode_gemv_c3_sweep"] = bench_decode_gemv_sweep(torch, dev)
-        _log(f"decode gemv sweep {extra['decode_gemv_c3_sweep']}")
-        extra["moe_c5"] = bench_moe_c5(torch, dev)
-        _log(f"moe c5 {extra['moe_c5']}")
-        extra["decode_step_c5"] = bench_decode_step(torch, dev)
-        _log(f"decode step {extra['decode_step_c5']}")
-        extra["mamba2_prefill"] = bench_mamba2_prefill(torch, dev)
-        _log(f"mamba2 prefill {extra['mamba2_prefill']}")
-        extra["mamba2_decode_step"] = bench_mamba2_decode(torch, dev)
-        _log(f"mamba2 decode step {extra['mamba2_decode_step']}")
-        extra["scan_shapes"] = bench_scan_shapes(torch, dev)
-        _log(f"scan shapes {extra['scan_shapes']}")
-        extra["linear_f32"] = bench_linear_f32(torch, dev)
-        _log(f"linear f32 {extra['linear_f32']}")
-        extra["ste_backward"] = bench_ste_backward(torch, dev)
-        _log(f"ste backward {extra['ste_backward']}")
-        extra["gemv_published_shapes"] = bench_gemv_published(torch, dev)
-        _log(f"gemv published shapes {extra['gemv_published_shapes']}")
+        for key, label, fn in extras:
+            if args.only and key != args.only:
+                continue
+            extra[key] = fn()
+            _log(f"{label} {extra[key]}")
         sc = stages.get("conv_scan")
         if sc:
             _, work = layer_roofline(T, {"conv_scan": sc})
