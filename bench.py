@@ -216,10 +216,13 @@ def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=3
             issue_s = pairs * d_state * (2 + 4) * 4 / 64 / 1024 / 2.4e9
             roof["valu_issue_bound_ms"] = round(issue_s * 1e3, 4)
             roof["valu_issue_frac"] = round(issue_s / sec, 4)
+            roof["valu_busy_pct_measured"] = pmc_valu_busy("conv + scan")
             roof["note"] = ("VALU/transcendental-issue bound, not HBM: the recurrence alone needs "
                             f"{issue_s * 1e3:.3f} ms of issue at 2.4 GHz (exp = 2 FMA slots) "
                             f"against {amount / HBM_PEAK_GBS / 1e6:.3f} ms of HBM time; "
-                            "valu_issue_frac = that bound / the kernel's time")
+                            "valu_issue_frac = that bound / the kernel's time; "
+                            "valu_busy_pct_measured = rocprofv3 VALUBusy of the kernel "
+                            "(profiles/hybrid_layer_c4_pmc_valu.md)")
     return roof, work
 
 
@@ -242,6 +245,28 @@ def pmc_traffic(stage: str):
         if len(cells) == 5 and cells[0] == stage:
             try:
                 return int(cells[4].replace(",", ""))
+            except ValueError:
+                return None
+    return None
+
+
+PMC_VALU_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                "hybrid_layer_c4_pmc_valu.md")
+
+
+def pmc_valu_busy(stage: str):
+    """VALU busy % of a layer stage's kernel from the committed rocprofv3 VALU summary (rows
+    `| stage | kernel | dispatches | VALU instructions | active cycles | VALU busy % | wait % |`),
+    or None when the summary or the row is absent."""
+    try:
+        text = open(PMC_VALU_SUMMARY).read()
+    except OSError:
+        return None
+    for line in text.splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 7 and cells[0] == stage:
+            try:
+                return float(cells[5])
             except ValueError:
                 return None
     return None
