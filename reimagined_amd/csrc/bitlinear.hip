@@ -1877,7 +1877,7 @@ __device__ __forceinline__ void gemm3_epilogue_rows_f32(const GemmProblem& pb,
 }
 
 // MB: 32-row blocks of the tile that hold rows (a partial last tile of an expert's
-// segment skips the DMA and MFMAs of its empty blocks; their accumulators stay zero
+// segment skips the loads and MFMAs of its empty blocks; their accumulators stay zero
 // and their rows are never stored).
 template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU, bool SWZ = false, int MB = 4>
 __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* __restrict__ q,
@@ -1891,7 +1891,7 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
     const int W16 = pb.K >> 4;
     const int KT = pb.K / kG3BK;
 
-    // DMA sources.  Weights: wave-load j (0, 1) of a wave fills LDS rows
+    // Stage sources.  Weights: wave-load j (0, 1) of a wave fills LDS rows
     // 64 wave + 32 j .. +31, lane -> row + lane / 2, slot lane % 2.
     const char* wsrc[2];
 #pragma unroll
