@@ -461,3 +461,25 @@ def test_grouped_decode_projections_match_single_calls(dev, dtype):
             assert (got[i] == 7.0).all()
         else:
             np.testing.assert_array_equal(got[i, :n], want.float().cpu().numpy()[0])
+
+
+@pytest.mark.parametrize("m,k", [(2, 1024), (7, 2048), (16, 1024), (32, 2048), (300, 1024)])
+def test_layer_bitlinear_decode_batches_bit_exact(dev, orc, m, k):
+    """layers.BitLinear at decode-batch sizes runs the skinny MFMA kernel on its MFMA-layout
+    copy (and the prefill GEMM above 128 rows): RMS_PERI, magnitude and bias included, the
+    outputs equal the reference BitLinear::forward restatement bit for bit."""
+    from reimagined_amd.layers import BitLinear
+    rng = np.random.default_rng(m * 31 + k)
+    n = 520
+    w = _weights(rng, n, k)
+    mg = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    bs = rng.standard_normal(n).astype(np.float32)
+    lin = BitLinear(w, dev, rms_input=True, magnitude=torch.from_numpy(mg).to(dev),
+                    bias=torch.from_numpy(bs).to(dev))
+    assert lin.packed_mfma is not None
+    packed, ws, _ = orc.pack_weights(w)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    want = orc.bitlinear_forward(x, packed, ws, n, bits=8, rms_input=True, magnitude=mg, bias=bs)
+    y = lin.forward(torch.from_numpy(x).to(dev), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), want)
