@@ -86,7 +86,10 @@ def bench_layer(torch, dev, steps, warmup):
     for _ in range(warmup):
         layer.forward(x, dt, B, C, cu, final_state=fin)
     torch.cuda.synchronize()
-    _log(f"layer warm: T={T}")
+    # then the same ~150 ms of the layer's own launches every extra gets: `warmup` steps alone
+    # (5 under the driver, ~4 ms) leave the clocks still rising when the timed loop starts
+    settle_ms = _settle(torch, lambda: layer.forward(x, dt, B, C, cu, final_state=fin))
+    _log(f"layer warm: T={T}, settled {settle_ms:.0f} ms")
     # wall-clock timed region: K steps, no per-kernel events
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -100,7 +103,7 @@ def bench_layer(torch, dev, steps, warmup):
         layer.forward(x, dt, B, C, cu, final_state=fin, marker=timer)
     torch.cuda.synchronize()
     stages = {k: v / steps for k, v in timer.totals_ms().items()}
-    return T, wall, stages, params, inp
+    return T, wall, stages, params, inp, settle_ms
 
 
 def bench_mamba2_decode(torch, dev, rows=1, reps=200):
@@ -457,12 +460,13 @@ def bench_decode_step(torch, dev, reps=8):
 def _settle(torch, fn, ms=150.0):
     """Runs fn back to back for about `ms` of wall time: the GPU raises its clocks over
     the first ~100 ms of sustained load, so short HBM-bound timings taken from a cold
-    start read low by up to a fifth."""
+    start read low by up to a fifth.  Returns the wall time spent, in ms."""
     t0 = time.perf_counter()
     while (time.perf_counter() - t0) * 1e3 < ms:
         for _ in range(20):
             fn()
         torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3
 
 
 def _time_ms(torch, fn, reps):
@@ -803,7 +807,7 @@ def main():
     import reimagined_amd
     reimagined_amd.lib()
     _log("library loaded")
-    T, wall, stages, params, inp = bench_layer(torch, dev, args.steps, args.warmup)
+    T, wall, stages, params, inp, settle_ms = bench_layer(torch, dev, args.steps, args.warmup)
     ms_step = wall / args.steps * 1e3
     roof, _ = layer_roofline(T, stages)
     _log(f"layer: {ms_step:.3f} ms/step, stages {stages}")
@@ -846,6 +850,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        # untimed layer steps run after the warmup steps, before the timed loop
+        "settle_ms": round(settle_ms, 1),
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
