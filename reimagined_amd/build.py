@@ -40,7 +40,7 @@ def hipcc() -> str:
 
 
 def _compile(src: str) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.basename(src).replace(".hip", ".o"))
+    obj = _obj(src)
     cmd = [hipcc(), *CFLAGS, "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
@@ -52,11 +52,29 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
+def _obj(src: str) -> str:
+    return os.path.join(BUILD_DIR, os.path.basename(src).replace(".hip", ".o"))
+
+
+def build(verbose: bool = False, incremental: bool = False) -> str:
+    """Compiles every csrc/*.hip and links the library.  incremental: keep an object
+    newer than its source and than every csrc/*.hpp (a header change rebuilds all)."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
+    hdr_time = max((os.path.getmtime(os.path.join(CSRC, f)) for f in os.listdir(CSRC)
+                    if f.endswith(".hpp")), default=0.0)
+
+    def stale(src: str) -> bool:
+        obj = _obj(src)
+        return (not incremental or not os.path.exists(obj) or
+                os.path.getmtime(obj) < max(os.path.getmtime(src), hdr_time))
+
+    todo = [s for s in srcs if stale(s)]
+    # longest units first, so the slowest compile starts at once
+    todo.sort(key=os.path.getsize, reverse=True)
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(8, len(todo)))) as ex:
+        list(ex.map(_compile, todo))
+    objs = [_obj(s) for s in srcs]
     tmp = OUT + ".tmp"
     # --no-undefined: a kernel whose host launch stub was not emitted fails here, at build
     # time, instead of when the library is loaded
@@ -96,5 +114,5 @@ def build_consumer(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv)
     build_consumer(verbose=True)
