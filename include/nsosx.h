@@ -190,7 +190,10 @@ int nsosx_bitlinear_forward(const void* x, int x_dtype, const uint32_t* packed,
  * The workspace takes round256(M*K) + 2*round256(4*M) bytes; larger shapes
  * return NSOSX_ERR_OVERFLOW.  Every call on one GPU shares that array, so
  * calls that overlap on one GPU (different streams, or different host threads)
- * race; calls enqueued on one stream are ordered and safe. */
+ * race; calls enqueued on one stream are ordered and safe.  The first call on
+ * each device looks up the array's device address and must be made outside
+ * HIP graph capture (under capture it returns NSOSX_ERR_INVALID); later calls
+ * may be captured and replayed. */
 int64_t nsosx_bitlinear_forward_noalloc_max_bytes(void);
 int nsosx_bitlinear_forward_noalloc(const void* x, int x_dtype, const uint32_t* packed,
                                     float weight_scale, int M, int K, int N, int precision_bits,
@@ -441,24 +444,39 @@ int nsosx_mamba2_step_out(const void* x, const void* z, const void* B, const voi
  * Top-k MoE routing.
  * ------------------------------------------------------------------------- */
 
-/* MoERouter::forward from logits (src/jamba.cpp:8140-8319): softmax
- * (src/tensor.cpp:3428-3450), top-k by (probability desc, index asc),
- * renormalised by 1/max(sum, 1e-9f); then the expert-major, rows-ascending
- * dispatch of JambaBlock::forward_moe (src/jamba.cpp:3882-3894).
+/* MoERouter::forward(x, valid_rows) from logits (src/jamba.cpp:8140-8319):
+ * softmax (src/tensor.cpp:3428-3450), top-k by (probability desc, index asc),
+ * renormalised by 1/max(sum, 1e-9f); padding rows zeroed; then the
+ * expert-major, rows-ascending dispatch of JambaBlock::forward_moe
+ * (src/jamba.cpp:3882-3894; the device path's ordered assignment,
+ * src/cuda/moe_kernels.cu:305-319).
  *   logits f32 [rows, E]; weights f32 [rows, E] (masked, renormalised);
+ *   valid_rows uint8 [rows], device, or NULL (every row valid): a row whose
+ *   byte is 0 is padding, as launch_moe_zero_invalid_rows_kernel reads the
+ *   mask (src/cuda/moe_kernels.cu:118-125).  A padding row gets all-zero
+ *   weights, selected -1 and slot_of -1, takes no slot in counts / offsets /
+ *   perm, and nsosx_moe_combine writes it as zeros.  MoERouter::forward
+ *   rejects a host mask holding any value other than 0 or 1 before it is
+ *   uploaded (src/jamba.cpp:8145-8153); the C++ and Python mirrors of this
+ *   entry do the same.
  *   selected int32 [rows, k] (rank order); counts int32 [E];
- *   offsets int32 [E+1] (exclusive scan); perm int32 [rows*k] (slot -> row);
+ *   offsets int32 [E+1] (exclusive scan; offsets[E] = valid rows * k);
+ *   perm int32 [rows*k] (slot -> row; the first offsets[E] entries are set);
  *   slot_of int32 [rows, k]: slot_of[r, i] is the slot of selected[r, i]
  *   (rank order), so perm[slot_of[r, i]] == r.
+ *   loads f32 [E] or NULL: expert_loads, loads[e] = sum over rows in
+ *   ascending order of weights[r, e] (src/jamba.cpp:8299-8307, the order of
+ *   launch_moe_load_ordered_kernel, src/cuda/moe_kernels.cu:108-116).
  *   workspace: int32, nsosx_moe_route_workspace(rows, E) elements.
  * counts, offsets, perm, slot_of and workspace all NULL: selection only
  * (weights and selected, one launch), what the sparse decode consumes.
  * E <= 64, k <= min(E, 8) (the reference allows any k <= E; routing wider than
  * top-8 is not supported here). */
 int64_t nsosx_moe_route_workspace(int rows, int experts);
-int nsosx_moe_route(const float* logits, int rows, int experts, int k, float* weights,
-                    int32_t* selected, int32_t* counts, int32_t* offsets, int32_t* perm,
-                    int32_t* slot_of, int32_t* workspace, void* stream);
+int nsosx_moe_route(const float* logits, const uint8_t* valid_rows, int rows, int experts, int k,
+                    float* weights, int32_t* selected, int32_t* counts, int32_t* offsets,
+                    int32_t* perm, int32_t* slot_of, float* loads, int32_t* workspace,
+                    void* stream);
 
 /* Grouped ternary GEMM over expert segments: for each expert e the rows
  * perm[offsets[e] .. offsets[e+1]) of q (int8 [rows_in, K], gathered through
@@ -477,10 +495,12 @@ int nsosx_grouped_ternary_gemm(const nsosx_linear_view* views_dev, int experts,
                                void* y, int y_dtype, void* stream);
 
 /* nsosx_grouped_ternary_gemm on views whose packed words are in the MFMA
- * layout (nsosx_pack_mfma_layout), launching only the experts' real row tiles
- * (total_rows: offsets[experts] or an upper bound).  K % 128 == 0,
- * K <= 264208 (as nsosx_ternary_gemm_mfma), <= 1024 experts.  Same results bit
- * for bit. */
+ * layout (nsosx_pack_mfma_layout), launching only the experts' real row tiles.
+ * total_rows sizes the launch and is required: offsets[experts] or an upper
+ * bound, > 0 (0, which nsosx_grouped_ternary_gemm reads as "unknown", is
+ * NSOSX_ERR_INVALID here: with no row bound the grid cannot be sized; a routing
+ * with no rows needs no call).  K % 128 == 0, K <= 264208 (as
+ * nsosx_ternary_gemm_mfma), <= 1024 experts.  Same results bit for bit. */
 int nsosx_grouped_ternary_gemm_mfma(const nsosx_linear_view* views_dev, int experts,
                                     const int32_t* offsets, const int32_t* perm, int gather,
                                     const int8_t* q, const float* act_scale, int K, int N,
@@ -491,7 +511,8 @@ int nsosx_grouped_ternary_gemm_mfma(const nsosx_linear_view* views_dev, int expe
  * out[r] = sum over the row's selected experts, lowest id first, of
  * expert_out[slot] * weights[r, e], starting from 0.
  * expert_out [slots, dim] (in_dtype), out [rows, dim] (out_dtype).
- * slot_of NULL: the slot of (row r, choice i) is r * k + i.  rows <= 65535 unless
+ * A row with selected[r, 0] < 0 (a padding row of nsosx_moe_route) is written
+ * as zeros.  slot_of NULL: the slot of (row r, choice i) is r * k + i.  rows <= 65535 unless
  * dim % 4 == 0 and expert_out / out are 16-byte aligned (8 with both bf16). */
 int nsosx_moe_combine(const void* expert_out, int in_dtype, const int32_t* slot_of,
                       const int32_t* selected, const float* weights, int rows, int experts, int k,

@@ -494,18 +494,46 @@ void orc_topk_mask(float* weights, int rows, int experts, int k, int32_t* select
     free(rank);
 }
 
-/* Expert-major, rows-ascending dispatch: each row joins the lists of its k
- * highest-weighted experts; offsets is the exclusive scan of counts and
- * perm[offsets[e] + i] is the i-th row routed to e.
+/* Padding rows of MoERouter::forward(x, valid_rows): after the top-k mask a row
+ * whose valid byte is 0 gets all-zero weights (CPU path OXN/nsos/src/jamba.cpp:
+ * 8299-8304; device path 8195-8214 through moe_zero_invalid_rows_kernel,
+ * OXN/nsos/src/cuda/moe_kernels.cu:118-125, which reads 0 as padding) and no
+ * selection (-1): the device dispatch takes only nonzero weights
+ * (moe_count_per_expert_kernel / moe_ordered_assign_kernel,
+ * OXN/nsos/src/cuda/moe_kernels.cu:226-235, 305-319). */
+void orc_zero_invalid_rows(float* weights, int32_t* selected, const uint8_t* valid, int rows,
+                           int experts, int k) {
+    for (int r = 0; r < rows; ++r) {
+        if (valid[r] != 0) continue;
+        for (int e = 0; e < experts; ++e) weights[(int64_t)r * experts + e] = 0.0f;
+        if (selected)
+            for (int i = 0; i < k; ++i) selected[(int64_t)r * k + i] = -1;
+    }
+}
+
+/* expert_loads of MoERouter::forward: loads[e] = sum over rows, in ascending order,
+ * of the masked weights[r, e] (OXN/nsos/src/jamba.cpp:8299-8307, skipping padding
+ * rows; the order of moe_load_ordered_kernel, OXN/nsos/src/cuda/moe_kernels.cu:
+ * 108-116). */
+void orc_expert_loads(const float* weights, const uint8_t* valid, int rows, int experts,
+                      float* loads) {
+    for (int e = 0; e < experts; ++e) loads[e] = 0.0f;
+    for (int r = 0; r < rows; ++r) {
+        if (valid && valid[r] == 0) continue;
+        for (int e = 0; e < experts; ++e) loads[e] = loads[e] + weights[(int64_t)r * experts + e];
+    }
+}
+
+/* Expert-major, rows-ascending dispatch of a selection [rows, k] (-1 = none):
+ * each row joins the lists of its selected experts; offsets is the exclusive
+ * scan of counts and perm[offsets[e] + i] is the i-th row routed to e.
  * JambaBlock::forward_moe, OXN/nsos/src/jamba.cpp:3882-3894 */
-void orc_moe_dispatch(const float* weights, int rows, int experts, int k,
-                      int32_t* counts, int32_t* offsets, int32_t* perm) {
-    float* tmp = (float*)malloc(sizeof(float) * (size_t)rows * (size_t)experts);
-    int32_t* sel = (int32_t*)malloc(sizeof(int32_t) * (size_t)rows * (size_t)k);
-    memcpy(tmp, weights, sizeof(float) * (size_t)rows * (size_t)experts);
-    orc_topk_mask(tmp, rows, experts, k, sel);
+void orc_moe_dispatch_sel(const int32_t* sel, int rows, int experts, int k, int32_t* counts,
+                          int32_t* offsets, int32_t* perm) {
+    if (experts <= 0) return;
     for (int e = 0; e < experts; ++e) counts[e] = 0;
-    for (int64_t i = 0; i < (int64_t)rows * k; ++i) counts[sel[i]]++;
+    for (int64_t i = 0; i < (int64_t)rows * k; ++i)
+        if (sel[i] >= 0) counts[sel[i]]++;
     offsets[0] = 0;
     for (int e = 0; e < experts; ++e) offsets[e + 1] = offsets[e] + counts[e];
     int32_t* fill = (int32_t*)calloc((size_t)experts, sizeof(int32_t));
@@ -514,6 +542,17 @@ void orc_moe_dispatch(const float* weights, int rows, int experts, int k,
             for (int i = 0; i < k; ++i)
                 if (sel[(int64_t)r * k + i] == e) perm[offsets[e] + fill[e]++] = r;
     free(fill);
+}
+
+/* The same dispatch from routing weights: each row's k highest-weighted experts
+ * (orc_topk_mask's order).  OXN/nsos/src/jamba.cpp:3882-3894 */
+void orc_moe_dispatch(const float* weights, int rows, int experts, int k,
+                      int32_t* counts, int32_t* offsets, int32_t* perm) {
+    float* tmp = (float*)malloc(sizeof(float) * (size_t)rows * (size_t)experts);
+    int32_t* sel = (int32_t*)malloc(sizeof(int32_t) * (size_t)rows * (size_t)k);
+    memcpy(tmp, weights, sizeof(float) * (size_t)rows * (size_t)experts);
+    orc_topk_mask(tmp, rows, experts, k, sel);
+    orc_moe_dispatch_sel(sel, rows, experts, k, counts, offsets, perm);
     free(sel);
     free(tmp);
 }

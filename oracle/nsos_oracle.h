@@ -84,6 +84,12 @@ void orc_bitlinear_ste_backward(const float* x, const int8_t* q, const float* as
 /* ---- MoE routing / dispatch ---------------------------------------------- */
 void orc_softmax_rows(const float* logits, int rows, int cols, float* probs);
 void orc_topk_mask(float* weights, int rows, int experts, int k, int32_t* selected);
+void orc_zero_invalid_rows(float* weights, int32_t* selected, const uint8_t* valid, int rows,
+                           int experts, int k);
+void orc_expert_loads(const float* weights, const uint8_t* valid, int rows, int experts,
+                      float* loads);
+void orc_moe_dispatch_sel(const int32_t* sel, int rows, int experts, int k, int32_t* counts,
+                          int32_t* offsets, int32_t* perm);
 void orc_moe_dispatch(const float* weights, int rows, int experts, int k,
                       int32_t* counts, int32_t* offsets, int32_t* perm);
 void orc_moe_combine(const float* expert_out, const int32_t* perm, const int32_t* offsets,

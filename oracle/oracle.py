@@ -77,6 +77,9 @@ def _load() -> ctypes.CDLL:
         "orc_softmax_rows": (None, [_f32p, _i, _i, _f32p]),
         "orc_topk_mask": (None, [_f32p, _i, _i, _i, _vp]),
         "orc_moe_dispatch": (None, [_f32p, _i, _i, _i, _i32p, _i32p, _i32p]),
+        "orc_zero_invalid_rows": (None, [_f32p, _i32p, _u8p, _i, _i, _i]),
+        "orc_expert_loads": (None, [_f32p, _vp, _i, _i, _f32p]),
+        "orc_moe_dispatch_sel": (None, [_i32p, _i, _i, _i, _i32p, _i32p, _i32p]),
         "orc_moe_combine": (None, [_f32p, _i32p, _i32p, _f32p, _i, _i, _i, _f32p]),
     }
     for name, (res, args) in sig.items():
@@ -337,12 +340,17 @@ def softmax_rows(logits) -> np.ndarray:
     return out
 
 
-def topk_mask(probs, k: int):
-    """-> (masked renormalised weights, selected expert ids [rows, k] in rank order)."""
+def topk_mask(probs, k: int, valid=None):
+    """-> (masked renormalised weights, selected expert ids [rows, k] in rank order).
+    valid: the 0/1 padding mask of MoERouter::forward(x, valid_rows); padding rows get
+    zero weights and selections -1."""
     w = _f32(probs).copy()
     rows, e = w.shape
     sel = np.empty((rows, k), np.int32)
     _lib.orc_topk_mask(w, rows, e, k, _ptr(sel))
+    if valid is not None:
+        v = np.ascontiguousarray(valid, dtype=np.uint8)
+        _lib.orc_zero_invalid_rows(w, sel, v, rows, e, k)
     return w, sel
 
 
@@ -355,6 +363,29 @@ def moe_dispatch(weights, k: int):
     perm = np.empty(rows * k, np.int32)
     _lib.orc_moe_dispatch(w, rows, e, k, counts, offsets, perm)
     return counts, offsets, perm
+
+
+def moe_dispatch_sel(selected, experts: int):
+    """The dispatch of a selection [rows, k] (-1 = no expert) -> (counts, offsets, perm);
+    perm holds offsets[E] rows (the rest of its rows * k entries are -1)."""
+    sel = np.ascontiguousarray(selected, dtype=np.int32)
+    rows, k = sel.shape
+    counts = np.empty(experts, np.int32)
+    offsets = np.empty(experts + 1, np.int32)
+    perm = np.full(rows * k, -1, np.int32)
+    _lib.orc_moe_dispatch_sel(sel, rows, experts, k, counts, offsets, perm)
+    return counts, offsets, perm
+
+
+def expert_loads(weights, valid=None) -> np.ndarray:
+    """MoERouter::forward's expert_loads: per-expert in-order sums of the weights over
+    the valid rows."""
+    w = _f32(weights)
+    rows, e = w.shape
+    loads = np.empty(e, np.float32)
+    v = None if valid is None else np.ascontiguousarray(valid, dtype=np.uint8)
+    _lib.orc_expert_loads(w, None if v is None else v.ctypes.data_as(_vp), rows, e, loads)
+    return loads
 
 
 def moe_combine(expert_out, perm, offsets, weights) -> np.ndarray:

@@ -62,7 +62,8 @@ SIGNATURES = {
                                    _vp, _f, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp,
                                    _f, _i, _vp, _vp, _vp, _i, _vp]),
     "nsosx_moe_route_workspace": (_i64, [_i, _i]),
-    "nsosx_moe_route": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "nsosx_moe_route": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                             _vp]),
     "nsosx_grouped_ternary_gemm": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i, _i,
                                         _vp, _i, _vp]),
     "nsosx_moe_combine": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _i, _vp]),

@@ -23,10 +23,25 @@ constexpr int kRouteBlock = 256;  // rows per dispatch block
 // loop at compile time, so the row's probabilities stay in registers (a
 // runtime-indexed array of 64 lives in scratch memory); experts past E are
 // masked out.
+// A padding row (valid_rows[r] == 0, as launch_moe_zero_invalid_rows_kernel reads the
+// mask, src/cuda/moe_kernels.cu:118-125) is absent from routing: its weights are all
+// zero (MoERouter::forward zeroes them after the top-k, src/jamba.cpp:8195-8214,
+// 8299-8304), its selections are -1, and it takes no dispatch slot (the reference's
+// dispatch counts only nonzero weights, src/cuda/moe_kernels.cu:226-235, 305-319).
 template <int EMAX>
-__device__ __forceinline__ void route_one_row(const float* __restrict__ logits, int r, int E, int k,
-                                              float* __restrict__ weights,
+__device__ __forceinline__ void route_one_row(const float* __restrict__ logits,
+                                              const uint8_t* __restrict__ valid_rows, int r,
+                                              int E, int k, float* __restrict__ weights,
                                               int32_t* __restrict__ selected, int (&sel)[8]) {
+    if (valid_rows && valid_rows[r] == 0) {
+        float* w = weights + (int64_t)r * E;
+        for (int j = 0; j < E; ++j) w[j] = 0.0f;
+        for (int i = 0; i < k; ++i) {
+            selected[(int64_t)r * k + i] = -1;
+            if (i < 8) sel[i] = -1;
+        }
+        return;
+    }
     const float* src = logits + (int64_t)r * E;
     float p[EMAX];
 #pragma unroll
@@ -74,12 +89,14 @@ __device__ __forceinline__ void route_one_row(const float* __restrict__ logits, 
 }
 
 template <int EMAX>
-__global__ __launch_bounds__(256) void route_rows_kernel(const float* __restrict__ logits, int rows,
-                                                         int E, int k, float* __restrict__ weights,
+__global__ __launch_bounds__(256) void route_rows_kernel(const float* __restrict__ logits,
+                                                         const uint8_t* __restrict__ valid_rows,
+                                                         int rows, int E, int k,
+                                                         float* __restrict__ weights,
                                                          int32_t* __restrict__ selected) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
     int sel[8];
-    if (r < rows) route_one_row<EMAX>(logits, r, E, k, weights, selected, sel);
+    if (r < rows) route_one_row<EMAX>(logits, valid_rows, r, E, k, weights, selected, sel);
 }
 
 // Routing fused with the per-block expert counts: one thread per row of a
@@ -87,6 +104,7 @@ __global__ __launch_bounds__(256) void route_rows_kernel(const float* __restrict
 // selected each expert (LDS counters; counts are order-free).
 template <int EMAX>
 __global__ __launch_bounds__(256) void route_rows_count_kernel(const float* __restrict__ logits,
+                                                               const uint8_t* __restrict__ valid_rows,
                                                                int rows, int E, int k,
                                                                float* __restrict__ weights,
                                                                int32_t* __restrict__ selected,
@@ -98,8 +116,9 @@ __global__ __launch_bounds__(256) void route_rows_count_kernel(const float* __re
     const int r = blockIdx.x * kRouteBlock + tid;
     if (r < rows) {
         int sel[8];
-        route_one_row<EMAX>(logits, r, E, k, weights, selected, sel);
-        for (int i = 0; i < k; ++i) atomicAdd(&cnt[sel[i]], 1);
+        route_one_row<EMAX>(logits, valid_rows, r, E, k, weights, selected, sel);
+        for (int i = 0; i < k; ++i)
+            if (sel[i] >= 0) atomicAdd(&cnt[sel[i]], 1);
     }
     __syncthreads();
     if (tid < E) block_counts[(int64_t)blockIdx.x * E + tid] = cnt[tid];
@@ -115,7 +134,10 @@ __global__ __launch_bounds__(256) void route_count_kernel(const int32_t* __restr
     __syncthreads();
     const int r = blockIdx.x * kRouteBlock + tid;
     if (r < rows)
-        for (int i = 0; i < k; ++i) atomicAdd(&cnt[selected[(int64_t)r * k + i]], 1);
+        for (int i = 0; i < k; ++i) {
+            const int e = selected[(int64_t)r * k + i];
+            if (e >= 0) atomicAdd(&cnt[e], 1);  // -1: a padding row
+        }
     __syncthreads();
     if (tid < E) block_counts[(int64_t)blockIdx.x * E + tid] = cnt[tid];
 }
@@ -165,6 +187,8 @@ __global__ __launch_bounds__(256) void route_assign_kernel(const int32_t* __rest
     int mine[kMaxExperts > 8 ? 8 : kMaxExperts];  // k <= 8 handled here
     const int kk = k < 8 ? k : 8;
     for (int i = 0; i < kk; ++i) mine[i] = valid ? selected[(int64_t)r * k + i] : -1;
+    if (valid && mine[0] < 0)  // a padding row: no slots
+        for (int i = 0; i < kk; ++i) slot_of[(int64_t)r * k + i] = -1;
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (int e = 0; e < E; ++e) {
         bool has = false;
@@ -240,6 +264,8 @@ __global__ __launch_bounds__(256) void route_place_kernel(const int32_t* __restr
     int mine[8];
     const int kk = k < 8 ? k : 8;
     for (int i = 0; i < kk; ++i) mine[i] = valid ? selected[(int64_t)r * k + i] : -1;
+    if (valid && mine[0] < 0)  // a padding row: no slots
+        for (int i = 0; i < kk; ++i) slot_of[(int64_t)r * k + i] = -1;
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (int e = 0; e < E; ++e) {
         bool has = false;
@@ -279,6 +305,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ e
     if (r >= rows || d >= dim) return;
     int es[8], ss[8];
     const int kk = k < 8 ? k : 8;
+    if (selected[(int64_t)r * k] < 0) {  // a padding row (no experts): zero
+        store_act<ODT>(out, (int64_t)r * dim + d, 0.0f);
+        return;
+    }
     for (int i = 0; i < kk; ++i) {
         es[i] = selected[(int64_t)r * k + i];
         ss[i] = slot_of ? slot_of[(int64_t)r * k + i] : r * k + i;
@@ -358,6 +388,14 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const void* __restric
     int es[8], ss[8];
     float ws[8];
     const int kk = k < 8 ? k : 8;
+    if (selected[(int64_t)r * k] < 0) {  // a padding row (no experts): zero
+        float zero[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) zero[j] = 0.0f;
+        for (int d = V * lane; d < dim; d += V * kWave)
+            combine_store<ODT, V>(out, (int64_t)r * dim + d, zero);
+        return;
+    }
     for (int i = 0; i < kk; ++i) {
         es[i] = selected[(int64_t)r * k + i];
         ss[i] = slot_of ? slot_of[(int64_t)r * k + i] : r * k + i;
@@ -412,6 +450,35 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const void* __restric
     }
 }
 
+// Per-expert loads: loads[e] = the sum over rows, in ascending row order, of
+// weights[r, e] (MoERouter::forward's expert_loads, src/jamba.cpp:8299-8307, the
+// order of launch_moe_load_ordered_kernel, src/cuda/moe_kernels.cu:108-116; padding
+// rows add their zero weights).  A wave per expert: each lane holds 64 consecutive
+// rows' values at a time and lane 0 adds them in order, so the loads of the next
+// 64 rows are in flight while the sum runs.
+__global__ __launch_bounds__(64) void route_loads_kernel(const float* __restrict__ weights,
+                                                         int rows, int E,
+                                                         float* __restrict__ loads) {
+    const int e = blockIdx.x;
+    const int lane = threadIdx.x;
+    __shared__ float s_v[2][kWave];
+    float total = 0.0f;
+    int buf = 0;
+    float v = lane < rows ? weights[(int64_t)lane * E + e] : 0.0f;
+    for (int r0 = 0; r0 < rows; r0 += kWave) {
+        s_v[buf][lane] = v;
+        const int rn = r0 + kWave + lane;
+        v = rn < rows ? weights[(int64_t)rn * E + e] : 0.0f;
+        __syncthreads();
+        if (lane == 0) {
+            const int n = min(kWave, rows - r0);
+            for (int i = 0; i < n; ++i) total = total + s_v[buf][i];
+        }
+        buf ^= 1;
+    }
+    if (lane == 0) loads[e] = total;
+}
+
 }  // namespace nsosx
 
 using namespace nsosx;
@@ -422,9 +489,10 @@ extern "C" int64_t nsosx_moe_route_workspace(int rows, int experts) {
     return nblocks * experts;
 }
 
-extern "C" int nsosx_moe_route(const float* logits, int rows, int experts, int k, float* weights,
-                               int32_t* selected, int32_t* counts, int32_t* offsets, int32_t* perm,
-                               int32_t* slot_of, int32_t* workspace, void* stream) {
+extern "C" int nsosx_moe_route(const float* logits, const uint8_t* valid_rows, int rows,
+                               int experts, int k, float* weights, int32_t* selected,
+                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* slot_of,
+                               float* loads, int32_t* workspace, void* stream) {
     // counts/offsets/perm/slot_of/workspace all NULL: selection only (the sparse decode
     // reads selected and weights and needs no expert-major permutation)
     const bool select_only = !counts && !offsets && !perm && !slot_of && !workspace;
@@ -441,26 +509,32 @@ extern "C" int nsosx_moe_route(const float* logits, int rows, int experts, int k
         // two launches: routing + block counts, then scans + stable ranks
         if (experts <= 8)
             hipLaunchKernelGGL(route_rows_count_kernel<8>, dim3(nblocks), rblock, 0, st, logits,
-                               rows, experts, k, weights, selected, workspace);
+                               valid_rows, rows, experts, k, weights, selected, workspace);
         else if (experts <= 16)
             hipLaunchKernelGGL(route_rows_count_kernel<16>, dim3(nblocks), rblock, 0, st, logits,
-                               rows, experts, k, weights, selected, workspace);
+                               valid_rows, rows, experts, k, weights, selected, workspace);
         else
             hipLaunchKernelGGL(route_rows_count_kernel<kMaxExperts>, dim3(nblocks), rblock, 0, st,
-                               logits, rows, experts, k, weights, selected, workspace);
+                               logits, valid_rows, rows, experts, k, weights, selected, workspace);
         hipLaunchKernelGGL(route_place_kernel, dim3(nblocks), rblock, 0, st, selected, rows,
                            experts, k, nblocks, workspace, counts, offsets, perm, slot_of);
+        if (loads)
+            hipLaunchKernelGGL(route_loads_kernel, dim3(experts), dim3(kWave), 0, st, weights,
+                               rows, experts, loads);
         return check_launch("moe_route");
     }
     if (experts <= 8)
-        hipLaunchKernelGGL(route_rows_kernel<8>, rgrid, rblock, 0, st, logits, rows, experts, k,
-                           weights, selected);
-    else if (experts <= 16)
-        hipLaunchKernelGGL(route_rows_kernel<16>, rgrid, rblock, 0, st, logits, rows, experts, k,
-                           weights, selected);
-    else
-        hipLaunchKernelGGL(route_rows_kernel<kMaxExperts>, rgrid, rblock, 0, st, logits, rows,
+        hipLaunchKernelGGL(route_rows_kernel<8>, rgrid, rblock, 0, st, logits, valid_rows, rows,
                            experts, k, weights, selected);
+    else if (experts <= 16)
+        hipLaunchKernelGGL(route_rows_kernel<16>, rgrid, rblock, 0, st, logits, valid_rows, rows,
+                           experts, k, weights, selected);
+    else
+        hipLaunchKernelGGL(route_rows_kernel<kMaxExperts>, rgrid, rblock, 0, st, logits,
+                           valid_rows, rows, experts, k, weights, selected);
+    if (loads)
+        hipLaunchKernelGGL(route_loads_kernel, dim3(experts), dim3(kWave), 0, st, weights, rows,
+                           experts, loads);
     if (select_only) return check_launch("moe_route");
     hipLaunchKernelGGL(route_count_kernel, dim3(nblocks), dim3(kRouteBlock), 0, st, selected, rows,
                        experts, k, workspace);

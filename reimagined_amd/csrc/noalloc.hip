@@ -7,7 +7,11 @@
 // holds its own copy at its own address from module load until the process
 // ends.  Host code never passes the symbol's name to a kernel (on the host it
 // is only a stand-in, not a device address); the device address is looked up
-// once per device with hipGetSymbolAddress and kept in g_scratch_ptr.
+// once per device with hipGetSymbolAddress, on the first call made on that
+// device outside HIP graph capture, and kept in g_scratch_ptr.  A first call
+// on a device whose stream is capturing is refused (the lookup may load the
+// code object, which has no place inside a capture): run the entry once
+// eagerly on each device, then capture it.
 #include "common.hpp"
 
 #include <mutex>
@@ -22,14 +26,13 @@ constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 
 static void* g_scratch_ptr[kMaxDevices];
-static std::once_flag g_scratch_once[kMaxDevices];
-static hipError_t g_scratch_status[kMaxDevices];
+static std::mutex g_scratch_mu;
 
 static int64_t round256(int64_t v) { return (v + 255) & ~int64_t(255); }
 
-// Device address of this device's scratch array (looked up on the first call
-// on each device, with that device current).
-static int scratch_for_current_device(unsigned char** out) {
+// Device address of this device's scratch array (looked up on the first call on
+// each device, with that device current and its stream not capturing).
+static int scratch_for_current_device(hipStream_t st, unsigned char** out) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess)
@@ -37,15 +40,22 @@ static int scratch_for_current_device(unsigned char** out) {
                                           hipGetErrorString(e));
     if (dev < 0 || dev >= kMaxDevices)
         return fail(NSOSX_ERR_INVALID, "bitlinear_forward_noalloc: device index out of range");
-    std::call_once(g_scratch_once[dev], [dev] {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(st, &cs);
+        if (e != hipSuccess || cs != hipStreamCaptureStatusNone)
+            return fail(NSOSX_ERR_INVALID,
+                        "bitlinear_forward_noalloc: the first call on a device must be made "
+                        "outside HIP graph capture (it looks up the scratch array's address)");
         void* p = nullptr;
-        g_scratch_status[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        g_scratch_ptr[dev] = g_scratch_status[dev] == hipSuccess ? p : nullptr;
-    });
-    if (g_scratch_status[dev] != hipSuccess || !g_scratch_ptr[dev])
-        return fail(NSOSX_ERR_LAUNCH,
-                    std::string("bitlinear_forward_noalloc: hipGetSymbolAddress: ") +
-                        hipGetErrorString(g_scratch_status[dev]));
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(NSOSX_ERR_LAUNCH,
+                        std::string("bitlinear_forward_noalloc: hipGetSymbolAddress: ") +
+                            hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
     *out = static_cast<unsigned char*>(g_scratch_ptr[dev]);
     return NSOSX_OK;
 }
@@ -71,7 +81,7 @@ extern "C" int nsosx_bitlinear_forward_noalloc(const void* x, int x_dtype,
                     "bitlinear_forward_noalloc: M*K + 8*M bytes of workspace exceed the "
                     "library's 8 MiB scratch; use nsosx_bitlinear_forward with caller buffers");
     unsigned char* base = nullptr;
-    int rc = scratch_for_current_device(&base);
+    int rc = scratch_for_current_device(static_cast<hipStream_t>(stream), &base);
     if (rc) return rc;
     int8_t* q = reinterpret_cast<int8_t*>(base);
     float* scale = reinterpret_cast<float*>(base + q_bytes);

@@ -1448,8 +1448,8 @@ extern "C" int nsosx_scan_fwd_planned(const void* x, int64_t x_stride, const flo
     if (reinterpret_cast<uintptr_t>(workspace) % 256)
         return fail(NSOSX_ERR_INVALID, "scan_fwd_planned: workspace must be 256-byte aligned");
     if (!cu_seqlens || num_seqs <= 0 || num_seqs > 65535 || total_tokens < 0 || H <= 0 || P <= 0 ||
-        N <= 0)
-        return fail(NSOSX_ERR_INVALID, "scan_fwd_planned: bad shape");
+        N <= 0 || N > 64 || G <= 0 || H % G != 0)
+        return fail(NSOSX_ERR_INVALID, "scan_fwd_planned: bad shape (N <= 64, G > 0, H % G == 0)");
     if (chunk_tokens > 0 && chunk_tokens < 4)
         return fail(NSOSX_ERR_INVALID, "scan_fwd_planned: chunk_tokens must be >= 4, 0 or -1");
     const int Cn = resolve_chunk(num_seqs, total_tokens, H, P, N, chunk_tokens);

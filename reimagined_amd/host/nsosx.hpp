@@ -222,8 +222,8 @@ class BitLinear {
     DeviceBuffer q_ws_, scale_ws_, rms_ws_;
 };
 
-// MoERouter::forward from logits (src/jamba.cpp:8140-8319) with the ordered
-// dispatch of forward_moe: device outputs, owned by the router.
+// MoERouter::forward(x, valid_rows) from logits (src/jamba.cpp:8140-8319) with the
+// ordered dispatch of forward_moe: device outputs, owned by the router.
 class MoERouter {
   public:
     MoERouter(int num_experts, int top_k) : e_(num_experts), k_(top_k) {
@@ -232,31 +232,49 @@ class MoERouter {
     }
     struct Routing {
         const float* weights;     // [rows, E]
-        const int32_t* selected;  // [rows, k]
+        const int32_t* selected;  // [rows, k] (-1 on padding rows)
         const int32_t* counts;    // [E]
         const int32_t* offsets;   // [E + 1]
-        const int32_t* perm;      // [rows * k]
-        const int32_t* slot_of;   // [rows, k]
+        const int32_t* perm;      // [rows * k] (the first offsets[E] entries)
+        const int32_t* slot_of;   // [rows, k] (-1 on padding rows)
+        const float* loads;       // [E] (expert_loads) when asked for, else nullptr
     };
-    Routing route(const float* logits, int rows, hipStream_t stream = nullptr) {
+    // valid_rows: the reference's host mask, empty (every row valid) or one 0 / 1 per
+    // row, validated as MoERouter::forward does (src/jamba.cpp:8145-8153) and uploaded
+    // on `stream`.  want_loads: also the per-expert loads.
+    Routing route(const float* logits, int rows, hipStream_t stream = nullptr,
+                  const std::vector<uint8_t>& valid_rows = {}, bool want_loads = false) {
+        if (!valid_rows.empty()) {
+            if (valid_rows.size() != static_cast<size_t>(rows))
+                throw std::invalid_argument("MoERouter valid-row mask size mismatch");
+            for (uint8_t v : valid_rows)
+                if (v > 1) throw std::invalid_argument("MoERouter valid-row mask must contain only 0 or 1");
+            mask_.reserve((size_t)rows);
+            check_hip(hipMemcpyAsync(mask_.data(), valid_rows.data(), (size_t)rows,
+                                     hipMemcpyHostToDevice, stream),
+                      "MoE valid-row mask upload");
+        }
         weights_.reserve((size_t)rows * e_ * 4);
         selected_.reserve((size_t)rows * k_ * 4);
         counts_.reserve((size_t)e_ * 4);
         offsets_.reserve((size_t)(e_ + 1) * 4);
         perm_.reserve((size_t)rows * k_ * 4);
         slot_of_.reserve((size_t)rows * k_ * 4);
+        if (want_loads) loads_.reserve((size_t)e_ * 4);
         ws_.reserve((size_t)nsosx_moe_route_workspace(rows, e_) * 4 + 4);
-        check(nsosx_moe_route(logits, rows, e_, k_, weights_.as<float>(), selected_.as<int32_t>(),
+        float* loads = want_loads ? loads_.as<float>() : nullptr;
+        check(nsosx_moe_route(logits, valid_rows.empty() ? nullptr : mask_.as<uint8_t>(), rows,
+                              e_, k_, weights_.as<float>(), selected_.as<int32_t>(),
                               counts_.as<int32_t>(), offsets_.as<int32_t>(), perm_.as<int32_t>(),
-                              slot_of_.as<int32_t>(), ws_.as<int32_t>(), stream),
+                              slot_of_.as<int32_t>(), loads, ws_.as<int32_t>(), stream),
               "MoERouter::forward");
         return {weights_.as<float>(), selected_.as<int32_t>(), counts_.as<int32_t>(),
-                offsets_.as<int32_t>(), perm_.as<int32_t>(), slot_of_.as<int32_t>()};
+                offsets_.as<int32_t>(), perm_.as<int32_t>(), slot_of_.as<int32_t>(), loads};
     }
 
   private:
     int e_, k_;
-    DeviceBuffer weights_, selected_, counts_, offsets_, perm_, slot_of_, ws_;
+    DeviceBuffer weights_, selected_, counts_, offsets_, perm_, slot_of_, loads_, mask_, ws_;
 };
 
 // The Mamba selective scan over a packed ragged batch (src/mamba2.cpp:2602-2675)

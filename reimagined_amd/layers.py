@@ -230,20 +230,22 @@ class MoEFFN:
         return b
 
     def forward(self, x: torch.Tensor, logits: torch.Tensor, out_dtype=None,
-                marker=None) -> dict:
+                marker=None, valid_rows=None) -> dict:
         """Returns {"out": a fresh [rows, d_model] tensor, plus the routing tensors and the
         expert hidden / output rows}.  Those extras are views of this layer's per-row-count
         workspaces: the next forward with the same row count overwrites them.  marker(name),
         when given, is called after each kernel (route, quant_in, up, quant_hidden, down,
-        combine)."""
+        combine).  valid_rows: the reference's 0/1 padding mask (ops.moe_route); padding
+        rows take no expert slots and come out as zeros."""
         rows = x.shape[0]
         b = self._buffers(rows, x.device)
         e, k = self.experts, self.k
         st = _stream()
         mk = marker or (lambda name: None)
-        call("nsosx_moe_route", _p(logits), rows, e, k, _p(b["weights"]), _p(b["selected"]),
-             _p(b["counts"]), _p(b["offsets"]), _p(b["perm"]), _p(b["slot_of"]),
-             _p(b["route_ws"]), st)
+        mask = ops.valid_rows_mask(valid_rows, rows, x.device)
+        call("nsosx_moe_route", _p(logits), _p(mask), rows, e, k, _p(b["weights"]),
+             _p(b["selected"]), _p(b["counts"]), _p(b["offsets"]), _p(b["perm"]),
+             _p(b["slot_of"]), None, _p(b["route_ws"]), st)
         mk("route")
         call("nsosx_quantize_act_i8", _p(x), ops._dt(x), rows, self.d_model, 8,
              int(self.rms_input), _p(b["q1"]), _p(b["s1"]), _p(b["r1"]), st)
@@ -278,15 +280,18 @@ class MoEFFN:
         return {"out": out, **{n: b[n] for n in ("weights", "selected", "counts", "offsets",
                                                  "perm", "slot_of", "h", "o")}}
 
-    def decode(self, x: torch.Tensor, logits: torch.Tensor, out_dtype=None) -> dict:
+    def decode(self, x: torch.Tensor, logits: torch.Tensor, out_dtype=None,
+               valid_rows=None) -> dict:
         """Sparse decode for a few rows (launch_moe_sparse_decode's role): routing on the
-        device, then grouped GEMVs over the (row, routed expert) pairs and the combine."""
+        device, then grouped GEMVs over the (row, routed expert) pairs and the combine.
+        valid_rows as forward()."""
         rows = x.shape[0]
         b = self._buffers(rows, x.device)
         e, k = self.experts, self.k
         st = _stream()
-        call("nsosx_moe_route", _p(logits), rows, e, k, _p(b["weights"]), _p(b["selected"]),
-             None, None, None, None, None, st)
+        mask = ops.valid_rows_mask(valid_rows, rows, x.device)
+        call("nsosx_moe_route", _p(logits), _p(mask), rows, e, k, _p(b["weights"]),
+             _p(b["selected"]), None, None, None, None, None, None, st)
         nbytes = int(ops.lib().nsosx_moe_sparse_decode_workspace(rows, k, self.d_model,
                                                                  self.d_ff))
         ws = b.get("sparse_ws")
@@ -343,8 +348,11 @@ class HybridBlock:
         return ops.linear_f32(f, self.gate_w, rms_input=True, magnitude=self.gate_mag,
                               bias=self.gate_bias)
 
-    def forward(self, x, dt, B, C, cu_seqlens, logits=None, final_state=None) -> dict:
-        """x [T, d_model] (f32 or bf16); the remaining scan inputs as HybridMambaLayer."""
+    def forward(self, x, dt, B, C, cu_seqlens, logits=None, final_state=None,
+                valid_rows=None) -> dict:
+        """x [T, d_model] (f32 or bf16); the remaining scan inputs as HybridMambaLayer.
+        valid_rows: the 0/1 padding mask forward_moe builds from the batch's valid
+        lengths (src/jamba.cpp:3708-3710), None for none."""
         ops._dev(cu_seqlens, "cu_seqlens", torch.int32)
         if logits is None and self.gate is None and self.gate_w is None:
             raise ValueError("HybridBlock: pass router logits or build the block with gate_w")
@@ -354,7 +362,7 @@ class HybridBlock:
         r, f = ops.add_rmsnorm(x, core, self.ff_gamma, eps=self.ff_eps)
         if logits is None:
             logits = self.router_logits(f)
-        ff = self.moe.forward(f, logits, out_dtype=x.dtype)["out"]
+        ff = self.moe.forward(f, logits, out_dtype=x.dtype, valid_rows=valid_rows)["out"]
         out, _ = ops.add_rmsnorm(r, ff, want_norm=False)
         return {"out": out, "residual": r, "core": core, "ff": ff, "logits": logits,
                 "h": h, "f": f}

@@ -574,19 +574,49 @@ def mamba2_step(x, z, B, C, dt, conv_w, conv_b, ring, a_log, D, norm_w, state, H
 
 # ---- MoE ------------------------------------------------------------------------
 
-def moe_route(logits: torch.Tensor, k: int = 2, select_only: bool = False) -> dict:
-    """MoERouter::forward from logits + forward_moe's ordered dispatch, on the device.
-    select_only: weights and selected only (one launch), as the sparse decode needs."""
+def valid_rows_mask(valid_rows, rows: int, device) -> torch.Tensor | None:
+    """The reference's 0/1 valid-row mask on the device (None: every row valid).  A host
+    mask is checked as MoERouter::forward checks it (src/jamba.cpp:8145-8153): one entry
+    per row, each 0 or 1, else ValueError; a uint8 device tensor is taken as is (the
+    routing then treats any nonzero byte as valid, as the reference's device kernel
+    does)."""
+    if valid_rows is None:
+        return None
+    if isinstance(valid_rows, torch.Tensor) and valid_rows.is_cuda:
+        if valid_rows.dtype != torch.uint8 or valid_rows.numel() != rows:
+            raise ValueError("MoERouter valid-row mask size mismatch")
+        return valid_rows.contiguous()
+    v = np.asarray(valid_rows.cpu() if isinstance(valid_rows, torch.Tensor) else valid_rows)
+    if v.size == 0:
+        return None
+    if v.size != rows:
+        raise ValueError("MoERouter valid-row mask size mismatch")
+    if np.any((v != 0) & (v != 1)):
+        raise ValueError("MoERouter valid-row mask must contain only 0 or 1")
+    return torch.from_numpy(v.astype(np.uint8).reshape(-1)).to(device)
+
+
+def moe_route(logits: torch.Tensor, k: int = 2, select_only: bool = False, valid_rows=None,
+              want_loads: bool = False) -> dict:
+    """MoERouter::forward(x, valid_rows) from logits + forward_moe's ordered dispatch, on the
+    device.  select_only: weights and selected only (one launch), as the sparse decode needs.
+    valid_rows: the reference's 0/1 padding mask (host array or uint8 device tensor), None
+    for every row valid; padding rows get zero weights, selections -1 and no slots.
+    want_loads: also "loads", the per-expert sums of the weights (expert_loads)."""
     _dev(logits, "logits", torch.float32)
     rows, e = logits.shape
     dev = logits.device
+    mask = valid_rows_mask(valid_rows, rows, dev)
     out = {
         "weights": torch.empty((rows, e), dtype=torch.float32, device=dev),
         "selected": torch.empty((rows, k), dtype=torch.int32, device=dev),
     }
+    if want_loads:
+        out["loads"] = torch.empty(e, dtype=torch.float32, device=dev)
+    loads = _p(out["loads"]) if want_loads else None
     if select_only:
-        call("nsosx_moe_route", _p(logits), rows, e, k, _p(out["weights"]), _p(out["selected"]),
-             None, None, None, None, None, _stream())
+        call("nsosx_moe_route", _p(logits), _p(mask), rows, e, k, _p(out["weights"]),
+             _p(out["selected"]), None, None, None, None, loads, None, _stream())
         return out
     out.update({
         "counts": torch.empty(e, dtype=torch.int32, device=dev),
@@ -596,9 +626,9 @@ def moe_route(logits: torch.Tensor, k: int = 2, select_only: bool = False) -> di
     })
     ws = torch.empty(max(1, int(lib().nsosx_moe_route_workspace(rows, e))), dtype=torch.int32,
                      device=dev)
-    call("nsosx_moe_route", _p(logits), rows, e, k, _p(out["weights"]), _p(out["selected"]),
-         _p(out["counts"]), _p(out["offsets"]), _p(out["perm"]), _p(out["slot_of"]), _p(ws),
-         _stream())
+    call("nsosx_moe_route", _p(logits), _p(mask), rows, e, k, _p(out["weights"]),
+         _p(out["selected"]), _p(out["counts"]), _p(out["offsets"]), _p(out["perm"]),
+         _p(out["slot_of"]), loads, _p(ws), _stream())
     return out
 
 

@@ -61,10 +61,13 @@ def test_hybrid_layer_matches_oracle(dev, orc):
 def test_hybrid_layer_full_size_sampled(dev, orc):
     """Config 4 at full size (T = 40796 tokens in 32 ragged sequences, d_model 1024, d_inner
     2048): the kernels the bench times, at the shapes it times them.  Rows are independent in
-    the projections and sequences in the scan, so sampled rows and the two shortest sequences
-    are checked against the oracle: in_proj and out_proj bit-exact (given the GPU's own scan
-    output for out_proj), conv + scan within the fp32 scan bound and the final states of those
-    sequences within 1e-4."""
+    the projections, so sampled rows of in_proj and out_proj are checked bit-exact (given the
+    GPU's own scan output for out_proj).  The conv + scan is checked whole: every sequence's
+    output rows within the bf16 bound and all 32 final states within the fp32 scan bound
+    (1e-4 / 1e-5), the oracle run on the GPU's own in_proj output, one sequence per host
+    thread."""
+    import concurrent.futures as cf
+    import os
     params, inp = workloads.config4()
     T = int(inp["cu_seqlens"][-1])
     di = params["w_out"].shape[1]
@@ -88,20 +91,29 @@ def test_hybrid_layer_full_size_sampled(dev, orc):
     y = orc.bitlinear_forward(ys_rows, pout, wso, params["w_out"].shape[0], rms_input=True)
     np.testing.assert_array_equal(out[torch.from_numpy(rows).to(dev)].float().cpu().numpy(),
                                   _bf(y).float().numpy())
-    # conv + scan of the two shortest sequences on the GPU's in_proj output
+    # conv + scan of every sequence on the GPU's in_proj output
     c = inp["cu_seqlens"]
-    lens = np.diff(c)
-    for s in np.argsort(lens, kind="stable")[:2]:
+    xz_all = buf["xz"].cpu()
+    ys_all = buf["ys"].cpu()
+    fin_all = fin.cpu().numpy()
+    dtf, Bf, Cf = dtb.float().numpy(), Bb.float().numpy(), Cb.float().numpy()
+
+    def check(s):
         a, b = int(c[s]), int(c[s + 1])
-        xz_s = buf["xz"][a:b].float().cpu().numpy()
+        xz_s = xz_all[a:b].float().numpy()
         cs = np.array([0, b - a], np.int32)
         xc = orc.conv1d_causal(np.ascontiguousarray(xz_s[:, :di]), params["conv_w"], cs,
                                bias=params["conv_b"], silu_act=True)
-        ys, wfin = orc.selective_scan(xc, dtb[a:b].float().numpy(), params["a_log"],
-                                      Bb[a:b].float().numpy(), Cb[a:b].float().numpy(),
+        ys, wfin = orc.selective_scan(xc, dtf[a:b], params["a_log"], Bf[a:b], Cf[a:b],
                                       params["d_skip"], np.ascontiguousarray(xz_s[:, di:]), cs,
                                       di, 1, n, 1)
         scale = np.abs(ys).max()
-        np.testing.assert_allclose(buf["ys"][a:b].float().cpu().numpy(), ys, rtol=2e-2,
-                                   atol=2e-2 * scale / 64)
-        np.testing.assert_allclose(fin[s].cpu().numpy(), wfin[0], rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(ys_all[a:b].float().numpy(), ys, rtol=2e-2,
+                                   atol=2e-2 * scale / 64, err_msg=f"sequence {s} y")
+        np.testing.assert_allclose(fin_all[s], wfin[0], rtol=1e-4, atol=1e-5,
+                                   err_msg=f"sequence {s} final state")
+        return b - a
+    workers = max(1, min(16, os.cpu_count() or 1))
+    with cf.ThreadPoolExecutor(max_workers=workers) as ex:
+        checked = sum(ex.map(check, range(len(c) - 1)))
+    assert checked == T

@@ -55,10 +55,58 @@ def test_route_partial_null_outputs_rejected(dev):
     w = torch.empty((4, 8), dtype=torch.float32, device=dev)
     s = torch.empty((4, 2), dtype=torch.int32, device=dev)
     counts = torch.empty(8, dtype=torch.int32, device=dev)
-    rc = ops.lib().nsosx_moe_route(logits.data_ptr(), 4, 8, 2, w.data_ptr(),
-                                   s.data_ptr(), counts.data_ptr(), None, None, None, None, None)
+    rc = ops.lib().nsosx_moe_route(logits.data_ptr(), None, 4, 8, 2, w.data_ptr(),
+                                   s.data_ptr(), counts.data_ptr(), None, None, None, None, None,
+                                   None)
     assert rc != 0
     assert b"null pointer" in ops.lib().nsosx_last_error()
+
+
+@pytest.mark.parametrize("rows,E,k", [(8192, 8, 2), (1000, 64, 8), (300, 8, 1)])
+def test_route_padding_rows_match_oracle(dev, orc, rows, E, k):
+    """MoERouter::forward(x, valid_rows): padding rows get zero weights, selections -1,
+    slot_of -1 and no slots; the rest route as without the mask.  loads = expert_loads."""
+    rng = np.random.default_rng(3 * rows + E)
+    logits = rng.standard_normal((rows, E)).astype(np.float32)
+    valid = (rng.random(rows) < 0.75).astype(np.uint8)
+    valid[-1] = 0
+    r = ops.moe_route(torch.from_numpy(logits).to(dev), k, valid_rows=valid, want_loads=True)
+    w, sel = orc.topk_mask(orc.softmax_rows(logits), k, valid)
+    counts, offsets, perm = orc.moe_dispatch_sel(sel, E)
+    np.testing.assert_array_equal(r["selected"].cpu().numpy(), sel)
+    np.testing.assert_array_equal(r["counts"].cpu().numpy(), counts)
+    np.testing.assert_array_equal(r["offsets"].cpu().numpy(), offsets)
+    n = int(offsets[-1])
+    assert n == int(valid.sum()) * k
+    np.testing.assert_array_equal(r["perm"].cpu().numpy()[:n], perm[:n])
+    gw = r["weights"].cpu().numpy()
+    np.testing.assert_allclose(gw, w, rtol=1e-6, atol=1e-7)
+    assert np.all(gw[valid == 0] == 0.0)
+    slot_of = r["slot_of"].cpu().numpy()
+    assert np.all(slot_of[valid == 0] == -1)
+    pm = r["perm"].cpu().numpy()
+    idx = np.flatnonzero(valid)
+    for i in range(k):
+        np.testing.assert_array_equal(pm[slot_of[idx, i]], idx)
+    # the device loads sum the device weights in the oracle's order: bit-exact on them
+    np.testing.assert_array_equal(r["loads"].cpu().numpy(), orc.expert_loads(gw, valid))
+    np.testing.assert_allclose(r["loads"].cpu().numpy(), orc.expert_loads(w, valid), rtol=1e-5)
+
+
+def test_route_loads_without_mask_select_only(dev, orc):
+    rng = np.random.default_rng(77)
+    logits = torch.from_numpy(rng.standard_normal((777, 8)).astype(np.float32)).to(dev)
+    r = ops.moe_route(logits, 2, select_only=True, want_loads=True)
+    np.testing.assert_array_equal(r["loads"].cpu().numpy(),
+                                  orc.expert_loads(r["weights"].cpu().numpy()))
+
+
+def test_route_mask_checked_on_host(dev):
+    logits = torch.zeros((4, 8), dtype=torch.float32, device=dev)
+    with pytest.raises(ValueError, match="only 0 or 1"):
+        ops.moe_route(logits, 2, valid_rows=np.array([1, 2, 1, 1], np.uint8))
+    with pytest.raises(ValueError, match="size mismatch"):
+        ops.moe_route(logits, 2, valid_rows=np.array([1, 1, 1], np.uint8))
 
 
 def test_route_ties_prefer_lower_index(dev, orc):
@@ -167,6 +215,52 @@ def test_moe_sparse_decode_matches_oracle(dev, orc, rows):
     np.testing.assert_array_equal(res["out"].cpu().numpy(), want)
     w_orc, sel_orc = orc.topk_mask(orc.softmax_rows(logits), k)
     np.testing.assert_array_equal(sel, sel_orc)
+
+
+@pytest.mark.parametrize("hidden_dtype", [torch.float32, torch.bfloat16])
+def test_moe_ffn_padding_rows(dev, hidden_dtype):
+    """forward_moe over a padded batch (valid_rows from the batch's valid lengths,
+    src/jamba.cpp:3708-3710): the valid rows come out bit for bit as a forward over the
+    valid rows alone, the padding rows as zeros, and no expert slot holds a padding row."""
+    rng = np.random.default_rng(81)
+    rows, E, k, d, f = 700, 8, 2, 256, 512
+    w_up = [_ternary(rng, f, d) for _ in range(E)]
+    w_down = [_ternary(rng, d, f) for _ in range(E)]
+    x = torch.from_numpy(rng.standard_normal((rows, d)).astype(np.float32)).to(dev)
+    logits = torch.from_numpy(rng.standard_normal((rows, E)).astype(np.float32)).to(dev)
+    valid = (rng.random(rows) < 0.6).astype(np.uint8)
+    idx = torch.from_numpy(np.flatnonzero(valid)).to(dev)
+    moe = MoEFFN(w_up, w_down, dev, k=k, rms_input=True, hidden_dtype=hidden_dtype)
+    got = moe.forward(x, logits, out_dtype=torch.float32, valid_rows=valid)
+    out = got["out"].clone()
+    n = int(got["offsets"][-1])
+    assert n == int(valid.sum()) * k
+    assert set(got["perm"][:n].cpu().numpy().tolist()) <= set(idx.cpu().numpy().tolist())
+    ref = moe.forward(x[idx].contiguous(), logits[idx].contiguous(), out_dtype=torch.float32)
+    assert torch.equal(out[idx], ref["out"])
+    assert torch.count_nonzero(out[torch.from_numpy(valid == 0).to(dev)]) == 0
+    # a device mask reads the same
+    got2 = moe.forward(x, logits, out_dtype=torch.float32,
+                       valid_rows=torch.from_numpy(valid).to(dev))
+    assert torch.equal(got2["out"], out)
+
+
+def test_moe_sparse_decode_padding_rows(dev):
+    """Sparse decode with padding rows: they take no expert GEMV and come out as zeros; the
+    valid rows equal a decode of the valid rows alone."""
+    rng = np.random.default_rng(82)
+    rows, E, k, d, f = 9, 8, 2, 256, 512
+    w_up = [_ternary(rng, f, d) for _ in range(E)]
+    w_down = [_ternary(rng, d, f) for _ in range(E)]
+    x = torch.from_numpy(rng.standard_normal((rows, d)).astype(np.float32)).to(dev)
+    logits = torch.from_numpy(rng.standard_normal((rows, E)).astype(np.float32)).to(dev)
+    valid = np.array([1, 0, 1, 1, 0, 0, 1, 1, 0], np.uint8)
+    idx = torch.from_numpy(np.flatnonzero(valid)).to(dev)
+    moe = MoEFFN(w_up, w_down, dev, k=k, rms_input=True)
+    out = moe.decode(x, logits, out_dtype=torch.float32, valid_rows=valid)["out"].clone()
+    ref = moe.decode(x[idx].contiguous(), logits[idx].contiguous(), out_dtype=torch.float32)
+    assert torch.equal(out[idx], ref["out"])
+    assert torch.count_nonzero(out[torch.from_numpy(valid == 0).to(dev)]) == 0
 
 
 def test_moe_ffn_full_size_sampled(dev, orc):

@@ -6,6 +6,7 @@ conv weight would otherwise be read or written out of bounds on the device.
 These run on CPU tensors; a wrapper must reject the bad shape with ValueError
 before it looks at the device, and a well-shaped CPU tensor gets as far as
 the device check."""
+import numpy as np
 import pytest
 import torch
 
@@ -108,3 +109,58 @@ def test_mfma_layout_gemm_rejects_k_past_int32_range():
     rc = f(p, p, p, ctypes.c_float(1.0), 1, k_big, 16, None, None, p, 1, None, None)
     assert rc == 2, lib.nsosx_last_error().decode()   # NSOSX_ERR_OVERFLOW
     assert "64x-scaled" in lib.nsosx_last_error().decode()
+
+
+# ---- C-ABI argument checks that run before anything touches the device --------------
+# The pointers below are non-null placeholders: each call is refused by its argument
+# checks, which run before any pointer is dereferenced or any launch is made.
+_FAKE = 1 << 20  # a 256-byte-aligned placeholder address, never dereferenced
+
+
+def test_planned_scan_rejects_bad_group_count():
+    """G == 0 (or H % G != 0) is NSOSX_ERR_INVALID, not a host divide-by-zero."""
+    from reimagined_amd._lib import lib
+    L = lib()
+    for G in (0, 3):
+        rc = L.nsosx_scan_fwd_planned(_FAKE, 0, None, None, 0, _FAKE, _FAKE, 1, _FAKE, _FAKE,
+                                      _FAKE, None, 0, _FAKE, 2, 100, 4, 16, 16, G, 0, None, None,
+                                      _FAKE, -1, _FAKE, None)
+        assert rc == 1, (G, rc)
+        assert b"H % G" in L.nsosx_last_error()
+
+
+def test_grouped_mfma_gemm_requires_total_rows():
+    """total_rows == 0 is refused (the MFMA-layout grouped GEMM sizes its grid from it),
+    where it used to return success with the output untouched."""
+    from reimagined_amd._lib import lib
+    L = lib()
+    rc = L.nsosx_grouped_ternary_gemm_mfma(_FAKE, 8, _FAKE, _FAKE, 1, _FAKE, _FAKE, 1024, 4096,
+                                           0, 1, _FAKE, 1, None)
+    assert rc == 1
+    assert b"total_rows > 0" in L.nsosx_last_error()
+
+
+def test_moe_route_argument_checks():
+    from reimagined_amd._lib import lib
+    L = lib()
+    # k above 8, and partial null outputs
+    rc = L.nsosx_moe_route(_FAKE, None, 16, 16, 9, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE,
+                           None, _FAKE, None)
+    assert rc == 1
+    rc = L.nsosx_moe_route(_FAKE, None, 16, 8, 2, _FAKE, _FAKE, _FAKE, None, None, None, None,
+                           None, None)
+    assert rc == 1 and b"null pointer" in L.nsosx_last_error()
+
+
+def test_moe_route_host_mask_validation():
+    """The host mirror checks a host mask as MoERouter::forward does (src/jamba.cpp:
+    8145-8153) before touching the device."""
+    from reimagined_amd.ops import valid_rows_mask
+    with pytest.raises(ValueError, match="only 0 or 1"):
+        valid_rows_mask([1, 0, 2], 3, "cpu")
+    with pytest.raises(ValueError, match="size mismatch"):
+        valid_rows_mask([1, 0], 3, "cpu")
+    assert valid_rows_mask(None, 3, "cpu") is None
+    assert valid_rows_mask([], 3, "cpu") is None
+    m = valid_rows_mask(np.array([1, 0, 1]), 3, "cpu")
+    assert m.dtype == torch.uint8 and m.tolist() == [1, 0, 1]

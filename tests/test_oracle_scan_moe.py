@@ -221,3 +221,59 @@ def test_combine_expert_ascending(orc):
         for s in range(offsets[e], offsets[e + 1]):
             want[perm[s]] = (want[perm[s]] + eo[s] * w[perm[s], e]).astype(np.float32)
     np.testing.assert_array_equal(out, want)
+
+
+# ---- padding rows (MoERouter::forward(x, valid_rows), src/jamba.cpp:8140-8319) --------
+
+@pytest.mark.parametrize("rows,E,k", [(300, 8, 2), (64, 16, 4), (7, 8, 8)])
+def test_padding_rows_are_absent_from_dispatch(orc, rows, E, k):
+    """Masked routing equals routing the valid rows alone, with the row ids mapped back:
+    padding rows take no slot (the device dispatch counts only nonzero weights,
+    src/cuda/moe_kernels.cu:226-235, 305-319) and keep all-zero weights."""
+    rng = np.random.default_rng(rows + 7 * E)
+    p = orc.softmax_rows(rng.standard_normal((rows, E)).astype(np.float32))
+    valid = (rng.random(rows) < 0.7).astype(np.uint8)
+    valid[0] = 0
+    w, sel = orc.topk_mask(p, k, valid)
+    idx = np.flatnonzero(valid)
+    w_v, sel_v = orc.topk_mask(p[idx], k)
+    np.testing.assert_array_equal(w[idx], w_v)
+    np.testing.assert_array_equal(sel[idx], sel_v)
+    assert np.all(w[valid == 0] == 0.0) and np.all(sel[valid == 0] == -1)
+    counts, offsets, perm = orc.moe_dispatch_sel(sel, E)
+    c_v, o_v, p_v = orc.moe_dispatch(w_v, k)
+    np.testing.assert_array_equal(counts, c_v)
+    np.testing.assert_array_equal(offsets, o_v)
+    np.testing.assert_array_equal(perm[:offsets[-1]], idx[p_v])
+    assert np.all(perm[offsets[-1]:] == -1) and offsets[-1] == len(idx) * k
+
+
+def test_dispatch_of_selection_matches_dispatch_of_weights(orc):
+    rng = np.random.default_rng(29)
+    p = orc.softmax_rows(rng.standard_normal((257, 8)).astype(np.float32))
+    w, sel = orc.topk_mask(p, 2)
+    for a, b in zip(orc.moe_dispatch_sel(sel, 8), orc.moe_dispatch(w, 2)):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_expert_loads(orc):
+    """expert_loads (src/jamba.cpp:8299-8307): per-expert sums over the valid rows in
+    ascending order; they sum to the number of valid rows (each renormalised row sums to
+    1) and match a float64 column sum."""
+    rng = np.random.default_rng(30)
+    rows, E, k = 1000, 8, 2
+    p = orc.softmax_rows(rng.standard_normal((rows, E)).astype(np.float32))
+    valid = (rng.random(rows) < 0.8).astype(np.uint8)
+    w, _ = orc.topk_mask(p, k, valid)
+    loads = orc.expert_loads(w, valid)
+    want = w[valid == 1].astype(np.float64).sum(axis=0)
+    np.testing.assert_allclose(loads, want, rtol=1e-5)
+    assert abs(float(loads.astype(np.float64).sum()) - int(valid.sum())) < 1e-2
+    # in order: the running float sum, row by row
+    run = np.zeros(E, np.float32)
+    for r in range(rows):
+        if valid[r]:
+            run = (run + w[r]).astype(np.float32)
+    np.testing.assert_array_equal(loads, run)
+    # padding rows hold zero weights, so summing them too changes nothing
+    np.testing.assert_array_equal(orc.expert_loads(w), loads)

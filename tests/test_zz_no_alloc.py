@@ -1,7 +1,8 @@
 """The allocation-free BitLinear forward (library-owned scratch) against the
 caller-workspace entry point it shares its kernels with: bit-exact outputs on
 two calls in a row, the second with a smaller input (the scratch keeps the
-first call's contents), and the size limit rejected with a clear error."""
+first call's contents), the same under HIP graph capture and replay, and the
+size limit rejected with a clear error."""
 import numpy as np
 import pytest
 import torch
@@ -56,3 +57,44 @@ def test_noalloc_rejects_oversize(dev):
                     ops._stream())
     assert rc == 2
     assert "scratch" in lib().nsosx_last_error().decode()
+
+
+def test_noalloc_captured_in_graph(dev):
+    """The documented use: a noalloc call captured into a HIP graph (after one eager call on
+    the device, which looks the scratch address up) and replayed; every replay, with eager
+    work of other shapes on the same scratch in between, is bit-exact with the
+    caller-workspace entry."""
+    rng = np.random.default_rng(12)
+    k, n, m = 2048, 512, 64
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    packed, ws = ops.pack_ternary(w)
+    pk = torch.from_numpy(packed.view(np.int32)).to(dev)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).to(dev)
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    fwd = _noalloc()
+
+    def run():
+        return fwd(ops._p(x), ops._dt(x), ops._p(pk), ws, m, k, n, 8, 1, None, None, ops._p(y),
+                   ops._DT[torch.float32], ops._stream())
+    assert run() == 0, lib().nsosx_last_error().decode()  # eager first call on the device
+    torch.cuda.synchronize()
+    want = ops.bitnet_gemm_158bit_gpu(x, pk, ws, m, k, n, 8, None, None, rms_input=True,
+                                      out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            rc = run()
+    torch.cuda.current_stream().wait_stream(s)
+    assert rc == 0, lib().nsosx_last_error().decode()
+    other = torch.from_numpy(rng.standard_normal((300, k)).astype(np.float32)).to(dev)
+    for rep in range(4):
+        y.fill_(float("nan"))
+        # eager noalloc work of another shape leaves other contents in the scratch
+        _run_noalloc(other, pk, ws, n, True, None, None, torch.float32)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), f"replay {rep}"
