@@ -148,15 +148,17 @@ def bench_mamba2_decode(torch, dev, rows=1, reps=200):
             "graph_us_per_step": round(graph_us, 1)}
 
 
-def bench_mamba2_prefill(torch, dev, reps=5):
-    """Faithful Mamba-2 block forward (d_model 1024, 32 heads x 64, N 16, one A per head, conv 4,
-    f32 activations as in the reference) over config 4's 32 ragged sequences (T = 40796): the
-    ternary x / z projections, the fp32 B / C / dt projection, B/C conv, fused conv + scan,
-    gated norm and out_proj."""
+def bench_mamba2_prefill(torch, dev, reps=5, N=16):
+    """Faithful Mamba-2 block forward (d_model 1024, 32 heads x 64, d_state N, one A per head,
+    conv 4, f32 activations as in the reference) over config 4's 32 ragged sequences
+    (T = 40796): the ternary x / z projections, the fp32 B / C / dt projection, B/C conv, fused
+    conv + scan, gated norm and out_proj.  N = 64 is the reference model's default
+    mamba_d_state (include/nsos_config.h:147); its scan is timed alone as well, with
+    stream events around the block's scan launch."""
     from reimagined_amd import workloads
     from reimagined_amd.layers import Mamba2Block
     rng = np.random.default_rng(42)
-    d, H, P, N, G, K = 1024, 32, 64, 16, 1, 4
+    d, H, P, G, K = 1024, 32, 64, 1, 4
     inner, gs = H * P, G * N
     w = lambda n, k: rng.standard_normal((n, k)).astype(np.float32)
     params = {"w_x": w(inner, d), "w_z": w(inner, d), "w_B": w(gs, d) / 32,
@@ -180,7 +182,15 @@ def bench_mamba2_prefill(torch, dev, reps=5):
     b.record()
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / reps
-    return {"tokens": T, "ms": round(ms, 4), "tokens_per_s": round(T / (ms / 1e3), 1)}
+    out = {"d_state": N, "tokens": T, "ms": round(ms, 4), "tokens_per_s": round(T / (ms / 1e3), 1)}
+    # the scan stage alone, on the block's own projected inputs
+    from reimagined_amd import ops
+    res = blk.forward(u, cu)
+    scan = lambda: ops.conv_scan_fwd(res["x"], blk.conv_w[0], blk.conv_b[0], res["dt"],
+                                     blk.a_log, res["B"], res["C"], blk.d_skip, None, cu, H, P, N,
+                                     G, want_final=True)
+    out["scan_ms"] = round(_time_ms(torch, scan, reps), 4)
+    return out
 
 
 def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=32):
@@ -819,6 +829,8 @@ def main():
         ("moe_c5", "moe c5", lambda: bench_moe_c5(torch, dev)),
         ("decode_step_c5", "decode step", lambda: bench_decode_step(torch, dev)),
         ("mamba2_prefill", "mamba2 prefill", lambda: bench_mamba2_prefill(torch, dev)),
+        ("mamba2_prefill_d_state_64", "mamba2 prefill d_state 64",
+         lambda: bench_mamba2_prefill(torch, dev, N=64)),
         ("mamba2_decode_step", "mamba2 decode step", lambda: bench_mamba2_decode(torch, dev)),
         ("scan_shapes", "scan shapes", lambda: bench_scan_shapes(torch, dev)),
         ("linear_f32", "linear f32", lambda: bench_linear_f32(torch, dev)),

@@ -363,9 +363,11 @@ int nsosx_conv_scan_fwd(const void* x_raw, int64_t x_stride, const float* conv_w
  *     a chunk is exp of its summed exponents), and a second pass runs each
  *     chunk from its carried state, its causal conv window taken from the
  *     sequence's previous tokens.  For batches whose sequences x 16-channel
- *     blocks cannot fill the GPU (one long prefill).  Needs N <= 16, channels
- *     per group a multiple of 16, conv width <= 4.  Outputs equal the
- *     sequential scan to rounding (the carried states differ by a few ulp);
+ *     blocks cannot fill the GPU (one long prefill).  Needs channels per group
+ *     a multiple of 64 and conv width <= 8 (any N <= 64, the faithful block's
+ *     d_state 64 included), or, with N <= 16, a multiple of 16 and conv width
+ *     <= 4.  Outputs equal the sequential scan to rounding (the carried states
+ *     differ by a few ulp);
  *   - chunk_tokens == 0: never chunk; -1: chunk when sequences x (H*P/16) <
  *     2048 and the sequences are at least two chunks long (chunk size aiming
  *     at 8192 waves, at least 64 tokens).

@@ -101,7 +101,28 @@ __device__ __forceinline__ int scan_pick_sequence(const int32_t* cu, int num_seq
     return s_order[blockIdx.y];
 }
 
-template <int ADT, int SPL, bool GATE, bool CONV>
+// How a launch of the prefill scan kernels maps its work items onto the tokens.  Plain
+// launches leave every pointer NULL: item = sequence.  The time-chunked scan
+// runs the kernel over chunks of sequences (item = chunk):
+//   order      rank -> item (the longest-first order computed once per launch)
+//   seq_start  per item: first token of the item's sequence (the causal conv
+//              window at a chunk start holds the sequence's previous tokens)
+//   init_row   per item: row of init_state to start from (-1: zeros)
+//   state_row  per item: row of final_state to write (-1: none)
+//   sum_dl     LOCAL pass: per (item, channel) sum of delta over the item
+struct QuadPlan {
+    const int32_t* order;
+    const int32_t* seq_start;
+    const int32_t* init_row;
+    const int32_t* state_row;
+    float* sum_dl;
+};
+
+// PH: one A per head (the faithful Mamba-2 block): every state of a channel decays
+// alike, one exp per token.  LOCAL: the first pass of the time-chunked scan (the
+// recurrence only: each item's end state and sum of delta, no output).  The plan
+// fields are read as in scan_quad_kernel.
+template <int ADT, int SPL, bool GATE, bool CONV, bool PH = false, bool LOCAL = false>
 __global__ __launch_bounds__(256) void scan_fwd_kernel(
     const void* __restrict__ x, int64_t x_stride, const void* __restrict__ dt,
     const float* __restrict__ a_log, int a_per_state, const void* __restrict__ Bm,
@@ -109,7 +130,7 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
     int64_t z_stride, const int32_t* __restrict__ cu_seqlens, int num_seqs, int total_tokens,
     int H, int P, int N, int G, const float* __restrict__ conv_w, const float* __restrict__ conv_b,
     int W, const float* __restrict__ init_state, float* __restrict__ final_state,
-    void* __restrict__ y, const int32_t* __restrict__ order) {
+    void* __restrict__ y, QuadPlan plan) {
     constexpr int NPAD = 4 * SPL;
     constexpr int NRAW = CONV ? 8 + kMaxConvW - 1 : 8;
     constexpr int BCPT = (kScanTC * NPAD + 255) / 256;  // B/C elements per thread per chunk
@@ -123,8 +144,10 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
     const int D = H * P;
     const int GN = G * N;
     const int c0 = blockIdx.x * kScanCh;
-    const int seq = order ? order[blockIdx.y]
-                          : scan_pick_sequence(cu_seqlens, num_seqs, total_tokens, s_order);
+    const int seq = plan.order ? plan.order[blockIdx.y]
+                               : (plan.seq_start ? (int)blockIdx.y
+                                                 : scan_pick_sequence(cu_seqlens, num_seqs,
+                                                                      total_tokens, s_order));
     // a malformed cu_seqlens can only shorten a sequence, never address past T
     const int t0 = min(max(cu_seqlens[seq], 0), total_tokens);
     const int t1 = min(max(cu_seqlens[seq + 1], t0), total_tokens);
@@ -148,14 +171,20 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
     }
 
     float a2[SPL], st[SPL];
+    const int irow = plan.init_row ? plan.init_row[seq] : seq;
 #pragma unroll
     for (int i = 0; i < SPL; ++i) {
         const int n = q * SPL + i;
         const bool ok = n < N;
         const float al = a_per_state ? a_log[(int64_t)h * N + min(n, N - 1)] : a_log[h];
         a2[i] = ok ? a2_from_log(al) : 0.0f;
-        st[i] = (ok && init_state) ? init_state[((int64_t)seq * D + c) * N + n] : 0.0f;
+        st[i] = (ok && init_state && irow >= 0) ? init_state[((int64_t)irow * D + c) * N + n]
+                                                : 0.0f;
     }
+    float sdl = 0.0f;  // LOCAL: this lane's channel's sum of delta over the item
+    // first token the causal conv window may read: the sequence start (a time chunk that
+    // starts inside its sequence takes the sequence's previous raw x)
+    const int tw = plan.seq_start ? max(plan.seq_start[seq], 0) : t0;
 
     // next chunk's global inputs, loaded one chunk ahead of their use
     float raw[NRAW], dtv[8], zv[8], bcv[2][BCPT];
@@ -165,7 +194,7 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
 #pragma unroll
         for (int j = 0; j < NRAW; ++j) {
             const int tr = tb + rbase + j - (CONV ? W - 1 : 0);
-            const bool ok = (!CONV || j < 8 + W - 1) && tr >= t0 && tr < tb + tcn;
+            const bool ok = (!CONV || j < 8 + W - 1) && tr >= (CONV ? tw : t0) && tr < tb + tcn;
             raw[j] = ok ? load_act<ADT>(x, (int64_t)tr * x_stride + sch) : 0.0f;
         }
 #pragma unroll
@@ -235,17 +264,21 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
 #pragma unroll
                 for (int i = 0; i < SPL; ++i) {
                     bq[i] = s_bc[r][q * SPL + i];
-                    cq[i] = s_bc[r][NPAD + q * SPL + i];
+                    cq[i] = LOCAL ? 0.0f : s_bc[r][NPAD + q * SPL + i];
                 }
+                // (PH: padded states carry B = C = 0, so their shared decay is harmless)
+                const float aph = PH ? __builtin_amdgcn_exp2f(dd.x * a2[0]) : 0.0f;
                 float p = 0.0f;
 #pragma unroll
                 for (int i = 0; i < SPL; ++i) {
-                    const float a = __builtin_amdgcn_exp2f(dd.x * a2[i]);
+                    const float a = PH ? aph : __builtin_amdgcn_exp2f(dd.x * a2[i]);
                     st[i] = __fmaf_rn(a, st[i], dd.y * bq[i]);
-                    p = __fmaf_rn(st[i], cq[i], p);
+                    if constexpr (!LOCAL) p = __fmaf_rn(st[i], cq[i], p);
                 }
                 part[u] = p;
+                if constexpr (LOCAL) sdl += dd.x;
             }
+            if constexpr (LOCAL) continue;
             // lanes q: after xor-2 exchange keep tokens {0,1} (q<2) or {2,3};
             // after xor-1 exchange keep one token: lane q owns token kq.
             const bool hi2 = (q & 2) != 0;
@@ -267,7 +300,7 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int r = 8 * rg + i;
-            if (r < tc) {
+            if (!LOCAL && r < tc) {
                 const int64_t t = tb + r;
                 float out = __fmaf_rn(sdsk, s_x[r][sc], s_y[r][sc]);
                 if (GATE) out = out * silu_fast(zcur[i]);
@@ -276,11 +309,13 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
         }
         __syncthreads();
     }
-    if (final_state) {
+    if (LOCAL && q == 0) plan.sum_dl[(int64_t)seq * D + c] = sdl;
+    const int frow = plan.state_row ? plan.state_row[seq] : seq;
+    if (final_state && frow >= 0) {
 #pragma unroll
         for (int i = 0; i < SPL; ++i) {
             const int n = q * SPL + i;
-            if (n < N) final_state[((int64_t)seq * D + c) * N + n] = st[i];
+            if (n < N) final_state[((int64_t)frow * D + c) * N + n] = st[i];
         }
     }
 }
@@ -344,22 +379,6 @@ __device__ __forceinline__ int quad_pick_sequence(const int32_t* cu, int num_seq
     return *s_pick;
 }
 
-// How a launch of the quad kernel maps its work items onto the tokens.  Plain
-// launches leave every pointer NULL: item = sequence.  The time-chunked scan
-// runs the kernel over chunks of sequences (item = chunk):
-//   order      rank -> item (the longest-first order computed once per launch)
-//   seq_start  per item: first token of the item's sequence (the causal conv
-//              window at a chunk start holds the sequence's previous tokens)
-//   init_row   per item: row of init_state to start from (-1: zeros)
-//   state_row  per item: row of final_state to write (-1: none)
-//   sum_dl     LOCAL pass: per (item, channel) sum of delta over the item
-struct QuadPlan {
-    const int32_t* order;
-    const int32_t* seq_start;
-    const int32_t* init_row;
-    const int32_t* state_row;
-    float* sum_dl;
-};
 
 // softplus_fast() without branches: the three regimes are formed and selected.
 __device__ __forceinline__ float softplus_sel(float v) {
@@ -1168,21 +1187,31 @@ static int scan_fwd_launch(const void* x, int64_t x_stride, const void* dt, cons
 #undef NSOSX_QSCAN_C
 #undef NSOSX_QSCAN
 #undef NSOSX_QK
-    } else if (local || plan.seq_start) {
-        return fail(NSOSX_ERR_INVALID, "selective_scan_fwd: the time-chunked scan needs N <= 16, "
-                                       "channels per group a multiple of 16, conv width <= 4");
     } else if (per_group % kScanCh == 0) {
+        // the LDS-staged form: any N <= 64, conv width <= 8, sequential or time-chunked
         const dim3 grid(Dm / kScanCh, num_seqs), block(256);
         const int spl = N <= 4 ? 1 : N <= 8 ? 2 : N <= 16 ? 4 : N <= 32 ? 8 : 16;
+        // one A per head above N = 16 (the faithful Mamba-2 block at the reference's
+        // d_state 64): one decay exp per token
+        const bool ph = !a_per_state && spl >= 8;
+#define NSOSX_SK(ADT, SPL, GATE, CONV, PH, LOC)                                                 \
+    hipLaunchKernelGGL((scan_fwd_kernel<ADT, SPL, GATE, CONV, PH, LOC>), grid, block, 0, st, x,   \
+                       x_stride, dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens,        \
+                       num_seqs, total_tokens, H, P, N, G, conv_w, conv_b, conv_width,            \
+                       initial_state, final_state, y, plan);
 #define NSOSX_SCAN(ADT, SPL, GATE, CONV)                                                        \
-    hipLaunchKernelGGL((scan_fwd_kernel<ADT, SPL, GATE, CONV>), grid, block, 0, st, x, x_stride, \
-                       dt, A_log, a_per_state, B, C, D, z, z_stride, cu_seqlens, num_seqs,      \
-                       total_tokens, H, P, N, G, conv_w, conv_b, conv_width, initial_state,     \
-                       final_state, y, plan.order);
+    if (local) {                                                                                \
+        if (SPL >= 8 && ph) { NSOSX_SK(ADT, SPL, false, CONV, SPL >= 8, true) }                 \
+        else { NSOSX_SK(ADT, SPL, false, CONV, false, true) }                                   \
+    } else if (SPL >= 8 && ph) {                                                                \
+        NSOSX_SK(ADT, SPL, GATE, CONV, SPL >= 8, false)                                         \
+    } else {                                                                                    \
+        NSOSX_SK(ADT, SPL, GATE, CONV, false, false)                                            \
+    }
 #define NSOSX_SCAN_C(ADT, SPL, GATE) \
     if (conv) { NSOSX_SCAN(ADT, SPL, GATE, true) } else { NSOSX_SCAN(ADT, SPL, GATE, false) }
 #define NSOSX_SCAN_G(ADT, SPL) \
-    if (z) { NSOSX_SCAN_C(ADT, SPL, true) } else { NSOSX_SCAN_C(ADT, SPL, false) }
+    if (z && !local) { NSOSX_SCAN_C(ADT, SPL, true) } else { NSOSX_SCAN_C(ADT, SPL, false) }
 #define NSOSX_SCAN_S(ADT)                          \
     switch (spl) {                                 \
         case 1: NSOSX_SCAN_G(ADT, 1) break;        \
@@ -1196,6 +1225,11 @@ static int scan_fwd_launch(const void* x, int64_t x_stride, const void* dt, cons
 #undef NSOSX_SCAN_G
 #undef NSOSX_SCAN_C
 #undef NSOSX_SCAN
+#undef NSOSX_SK
+    } else if (local || plan.seq_start) {
+        return fail(NSOSX_ERR_INVALID, "selective_scan_fwd: the time-chunked scan needs channels "
+                                       "per group a multiple of 64 (or of 16 with N <= 16 and "
+                                       "conv width <= 4)");
     } else {
         const int64_t lanes = (int64_t)num_seqs * Dm;
         const dim3 grid((unsigned)((lanes + 63) / 64)), block(64);
@@ -1381,7 +1415,9 @@ static int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
 static int resolve_chunk(int S, int T, int H, int P, int N, int chunk_tokens) {
     if (chunk_tokens >= 0) return chunk_tokens;
     const int D = H * P;
-    if (N > 16 || D % kQuadCh != 0 || S <= 0 || T <= 0) return 0;
+    if (S <= 0 || T <= 0 || D % kQuadCh != 0 || (N > 16 && D % kScanCh != 0)) return 0;
+    // waves per sequence: 16 channels per wave in either form (the quad kernel's one-wave
+    // workgroups, the LDS-staged form's four-wave workgroups of 64 channels)
     const int64_t blocks = D / kQuadCh;
     if ((int64_t)S * blocks >= 2048) return 0;
     int64_t c = ((int64_t)T * blocks + 8191) / 8192;
@@ -1469,9 +1505,13 @@ extern "C" int nsosx_scan_fwd_planned(const void* x, int64_t x_stride, const flo
                                cu_seqlens, num_seqs, total_tokens, H, P, N, G, act_dtype, conv_w,
                                conv_b, conv_width, initial_state, final_state, y, stream, plan);
     }
-    if (N > 16 || (Dm / G) % kQuadCh != 0 || (conv_w && conv_width > kQuadMaxW))
-        return fail(NSOSX_ERR_INVALID, "scan_fwd_planned: the time-chunked scan needs N <= 16, "
-                                       "channels per group a multiple of 16, conv width <= 4");
+    const int pg = Dm / G;
+    const bool quad_form = N <= 16 && pg % kQuadCh == 0 && (!conv_w || conv_width <= kQuadMaxW);
+    const bool lds_form = pg % kScanCh == 0 && (!conv_w || conv_width <= kMaxConvW);
+    if (!quad_form && !lds_form)
+        return fail(NSOSX_ERR_INVALID, "scan_fwd_planned: the time-chunked scan needs channels "
+                                       "per group a multiple of 64 (or of 16 with N <= 16 and "
+                                       "conv width <= 4)");
     if ((int64_t)ws.maxc * Dm * N >= ((int64_t)1 << 31) || ws.maxc > 65535)
         return fail(NSOSX_ERR_OVERFLOW, "scan_fwd_planned: too many chunks (at most 65535 and "
                                         "chunks * H*P * N < 2^31): use longer chunks");

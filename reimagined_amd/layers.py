@@ -464,18 +464,21 @@ class Mamba2Block:
         return [xv, z, sens[:, :g], sens[:, g:2 * g], dt.contiguous() if contiguous_dt else dt]
 
     def forward(self, u: torch.Tensor, cu_seqlens: torch.Tensor, initial_state=None,
-                final_state=None, keep_normed: bool = False) -> dict:
+                final_state=None, keep_normed: bool = False, chunk_tokens: int = -1) -> dict:
         """u [T, d_model] over the packed ragged batch cu_seqlens (int32 [S+1]).
 
         The gated norm and out_proj's input quantization run as one pass
-        (nsosx_rmsnorm_gated_quant); the normed rows are stored only with keep_normed."""
+        (nsosx_rmsnorm_gated_quant); the normed rows are stored only with keep_normed.
+        chunk_tokens: the scan's time chunking (-1 the library's choice, 0 never, > 0 that
+        chunk length)."""
         ops._dev(cu_seqlens, "cu_seqlens", torch.int32)
         xv, z, Bv, Cv, dt = self._project(u)
         Bc = ops.conv1d_causal(Bv, self.conv_w[1], cu_seqlens, self.conv_b[1], True)
         Cc = ops.conv1d_causal(Cv, self.conv_w[2], cu_seqlens, self.conv_b[2], True)
         y, fin = ops.conv_scan_fwd(xv, self.conv_w[0], self.conv_b[0], dt, self.a_log, Bc, Cc,
                                    self.d_skip, None, cu_seqlens, self.H, self.P, self.N, self.G,
-                                   initial_state=initial_state, want_final=True)
+                                   initial_state=initial_state, want_final=True,
+                                   chunk_tokens=chunk_tokens)
         if final_state is not None:
             final_state.copy_(fin)
         q, s, normed = ops.rmsnorm_gated_quant(y, z, self.norm_w, eps=self.eps,

@@ -13,12 +13,17 @@ needs) and records that library's outputs for seeded and constructed inputs:
                      the packed STE backward
   mamba2_ref.npz     Mamba2SSD::forward on the faithful Mamba-2 path, the
                      non-sensitive projections packed ternary
+  mamba2_n64_ref.npz the same at the reference's default state width
+                     (mamba_d_state 64) with head_dim 64 and two groups
 
 Inputs are stored as float16-representable values (cast to float32 before
 use) so the fixtures stay small.  The fixtures are data (inputs and expected
 outputs); the GPU box and CPU tests read them without the reference.
 
-    python tests/golden/gen_golden.py
+    python tests/golden/gen_golden.py [file.npz ...]
+
+With file names, only those fixtures are written (the others and their
+MANIFEST lines are kept as they are).
 """
 from __future__ import annotations
 
@@ -51,7 +56,7 @@ def tie_rows() -> np.ndarray:
     return np.stack([base, alt])
 
 
-def main() -> None:
+def main(only=()) -> None:
     oracle.build()
     if not oracle.ref_available():
         raise SystemExit("oracle/_ref not built: the reference tree is not mounted here")
@@ -73,17 +78,25 @@ def main() -> None:
     w = rng.integers(-1, 2, size=(6, 1000)).astype(np.int8)
     out["rowsum__w"] = w
     out["rowsum__sums"] = np.array([oracle.ref_row_sum_i8(r) for r in w], np.int32)
-    files = {"quant_ref.npz": out, "tensor_ref.npz": tensor_cases(),
-             "bitlinear_ref.npz": bitlinear_cases(), "mamba2_ref.npz": mamba2_cases()}
-    lines = []
-    for name, data in files.items():
+    makers = {"quant_ref.npz": lambda: out, "tensor_ref.npz": tensor_cases,
+              "bitlinear_ref.npz": bitlinear_cases, "mamba2_ref.npz": mamba2_cases,
+              "mamba2_n64_ref.npz": mamba2_n64_cases}
+    unknown = set(only) - set(makers)
+    if unknown:
+        raise SystemExit(f"unknown fixtures: {sorted(unknown)}")
+    manifest = os.path.join(HERE, "MANIFEST.sha256")
+    digests = {}
+    if only and os.path.exists(manifest):
+        digests = {name: d for d, name in (l.split() for l in open(manifest) if l.strip())}
+    for name, make in makers.items():
+        if only and name not in only:
+            continue
         path = os.path.join(HERE, name)
-        np.savez_compressed(path, **data)
-        digest = hashlib.sha256(open(path, "rb").read()).hexdigest()
-        lines.append(f"{digest}  {name}\n")
-        print(f"wrote {path} sha256={digest}")
-    with open(os.path.join(HERE, "MANIFEST.sha256"), "w") as fh:
-        fh.writelines(lines)
+        np.savez_compressed(path, **make())
+        digests[name] = hashlib.sha256(open(path, "rb").read()).hexdigest()
+        print(f"wrote {path} sha256={digests[name]}")
+    with open(manifest, "w") as fh:
+        fh.writelines(f"{digests[n]}  {n}\n" for n in makers if n in digests)
 
 
 def _h(rng, shape, scale=1.0, loc=0.0) -> np.ndarray:
@@ -157,6 +170,28 @@ def mamba2_cases() -> dict:
     return out
 
 
+def mamba2_n64_cases() -> dict:
+    """The faithful block at d_state 64 (nsos_config.h's mamba_d_state default), head_dim
+    64, two B / C groups, conv 4: two sequences of 41 tokens."""
+    rng = np.random.default_rng(20261205)
+    d, H, P, N, G, K = 128, 4, 64, 64, 2, 4
+    inner, gs = H * P, G * N
+    p = {"w_x": _h(rng, (inner, d), 0.1), "w_z": _h(rng, (inner, d), 0.1),
+         "w_B": _h(rng, (gs, d), 0.1), "w_C": _h(rng, (gs, d), 0.1),
+         "w_dt": _h(rng, (H, d), 0.1), "dt_bias": _h(rng, (H,), 1.0, -2.0),
+         "w_out": _h(rng, (d, inner), 0.1), "conv_w": _h(rng, (inner + 2 * gs, K), 0.5),
+         "conv_b": _h(rng, (inner + 2 * gs,), 0.1), "a_log": _h(rng, (H,)),
+         "d_skip": _h(rng, (H,)), "norm_w": rng.uniform(0.5, 1.5, inner).astype(np.float16)}
+    u = _h(rng, (2, 41, d))
+    f32 = {k: v.astype(np.float32) for k, v in p.items()}
+    f32.update(H=H, P=P, N=N, G=G)
+    out = dict(p)
+    out["shape"] = np.array([H, P, N, G], np.int32)
+    out["u"] = u
+    out["out_packed"] = ref.mamba2_faithful_forward(f32, u.astype(np.float32), packed=True)
+    return out
+
+
 def bitlinear_cases() -> dict:
     rng = np.random.default_rng(20261203)
     out = {}
@@ -193,4 +228,4 @@ def bitlinear_cases() -> dict:
 
 
 if __name__ == "__main__":
-    main()
+    main(tuple(sys.argv[1:]))

@@ -47,9 +47,12 @@ def _np(t):
     return t.float().cpu().numpy()
 
 
-def test_mamba2_block_prefill_matches_oracle(dev, orc):
-    rng = np.random.default_rng(3)
-    p = _params(rng)
+@pytest.mark.parametrize("P,N,chunk", [(16, 16, -1), (64, 64, 0), (64, 64, 8), (64, 32, 4)])
+def test_mamba2_block_prefill_matches_oracle(dev, orc, P, N, chunk):
+    """Stage by stage against the oracle, at d_state 16 (the quad scan) and at 32 / 64 (the
+    LDS-staged scan, sequential and time-chunked)."""
+    rng = np.random.default_rng(3 + N + P + chunk)
+    p = _params(rng, P=P, N=N)
     H, P, N, G = p["H"], p["P"], p["N"], p["G"]
     inner, gs = H * P, G * N
     blk = Mamba2Block(p, dev)
@@ -57,7 +60,8 @@ def test_mamba2_block_prefill_matches_oracle(dev, orc):
     cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
     T = int(cu[-1])
     u = rng.standard_normal((T, 64)).astype(np.float32)
-    res = blk.forward(torch.from_numpy(u).to(dev), torch.from_numpy(cu).to(dev), keep_normed=True)
+    res = blk.forward(torch.from_numpy(u).to(dev), torch.from_numpy(cu).to(dev), keep_normed=True,
+                      chunk_tokens=chunk)
     # x, z: ternary exact-linear (no RMS_PERI, no magnitude), bit-exact
     for key, wk in (("x", "w_x"), ("z", "w_z")):
         pk, ws, _ = orc.pack_weights(p[wk])
@@ -146,6 +150,32 @@ def test_mamba2_block_matches_reference_build(dev):
     blk = Mamba2Block(p, dev)
     cu = torch.tensor([0, s, 2 * s], dtype=torch.int32, device=dev)
     got = _np(blk.forward(torch.from_numpy(u.reshape(b * s, d)).to(dev), cu)["out"]).reshape(u.shape)
+    want = g["out_packed"]
+    scale = np.abs(want).max()
+    err = np.abs(got - want)
+    assert err.max() <= scale / 127, (err.max(), scale)
+    assert err.mean() <= 1e-3 * scale, (err.mean(), scale)
+
+
+@pytest.mark.parametrize("chunk", [0, 8])
+def test_mamba2_block_matches_reference_build_d_state_64(dev, chunk):
+    """The block at the reference's default d_state 64 (tests/golden/mamba2_n64_ref.npz:
+    d_model 128, 4 heads of 64, 2 groups, two sequences of 41 tokens) against
+    Mamba2SSD::forward from a reference build, through the sequential scan (chunk 0) and the
+    time-chunked one (chunks of 8 tokens: carried states and conv windows across chunk
+    boundaries), with the bound of the d_state 16 case above."""
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "mamba2_n64_ref.npz"),
+                allow_pickle=False)
+    p = {k: g[k].astype(np.float32) for k in g.files if not k.startswith(("u", "out", "shape"))}
+    H, P, N, G = (int(v) for v in g["shape"])
+    p.update(H=H, P=P, N=N, G=G)
+    u = g["u"].astype(np.float32)
+    b, s, d = u.shape
+    blk = Mamba2Block(p, dev)
+    cu = torch.tensor([0, s, 2 * s], dtype=torch.int32, device=dev)
+    res = blk.forward(torch.from_numpy(u.reshape(b * s, d)).to(dev), cu, chunk_tokens=chunk)
+    got = _np(res["out"]).reshape(u.shape)
     want = g["out_packed"]
     scale = np.abs(want).max()
     err = np.abs(got - want)

@@ -322,6 +322,71 @@ def test_chunked_scan_matches_oracle(dev, orc, conv, chunk, per_state, P, gate, 
     np.testing.assert_allclose(fin, fin0, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("chunk", [4, 37, 200])
+@pytest.mark.parametrize("N,per_state,conv_w", [(64, False, 4), (64, True, 0), (32, False, 7),
+                                                 (32, True, 4), (40, False, 0)])
+def test_chunked_scan_wide_state_matches_oracle(dev, orc, chunk, N, per_state, conv_w):
+    """The time-chunked scan above d_state 16 (the LDS-staged form): the faithful Mamba-2
+    block's one A per head at the reference's default d_state 64 (src/include/nsos_config.h
+    mamba_d_state), d_state 32, an N that is not a multiple of 16 (40), a conv window of 7
+    that crosses several 4-token chunk boundaries, two groups of 64 channels: against the
+    oracle within the fp32 bound and against the unchunked scan to 1e-5, final states
+    included."""
+    rng = np.random.default_rng(chunk * 13 + N + int(per_state) + conv_w)
+    H, P, G = 2, 64, 2
+    lengths = [300, 0, 7, 64, 129, 1]
+    cu = _cu(lengths)
+    T = int(cu[-1])
+    inp = _inputs(rng, T, H, P, N, G, per_state)
+    a = _scan_args(dev, inp, cu, torch.float32, True)
+    st0 = rng.normal(0, 0.1, (len(lengths), H * P, N)).astype(np.float32)
+    if conv_w:
+        w = (rng.standard_normal((H * P, conv_w)) * 0.5).astype(np.float32)
+        b = (rng.standard_normal(H * P) * 0.1).astype(np.float32)
+        run = lambda ck: ops.conv_scan_fwd(_t(dev, inp["x"]), _t(dev, w), _t(dev, b), a["dt"],
+                                           a["a_log"], a["B"], a["C"], a["D"], a["z"],
+                                           a["cu_seqlens"], H, P, N, G,
+                                           initial_state=_t(dev, st0), chunk_tokens=ck)
+        xc = orc.conv1d_causal(inp["x"], w, cu, bias=b, silu_act=True)
+    else:
+        run = lambda ck: ops.selective_scan_fwd(_t(dev, inp["x"]), a["dt"], a["a_log"], a["B"],
+                                                a["C"], a["D"], a["z"], a["cu_seqlens"], H, P, N,
+                                                G, initial_state=_t(dev, st0), chunk_tokens=ck)
+        xc = inp["x"]
+    y, fin = (v.cpu().numpy() for v in run(chunk))
+    y0, fin0 = (v.cpu().numpy() for v in run(0))
+    wy, wfin = orc.selective_scan(xc, inp["dt"], inp["a_log"], inp["B"], inp["C"], inp["D"],
+                                  inp["z"], cu, H, P, N, G, initial_state=st0)
+    np.testing.assert_allclose(y, wy, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(fin, wfin, rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(y, y0, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(fin, fin0, rtol=1e-5, atol=1e-6)
+
+
+def test_chunked_scan_auto_long_prefill_d_state_64(dev, orc):
+    """One 4096-token prefill of the faithful block's shape at d_state 64 (8 heads of 64,
+    one A per head, bf16 I/O): the library chunks it by itself; bf16 outputs within the
+    bf16 bound, fp32 final state within 1e-4."""
+    rng = np.random.default_rng(102)
+    H, P, N, G = 8, 64, 64, 1
+    cu = _cu([4096])
+    inp = _inputs(rng, 4096, H, P, N, G, per_state=False)
+    rd = lambda v: torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+    w = (rng.standard_normal((H * P, 4)) * 0.5).astype(np.float32)
+    a = _scan_args(dev, inp, cu, torch.bfloat16, True)
+    assert int(ops.lib().nsosx_scan_fwd_workspace(1, 4096, H, P, N, -1)) > \
+        int(ops.lib().nsosx_scan_fwd_workspace(1, 4096, H, P, N, 0))   # auto picks chunking
+    y, fin = ops.conv_scan_fwd(_t(dev, inp["x"], torch.bfloat16), _t(dev, w), None, a["dt"],
+                               a["a_log"], a["B"], a["C"], a["D"], a["z"], a["cu_seqlens"],
+                               H, P, N, G)
+    xc = orc.conv1d_causal(rd(inp["x"]), w, cu, silu_act=True)
+    wy, wfin = orc.selective_scan(xc, rd(inp["dt"]), inp["a_log"], rd(inp["B"]), rd(inp["C"]),
+                                  inp["D"], rd(inp["z"]), cu, H, P, N, G)
+    scale = np.abs(wy).max()
+    np.testing.assert_allclose(y.float().cpu().numpy(), wy, rtol=2e-2, atol=2e-2 * scale / 64)
+    np.testing.assert_allclose(fin.cpu().numpy(), wfin, rtol=1e-4, atol=1e-5)
+
+
 def test_chunked_scan_auto_long_prefill_bf16(dev, orc):
     """One 4096-token sequence over 512 channels: too few waves unchunked, so the library
     chunks it by itself; bf16 I/O within the bf16 bound, fp32 final state within 1e-4."""

@@ -210,3 +210,17 @@ def test_mamba2_chain_matches_reference_build(orc):
     assert np.abs(got - want).max() <= tol, np.abs(got - want).max()
     assert np.abs(_mamba2_chain(orc, g, out_rms=True) - want).max() > 100 * tol
     assert np.abs(_mamba2_chain(orc, g, dt_bias=False) - want).max() > 100 * tol
+
+
+def test_mamba2_chain_matches_reference_build_d_state_64(orc):
+    """tests/golden/mamba2_n64_ref.npz: Mamba2SSD::forward from a reference build at the
+    reference's default state width (d_state 64; d_model 128, 4 heads of 64, 2 groups,
+    conv 4, two sequences of 41 tokens), with the same bound and planted mistakes."""
+    g = _load("mamba2_n64_ref.npz")
+    assert tuple(int(v) for v in g["shape"]) == (4, 64, 64, 2)
+    want = g["out_packed"]
+    tol = 1e-5 * np.abs(want).max()
+    got = _mamba2_chain(orc, g)
+    assert np.abs(got - want).max() <= tol, np.abs(got - want).max()
+    assert np.abs(_mamba2_chain(orc, g, out_rms=True) - want).max() > 100 * tol
+    assert np.abs(_mamba2_chain(orc, g, dt_bias=False) - want).max() > 100 * tol
