@@ -45,11 +45,30 @@ typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 // ML: the weights are in the MFMA layout (nsosx_pack_mfma_layout): each word decodes by
 // shift and mask into natural k order (64 x the values, unpack_word_mfma), so the
 // activation fragments stay in natural order and the sums are shifted back by 6.
-template <int MT, int LT, int YDT, bool ACC_OUT, bool SQRELU, bool VEC4, bool ML = false>
+// 4 x 4 transpose of one dword per lane across the four 16-lane rows: lane row g
+// holds slots u = 0..3 (x, y, z, w), and comes out holding slot g of rows u = 0..3.
+__device__ __forceinline__ void transpose_rows4(uint32_t (&v)[4]) {
+    const auto p02 = __builtin_amdgcn_permlane32_swap(v[0], v[2], false, false);
+    const auto p13 = __builtin_amdgcn_permlane32_swap(v[1], v[3], false, false);
+    const auto p01 = __builtin_amdgcn_permlane16_swap(p02[0], p13[0], false, false);
+    const auto p23 = __builtin_amdgcn_permlane16_swap(p02[1], p13[1], false, false);
+    v[0] = p01[0]; v[1] = p01[1]; v[2] = p23[0]; v[3] = p23[1];
+}
+
+// RUN: tiles a wave takes back to back.  RUN = 1: tile ti of a wave is wave_id + ti *
+// num_waves, two per output batch.  RUN = 4 (N % 16 == 0 and at least one run per wave):
+// runs of 4 consecutive tiles (run i of a wave is wave_id + i * num_waves), one output
+// batch per run; the run's outputs are transposed across the four 16-lane rows so that
+// lane (g, li) holds tile g's 16 outputs of token li, and the four lanes of a token
+// store one whole 128-byte line of its bf16 output row (two lines for f32) where the
+// strided order stores 32-byte pieces of 16 rows.
+template <int MT, int LT, int YDT, bool ACC_OUT, bool SQRELU, bool VEC4, bool ML = false,
+          int RUN = 1>
 __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t* __restrict__ q,
                                             const float* __restrict__ act_scale, int M, void* y,
                                             int32_t* acc_out, int wave_id, int num_waves,
                                             char* lds) {
+    static_assert(RUN == 1 || (RUN % 4 == 0 && VEC4), "runs of tiles need whole 16-output tiles");
     constexpr int Q = 4 * LT;                       // words per lane per tile (MFMA steps)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -75,8 +94,11 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
     }
     __syncthreads();
     const int tiles = (pb.N + 15) >> 4;
-    if (wave_id >= tiles) return;
-    const int my_tiles = (tiles - 1 - wave_id) / num_waves + 1;
+    const int runs = (tiles + RUN - 1) / RUN;
+    if (wave_id >= runs) return;
+    const int my_tiles = ((runs - 1 - wave_id) / num_waves + 1) * RUN;
+    // the wave's ti-th tile (runs of RUN consecutive tiles, RUN = 1: strided tiles)
+    auto tile_of = [&](int ti) { return (wave_id + (ti / RUN) * num_waves) * RUN + ti % RUN; };
     // A tile's 16 rows are one contiguous block of 16 * K / 4 bytes.  The wave
     // reads it in LT loads of 1 KB (lane l: bytes 1024 j + 16 l), so every load
     // instruction covers eight whole 128-byte lines, and passes it through its own
@@ -89,7 +111,7 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
     char* stage = lds + MT * pb.K * 16 + (tid >> 6) * 16 * RB;
     const int64_t last_word = (int64_t)pb.N * W16 - 4;
     auto tile_src = [&](int ti) {
-        const int tile = wave_id + min(ti, my_tiles - 1) * num_waves;
+        const int tile = min(tile_of(min(ti, my_tiles - 1)), tiles - 1);
         return (int64_t)tile * 16 * W16 + 4 * lane;
     };
     auto load_piece = [&](int64_t base, int j) {
@@ -111,7 +133,7 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
     const bool has_mag = pb.mag != nullptr, has_bias = pb.bias != nullptr;
     const __amdgpu_buffer_rsrc_t rmag = make_rsrc(pb.mag, has_mag ? pb.N * 4u : 0u);
     const __amdgpu_buffer_rsrc_t rbias = make_rsrc(pb.bias, has_bias ? pb.N * 4u : 0u);
-    auto tile_n0 = [&](int ti) { return (wave_id + ti * num_waves) * 16 + 4 * g; };
+    auto tile_n0 = [&](int ti) { return tile_of(ti) * 16 + 4 * g; };
     auto load_affine = [&](int ti, float (&mg)[4], float (&bs)[4]) {
         const uint32_t off = static_cast<uint32_t>(tile_n0(min(ti, my_tiles - 1))) * 4u;
 #pragma unroll
@@ -146,10 +168,13 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
     // tile's wait for its weights; per batch it is one in kSkBatch.  The batch is
     // unrolled (straight-line, exact wait counts); tiles past the wave's last compute on
     // clamped loads and store nothing.
-    constexpr int kSkBatch = 2;
+    constexpr int kSkBatch = RUN == 1 ? 2 : RUN;
+    // bf16 outputs of a run are kept as packed pairs (outputs 4 g + {0, 1}, 4 g + {2, 3})
+    constexpr bool kPack = RUN > 1 && YDT == NSOSX_BF16;
     for (int t0 = 0; t0 < my_tiles; t0 += kSkBatch) {
         float vb[kSkBatch][MT][4];
         int ab[kSkBatch][MT][4];
+        uint32_t pk[kSkBatch][MT][2];
 #pragma unroll
         for (int u = 0; u < kSkBatch; ++u) {
             const int ti = t0 + u;
@@ -220,12 +245,78 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
                     vb[u][mt][r] = v;
                     ab[u][mt][r] = av[r];
                 }
+                if constexpr (kPack) {
+                    pk[u][mt][0] = pack_bf16x2(vb[u][mt][0], vb[u][mt][1]);
+                    pk[u][mt][1] = pack_bf16x2(vb[u][mt][2], vb[u][mt][3]);
+                }
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 mg_cur[r] = mg_nxt[r];
                 bs_cur[r] = bs_nxt[r];
             }
+        }
+        if constexpr (RUN > 1) {
+#pragma unroll
+            for (int qd = 0; qd < RUN / 4; ++qd) {
+            // lane (g, li): tile t0 + 4 qd + g of the run, token mt * 16 + li, all 16 outputs
+            const int tile = tile_of(t0 + 4 * qd + g);
+            const int n0 = tile * 16;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int m = mt * 16 + li;
+                const bool ok = tile < tiles && m < M;
+                const uint32_t e = static_cast<uint32_t>(m * pb.N + n0);
+                if (ACC_OUT) {
+                    uint32_t c[4][4];  // c[r][u]: output 4 u + r of the lane's tile
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+                            c[r][u] = static_cast<uint32_t>(ab[4 * qd + u][mt][r]);
+                        transpose_rows4(c[r]);
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            v4i{(int)c[0][u], (int)c[1][u], (int)c[2][u], (int)c[3][u]}, racc,
+                            ok ? (e + 4 * u) * 4u : 0x80000000u, 0, 0);
+                }
+                if (y) {
+                    if constexpr (YDT == NSOSX_F32) {
+                        uint32_t c[4][4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                            for (int u = 0; u < 4; ++u)
+                                c[r][u] = __float_as_uint(vb[4 * qd + u][mt][r]);
+                            transpose_rows4(c[r]);
+                        }
+#pragma unroll
+                        for (int u = 0; u < 4; ++u)
+                            __builtin_amdgcn_raw_buffer_store_b128(
+                                v4i{(int)c[0][u], (int)c[1][u], (int)c[2][u], (int)c[3][u]}, ry,
+                                ok ? (e + 4 * u) * 4u : 0x80000000u, 0, 0);
+                    } else {
+                        uint32_t lo[4], hi[4];  // outputs 4 u + {0, 1} and 4 u + {2, 3}
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            lo[u] = pk[4 * qd + u][mt][0];
+                            hi[u] = pk[4 * qd + u][mt][1];
+                        }
+                        transpose_rows4(lo);
+                        transpose_rows4(hi);
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+                            __builtin_amdgcn_raw_buffer_store_b128(
+                                v4i{(int)lo[2 * h], (int)hi[2 * h], (int)lo[2 * h + 1],
+                                    (int)hi[2 * h + 1]},
+                                ry, ok ? (e + 8 * h) * 2u : 0x80000000u, 0, 0);
+                    }
+                }
+            }
+            }
+            continue;
         }
 #pragma unroll
         for (int u = 0; u < kSkBatch; ++u) {
@@ -319,7 +410,15 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     // wave-uniform (readfirstlane): the tile loops then branch on scalars, with exact
     // memory wait counts
     const int wave_id = __builtin_amdgcn_readfirstlane(blockIdx.x * NW + (threadIdx.x >> 6));
-    if ((pb.N & 3) == 0)
+    const int num_waves = gridDim.x * NW;
+    // runs of 4 consecutive tiles at 9-16 token rows (one m tile), where every wave gets
+    // one: whole-line stores per token row (M = 16 at K = 2048: 0.63 -> 0.66 of HBM; at 8
+    // rows or fewer the stores are cheap and the strided order streams the weights
+    // better; at two m tiles, or with the int32 sums out, the run's registers spill)
+    if (MT == 1 && !ACC_OUT && M > 8 && (pb.N & 15) == 0 && ((pb.N >> 4) + 3) / 4 >= num_waves)
+        skinny_body<MT, LT, YDT, ACC_OUT, false, true, ML, MT == 1 ? 4 : 1>(
+            pb, q, act_scale, M, y, acc_out, wave_id, num_waves, lds_sk);
+    else if ((pb.N & 3) == 0)
         skinny_body<MT, LT, YDT, ACC_OUT, false, true, ML>(pb, q, act_scale, M, y, acc_out,
                                                            wave_id, gridDim.x * NW, lds_sk);
     else

@@ -121,6 +121,43 @@ def test_skinny_mfma_bit_exact(dev, orc, m, n, k):
     _gemm_case(dev, orc, m, n, k, path=2, mag=(m % 2 == 1), bias=(n % 2 == 0))
 
 
+@pytest.mark.parametrize("m,k", [(9, 1024), (12, 2048), (16, 2048)])
+@pytest.mark.parametrize("ydt", [torch.bfloat16, torch.float32])
+def test_skinny_runs_of_tiles_bit_exact(dev, orc, m, k, ydt):
+    """9-16 token rows over a matrix wide enough that every wave takes runs of 4
+    consecutive tiles with whole-line output stores (N = 140000: 8750 tiles, a partial last
+    run), on the reference words (path 2) and the MFMA layout: equal bit for bit to the MFMA
+    GEMM (path 1) on the same inputs, and to the oracle's dequantized sums on sampled
+    columns (first, last and the partial run's)."""
+    rng = np.random.default_rng(m * 7 + k + (ydt == torch.float32))
+    n = 140000
+    words = torch.randint(-2**31, 2**31 - 1, (n * k // 16,), dtype=torch.int32, device=dev)
+    words = (words ^ ((words & (words >> 1) & 0x55555555) << 1)).contiguous()  # no code 3
+    q_np = rng.integers(-127, 128, size=(m, k)).astype(np.int8)
+    s_np = rng.uniform(0.001, 0.02, m).astype(np.float32)
+    mag_np = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    bias_np = rng.standard_normal(n).astype(np.float32)
+    q, s = torch.from_numpy(q_np).to(dev), torch.from_numpy(s_np).to(dev)
+    mag, bias = torch.from_numpy(mag_np).to(dev), torch.from_numpy(bias_np).to(dev)
+    want = ops.ternary_gemm(q, s, words, 0.37, n, mag, bias, out_dtype=ydt, path=1)
+    got = ops.ternary_gemm(q, s, words, 0.37, n, mag, bias, out_dtype=ydt, path=2)
+    got_mf = ops.ternary_gemm_mfma(q, s, ops.pack_mfma_layout(words), 0.37, n, mag, bias,
+                                   out_dtype=ydt)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(got_mf, want)
+    cols = np.unique(np.concatenate([[0, 15, 16, n - 33, n - 1],
+                                     rng.choice(n, 251, replace=False)]))
+    w_np = words.cpu().numpy().view(np.uint32).reshape(n, k // 16)[cols]
+    codes = orc.unpack_codes(np.ascontiguousarray(w_np), cols.size * k).reshape(cols.size, k)
+    acc = orc.gemm_i8(q_np, codes)
+    y = orc.dequant(acc, s_np, 0.37, mag_np[cols], bias_np[cols])
+    g = got.float().cpu().numpy()[:, cols]
+    if ydt == torch.bfloat16:
+        y = _bf16_round(y)
+    np.testing.assert_array_equal(g, y)
+
+
 @pytest.mark.parametrize("m,k", [(4, 768), (4, 1040), (1, 1024), (33, 1024), (17, 4096)])
 def test_skinny_rejects_unsupported_shapes(dev, m, k):
     q = torch.zeros((m, k), dtype=torch.int8, device=dev)
