@@ -892,6 +892,17 @@ __device__ __forceinline__ void store_states(float* p, const float v[SPL]) {
     }
 }
 
+// Lane j's value of the lane's quad, in every lane of the quad (DPP quad_perm(j, j, j, j));
+// j must fold to a constant where this is inlined.
+template <int J>
+__device__ __forceinline__ float quad_bcast_c(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), J * 0x55, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float quad_bcast(float v, int j) {
+    return j == 0 ? quad_bcast_c<0>(v)
+                  : j == 1 ? quad_bcast_c<1>(v) : j == 2 ? quad_bcast_c<2>(v) : quad_bcast_c<3>(v);
+}
+
 template <int ADT, int SPL, bool GATE, bool VBC>
 __global__ __launch_bounds__(256) void scan_step_rows_kernel(
     const void* __restrict__ x, const void* __restrict__ dt, const float* __restrict__ a_log,
@@ -913,15 +924,20 @@ __global__ __launch_bounds__(256) void scan_step_rows_kernel(
         a2[i] = a2_from_log(a_per_state ? a_log[(int64_t)h * N + n] : a_log[h]);
     }
     const float dsk = Dskip[h];
+    // Rows r0 .. r0 + 3 (kStepRows == the 4 lanes of a channel's quad): lane q forms row
+    // r0 + q's per-(row, channel) terms (delta = softplus(dt), delta * x, the gate) once,
+    // the quad shares delta and delta * x through DPP broadcasts, and after the readout's
+    // transpose-reduce lane q finishes and stores row r0 + q's output.
+    static_assert(kStepRows == 4, "one row per lane of a channel's quad");
     float sv[kStepRows][SPL], bq[kStepRows][SPL], cq[kStepRows][SPL];
-    float xv[kStepRows], dtv[kStepRows], zv[kStepRows];
+    const int rq = min(r0 + q, rows - 1);  // rows past the end repeat the last (never stored)
+    const float xq = load_act<ADT>(x, (int64_t)rq * D + c);
+    const float dtq = load_act<ADT>(dt, (int64_t)rq * H + h);
+    const float zq = GATE ? load_act<ADT>(z, (int64_t)rq * D + c) : 0.0f;
 #pragma unroll
     for (int j = 0; j < kStepRows; ++j) {
-        const int r = min(r0 + j, rows - 1);  // rows past the end repeat the last (never stored)
+        const int r = min(r0 + j, rows - 1);
         load_states<SPL>(state + ((int64_t)r * D + c) * N + q * SPL, sv[j]);
-        xv[j] = load_act<ADT>(x, (int64_t)r * D + c);
-        dtv[j] = load_act<ADT>(dt, (int64_t)r * H + h);
-        zv[j] = GATE ? load_act<ADT>(z, (int64_t)r * D + c) : 0.0f;
         const int64_t boff = (int64_t)r * GN + grp * N + q * SPL;
         if constexpr (VBC && SPL == 4 && ADT == NSOSX_BF16) {
             // four consecutive bf16 states (N = 16, 8-byte aligned B and C): one 8-byte
@@ -940,11 +956,13 @@ __global__ __launch_bounds__(256) void scan_step_rows_kernel(
             }
         }
     }
+    const float dlq = softplus_sel(dtq);
+    const float dxq = dlq * xq;
+    float part[kStepRows];
 #pragma unroll
     for (int j = 0; j < kStepRows; ++j) {
-        const int r = r0 + j;
-        const float dl = softplus_sel(dtv[j]);
-        const float dx = dl * xv[j];
+        const float dl = quad_bcast(dlq, j);
+        const float dx = quad_bcast(dxq, j);
         float p = 0.0f;
 #pragma unroll
         for (int i = 0; i < SPL; ++i) {
@@ -952,16 +970,26 @@ __global__ __launch_bounds__(256) void scan_step_rows_kernel(
             sv[j][i] = __fmaf_rn(a, sv[j][i], dx * bq[j][i]);
             p = __fmaf_rn(sv[j][i], cq[j][i], p);
         }
-        p += dpp_xor2(p);
-        p += dpp_xor1(p);
-        if (r < rows) {
-            store_states<SPL>(state + ((int64_t)r * D + c) * N + q * SPL, sv[j]);
-            if (q == 0) {
-                float out = __fmaf_rn(dsk, xv[j], p);
-                if (GATE) out = out * silu_fast(zv[j]);
-                store_act<ADT>(y, (int64_t)r * D + c, out);
-            }
-        }
+        part[j] = p;
+        if (r0 + j < rows) store_states<SPL>(state + ((int64_t)(r0 + j) * D + c) * N + q * SPL, sv[j]);
+    }
+    // transpose-reduce over the quad: lane q ends with row q's sum,
+    // (p_q + p_{q^2}) + (p_{q^1} + p_{q^3}) over the lanes' partials
+    const bool hi2 = (q & 2) != 0;
+    const float s0 = hi2 ? part[0] : part[2];
+    const float s1 = hi2 ? part[1] : part[3];
+    const float k0 = hi2 ? part[2] : part[0];
+    const float k1 = hi2 ? part[3] : part[1];
+    const float m0 = k0 + dpp_xor2(s0);
+    const float m1 = k1 + dpp_xor2(s1);
+    const bool hi1 = (q & 1) != 0;
+    const float send = hi1 ? m0 : m1;
+    const float keep = hi1 ? m1 : m0;
+    const float tot = keep + dpp_xor1(send);
+    if (r0 + q < rows) {
+        float out = __fmaf_rn(dsk, xq, tot);
+        if (GATE) out = out * silu_fast(zq);
+        store_act<ADT>(y, (int64_t)(r0 + q) * D + c, out);
     }
 }
 
