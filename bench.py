@@ -241,16 +241,18 @@ def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=3
 
 PMC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                            "hybrid_layer_c4_pmc_traffic.md")
+PMC_DECODE_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                  "decode_pmc_traffic.md")
 
 
-def pmc_traffic(stage: str):
-    """HBM bytes per launch of a layer stage's kernel, from the committed rocprofv3 PMC summary.
+def pmc_traffic(stage: str, summary: str = PMC_SUMMARY):
+    """HBM bytes per launch of a stage's kernel, from a committed rocprofv3 PMC summary.
 
     The summary's table rows read `| stage | kernel | FETCH KiB | WRITE KiB | bytes |`, the
     bytes column already scaled by the copy-kernel calibration stated in that file.  None when
     the summary or the stage's row is absent."""
     try:
-        text = open(PMC_SUMMARY).read()
+        text = open(summary).read()
     except OSError:
         return None
     for line in text.splitlines():
@@ -394,7 +396,8 @@ def bench_decode_gemv(torch, dev, m=1, sets=128, reps=5):
     bytes_ = sets * (N * K / 4 + m * K + m * N * 2)
     gbs = bytes_ / (ms / 1e3) / 1e9
     return {"m": m, "weight_sets": sets, "bytes_per_launch": int(bytes_), "ms": round(ms, 4),
-            "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+            "gbs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": pmc_traffic(f"decode_gemv_c3_m{m}", PMC_DECODE_SUMMARY)}
 
 
 def bench_decode_gemv_sweep(torch, dev, ms=(1, 2, 4, 8, 16, 32), reps=20):
@@ -438,7 +441,8 @@ def bench_decode_gemv_sweep(torch, dev, ms=(1, 2, 4, 8, 16, 32), reps=20):
         bytes_ = N * K / 4 + m * K + m * N * 2
         gbs = bytes_ / (t / 1e3) / 1e9
         out[f"m{m}"] = {"ms": round(t, 4), "gbs": round(gbs, 1),
-                        "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+                        "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                        "traffic": pmc_traffic(f"decode_gemv_c3_sweep.m{m}", PMC_DECODE_SUMMARY)}
     del packed, packed_mfma
     return out
 
@@ -464,7 +468,8 @@ def bench_decode_step(torch, dev, reps=8):
     bytes_ = R * Dm * N * 4 * 2 + R * Dm * 2 * 4 + R * N * 2 * 2
     gbs = bytes_ / (ms / 1e3) / 1e9
     return {"rows": R, "ms": round(ms, 4), "gbs": round(gbs, 1),
-            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_launch": int(bytes_),
+            "traffic": pmc_traffic("decode_step_c5", PMC_DECODE_SUMMARY)}
 
 
 def _settle(torch, fn, ms=150.0):
@@ -802,7 +807,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default=None,
-                    help="run only this extra (e.g. prefill_gemm_c3), for counter runs")
+                    help="run only these extras (comma-separated, e.g. prefill_gemm_c3), for "
+                         "counter runs")
+    ap.add_argument("--skip-layer", action="store_true",
+                    help="counter runs: skip the headline layer and print the extras only")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="end with a plain 256 MiB device copy, the known-size kernel that "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by")
@@ -817,11 +825,12 @@ def main():
     import reimagined_amd
     reimagined_amd.lib()
     _log("library loaded")
-    T, wall, stages, params, inp, settle_ms = bench_layer(torch, dev, args.steps, args.warmup)
-    ms_step = wall / args.steps * 1e3
-    roof, _ = layer_roofline(T, stages)
-    _log(f"layer: {ms_step:.3f} ms/step, stages {stages}")
     extra = {}
+    if not args.skip_layer:
+        T, wall, stages, params, inp, settle_ms = bench_layer(torch, dev, args.steps, args.warmup)
+        ms_step = wall / args.steps * 1e3
+        roof, _ = layer_roofline(T, stages)
+        _log(f"layer: {ms_step:.3f} ms/step, stages {stages}")
     extras = [
         ("prefill_gemm_c3", "prefill gemm", lambda: bench_prefill_gemm(torch, dev)),
         ("decode_gemv_c3_m1", "decode gemv", lambda: bench_decode_gemv(torch, dev, m=1)),
@@ -837,15 +846,23 @@ def main():
         ("ste_backward", "ste backward", lambda: bench_ste_backward(torch, dev)),
         ("gemv_published_shapes", "gemv published shapes", lambda: bench_gemv_published(torch, dev)),
     ]
-    if args.only and args.only not in [k for k, _, _ in extras]:
-        print(f"--only: unknown extra {args.only!r}", file=sys.stderr)
+    only = set(args.only.split(",")) if args.only else None
+    if only and only - {k for k, _, _ in extras}:
+        print(f"--only: unknown extras {sorted(only - {k for k, _, _ in extras})}",
+              file=sys.stderr)
         sys.exit(2)
     if not args.no_extra:
         for key, label, fn in extras:
-            if args.only and key != args.only:
+            if only and key not in only:
                 continue
             extra[key] = fn()
             _log(f"{label} {extra[key]}")
+    if args.skip_layer:
+        print(json.dumps({"extra": extra}), flush=True)
+        if args.pmc_calibration:
+            _pmc_calibration(torch, dev)
+        return
+    if not args.no_extra:
         sc = stages.get("conv_scan")
         if sc:
             _, work = layer_roofline(T, {"conv_scan": sc})
@@ -880,10 +897,16 @@ def main():
     }
     print(json.dumps(line), flush=True)
     if args.pmc_calibration:
-        a = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev).fill_(1)
-        b = torch.empty_like(a)
-        b.copy_(a)
-        torch.cuda.synchronize()
+        _pmc_calibration(torch, dev)
+
+
+def _pmc_calibration(torch, dev):
+    """A plain 256 MiB device copy: the known-size kernel FETCH_SIZE / WRITE_SIZE are
+    scaled by."""
+    a = torch.empty(256 * 2**20, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    b.copy_(a)
+    torch.cuda.synchronize()
 
 
 if __name__ == "__main__":

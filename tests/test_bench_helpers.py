@@ -20,6 +20,13 @@ def test_committed_counter_summaries_parse():
     busy = b.pmc_valu_busy("conv + scan")
     assert isinstance(busy, float) and 0.0 < busy <= 100.0
     assert b.pmc_traffic("no_such_stage") is None and b.pmc_valu_busy("no such stage") is None
+    # decode kernels: counter bytes at least the algorithmic bytes each extra divides by
+    # (128 config-3 weight sets at M = 1; the stacked matrix at M = 16; the config-5 step)
+    algo = {"decode_gemv_c3_m1": 539_230_208, "decode_gemv_c3_sweep.m16": 570_458_112,
+            "decode_step_c5": 71_319_552}
+    for key, lo in algo.items():
+        t = b.pmc_traffic(key, b.PMC_DECODE_SUMMARY)
+        assert isinstance(t, int) and lo <= t < 1.1 * lo, key
 
 
 def test_layer_roofline_fields():
