@@ -472,8 +472,7 @@ int nsosx_mamba2_step_out(const void* x, const void* z, const void* B, const voi
  *   workspace: int32, nsosx_moe_route_workspace(rows, E) elements.
  * counts, offsets, perm, slot_of and workspace all NULL: selection only
  * (weights and selected, one launch), what the sparse decode consumes.
- * E <= 64, k <= min(E, 8) (the reference allows any k <= E; routing wider than
- * top-8 is not supported here). */
+ * E <= 64, any 0 < k <= E (rows * k < 2^31). */
 int64_t nsosx_moe_route_workspace(int rows, int experts);
 int nsosx_moe_route(const float* logits, const uint8_t* valid_rows, int rows, int experts, int k,
                     float* weights, int32_t* selected, int32_t* counts, int32_t* offsets,

@@ -613,7 +613,7 @@ extern "C" int nsosx_moe_sparse_decode(const nsosx_linear_view* up_views,
                                        void* stream) {
     if (!up_views || !down_views || !selected || !weights || !x || !workspace || !out)
         return fail(NSOSX_ERR_INVALID, "moe_sparse_decode: null pointer");
-    if (rows <= 0 || experts <= 0 || k <= 0 || k > 8 || k > experts || dim <= 0 || hidden <= 0 ||
+    if (rows <= 0 || experts <= 0 || experts > 64 || k <= 0 || k > experts || dim <= 0 || hidden <= 0 ||
         (int64_t)rows * k > 65535)
         return fail(NSOSX_ERR_INVALID, "moe_sparse_decode: bad shape (rows * k <= 65535)");
     if (!valid_dtype(x_dtype) || !valid_dtype(out_dtype))

@@ -28,19 +28,18 @@ constexpr int kRouteBlock = 256;  // rows per dispatch block
 // zero (MoERouter::forward zeroes them after the top-k, src/jamba.cpp:8195-8214,
 // 8299-8304), its selections are -1, and it takes no dispatch slot (the reference's
 // dispatch counts only nonzero weights, src/cuda/moe_kernels.cu:226-235, 305-319).
+// Any k <= E (MoERouter::forward's partial sort, src/jamba.cpp:8268-8297).  Returns the
+// row's selected experts as a bit mask (0 for a padding row).
 template <int EMAX>
-__device__ __forceinline__ void route_one_row(const float* __restrict__ logits,
-                                              const uint8_t* __restrict__ valid_rows, int r,
-                                              int E, int k, float* __restrict__ weights,
-                                              int32_t* __restrict__ selected, int (&sel)[8]) {
+__device__ __forceinline__ uint64_t route_one_row(const float* __restrict__ logits,
+                                                  const uint8_t* __restrict__ valid_rows, int r,
+                                                  int E, int k, float* __restrict__ weights,
+                                                  int32_t* __restrict__ selected) {
     if (valid_rows && valid_rows[r] == 0) {
         float* w = weights + (int64_t)r * E;
         for (int j = 0; j < E; ++j) w[j] = 0.0f;
-        for (int i = 0; i < k; ++i) {
-            selected[(int64_t)r * k + i] = -1;
-            if (i < 8) sel[i] = -1;
-        }
-        return;
+        for (int i = 0; i < k; ++i) selected[(int64_t)r * k + i] = -1;
+        return 0;
     }
     const float* src = logits + (int64_t)r * E;
     float p[EMAX];
@@ -75,7 +74,6 @@ __device__ __forceinline__ void route_one_row(const float* __restrict__ logits,
         }
         taken |= 1ull << best;
         selected[(int64_t)r * k + i] = best;
-        if (i < 8) sel[i] = best;
         ssum = ssum + bv;
     }
     // k == E keeps the raw softmax: the reference masks and renormalises only when
@@ -86,6 +84,37 @@ __device__ __forceinline__ void route_one_row(const float* __restrict__ logits,
 #pragma unroll
     for (int j = 0; j < EMAX; ++j)
         if (j < E) w[j] = ((taken >> j) & 1ull) ? (renorm ? p[j] * inv2 : p[j]) : 0.0f;
+    return taken;
+}
+
+// Row r's selection list as an expert bit mask (-1 entries, padding rows, add nothing),
+// with its first min(k, 8) choices kept in registers.
+__device__ __forceinline__ uint64_t row_selection(const int32_t* __restrict__ selected, int r,
+                                                  int k, int (&first)[8]) {
+    uint64_t mask = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        first[i] = i < k ? selected[(int64_t)r * k + i] : -1;
+        if (first[i] >= 0) mask |= 1ull << first[i];
+    }
+    for (int i = 8; i < k; ++i) {
+        const int e = selected[(int64_t)r * k + i];
+        if (e >= 0) mask |= 1ull << e;
+    }
+    return mask;
+}
+
+// Position of expert e in row r's selection list (e is in it).
+__device__ __forceinline__ int choice_of(const int32_t* __restrict__ selected, int r, int k, int e,
+                                         const int (&first)[8]) {
+    int which = -1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        if (first[i] == e) which = i;
+    if (which < 0)
+        for (int i = 8; i < k; ++i)
+            if (selected[(int64_t)r * k + i] == e) which = i;
+    return which;
 }
 
 template <int EMAX>
@@ -95,8 +124,7 @@ __global__ __launch_bounds__(256) void route_rows_kernel(const float* __restrict
                                                          float* __restrict__ weights,
                                                          int32_t* __restrict__ selected) {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    int sel[8];
-    if (r < rows) route_one_row<EMAX>(logits, valid_rows, r, E, k, weights, selected, sel);
+    if (r < rows) route_one_row<EMAX>(logits, valid_rows, r, E, k, weights, selected);
 }
 
 // Routing fused with the per-block expert counts: one thread per row of a
@@ -114,12 +142,10 @@ __global__ __launch_bounds__(256) void route_rows_count_kernel(const float* __re
     if (tid < E) cnt[tid] = 0;
     __syncthreads();
     const int r = blockIdx.x * kRouteBlock + tid;
-    if (r < rows) {
-        int sel[8];
-        route_one_row<EMAX>(logits, valid_rows, r, E, k, weights, selected, sel);
-        for (int i = 0; i < k; ++i)
-            if (sel[i] >= 0) atomicAdd(&cnt[sel[i]], 1);
-    }
+    if (r < rows)
+        for (uint64_t m = route_one_row<EMAX>(logits, valid_rows, r, E, k, weights, selected); m;
+             m &= m - 1)
+            atomicAdd(&cnt[__builtin_ctzll(m)], 1);
     __syncthreads();
     if (tid < E) block_counts[(int64_t)blockIdx.x * E + tid] = cnt[tid];
 }
@@ -184,24 +210,18 @@ __global__ __launch_bounds__(256) void route_assign_kernel(const int32_t* __rest
     const int lane = tid & 63, wave = tid >> 6;
     const int r = blockIdx.x * kRouteBlock + tid;
     const bool valid = r < rows;
-    int mine[kMaxExperts > 8 ? 8 : kMaxExperts];  // k <= 8 handled here
-    const int kk = k < 8 ? k : 8;
-    for (int i = 0; i < kk; ++i) mine[i] = valid ? selected[(int64_t)r * k + i] : -1;
-    if (valid && mine[0] < 0)  // a padding row: no slots
-        for (int i = 0; i < kk; ++i) slot_of[(int64_t)r * k + i] = -1;
+    int first[8];
+    const uint64_t mine = valid ? row_selection(selected, r, k, first) : 0;
+    if (valid && mine == 0)  // a padding row: no slots
+        for (int i = 0; i < k; ++i) slot_of[(int64_t)r * k + i] = -1;
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (int e = 0; e < E; ++e) {
-        bool has = false;
-        for (int i = 0; i < kk; ++i) has |= mine[i] == e;
-        const uint64_t bal = __ballot(has);
+        const uint64_t bal = __ballot((mine >> e) & 1ull);
         if (lane == 0) wave_cnt[wave][e] = __popcll(bal);
     }
     __syncthreads();
     for (int e = 0; e < E; ++e) {
-        bool has = false;
-        int which = -1;
-        for (int i = 0; i < kk; ++i)
-            if (mine[i] == e) { has = true; which = i; }
+        const bool has = (mine >> e) & 1ull;
         const uint64_t bal = __ballot(has);
         if (has) {
             int before = 0;
@@ -209,7 +229,7 @@ __global__ __launch_bounds__(256) void route_assign_kernel(const int32_t* __rest
             const int rank = before + __popcll(bal & lt);
             const int slot = offsets[e] + block_base[(int64_t)blockIdx.x * E + e] + rank;
             perm[slot] = r;
-            slot_of[(int64_t)r * k + which] = slot;
+            slot_of[(int64_t)r * k + choice_of(selected, r, k, e, first)] = slot;
         }
     }
 }
@@ -261,24 +281,18 @@ __global__ __launch_bounds__(256) void route_place_kernel(const int32_t* __restr
     }
     const int r = blockIdx.x * kRouteBlock + tid;
     const bool valid = r < rows;
-    int mine[8];
-    const int kk = k < 8 ? k : 8;
-    for (int i = 0; i < kk; ++i) mine[i] = valid ? selected[(int64_t)r * k + i] : -1;
-    if (valid && mine[0] < 0)  // a padding row: no slots
-        for (int i = 0; i < kk; ++i) slot_of[(int64_t)r * k + i] = -1;
+    int first[8];
+    const uint64_t mine = valid ? row_selection(selected, r, k, first) : 0;
+    if (valid && mine == 0)  // a padding row: no slots
+        for (int i = 0; i < k; ++i) slot_of[(int64_t)r * k + i] = -1;
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (int e = 0; e < E; ++e) {
-        bool has = false;
-        for (int i = 0; i < kk; ++i) has |= mine[i] == e;
-        const uint64_t bal = __ballot(has);
+        const uint64_t bal = __ballot((mine >> e) & 1ull);
         if (lane == 0) wave_cnt[wave][e] = __popcll(bal);
     }
     __syncthreads();
     for (int e = 0; e < E; ++e) {
-        bool has = false;
-        int which = -1;
-        for (int i = 0; i < kk; ++i)
-            if (mine[i] == e) { has = true; which = i; }
+        const bool has = (mine >> e) & 1ull;
         const uint64_t bal = __ballot(has);
         if (has) {
             int before = 0;
@@ -286,7 +300,7 @@ __global__ __launch_bounds__(256) void route_place_kernel(const int32_t* __restr
             const int rank = before + __popcll(bal & lt);
             const int slot = off[e] + base[e] + rank;
             perm[slot] = r;
-            slot_of[(int64_t)r * k + which] = slot;
+            slot_of[(int64_t)r * k + choice_of(selected, r, k, e, first)] = slot;
         }
     }
 }
@@ -307,6 +321,19 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ e
     const int kk = k < 8 ? k : 8;
     if (selected[(int64_t)r * k] < 0) {  // a padding row (no experts): zero
         store_act<ODT>(out, (int64_t)r * dim + d, 0.0f);
+        return;
+    }
+    if (k > 8) {  // wide routing: the row's experts in ascending id from its selection mask
+        int first[8];
+        float acc = 0.0f;
+        for (uint64_t m = row_selection(selected, r, k, first); m; m &= m - 1) {
+            const int e = __builtin_ctzll(m);
+            const int i = choice_of(selected, r, k, e, first);
+            const int64_t s = slot_of ? slot_of[(int64_t)r * k + i] : (int64_t)r * k + i;
+            acc = acc + __fmul_rn(load_act<IDT>(expert_out, s * dim + d),
+                                  weights[(int64_t)r * E + e]);
+        }
+        store_act<ODT>(out, (int64_t)r * dim + d, acc);
         return;
     }
     for (int i = 0; i < kk; ++i) {
@@ -394,6 +421,35 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const void* __restric
         for (int j = 0; j < V; ++j) zero[j] = 0.0f;
         for (int d = V * lane; d < dim; d += V * kWave)
             combine_store<ODT, V>(out, (int64_t)r * dim + d, zero);
+        return;
+    }
+    if (k > 8) {
+        // wide routing: lane e holds expert e's slot (-1 if the row did not select it) and
+        // weight; the sum walks the selected lanes in ascending id
+        int my_slot = -1;
+        float my_w = 0.0f;
+        if (lane < E) {
+            for (int i = 0; i < k; ++i)
+                if (selected[(int64_t)r * k + i] == lane)
+                    my_slot = slot_of ? slot_of[(int64_t)r * k + i] : r * k + i;
+            my_w = weights[(int64_t)r * E + lane];
+        }
+        const uint64_t has = __ballot(my_slot >= 0);
+        for (int d = V * lane; d < dim; d += V * kWave) {
+            float acc[V];
+#pragma unroll
+            for (int j = 0; j < V; ++j) acc[j] = 0.0f;
+            for (uint64_t m = has; m; m &= m - 1) {
+                const int e = __builtin_ctzll(m);
+                const int64_t sl = __builtin_amdgcn_readlane(my_slot, e);
+                const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_w), e));
+                float v[V];
+                combine_load<IDT, V>(expert_out, sl * dim + d, v);
+#pragma unroll
+                for (int j = 0; j < V; ++j) acc[j] = acc[j] + __fmul_rn(v[j], w);
+            }
+            combine_store<ODT, V>(out, (int64_t)r * dim + d, acc);
+        }
         return;
     }
     for (int i = 0; i < kk; ++i) {
@@ -499,8 +555,8 @@ extern "C" int nsosx_moe_route(const float* logits, const uint8_t* valid_rows, i
     if (!logits || !weights || !selected ||
         (!select_only && (!counts || !offsets || !perm || !slot_of || !workspace)))
         return fail(NSOSX_ERR_INVALID, "moe_route: null pointer");
-    if (rows <= 0 || experts <= 0 || experts > kMaxExperts || k <= 0 || k > experts || k > 8)
-        return fail(NSOSX_ERR_INVALID, "moe_route: need rows > 0, 0 < k <= min(E, 8), E <= 64");
+    if (rows <= 0 || experts <= 0 || experts > kMaxExperts || k <= 0 || k > experts)
+        return fail(NSOSX_ERR_INVALID, "moe_route: need rows > 0, 0 < k <= E <= 64");
     if ((int64_t)rows * k > 2147483647LL) return fail(NSOSX_ERR_OVERFLOW, "moe_route: rows*k too large");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int nblocks = (rows + kRouteBlock - 1) / kRouteBlock;
@@ -552,7 +608,7 @@ extern "C" int nsosx_moe_combine(const void* expert_out, int in_dtype, const int
     if (!expert_out || !selected || !weights || !out)
         return fail(NSOSX_ERR_INVALID, "moe_combine: null pointer");
     if (rows <= 0 || rows > 65535 * 256 || experts <= 0 || experts > kMaxExperts || k <= 0 ||
-        k > 8 || k > experts || dim <= 0)
+        k > experts || dim <= 0)
         return fail(NSOSX_ERR_INVALID, "moe_combine: bad shape");
     if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype))
         return fail(NSOSX_ERR_INVALID, "moe_combine: bad dtype");

@@ -20,7 +20,7 @@ def _route_oracle(orc, logits, k):
 
 
 @pytest.mark.parametrize("rows,E,k", [(8192, 8, 2), (1, 8, 2), (300, 8, 1), (1000, 64, 8),
-                                      (513, 3, 3)])
+                                      (513, 3, 3), (700, 16, 12), (300, 64, 64), (4000, 32, 9)])
 def test_route_matches_oracle(dev, orc, rows, E, k):
     rng = np.random.default_rng(rows + E)
     logits = rng.standard_normal((rows, E)).astype(np.float32)
@@ -62,7 +62,8 @@ def test_route_partial_null_outputs_rejected(dev):
     assert b"null pointer" in ops.lib().nsosx_last_error()
 
 
-@pytest.mark.parametrize("rows,E,k", [(8192, 8, 2), (1000, 64, 8), (300, 8, 1)])
+@pytest.mark.parametrize("rows,E,k", [(8192, 8, 2), (1000, 64, 8), (300, 8, 1), (900, 32, 9),
+                                      (300, 16, 16)])
 def test_route_padding_rows_match_oracle(dev, orc, rows, E, k):
     """MoERouter::forward(x, valid_rows): padding rows get zero weights, selections -1,
     slot_of -1 and no slots; the rest route as without the mask.  loads = expert_loads."""
@@ -168,7 +169,8 @@ def test_moe_ffn_matches_oracle(dev, orc, hidden_dtype):
                                            (torch.float32, torch.bfloat16),
                                            (torch.bfloat16, torch.bfloat16)])
 @pytest.mark.parametrize("rows,E,k,dim", [(300, 8, 2, 1024), (77, 8, 3, 1022), (1, 4, 1, 8),
-                                          (70000, 8, 2, 64)])
+                                          (70000, 8, 2, 64), (200, 16, 12, 1024),
+                                          (50, 64, 64, 520), (33, 32, 9, 1022)])
 def test_moe_combine_matches_oracle(dev, orc, in_dt, out_dt, rows, E, k, dim):
     """The weighted combine alone, both input and output dtypes, the row-per-wave vector form
     (dim % 4 == 0) and the element-wise one (dim = 1022), over the device routing: bit-exact
@@ -185,12 +187,12 @@ def test_moe_combine_matches_oracle(dev, orc, in_dt, out_dt, rows, E, k, dim):
     assert torch.equal(got.cpu(), want_t)
 
 
-@pytest.mark.parametrize("rows", [1, 5, 32])
-def test_moe_sparse_decode_matches_oracle(dev, orc, rows):
+@pytest.mark.parametrize("rows,E,k", [(1, 8, 2), (5, 8, 2), (32, 8, 2), (5, 16, 10)])
+def test_moe_sparse_decode_matches_oracle(dev, orc, rows, E, k):
     """Decode rows through (row, routed expert) grouped GEMVs: bit-exact against the oracle's
-    per-expert BitLinear chain combined with the same routing weights."""
-    rng = np.random.default_rng(90 + rows)
-    E, k, d, f = 8, 2, 256, 512
+    per-expert BitLinear chain combined with the same routing weights (also top-10 of 16)."""
+    rng = np.random.default_rng(90 + rows + k)
+    d, f = 256, 512
     w_up = [_ternary(rng, f, d) for _ in range(E)]
     w_down = [_ternary(rng, d, f) for _ in range(E)]
     x = rng.standard_normal((rows, d)).astype(np.float32)

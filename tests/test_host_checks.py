@@ -143,8 +143,11 @@ def test_grouped_mfma_gemm_requires_total_rows():
 def test_moe_route_argument_checks():
     from reimagined_amd._lib import lib
     L = lib()
-    # k above 8, and partial null outputs
-    rc = L.nsosx_moe_route(_FAKE, None, 16, 16, 9, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE,
+    # k above E, E above 64, and partial null outputs
+    rc = L.nsosx_moe_route(_FAKE, None, 16, 16, 17, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE,
+                           None, _FAKE, None)
+    assert rc == 1 and b"k <= E" in L.nsosx_last_error()
+    rc = L.nsosx_moe_route(_FAKE, None, 16, 65, 2, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE,
                            None, _FAKE, None)
     assert rc == 1
     rc = L.nsosx_moe_route(_FAKE, None, 16, 8, 2, _FAKE, _FAKE, _FAKE, None, None, None, None,
