@@ -335,9 +335,10 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
 // chunk's output rows in LDS; a finished 32-token chunk leaves with one 16-byte
 // store per lane.  B and C (shared by all channels of a group) are staged per
 // 32-token chunk in the wave's own LDS slice, converted to float once.  The
-// workgroup is one wave, so its barriers cost no waiting: the raw inputs of the
-// next group and the B/C rows of the next chunk are loaded into registers one
-// step ahead.
+// workgroup is one wave, so its barriers cost no waiting: the raw inputs of a
+// group are loaded into registers two groups ahead (two register sets that even
+// and odd groups alternate, so no copy waits on a load in flight) and the B/C rows
+// of the next chunk one chunk ahead.
 // ===========================================================================
 constexpr int kQuadTC = 32;       // tokens per B/C chunk
 constexpr int kQuadCh = 16;       // channels per wave
@@ -535,7 +536,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
     };
 
     // per-lane token stream through buffer resources: byte offsets of the next group's
-    // token (running; past the data the hardware returns 0), raw words one group ahead
+    // token (running; past the data the hardware returns 0), raw words two groups ahead
     constexpr uint32_t ES = ADT == NSOSX_F32 ? 4 : 2;
     const uint32_t xs = static_cast<uint32_t>(x_stride) * ES, zs = static_cast<uint32_t>(z_stride) * ES;
     // Each group's resources start at the group's first token (scalar arithmetic:
@@ -552,11 +553,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
         return make_rsrc(static_cast<const char*>(base) + off, static_cast<uint32_t>(left));
     };
     uint32_t tnext = static_cast<uint32_t>(t0);  // first token of the group to prefetch
-    raw_t xr = 0, dtr = 0, zr = 0;
-    auto prefetch_tok = [&]() {
-        xr = buf_load_raw<ADT>(group_rsrc(x, ex, tnext * xs), lx);
-        dtr = buf_load_raw<ADT>(group_rsrc(dt, edt, tnext * H * ES), ldt);
-        if (GATE) zr = buf_load_raw<ADT>(group_rsrc(z, ez, tnext * zs), lz);
+    // set (xr, dtr, zr) feeds the even groups of a chunk, (xr2, dtr2, zr2) the odd ones;
+    // a group consumes its set and refills it with the group two ahead (a chunk holds an
+    // even number of groups, so the alternation runs on across chunks)
+    raw_t xr = 0, dtr = 0, zr = 0, xr2 = 0, dtr2 = 0, zr2 = 0;
+    auto load_set = [&](raw_t& xo, raw_t& dto, raw_t& zo) {
+        xo = buf_load_raw<ADT>(group_rsrc(x, ex, tnext * xs), lx);
+        dto = buf_load_raw<ADT>(group_rsrc(dt, edt, tnext * H * ES), ldt);
+        if (GATE) zo = buf_load_raw<ADT>(group_rsrc(z, ez, tnext * zs), lz);
         tnext += 4;
     };
 
@@ -616,15 +620,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
     };
     if (t0 < t1) {
         prefetch_bc(t0);
-        prefetch_tok();
+        load_set(xr, dtr, zr);
+        load_set(xr2, dtr2, zr2);
     }
-    for (int tb = t0; tb < t1; tb += kQuadTC) {
-        __syncthreads();  // the previous chunk's B/C reads are done
-        stage_bc();
-        if (tb + kQuadTC < t1) prefetch_bc(tb + kQuadTC);
-        __syncthreads();
-        const int tc = min(kQuadTC, t1 - tb);
-        for (int r0 = 0; r0 < tc; r0 += 4) {
+    // one 4-token group at chunk row r0 of the chunk at tb, on the given input set
+    auto group = [&](const int tb, const int r0, raw_t& xs_, raw_t& dts_, raw_t& zs_) {
             const int tgrp = tb + r0;  // first token of the group (uniform)
             const bool valid = q < t1 - tgrp;
             // B/C of the group's four rows first: the reads overlap the staging math
@@ -644,10 +644,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
                 rd2 = s_red[red_r + 8]; rd3 = s_red[red_r + 12];
             }
             // tokens past the sequence feed only later tokens past it: no mask needed on x
-            const float xcur = raw_to_f32<ADT>(xr);
-            const float dtcur = raw_to_f32<ADT>(dtr);
-            const raw_t zraw = zr;
-            prefetch_tok();
+            const float xcur = raw_to_f32<ADT>(xs_);
+            const float dtcur = raw_to_f32<ADT>(dts_);
+            const raw_t zraw = zs_;
+            load_set(xs_, dts_, zs_);
             // ---- per-(token, channel) terms of token tg (formed unconditionally and
             // masked, so the group has no divergent branch) -------------------------
             float xv;
@@ -710,7 +710,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
             }
             if constexpr (LOCAL) {
                 sdl += (dlk[0] + dlk[1]) + (dlk[2] + dlk[3]);
-                continue;
+                return;
             }
             // ---- 4x4 transpose through the wave's LDS slice, one group behind:
             // lane q sums token q of the previous group over the channel's four state
@@ -723,6 +723,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
             pv_xv = xv;
             pv_z = zraw;
             pv_t = tgrp;
+    };
+    for (int tb = t0; tb < t1; tb += kQuadTC) {
+        __syncthreads();  // the previous chunk's B/C reads are done
+        stage_bc();
+        if (tb + kQuadTC < t1) prefetch_bc(tb + kQuadTC);
+        __syncthreads();
+        const int tc = min(kQuadTC, t1 - tb);
+        for (int r0 = 0; r0 < tc; r0 += 8) {
+            group(tb, r0, xr, dtr, zr);
+            if (r0 + 4 < tc) group(tb, r0 + 4, xr2, dtr2, zr2);
         }
     }
     if constexpr (!LOCAL) {
