@@ -127,10 +127,14 @@ def _ternary(rng, n, k):
     return rng.standard_normal((n, k)).astype(np.float32)
 
 
-@pytest.mark.parametrize("hidden_dtype", [torch.float32])
-def test_moe_ffn_matches_oracle(dev, orc, hidden_dtype):
-    rng = np.random.default_rng(77)
-    rows, E, k, d, f = 600, 8, 2, 256, 512
+@pytest.mark.parametrize("hidden_dtype,E,k", [(torch.float32, 8, 2), (torch.float32, 16, 10),
+                                               (torch.float32, 12, 12)])
+def test_moe_ffn_matches_oracle(dev, orc, hidden_dtype, E, k):
+    """The whole MoE feed-forward (routing, grouped up / squared ReLU / down GEMMs, combine)
+    against the oracle's per-expert BitLinear chain: top-2 of 8, top-10 of 16 (wider than the
+    register fast paths) and k = E = 12 (every row through every expert, raw softmax weights)."""
+    rng = np.random.default_rng(77 + k)
+    rows, d, f = 600, 256, 512
     w_up = [_ternary(rng, f, d) for _ in range(E)]
     w_down = [_ternary(rng, d, f) for _ in range(E)]
     x = rng.standard_normal((rows, d)).astype(np.float32)
