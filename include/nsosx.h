@@ -508,6 +508,25 @@ int nsosx_grouped_ternary_gemm_mfma(const nsosx_linear_view* views_dev, int expe
                                     int total_rows, int squared_relu, void* y, int y_dtype,
                                     void* stream);
 
+/* nsosx_grouped_ternary_gemm_mfma with a workspace for a split-K tail: when the
+ * launch's last round of tiles would leave at least three quarters of the
+ * resident workgroups idle and K >= 2048 (the routed config-5 down GEMM: 528
+ * tiles on 512), those tiles are split along K over 2-8 workgroups each, their
+ * int32 partial sums go to the workspace and a second launch adds them and
+ * applies the epilogue.
+ * Integer partial sums: the same bits as nsosx_grouped_ternary_gemm_mfma.  The
+ * same arguments and checks, plus workspace (device, 16-byte aligned) of at
+ * least nsosx_grouped_ternary_gemm_mfma_workspace() bytes (2 x CUs x 128 KiB on
+ * the current device; -1 without a device).  Two launches on `stream`; calls
+ * sharing a workspace must not overlap.  This entry has no counterpart in the
+ * reference (whose per-expert loop has no tail to balance). */
+int64_t nsosx_grouped_ternary_gemm_mfma_workspace(void);
+int nsosx_grouped_ternary_gemm_mfma_ws(const nsosx_linear_view* views_dev, int experts,
+                                       const int32_t* offsets, const int32_t* perm, int gather,
+                                       const int8_t* q, const float* act_scale, int K, int N,
+                                       int total_rows, int squared_relu, void* y, int y_dtype,
+                                       void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Weighted combine in ascending expert order (src/jamba.cpp:3947-3969):
  * out[r] = sum over the row's selected experts, lowest id first, of
  * expert_out[slot] * weights[r, e], starting from 0.

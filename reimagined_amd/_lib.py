@@ -42,6 +42,9 @@ SIGNATURES = {
     "nsosx_ternary_gemm_mfma": (_i, [_vp, _vp, _vp, _f, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp]),
     "nsosx_grouped_ternary_gemm_mfma": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i,
                                              _vp, _i, _vp]),
+    "nsosx_grouped_ternary_gemm_mfma_workspace": (_i64, []),
+    "nsosx_grouped_ternary_gemm_mfma_ws": (_i, [_vp, _i, _vp, _vp, _i, _vp, _vp, _i, _i, _i, _i,
+                                                _vp, _i, _vp, _i64, _vp]),
     "nsosx_grouped_gemv": (_i, [_vp, _i, _vp, _i64, _vp, _i64, _i, _vp, _i64, _i, _vp]),
     "nsosx_grouped_decode_projections": (_i, [_vp, _i, _vp, _i, _vp, _i64, _i, _vp]),
     "nsosx_conv1d_causal": (_i, [_vp, _i, _i64, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i,

@@ -722,20 +722,49 @@ __device__ __forceinline__ void gemm3_epilogue_rows_f32(const GemmProblem& pb,
     }
 }
 
+// A tile's int32 accumulators as raw partial sums: int4 j (0..31) of thread t, its
+// acc[j / 16][(j / 4) % 4][4 (j % 4) .. + 3], at (j * 256 + t) * 4 (consecutive threads,
+// consecutive 16 bytes).  32768 ints per tile.
+constexpr int kG3TileInts = kG3BN * kG3BM;
+
+__device__ __forceinline__ void gemm3_store_raw(const v16i (&acc)[2][4], int32_t* __restrict__ raw) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int j = (a * 4 + b) * 4 + c;
+                *reinterpret_cast<int4*>(raw + (j * kGemm3Threads + tid) * 4) =
+                    make_int4(acc[a][b][4 * c], acc[a][b][4 * c + 1], acc[a][b][4 * c + 2],
+                              acc[a][b][4 * c + 3]);
+            }
+}
+
+template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU>
+__device__ __forceinline__ void gemm3_store(const GemmProblem& pb, const float* __restrict__ act_scale,
+                                            const int32_t* __restrict__ perm, int seg_begin,
+                                            int seg_rows, int n0, int m0, void* y,
+                                            int32_t* acc_out, const v16i (&acc)[2][4], char* smem);
+
 // MB: 32-row blocks of the tile that hold rows (a partial last tile of an expert's
 // segment skips the loads and MFMAs of its empty blocks; their accumulators stay zero
-// and their rows are never stored).
+// and their rows are never stored).  k stages [kt0, kt1) (kt1 < 0: to the end); with
+// `raw` the tile's partial int32 sums are written there (gemm3_store_raw, before the
+// MFMA layout's shift) instead of the epilogue.
 template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU, bool SWZ = false, int MB = 4>
 __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* __restrict__ q,
                                            const float* __restrict__ act_scale,
                                            const int32_t* __restrict__ perm, int seg_begin,
                                            int seg_rows, int n0, int m0, void* y,
-                                           int32_t* acc_out, char* smem) {
+                                           int32_t* acc_out, char* smem, int kt0 = 0,
+                                           int kt1 = -1, int32_t* raw = nullptr) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;        // wave = 64-row slice of n
     const int W16 = pb.K >> 4;
-    const int KT = pb.K / kG3BK;
+    const int KT = kt1 < 0 ? pb.K / kG3BK : kt1;
 
     // Stage sources.  Weights: wave-load j (0, 1) of a wave fills LDS rows
     // 64 wave + 32 j .. +31, lane -> row + lane / 2, slot lane % 2.
@@ -789,11 +818,11 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
 #pragma unroll
         for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
 
-    fetch(0);
+    fetch(kt0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    put(0);
-    if (KT > 1) fetch(1);
-    for (int kt = 0; kt < KT; ++kt) {
+    put(kt0);
+    if (kt0 + 1 < KT) fetch(kt0 + 1);
+    for (int kt = kt0; kt < KT; ++kt) {
         if (kt + 1 < KT) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // stage kt + 1 is in registers
             put(kt + 1);
@@ -804,6 +833,10 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
         asm volatile("" ::: "memory");
         gemm3_stage<SWZ, MB>(smem + (kt % kG3Stages) * kG3StageBytes, wave, lane, acc);
     }
+    if (raw) {
+        gemm3_store_raw(acc, raw);
+        return;
+    }
     if constexpr (SWZ) {
         // MFMA-layout operands carry 64 x the ternary values (unpack_word_mfma)
 #pragma unroll
@@ -813,7 +846,18 @@ __device__ __forceinline__ void gemm3_tile(const GemmProblem& pb, const int8_t* 
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[a][b][e] >>= 6;
     }
+    gemm3_store<YDT, ACC_OUT, GATHER, SQRELU>(pb, act_scale, perm, seg_begin, seg_rows, n0, m0, y,
+                                              acc_out, acc, smem);
+}
 
+// The epilogue of a 256 x 128 tile from its int32 sums: whole-row-segment bf16 / f32
+// stores through the idle stage ring where the tile lies inside N and the pointers
+// allow, else gemm3_epilogue.
+template <int YDT, bool ACC_OUT, bool GATHER, bool SQRELU>
+__device__ __forceinline__ void gemm3_store(const GemmProblem& pb, const float* __restrict__ act_scale,
+                                            const int32_t* __restrict__ perm, int seg_begin,
+                                            int seg_rows, int n0, int m0, void* y,
+                                            int32_t* acc_out, const v16i (&acc)[2][4], char* smem) {
     if constexpr (YDT == NSOSX_BF16 && !ACC_OUT) {
         if (y && n0 + kG3BN <= pb.N && (pb.N & 7) == 0 &&
             ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(pb.mag) |
@@ -909,20 +953,22 @@ template <int YDT, bool GATHER, bool SQRELU, bool SWZ>
 __device__ __forceinline__ void gemm3_tile_rows(const GemmProblem& pb, const int8_t* __restrict__ q,
                                                 const float* __restrict__ act_scale,
                                                 const int32_t* __restrict__ perm, int seg_begin,
-                                                int seg_rows, int n0, int m0, void* y, char* smem) {
+                                                int seg_rows, int n0, int m0, void* y, char* smem,
+                                                int kt0 = 0, int kt1 = -1,
+                                                int32_t* raw = nullptr) {
     const int rows = seg_rows - m0;
     if (rows > 96)
         gemm3_tile<YDT, false, GATHER, SQRELU, SWZ, 4>(pb, q, act_scale, perm, seg_begin, seg_rows,
-                                                        n0, m0, y, nullptr, smem);
+                                                        n0, m0, y, nullptr, smem, kt0, kt1, raw);
     else if (rows > 64)
         gemm3_tile<YDT, false, GATHER, SQRELU, SWZ, 3>(pb, q, act_scale, perm, seg_begin, seg_rows,
-                                                        n0, m0, y, nullptr, smem);
+                                                        n0, m0, y, nullptr, smem, kt0, kt1, raw);
     else if (rows > 32)
         gemm3_tile<YDT, false, GATHER, SQRELU, SWZ, 2>(pb, q, act_scale, perm, seg_begin, seg_rows,
-                                                        n0, m0, y, nullptr, smem);
+                                                        n0, m0, y, nullptr, smem, kt0, kt1, raw);
     else
         gemm3_tile<YDT, false, GATHER, SQRELU, SWZ, 1>(pb, q, act_scale, perm, seg_begin, seg_rows,
-                                                        n0, m0, y, nullptr, smem);
+                                                        n0, m0, y, nullptr, smem, kt0, kt1, raw);
 }
 
 }  // namespace nsosx

@@ -203,6 +203,15 @@ class MoEFFN:
                                                        device)
         self._buf = {}
 
+    def _tail_workspace(self, device):
+        """The split-K tail workspace of the grouped MFMA GEMMs (one per layer: the up and down
+        launches run in stream order)."""
+        ws = getattr(self, "_tail_ws", None)
+        if ws is None:
+            ws = self._tail_ws = torch.empty(ops.grouped_mfma_workspace_bytes(),
+                                             dtype=torch.uint8, device=device)
+        return ws
+
     def _buffers(self, rows: int, device):
         b = self._buf.get(rows)
         if b is None:
@@ -252,9 +261,11 @@ class MoEFFN:
         mk("quant_in")
         slots = rows * k
         if self.mfma:
-            call("nsosx_grouped_ternary_gemm_mfma", self.up_views_mfma.ptr, e, _p(b["offsets"]),
-                 _p(b["perm"]), 1, _p(b["q1"]), _p(b["s1"]), self.d_model, self.d_ff, slots, 1,
-                 _p(b["h"]), _DT[self.hidden_dtype], st)
+            tail = self._tail_workspace(x.device)
+            call("nsosx_grouped_ternary_gemm_mfma_ws", self.up_views_mfma.ptr, e,
+                 _p(b["offsets"]), _p(b["perm"]), 1, _p(b["q1"]), _p(b["s1"]), self.d_model,
+                 self.d_ff, slots, 1, _p(b["h"]), _DT[self.hidden_dtype], _p(tail),
+                 tail.numel(), st)
         else:
             call("nsosx_grouped_ternary_gemm", self.up_views.ptr, e, _p(b["offsets"]),
                  _p(b["perm"]), 1, _p(b["q1"]), _p(b["s1"]), self.d_model, self.d_ff, rows, slots,
@@ -264,9 +275,9 @@ class MoEFFN:
              int(self.rms_input), _p(b["q2"]), _p(b["s2"]), _p(b["r2"]), st)
         mk("quant_hidden")
         if self.mfma:
-            call("nsosx_grouped_ternary_gemm_mfma", self.down_views_mfma.ptr, e, _p(b["offsets"]),
-                 None, 0, _p(b["q2"]), _p(b["s2"]), self.d_ff, self.d_model, slots, 0, _p(b["o"]),
-                 _DT[torch.float32], st)
+            call("nsosx_grouped_ternary_gemm_mfma_ws", self.down_views_mfma.ptr, e,
+                 _p(b["offsets"]), None, 0, _p(b["q2"]), _p(b["s2"]), self.d_ff, self.d_model,
+                 slots, 0, _p(b["o"]), _DT[torch.float32], _p(tail), tail.numel(), st)
         else:
             call("nsosx_grouped_ternary_gemm", self.down_views.ptr, e, _p(b["offsets"]), None, 0,
                  _p(b["q2"]), _p(b["s2"]), self.d_ff, self.d_model, rows, slots, 0, _p(b["o"]),

@@ -12,7 +12,7 @@ import ctypes
 import numpy as np
 import torch
 
-from ._lib import call, lib
+from ._lib import NsosxError, call, lib
 
 F32, BF16 = 0, 1
 _DT = {torch.float32: F32, torch.bfloat16: BF16}
@@ -657,8 +657,10 @@ def grouped_ternary_gemm(views: LinearViewArray, offsets, perm, q, act_scale, n_
 
 def grouped_ternary_gemm_mfma(views: LinearViewArray, offsets, perm, q, act_scale, n_out: int,
                               total_rows: int, squared_relu: bool = False, gather: bool = True,
-                              out_dtype=torch.float32) -> torch.Tensor:
-    """grouped_ternary_gemm on views holding MFMA-layout weights (compact row tiles)."""
+                              out_dtype=torch.float32, workspace=None) -> torch.Tensor:
+    """grouped_ternary_gemm on views holding MFMA-layout weights (compact row tiles).  With a
+    workspace (uint8 device tensor of grouped_mfma_workspace_bytes()), the entry that splits a
+    sparse last round of tiles along K (nsosx_grouped_ternary_gemm_mfma_ws; same bits)."""
     _dev(offsets, "offsets", torch.int32)
     if gather:
         _dev(perm, "perm", torch.int32)
@@ -667,10 +669,25 @@ def grouped_ternary_gemm_mfma(views: LinearViewArray, offsets, perm, q, act_scal
     slots = int(perm.numel()) if gather else q.shape[0]
     k = q.shape[1]
     y = torch.empty((slots, n_out), dtype=out_dtype, device=q.device)
-    call("nsosx_grouped_ternary_gemm_mfma", views.ptr, views.count, _p(offsets), _p(perm),
-         int(gather), _p(q), _p(act_scale), k, n_out, int(total_rows), int(squared_relu), _p(y),
-         _DT[out_dtype], _stream())
+    if workspace is None:
+        call("nsosx_grouped_ternary_gemm_mfma", views.ptr, views.count, _p(offsets), _p(perm),
+             int(gather), _p(q), _p(act_scale), k, n_out, int(total_rows), int(squared_relu),
+             _p(y), _DT[out_dtype], _stream())
+    else:
+        _dev(workspace, "workspace", torch.uint8)
+        call("nsosx_grouped_ternary_gemm_mfma_ws", views.ptr, views.count, _p(offsets), _p(perm),
+             int(gather), _p(q), _p(act_scale), k, n_out, int(total_rows), int(squared_relu),
+             _p(y), _DT[out_dtype], _p(workspace), int(workspace.numel()), _stream())
     return y
+
+
+def grouped_mfma_workspace_bytes() -> int:
+    """Bytes of the split-K tail workspace of nsosx_grouped_ternary_gemm_mfma_ws on the current
+    device (2 x CUs x 128 KiB)."""
+    n = int(lib().nsosx_grouped_ternary_gemm_mfma_workspace())
+    if n <= 0:
+        raise NsosxError("nsosx_grouped_ternary_gemm_mfma_workspace", n, "no device")
+    return n
 
 
 def moe_combine(expert_out, slot_of, selected, weights, out_dtype=torch.float32) -> torch.Tensor:

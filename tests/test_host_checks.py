@@ -167,3 +167,19 @@ def test_moe_route_host_mask_validation():
     assert valid_rows_mask([], 3, "cpu") is None
     m = valid_rows_mask(np.array([1, 0, 1]), 3, "cpu")
     assert m.dtype == torch.uint8 and m.tolist() == [1, 0, 1]
+
+
+def test_grouped_mfma_ws_argument_checks():
+    """The split-K tail entry checks its workspace pointer and the shapes before it asks the
+    device anything (no device here)."""
+    from reimagined_amd._lib import lib
+    L = lib()
+    rc = L.nsosx_grouped_ternary_gemm_mfma_ws(_FAKE, 8, _FAKE, _FAKE, 1, _FAKE, _FAKE, 1024,
+                                              4096, 100, 1, _FAKE, 1, None, 1 << 26, None)
+    assert rc == 1 and b"null pointer" in L.nsosx_last_error()
+    rc = L.nsosx_grouped_ternary_gemm_mfma_ws(_FAKE, 8, _FAKE, _FAKE, 1, _FAKE, _FAKE, 1024,
+                                              4096, 0, 1, _FAKE, 1, _FAKE, 1 << 26, None)
+    assert rc == 1 and b"total_rows > 0" in L.nsosx_last_error()
+    rc = L.nsosx_grouped_ternary_gemm_mfma_ws(_FAKE, 8, _FAKE, _FAKE, 1, _FAKE, _FAKE, 1000,
+                                              4096, 100, 1, _FAKE, 1, _FAKE, 1 << 26, None)
+    assert rc == 1 and b"K % 128" in L.nsosx_last_error()
