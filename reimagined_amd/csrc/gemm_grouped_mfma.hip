@@ -140,16 +140,29 @@ __global__ __launch_bounds__(kGemm3Threads) void grouped_gemm3_fixup_kernel(
         const int arow = GATHER ? perm[orow] : (int)orow;
         const float comb = __fmul_rn(act_scale[arow], v.weight_scale);
         const int nb = n0 + 64 * (t >> 6) + 4 * ((t >> 5) & 1) + 32 * a + 8 * c;
+        float val[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int n = nb + r;
-            if (n >= v.outputs) continue;
-            float val = dequant(accs[r], comb, v.magnitude, v.bias, n);
+            const int n = min(nb + r, v.outputs - 1);  // columns past N are never stored
+            val[r] = dequant(accs[r], comb, v.magnitude, v.bias, n);
             if (SQRELU) {
-                val = val > 0.0f ? val : 0.0f;
-                val = __fmul_rn(val, val);
+                val[r] = val[r] > 0.0f ? val[r] : 0.0f;
+                val[r] = __fmul_rn(val[r], val[r]);
             }
-            store_act<YDT>(y, orow * v.outputs + n, val);
+        }
+        const int64_t o = orow * v.outputs + nb;
+        if (nb + 3 < v.outputs && (o & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0) {
+            // the four outputs as one 16-byte (f32) or 8-byte (bf16) store
+            if constexpr (YDT == NSOSX_F32)
+                *reinterpret_cast<float4*>(static_cast<float*>(y) + o) =
+                    make_float4(val[0], val[1], val[2], val[3]);
+            else
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + o) =
+                    make_uint2(pack_bf16x2(val[0], val[1]), pack_bf16x2(val[2], val[3]));
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (nb + r < v.outputs) store_act<YDT>(y, o + r, val[r]);
         }
     }
 }
