@@ -7,6 +7,8 @@
 //   GEMM + affine    src/bitnet_adapter_avx2.cpp:52-158
 #include "gemm_tiles.hpp"
 
+#include <atomic>
+
 namespace nsosx {
 
 template <int YDT, bool GATHER, bool SQRELU>
@@ -167,13 +169,22 @@ __global__ __launch_bounds__(kGemm3Threads) void grouped_gemm3_fixup_kernel(
     }
 }
 
-// Workgroups resident at once on the current device for the 256 x 128 tile kernels.
+// Workgroups resident at once on the current device for the 256 x 128 tile kernels
+// (2 per CU), looked up once per device.
 static int gemm3_resident_wgs() {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cached[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < kMaxDev) {
+        const int w = cached[dev].load(std::memory_order_relaxed);
+        if (w > 0) return w;
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
         return 0;
+    if (dev < kMaxDev) cached[dev].store(2 * cus, std::memory_order_relaxed);
     return 2 * cus;
 }
 
