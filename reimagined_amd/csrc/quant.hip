@@ -17,6 +17,15 @@ namespace nsosx {
 // with 16-byte loads (eight bf16 or four f32 values per load, four loads in
 // flight).
 // ===========================================================================
+// sum + v * v with the square rounded first.  A bf16 value's square (at most 16
+// significant bits) is exact in float, so one fused multiply-add rounds the same
+// sum; an f32 square is rounded on its own, as the reference loop does.
+template <int DT>
+__device__ __forceinline__ float sq_add(float sum, float v) {
+    if constexpr (DT == NSOSX_F32) return __fadd_rn(sum, __fmul_rn(v, v));
+    else return __fmaf_rn(v, v, sum);
+}
+
 template <int DT>
 __device__ __forceinline__ void load16_f32(const char* p, float v[DT == NSOSX_F32 ? 4 : 8]) {
     const uint4 a = *reinterpret_cast<const uint4*>(p);
@@ -53,7 +62,7 @@ __global__ __launch_bounds__(64) void rms_inv_kernel(const void* __restrict__ x,
 #pragma unroll
             for (int u = 0; u < U; ++u)
 #pragma unroll
-                for (int j = 0; j < PER; ++j) sum = __fadd_rn(sum, __fmul_rn(v[u][j], v[u][j]));
+                for (int j = 0; j < PER; ++j) sum = sq_add<DT>(sum, v[u][j]);
         }
     }
     for (; k < K; ++k) {
@@ -124,7 +133,7 @@ __global__ __launch_bounds__(64) void rms_inv_tiled_kernel(const void* __restric
                 float v[PER];
                 load16_f32<DT>(my + p * 16, v);
 #pragma unroll
-                for (int j = 0; j < PER; ++j) sum = __fadd_rn(sum, __fmul_rn(v[j], v[j]));
+                for (int j = 0; j < PER; ++j) sum = sq_add<DT>(sum, v[j]);
             }
         }
     }
@@ -346,8 +355,22 @@ __global__ __launch_bounds__(256) void quantize_rows_vec_kernel(
 // all RPW x CH chunk loads (8 elements per lane each) before it uses any, so a
 // wave keeps 8 KB of bf16 in flight where one row per wave kept 1-2 KB (the
 // row-per-wave kernel is latency-bound at ~3.9 TB/s).  The float operations
-// are those of quantize_rows_vec_kernel (x * inv is formed again for the codes,
-// the same product), so the same bits.
+// are those of quantize_rows_vec_kernel (a row's x * inv products are kept in
+// registers for the codes), so the same bits.
+// clamp127(rintf(t)) as the low byte of a float's bits: the clamp comes first
+// (rounding a value inside [-127, 127] cannot leave it, and a NaN clamps to -127
+// either way), then adding 1.5 * 2^23 rounds to an integer, ties to even, and
+// leaves it in the low mantissa bits as two's complement.
+__device__ __forceinline__ uint32_t code_bits(float t) {
+    return __float_as_uint(__fadd_rn(clamp127(t), 12582912.0f));
+}
+// the low bytes of four code_bits words, a in byte 0
+__device__ __forceinline__ uint32_t pack4_code_bits(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);
+    const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+
 template <int DT, bool RMS, int CH>
 __global__ __launch_bounds__(256) void quantize_rows_multi_kernel(
     const void* __restrict__ x, int M, float q_max, const float* __restrict__ rms_inv,
@@ -391,13 +414,16 @@ __global__ __launch_bounds__(256) void quantize_rows_multi_kernel(
     for (int r = 0; r < RPW; ++r) {
         const int row = row0 + r;
         const float inv = invs[r];
+        float v[CH][8];  // the row's normalized values, kept for the codes
         float m = 0.0f;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            float v[8];
-            unpack(raw[r][c], v);
+            unpack(raw[r][c], v[c]);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(RMS ? __fmul_rn(v[j], inv) : v[j]));
+            for (int j = 0; j < 8; ++j) {
+                if (RMS) v[c][j] = __fmul_rn(v[c][j], inv);
+                m = fmaxf(m, fabsf(v[c][j]));
+            }
         }
         m = wave_max(m);
         if (row >= M) break;
@@ -407,14 +433,12 @@ __global__ __launch_bounds__(256) void quantize_rows_multi_kernel(
         int8_t* dst = q + (int64_t)row * K + lane * 8;
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
-            float v[8], code[8];
-            unpack(raw[r][c], v);
+            uint32_t code[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                code[j] = clamp127(rintf(__fmul_rn(RMS ? __fmul_rn(v[j], inv) : v[j], sc)));
+            for (int j = 0; j < 8; ++j) code[j] = code_bits(__fmul_rn(v[c][j], sc));
             *reinterpret_cast<uint2*>(dst + c * kWave * 8) =
-                make_uint2(pack4_i8(code[0], code[1], code[2], code[3]),
-                           pack4_i8(code[4], code[5], code[6], code[7]));
+                make_uint2(pack4_code_bits(code[0], code[1], code[2], code[3]),
+                           pack4_code_bits(code[4], code[5], code[6], code[7]));
         }
     }
 }
