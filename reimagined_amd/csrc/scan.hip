@@ -941,6 +941,18 @@ __global__ __launch_bounds__(256) void scan_step_rows_kernel(
     static_assert(kStepRows == 4, "one row per lane of a channel's quad");
     float sv[kStepRows][SPL], bq[kStepRows][SPL], cq[kStepRows][SPL];
     const int rq = min(r0 + q, rows - 1);  // rows past the end repeat the last (never stored)
+    // VBC (bf16, N = 16, one B / C group per 16 channels: the host checks): the wave's B and
+    // C segments of rows r0 .. r0 + 3 (32 bytes each) come in with one 4-byte load per lane
+    // (lanes 0-31 B, 32-63 C) and pass through the wave's LDS slice, in place of eight
+    // 8-byte loads per wave of the same few lines (13.7 against 14.4 us at config 5)
+    __shared__ __align__(16) uint32_t s_bcw[4][64];
+    if constexpr (VBC && SPL == 4 && ADT == NSOSX_BF16) {
+        const int lane = threadIdx.x & 63;
+        const int rr = min(r0 + ((lane & 31) >> 3), rows - 1);
+        const uint16_t* m = static_cast<const uint16_t*>(lane < 32 ? Bm : Cm);
+        s_bcw[threadIdx.x >> 6][lane] = *reinterpret_cast<const uint32_t*>(
+            m + (int64_t)rr * GN + __builtin_amdgcn_readfirstlane(grp) * N + (lane & 7) * 2);
+    }
     const float xq = load_act<ADT>(x, (int64_t)rq * D + c);
     const float dtq = load_act<ADT>(dt, (int64_t)rq * H + h);
     const float zq = GATE ? load_act<ADT>(z, (int64_t)rq * D + c) : 0.0f;
@@ -950,10 +962,11 @@ __global__ __launch_bounds__(256) void scan_step_rows_kernel(
         load_states<SPL>(state + ((int64_t)r * D + c) * N + q * SPL, sv[j]);
         const int64_t boff = (int64_t)r * GN + grp * N + q * SPL;
         if constexpr (VBC && SPL == 4 && ADT == NSOSX_BF16) {
-            // four consecutive bf16 states (N = 16, 8-byte aligned B and C): one 8-byte
-            // load each
-            const uint2 b2 = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(Bm) + boff);
-            const uint2 c2 = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(Cm) + boff);
+            // the quad's four states of row j from the wave's slice (LDS operations of one
+            // wave complete in order)
+            const uint32_t* sw = s_bcw[threadIdx.x >> 6];
+            const uint2 b2 = *reinterpret_cast<const uint2*>(sw + j * 8 + q * 2);
+            const uint2 c2 = *reinterpret_cast<const uint2*>(sw + 32 + j * 8 + q * 2);
             bq[j][0] = __uint_as_float(b2.x << 16); bq[j][1] = __uint_as_float(b2.x & 0xFFFF0000u);
             bq[j][2] = __uint_as_float(b2.y << 16); bq[j][3] = __uint_as_float(b2.y & 0xFFFF0000u);
             cq[j][0] = __uint_as_float(c2.x << 16); cq[j][1] = __uint_as_float(c2.x & 0xFFFF0000u);
@@ -1597,9 +1610,11 @@ extern "C" int nsosx_selective_scan_step(const void* x, const void* dt, const fl
         rows <= 65535 * kStepRows) {
         // states of a channel split evenly over the quad: the row-blocked kernel
         const dim3 grid((H * P + 63) / 64, (rows + kStepRows - 1) / kStepRows), block(256);
-        // B and C of a quad in one 8-byte load when N = 16 and they are 8-byte aligned (chosen
-        // here: a branch on the alignment inside the kernel would drain its loads)
-        const bool vbc = ((reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) & 7) == 0;
+        // B and C staged per wave when N = 16, they are 8-byte aligned and a wave's 16
+        // channels share one group (chosen here: a branch on the alignment inside the kernel
+        // would drain its loads)
+        const bool vbc = ((reinterpret_cast<uintptr_t>(B) | reinterpret_cast<uintptr_t>(C)) & 7) == 0 &&
+                         ((int64_t)H * P / G) % 16 == 0;
 #define NSOSX_STEPR(ADT, SPL, GATE, V)                                                             \
     hipLaunchKernelGGL((scan_step_rows_kernel<ADT, SPL, GATE, V>), grid, block, 0, st, x, dt, A_log, \
                        a_per_state, B, C, D, z, rows, H, P, N, G, state, y);

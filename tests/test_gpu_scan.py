@@ -208,6 +208,29 @@ def test_step_bf16_config5(dev, orc, R, offset_bc):
     np.testing.assert_allclose(state.cpu().numpy(), wst, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("H,G", [(2048, 4), (96, 2), (2040, 3)])
+def test_step_bf16_groups(dev, orc, H, G):
+    """bf16 decode steps with several B / C groups (P = 1, N = 16, 37 rows): groups of 512 and
+    of 48 channels take the per-wave staged B / C (a workgroup of 64 channels spans two
+    groups of 48, each wave one), groups of 680 channels are not whole 16-channel waves and
+    take per-lane loads (2040 channels also leave a partial workgroup)."""
+    rng = np.random.default_rng(700 + H + G)
+    R, P, N = 37, 1, 16
+    inp = _inputs(rng, R, H, P, N, G, True)
+    rb = {k: (torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+              if k in ("x", "dt", "B", "C", "z") else v) for k, v in inp.items()}
+    st0 = rng.normal(0, 0.1, (R, H * P, N)).astype(np.float32)
+    state = _t(dev, st0)
+    bf = lambda k: _t(dev, inp[k], torch.bfloat16)
+    y = ops.selective_scan_step(bf("x"), bf("dt"), _t(dev, inp["a_log"]), bf("B"), bf("C"),
+                                _t(dev, inp["D"]), bf("z"), state, H, P, N, G)
+    wy, wst = orc.scan_step(rb["x"], rb["dt"], rb["a_log"], rb["B"], rb["C"], rb["D"], rb["z"],
+                            st0, H, P, N, G)
+    scale = np.abs(wy).max()
+    np.testing.assert_allclose(y.float().cpu().numpy(), wy, rtol=2e-2, atol=2e-2 * scale / 64)
+    np.testing.assert_allclose(state.cpu().numpy(), wst, rtol=RTOL, atol=ATOL)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_conv1d_matches_oracle(dev, orc, dtype):
     rng = np.random.default_rng(2)
