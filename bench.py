@@ -190,6 +190,14 @@ def bench_mamba2_prefill(torch, dev, reps=5, N=16):
                                      blk.a_log, res["B"], res["C"], blk.d_skip, None, cu, H, P, N,
                                      G, want_final=True)
     out["scan_ms"] = round(_time_ms(torch, scan, reps), 4)
+    # its roofline: f32 x in and y out per (token, channel), dt per (token, head), B and C
+    # per token, the final states; the per-state recurrence bounds it by issue, not HBM
+    S = int(cu.numel()) - 1
+    scan_bytes = (T * inner * 4 * 2 + T * H * 4 + 2 * T * gs * 4 + S * inner * N * 4
+                  + inner * (K + 1) * 4 + 2 * H * 4)
+    gbs = scan_bytes / (out["scan_ms"] / 1e3) / 1e9
+    out["scan_roofline"] = {"bound": "valu", "bytes": int(scan_bytes), "gbs": round(gbs, 1),
+                            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
     return out
 
 
