@@ -121,7 +121,7 @@ def test_skinny_mfma_bit_exact(dev, orc, m, n, k):
     _gemm_case(dev, orc, m, n, k, path=2, mag=(m % 2 == 1), bias=(n % 2 == 0))
 
 
-@pytest.mark.parametrize("m,k", [(9, 1024), (12, 2048), (16, 2048)])
+@pytest.mark.parametrize("m,k", [(9, 1024), (12, 2048), (16, 2048), (14, 4096)])
 @pytest.mark.parametrize("ydt", [torch.bfloat16, torch.float32])
 def test_skinny_runs_of_tiles_bit_exact(dev, orc, m, k, ydt):
     """9-16 token rows over a matrix wide enough that every wave takes runs of 4
