@@ -345,6 +345,42 @@ def test_chunked_scan_matches_oracle(dev, orc, conv, chunk, per_state, P, gate, 
     np.testing.assert_allclose(fin, fin0, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("D", [128, 2048])
+def test_chunked_auto_long_prefill(dev, orc, D):
+    """The bench's long prefill: one 32768-token bf16 sequence with the fused conv and the
+    chunk length the library picks (chunk_tokens = -1).  At 128 channels against the oracle
+    (fp32 on the bf16-rounded inputs: y within the bf16 bound, the final state within the fp32
+    bound); at the bench's 2048 channels against the sequential scan (y to one bf16 rounding,
+    the final state to 1e-5)."""
+    rng = np.random.default_rng(3 + D)
+    T, H, P, N, G = 32768, D, 1, 16, 1
+    inp = _inputs(rng, T, H, P, N, G, True)
+    rb = {k: (torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+              if k in ("x", "dt", "B", "C", "z") else v) for k, v in inp.items()}
+    w = (rng.standard_normal((D, 4)) * 0.5).astype(np.float32)
+    b = (rng.standard_normal(D) * 0.1).astype(np.float32)
+    cu = _cu([T])
+    bf = lambda k: _t(dev, inp[k], torch.bfloat16)
+    run = lambda ck: ops.conv_scan_fwd(bf("x"), _t(dev, w), _t(dev, b), bf("dt"),
+                                       _t(dev, inp["a_log"]), bf("B"), bf("C"), _t(dev, inp["D"]),
+                                       bf("z"), _t(dev, cu), H, P, N, G, chunk_tokens=ck,
+                                       want_final=True)
+    y, fin = run(-1)
+    y, fin = y.float().cpu().numpy(), fin.cpu().numpy()
+    if D == 128:
+        xc = orc.conv1d_causal(rb["x"], w, cu, bias=b, silu_act=True)
+        wy, wfin = orc.selective_scan(xc, rb["dt"], rb["a_log"], rb["B"], rb["C"], rb["D"],
+                                      rb["z"], cu, H, P, N, G, gate_silu=True)
+        scale = np.abs(wy).max()
+        np.testing.assert_allclose(y, wy, rtol=2e-2, atol=2e-2 * scale / 64)
+        np.testing.assert_allclose(fin, wfin, rtol=RTOL, atol=ATOL)
+    else:
+        y0, fin0 = run(0)
+        y0, fin0 = y0.float().cpu().numpy(), fin0.cpu().numpy()
+        np.testing.assert_allclose(y, y0, rtol=2 ** -7, atol=1e-6)
+        np.testing.assert_allclose(fin, fin0, rtol=1e-5, atol=1e-6)
+
+
 @pytest.mark.parametrize("chunk", [4, 37, 200])
 @pytest.mark.parametrize("N,per_state,conv_w", [(64, False, 4), (64, True, 0), (32, False, 7),
                                                  (32, True, 4), (40, False, 0)])
