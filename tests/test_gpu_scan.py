@@ -176,11 +176,11 @@ def test_step_matches_oracle_and_prefill(dev, orc, H, P, N, G, per_state):
     np.testing.assert_allclose(state.cpu().numpy(), fp, rtol=RTOL, atol=ATOL)
 
 
-@pytest.mark.parametrize("R,offset_bc", [(256, 0), (37, 0), (37, 1)])
+@pytest.mark.parametrize("R,offset_bc", [(256, 0), (37, 0), (37, 1), (1, 0), (3, 1)])
 def test_step_bf16_config5(dev, orc, R, offset_bc):
     """Config 5's decode step: bf16 x, dt, z, B, C against an fp32 state [R, 2048, 16]
-    (R = 256 is the bench's launch; 37 rows leave a partial row block; B and C one element
-    off 8-byte alignment take the two-byte loads).  The oracle runs in fp32 on the same
+    (R = 256 is the bench's launch; 37, 3 and 1 rows leave a partial row block; B and C one
+    element off 8-byte alignment take the two-byte loads).  The oracle runs in fp32 on the same
     bf16-rounded inputs; y within the bf16 bound, the state within the fp32 bound."""
     rng = np.random.default_rng(500 + R + offset_bc)
     H, P, N, G = 2048, 1, 16, 1
