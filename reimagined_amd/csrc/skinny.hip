@@ -61,7 +61,8 @@ __device__ __forceinline__ void transpose_rows4(uint32_t (&v)[4]) {
 // batch per run; the run's outputs are transposed across the four 16-lane rows so that
 // lane (g, li) holds tile g's 16 outputs of token li, and the four lanes of a token
 // store one whole 128-byte line of its bf16 output row (two lines for f32) where the
-// strided order stores 32-byte pieces of 16 rows.
+// strided order stores 32-byte pieces of 16 rows (bf16: regrouped so that each store
+// instruction covers 64 contiguous bytes of the row).
 template <int MT, int LT, int YDT, bool ACC_OUT, bool SQRELU, bool VEC4, bool ML = false,
           int RUN = 1>
 __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t* __restrict__ q,
@@ -306,15 +307,33 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
                         }
                         transpose_rows4(lo);
                         transpose_rows4(hi);
-                        // whole 128-byte lines, stored non-temporal (cache policy nt:
-                        // M = 16 at K = 2048 0.655 -> 0.676 of HBM; on the 32-byte row
-                        // pieces of the strided order the same hint is 20 % slower)
+                        // lane row g now holds tile g of the run: halves A (outputs 0-7) and
+                        // B (8-15); two more swaps give row g half g & 1 of tile g >> 1 (in A)
+                        // and of tile 2 + (g >> 1) (in B), so each store covers 64 contiguous
+                        // bytes of the token's row
+                        uint32_t A[4] = {lo[0], hi[0], lo[1], hi[1]};
+                        uint32_t Bh[4] = {lo[2], hi[2], lo[3], hi[3]};
 #pragma unroll
-                        for (int h = 0; h < 2; ++h)
+                        for (int d = 0; d < 4; ++d) {
+                            const auto p = __builtin_amdgcn_permlane16_swap(A[d], Bh[d], false, false);
+                            A[d] = p[0]; Bh[d] = p[1];
+                        }
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) {
+                            const auto p = __builtin_amdgcn_permlane32_swap(A[d], Bh[d], false, false);
+                            A[d] = p[0]; Bh[d] = p[1];
+                        }
+                        const int run0 = tile_of(t0 + 4 * qd);
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const int ti = t0 + 4 * qd + 2 * h + (g >> 1);
+                            const bool okh = ti < my_tiles && run0 + 2 * h + (g >> 1) < tiles && m < M;
+                            const uint32_t eh = static_cast<uint32_t>(m * pb.N + run0 * 16 + 32 * h + 8 * g);
+                            const uint32_t* d4 = h == 0 ? A : Bh;
                             __builtin_amdgcn_raw_buffer_store_b128(
-                                v4i{(int)lo[2 * h], (int)hi[2 * h], (int)lo[2 * h + 1],
-                                    (int)hi[2 * h + 1]},
-                                ry, ok ? (e + 8 * h) * 2u : 0x80000000u, 0, 2);
+                                v4i{(int)d4[0], (int)d4[1], (int)d4[2], (int)d4[3]},
+                                ry, okh ? eh * 2u : 0x80000000u, 0, 2);
+                        }
                     }
                 }
             }
