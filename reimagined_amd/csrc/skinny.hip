@@ -62,14 +62,18 @@ __device__ __forceinline__ void transpose_rows4(uint32_t (&v)[4]) {
 // lane (g, li) holds tile g's 16 outputs of token li, and the four lanes of a token
 // store one whole 128-byte line of its bf16 output row (two lines for f32) where the
 // strided order stores 32-byte pieces of 16 rows (bf16: regrouped so that each store
-// instruction covers 64 contiguous bytes of the row).
+// instruction covers 64 contiguous bytes of the row).  RUN = 2 (two m tiles, bf16 out,
+// N % 32 == 0): pairs of consecutive tiles in the two-tile batch's registers, the four
+// lanes of a token storing its 64 contiguous bytes with one instruction.
 template <int MT, int LT, int YDT, bool ACC_OUT, bool SQRELU, bool VEC4, bool ML = false,
           int RUN = 1>
 __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t* __restrict__ q,
                                             const float* __restrict__ act_scale, int M, void* y,
                                             int32_t* acc_out, int wave_id, int num_waves,
                                             char* lds) {
-    static_assert(RUN == 1 || (RUN % 4 == 0 && VEC4), "runs of tiles need whole 16-output tiles");
+    static_assert(RUN == 1 || (RUN % 4 == 0 && VEC4) ||
+                      (RUN == 2 && VEC4 && YDT == NSOSX_BF16 && !ACC_OUT),
+                  "runs of tiles need whole 16-output tiles");
     constexpr int Q = 4 * LT;                       // words per lane per tile (MFMA steps)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -257,6 +261,31 @@ __device__ __forceinline__ void skinny_body(const GemvProblem& pb, const int8_t*
                 bs_cur[r] = bs_nxt[r];
             }
         }
+        if constexpr (RUN == 2) {
+            // a pair of consecutive tiles: row g of the lane rows holds outputs 4 g .. 4 g + 3
+            // of both (two packed dwords each); a permlane32 then a permlane16 swap give row g
+            // outputs 8 (g & 1) .. + 7 of tile g >> 1, so the four lanes of a token store
+            // its 64 contiguous bytes with one instruction (non-temporal)
+            const int run0 = tile_of(t0);
+            const int ti = t0 + (g >> 1);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int m = mt * 16 + li;
+                uint32_t a[2] = {pk[0][mt][0], pk[0][mt][1]}, b[2] = {pk[1][mt][0], pk[1][mt][1]};
+#pragma unroll
+                for (int d = 0; d < 2; ++d) {
+                    const auto p = __builtin_amdgcn_permlane32_swap(a[d], b[d], false, false);
+                    const auto s = __builtin_amdgcn_permlane16_swap(p[0], p[1], false, false);
+                    a[d] = s[0];
+                    b[d] = s[1];
+                }
+                const bool ok = ti < my_tiles && run0 + (g >> 1) < tiles && m < M;
+                const uint32_t e = static_cast<uint32_t>(m * pb.N + (run0 + (g >> 1)) * 16 + 8 * (g & 1));
+                __builtin_amdgcn_raw_buffer_store_b128(v4i{(int)a[0], (int)a[1], (int)b[0], (int)b[1]},
+                                                       ry, ok ? e * 2u : 0x80000000u, 0, 2);
+            }
+            continue;
+        }
         if constexpr (RUN > 1) {
 #pragma unroll
             for (int qd = 0; qd < RUN / 4; ++qd) {
@@ -439,6 +468,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     // better; at two m tiles, or with the int32 sums out, the run's registers spill)
     if (MT == 1 && !ACC_OUT && M > 8 && (pb.N & 15) == 0 && ((pb.N >> 4) + 3) / 4 >= num_waves)
         skinny_body<MT, LT, YDT, ACC_OUT, false, true, ML, MT == 1 ? 4 : 1>(
+            pb, q, act_scale, M, y, acc_out, wave_id, num_waves, lds_sk);
+    else if (MT == 2 && YDT == NSOSX_BF16 && !ACC_OUT && (pb.N & 31) == 0 &&
+             ((pb.N >> 4) + 1) / 2 >= num_waves)
+        skinny_body<MT, LT, YDT, ACC_OUT, false, true, ML,
+                    (MT == 2 && YDT == NSOSX_BF16 && !ACC_OUT) ? 2 : 1>(
             pb, q, act_scale, M, y, acc_out, wave_id, num_waves, lds_sk);
     else if ((pb.N & 3) == 0)
         skinny_body<MT, LT, YDT, ACC_OUT, false, true, ML>(pb, q, act_scale, M, y, acc_out,

@@ -121,14 +121,16 @@ def test_skinny_mfma_bit_exact(dev, orc, m, n, k):
     _gemm_case(dev, orc, m, n, k, path=2, mag=(m % 2 == 1), bias=(n % 2 == 0))
 
 
-@pytest.mark.parametrize("m,k", [(9, 1024), (12, 2048), (16, 2048), (14, 4096)])
+@pytest.mark.parametrize("m,k", [(9, 1024), (12, 2048), (16, 2048), (14, 4096), (17, 2048),
+                                 (24, 1024), (32, 2048)])
 @pytest.mark.parametrize("ydt", [torch.bfloat16, torch.float32])
 def test_skinny_runs_of_tiles_bit_exact(dev, orc, m, k, ydt):
     """9-16 token rows over a matrix wide enough that every wave takes runs of 4
     consecutive tiles with whole-line output stores (N = 140000: 8750 tiles, a partial last
-    run), on the reference words (path 2) and the MFMA layout: equal bit for bit to the MFMA
-    GEMM (path 1) on the same inputs, and to the oracle's dequantized sums on sampled
-    columns (first, last and the partial run's)."""
+    run), and 17-32 rows (two m tiles: bf16 outputs in runs of 2 tiles), on the reference
+    words (path 2) and the MFMA layout: equal bit for bit to the MFMA GEMM (path 1) on the
+    same inputs, and to the oracle's dequantized sums on sampled columns (first, last and
+    the partial run's)."""
     rng = np.random.default_rng(m * 7 + k + (ydt == torch.float32))
     n = 140000
     words = torch.randint(-2**31, 2**31 - 1, (n * k // 16,), dtype=torch.int32, device=dev)
