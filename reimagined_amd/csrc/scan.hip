@@ -322,24 +322,31 @@ __global__ __launch_bounds__(256) void scan_fwd_kernel(
 
 // ===========================================================================
 // Prefill scan, quad form (N <= 16, conv width <= 4).  A workgroup is one
-// wave: 16 channels x 4 state quads, lane = 4 * channel + quad, each lane
-// holding SPL = N/4 (rounded up) states in registers.  The wave walks its
-// sequence in groups of 4 tokens.  Lane q of a channel forms the
-// per-(token, channel) terms of token r0 + q only: the causal convolution
-// (its window read from an 8-slot LDS row holding the previous and this
-// group's raw inputs), bias + SiLU, delta = softplus(dt) and delta * x; a 32-byte exchange
-// through the wave's LDS slice then hands every lane all four tokens' delta and
-// delta * x (two reads instead of eight VALU broadcasts).  The recurrence runs
-// the four tokens, the 4x4 transpose-reduce leaves lane q with the readout of token
-// r0 + q, and lane q applies the D skip and the SiLU(z) gate and writes it to the
-// chunk's output rows in LDS; a finished 32-token chunk leaves with one 16-byte
-// store per lane.  B and C (shared by all channels of a group) are staged per
-// 32-token chunk in the wave's own LDS slice, converted to float once.  The
+// wave: 16 channels x 4 state quads, each lane holding SPL = N/4 (rounded up)
+// states in registers; lane = 4 * channel + quad, or with 16 states (SPL = 4)
+// lane = channel + 16 * quad.  The wave walks its sequence in groups of 4
+// tokens.  Lane q of a channel forms the per-(token, channel) terms of token
+// r0 + q only: the causal convolution (its window read from an 8-slot LDS row
+// holding the previous and this group's raw inputs), bias + SiLU, delta =
+// softplus(dt) and delta * x; an exchange through the wave's LDS slice then
+// hands every lane all four tokens' delta (and delta * x, below 16 states).
+// With 16 states the group's delta * x (x) B terms come from one 4-block
+// 16 x 16 x 1 f32 MFMA (block k: B of token r0 + k times the lanes' delta * x
+// of token r0 + k), whose accumulator layout is the lane layout above: each
+// lane receives exactly its 4 states x 4 tokens, the same rounded products as
+// 16 multiplies, and the VALU is left the decays, the state updates and the
+// readout.  The recurrence runs the four tokens, the 4x4 transpose-reduce
+// leaves lane q with the readout of token r0 + q, and lane q applies the D
+// skip and the SiLU(z) gate and writes it to the chunk's output rows in LDS; a
+// finished 32-token chunk leaves with one 16-byte store per lane.  B and C
+// (shared by all channels of a group) are staged per 32-token chunk in the
+// wave's own LDS slice, converted to float once.  The
 // workgroup is one wave, so its barriers cost no waiting: the raw inputs of a
 // group are loaded into registers two groups ahead (two register sets that even
 // and odd groups alternate, so no copy waits on a load in flight) and the B/C rows
 // of the next chunk one chunk ahead.
 // ===========================================================================
+typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int kQuadTC = 32;       // tokens per B/C chunk
 constexpr int kQuadCh = 16;       // channels per wave
 constexpr int kQuadMaxW = 4;
@@ -406,6 +413,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
     __shared__ __align__(16) float s_bc[2][kQuadTC][NP];
     __shared__ __align__(16) float s_red[kQuadCh * kQuadRedStride];
     __shared__ __align__(16) float2 s_dx[kQuadCh][4];  // {delta, delta * x} of the group's 4 tokens
+    __shared__ __align__(16) float s_dl[kQuadCh][4];   // MF: delta of the group's 4 tokens
     __shared__ float s_xw[kQuadCh][8];  // conv window: raw x of the previous and this group
     __shared__ __align__(16) float s_out[kQuadTC][kQuadOutStride];  // the chunk's outputs
     __shared__ int s_pick;
@@ -413,14 +421,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
     const int lane = threadIdx.x;
     const int D = H * P;
     const int GN = G * N;
-    const int q = lane & 3;
+    // MF (16 states): lane = channel + 16 * state quad, the accumulator layout of the
+    // 4-block 16 x 16 x 1 f32 MFMA that forms a group's four (delta * x) (x) B products
+    constexpr bool MF = SPL == 4;
+    const int q = MF ? lane >> 4 : lane & 3;
+    const int cl = MF ? lane & 15 : lane >> 2;  // channel of the wave
     // readout transpose slots: channel row of kQuadRedStride floats, state lane j's
     // partial of token k at 4 j + k (row stride padded against bank conflicts)
-    const int red_w = (lane >> 2) * kQuadRedStride + 4 * q;
-    const int red_r = (lane >> 2) * kQuadRedStride + q;
+    const int red_w = cl * kQuadRedStride + 4 * q;
+    const int red_r = cl * kQuadRedStride + q;
     int rank, cblk;
     quad_work_item(rank, cblk);
-    const int c = cblk * kQuadCh + (lane >> 2);
+    const int c = cblk * kQuadCh + cl;
     const int h = c / P;
     const int grp = (h * G) / H;
     // uniform across the wave: keeps the token bases in scalar registers
@@ -573,7 +585,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
             if (tt >= plan.seq_start[seq] && tt >= 0)
                 w0 = load_act<ADT>(x, (int64_t)tt * x_stride + c);
         }
-        s_xw[lane >> 2][q] = w0;
+        s_xw[cl][q] = w0;
     }
     // the group whose readout is pending: its conv output, raw gate and base token
     float pv_xv = 0.0f;
@@ -588,7 +600,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
     auto finish_readout = [&](float tot) {
         float out = __fmaf_rn(dsk, pv_xv, tot);
         if (GATE) out = out * silu_fast(raw_to_f32<ADT>(pv_z));
-        s_out[((pv_t - t0) & (kQuadTC - 1)) + q][lane >> 2] = out;
+        s_out[((pv_t - t0) & (kQuadTC - 1)) + q][cl] = out;
     };
     // lane l stores token row l / 2 of the chunk at tbase, channels 8 (l % 2) .. + 7
     auto flush_out = [&](int tbase) {
@@ -634,9 +646,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
             for (int k = 0; k < 4; ++k)
 #pragma unroll
                 for (int i = 0; i < SPL; ++i) {
-                    bq[k][i] = s_bc[0][r0 + k][q * SPL + i];
+                    bq[k][i] = MF ? 0.0f : s_bc[0][r0 + k][q * SPL + i];
                     cq[k][i] = LOCAL ? 0.0f : s_bc[1][r0 + k][q * SPL + i];
                 }
+            // MF: the MFMA's A operand, B of token r0 + q at state cl
+            const float bA = MF ? s_bc[0][r0 + q][cl] : 0.0f;
             // the previous group's readout partials (written at the end of that group)
             float rd0 = 0.0f, rd1 = 0.0f, rd2 = 0.0f, rd3 = 0.0f;
             if constexpr (!LOCAL) {
@@ -657,7 +671,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
                 // slot q + 1 + j.  LDS operations of one wave complete in order; the
                 // compiler barriers keep the other lanes' slots from being read before
                 // this group's write or overwritten before the reads.
-                float* row = s_xw[lane >> 2];
+                float* row = s_xw[cl];
                 row[4 + q] = xcur;
                 asm volatile("" ::: "memory");
                 float acc = 0.0f;
@@ -673,12 +687,28 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
             const float dl = valid ? sp : 0.0f;
             const float dx = dl * xv;
             // the quad's four tokens through the wave's LDS slice (LDS operations of one
-            // wave complete in order): two reads instead of eight VALU broadcasts
-            s_dx[lane >> 2][q] = make_float2(dl, dx);
-            const float4 t01 = *reinterpret_cast<const float4*>(&s_dx[lane >> 2][0]);
-            const float4 t23 = *reinterpret_cast<const float4*>(&s_dx[lane >> 2][2]);
-            const float dlk[4] = {t01.x, t01.z, t23.x, t23.z};
-            const float dxk[4] = {t01.y, t01.w, t23.y, t23.w};
+            // wave complete in order): one or two reads instead of VALU broadcasts
+            float dlk[4], dxk[4];
+            v16f op = {};
+            if constexpr (MF) {
+                // block k of the MFMA: B of token r0 + k (A operand, row = state) times
+                // delta * x of token r0 + k (B operand, column = channel: lanes 16 k ..
+                // 16 k + 15 formed token r0 + k); lane (channel cl, quad q) receives the
+                // products for its states 4 q .. 4 q + 3 in registers 4 k .. 4 k + 3.
+                // K = 1 and a zero accumulator: each is the rounded product dx * B.
+                op = __builtin_amdgcn_mfma_f32_16x16x1f32(bA, dx, v16f{}, 0, 0, 0);
+                s_dl[cl][q] = dl;
+                const float4 t = *reinterpret_cast<const float4*>(&s_dl[cl][0]);
+                dlk[0] = t.x; dlk[1] = t.y; dlk[2] = t.z; dlk[3] = t.w;
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) dxk[kk] = 0.0f;
+            } else {
+                s_dx[cl][q] = make_float2(dl, dx);
+                const float4 t01 = *reinterpret_cast<const float4*>(&s_dx[cl][0]);
+                const float4 t23 = *reinterpret_cast<const float4*>(&s_dx[cl][2]);
+                dlk[0] = t01.x; dlk[1] = t01.z; dlk[2] = t23.x; dlk[3] = t23.z;
+                dxk[0] = t01.y; dxk[1] = t01.w; dxk[2] = t23.y; dxk[3] = t23.w;
+            }
             // ---- recurrence over the group's four tokens: all decays first --------
             // (PH, one A per head: every state of the channel decays alike, one exp per
             // token; padded states carry B = C = 0, so their shared decay is harmless)
@@ -703,7 +733,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void sc
                 float p = 0.0f;
 #pragma unroll
                 for (int i = 0; i < SPL; ++i) {
-                    st[i] = __fmaf_rn(a[k][i], st[i], dxk[k] * bq[k][i]);
+                    st[i] = __fmaf_rn(a[k][i], st[i], MF ? op[4 * k + i] : dxk[k] * bq[k][i]);
                     if constexpr (!LOCAL) p = __fmaf_rn(st[i], cq[k][i], p);
                 }
                 part[k] = p;
