@@ -231,15 +231,17 @@ def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=3
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "kernel": name, "algorithmic_bytes": int(amount)}
         if name in ("conv_scan", "scan"):
-            # 16 exp + 64 VALU ops per (token, channel) are irreducible (one exp per state and
-            # four FMA-class ops); at T*d_inner pairs this issue time exceeds the HBM time
+            # per (token, channel, state) the VALU must issue one exp (two FMA slots), delta * A,
+            # the state FMA and the readout FMA; the (delta * x) * B products are formed on the
+            # matrix core.  At T*d_inner pairs this issue time exceeds the HBM time
             pairs = T * d_inner
-            issue_s = pairs * d_state * (2 + 4) * 4 / 64 / 1024 / 2.4e9
+            issue_s = pairs * d_state * (2 + 3) * 4 / 64 / 1024 / 2.4e9
             roof["valu_issue_bound_ms"] = round(issue_s * 1e3, 4)
             roof["valu_issue_frac"] = round(issue_s / sec, 4)
             roof["valu_busy_pct_measured"] = pmc_valu_busy("conv + scan")
             roof["note"] = ("VALU/transcendental-issue bound, not HBM: the recurrence alone needs "
-                            f"{issue_s * 1e3:.3f} ms of issue at 2.4 GHz (exp = 2 FMA slots) "
+                            f"{issue_s * 1e3:.3f} ms of VALU issue at 2.4 GHz (exp = 2 FMA slots, "
+                            "the dx*B products on the matrix core) "
                             f"against {amount / HBM_PEAK_GBS / 1e6:.3f} ms of HBM time; "
                             "valu_issue_frac = that bound / the kernel's time; "
                             "valu_busy_pct_measured = rocprofv3 VALUBusy of the kernel "
