@@ -58,6 +58,8 @@ def _run(dev, orc, inp, cu, H, P, N, G, gate=True, init=None, dtype=torch.float3
     (128, 1, 16, 1, True, [5, 64, 1, 33, 100]),   # ragged, lengths not multiples of 4
     (2, 64, 16, 1, False, [40, 7]),               # reference faithful: per-head A, P = 64
     (64, 1, 8, 1, True, [17]),                    # N = 8
+    (64, 1, 13, 1, True, [21, 6]),                # N = 13: 16-state lanes, 3 padded states
+    (2, 64, 14, 1, False, [40, 7]),               # per-head A, 2 padded states
     (4, 32, 16, 2, False, [9, 30]),               # G = 2, one group per workgroup
     (32, 1, 4, 1, True, [9, 22]),                 # N = 4: one state per lane
     (16, 2, 16, 2, False, [18, 5]),               # 16 channels per group
@@ -262,6 +264,7 @@ def test_scan_rejects_float_cu_seqlens(dev):
     (torch.bfloat16, [200, 3, 77], 128, 16, 4),
     (torch.float32, [2, 31, 6], 48, 16, 3),      # 48 channels: 16-channel waves only
     (torch.float32, [1, 9, 40], 64, 8, 2),
+    (torch.bfloat16, [9, 30], 64, 15, 4),        # N = 15: one padded state
     (torch.float32, [7, 50], 64, 16, 6),        # width 6 -> LDS-staged kernel
     (torch.float32, [3, 26], 64, 32, 4),        # N = 32 -> LDS-staged kernel
 ])
