@@ -241,7 +241,8 @@ def layer_roofline(T, stages, d_model=1024, d_inner=2048, d_state=16, num_seqs=3
             roof["valu_busy_pct_measured"] = pmc_valu_busy("conv + scan")
             roof["note"] = ("VALU/transcendental-issue bound, not HBM: the recurrence alone needs "
                             f"{issue_s * 1e3:.3f} ms of VALU issue at 2.4 GHz (exp = 2 FMA slots, "
-                            "the dx*B products on the matrix core) "
+                            "the dx*B products on the matrix core; "
+                            f"{issue_s * 6 / 5 * 1e3:.3f} ms with them on the VALU) "
                             f"against {amount / HBM_PEAK_GBS / 1e6:.3f} ms of HBM time; "
                             "valu_issue_frac = that bound / the kernel's time; "
                             "valu_busy_pct_measured = rocprofv3 VALUBusy of the kernel "
